@@ -1,0 +1,335 @@
+// bindings.cpp — the pybind11 module `custom_rasterizer_cuda`: the reference's
+// six-function surface (csrc/bindings.cpp:141-153 of kmurungi/custom-3dgs-cuda)
+// with the same positional arguments, tensor layouts, return tuples, checks
+// and messages, implemented over the C ABI of libgsraster.so.  Outputs come
+// from torch's caching allocator on the inputs' device; every launch goes on
+// torch's current HIP stream.
+#include <torch/extension.h>
+
+#include <ATen/hip/impl/HIPGuardImplMasqueradingAsCUDA.h>
+#include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
+
+#include <tuple>
+
+#include "../../include/gsraster.h"
+
+namespace {
+
+using torch::Tensor;
+
+// The reference's validation macros (csrc/cuda_check.h:23-47).
+#define CHECK_CUDA(tensor) TORCH_CHECK((tensor).is_cuda(), #tensor " must be a CUDA tensor")
+#define CHECK_CONTIGUOUS(tensor) TORCH_CHECK((tensor).is_contiguous(), #tensor " must be contiguous")
+#define CHECK_FP32(tensor) \
+    TORCH_CHECK((tensor).scalar_type() == torch::kFloat32, #tensor " must be FP32")
+#define CHECK_INT32(tensor) \
+    TORCH_CHECK((tensor).scalar_type() == torch::kInt32, #tensor " must be int32")
+#define CHECK_INPUT_FP32(tensor) \
+    do {                         \
+        CHECK_CUDA(tensor);      \
+        CHECK_CONTIGUOUS(tensor);\
+        CHECK_FP32(tensor);      \
+    } while (0)
+#define CHECK_INPUT_INT32(tensor) \
+    do {                          \
+        CHECK_CUDA(tensor);       \
+        CHECK_CONTIGUOUS(tensor); \
+        CHECK_INT32(tensor);      \
+    } while (0)
+
+void check_rc(int rc, const char* what) {
+    TORCH_CHECK(rc == GSR_OK, "custom_rasterizer_cuda.", what, ": ", gsr_last_error());
+}
+
+void* current_stream() {
+    return static_cast<void*>(c10::hip::getCurrentHIPStreamMasqueradingAsCUDA().stream());
+}
+
+float* fp(const Tensor& t) { return t.data_ptr<float>(); }
+const float* cfp(const Tensor& t) { return t.data_ptr<float>(); }
+
+Tensor workspace(int64_t bytes, const Tensor& like) {
+    return torch::empty({std::max<int64_t>(bytes, 1)},
+                        torch::TensorOptions().dtype(torch::kUInt8).device(like.device()));
+}
+
+void check_numel(const Tensor& t, int64_t want, const char* msg) {
+    TORCH_CHECK(t.numel() >= want, msg);
+}
+
+// ---- project (bindings.cpp:12-29 / projection.cu:109-153) ----
+std::tuple<Tensor, Tensor, Tensor> project(int total_gaussians, const Tensor mu3d,
+                                           const Tensor q3d, const Tensor s3d,
+                                           const Tensor camera_rotation,
+                                           const Tensor camera_translation, float fx, float fy,
+                                           float cx, float cy) {
+    CHECK_INPUT_FP32(mu3d);
+    CHECK_INPUT_FP32(q3d);
+    CHECK_INPUT_FP32(s3d);
+    CHECK_INPUT_FP32(camera_rotation);
+    CHECK_INPUT_FP32(camera_translation);
+    TORCH_CHECK(total_gaussians >= 0, "total_gaussians must be non-negative");
+    const int64_t n = total_gaussians;
+    check_numel(mu3d, 3 * n, "mu3d must hold N x 3 values");
+    check_numel(q3d, 4 * n, "q3d must hold N x 4 values");
+    check_numel(s3d, 3 * n, "s3d must hold N x 3 values");
+    check_numel(camera_rotation, 9, "camera_rotation must hold 3 x 3 values");
+    check_numel(camera_translation, 3, "camera_translation must hold 3 values");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(mu3d.device());
+    auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mu3d.device());
+    Tensor mean_2d = torch::empty({n, 2}, options);
+    Tensor cov_2d = torch::empty({n, 3}, options);
+    Tensor depths = torch::empty({n}, options);
+    check_rc(gsr_project(total_gaussians, cfp(mu3d), cfp(q3d), cfp(s3d), cfp(camera_rotation),
+                         cfp(camera_translation), fx, fy, cx, cy, fp(mean_2d), fp(cov_2d),
+                         fp(depths), current_stream()),
+             "project");
+    return {mean_2d, cov_2d, depths};
+}
+
+// ---- SH (bindings.cpp:32-46 / SH.cu:95-131) ----
+Tensor spherical_harmonics(int total_gaussians, const Tensor camera_position,
+                           const Tensor mu_world, const Tensor albedo_coeff,
+                           const Tensor illumination_coeff) {
+    CHECK_INPUT_FP32(camera_position);
+    CHECK_INPUT_FP32(mu_world);
+    CHECK_INPUT_FP32(albedo_coeff);
+    CHECK_INPUT_FP32(illumination_coeff);
+    TORCH_CHECK(camera_position.numel() >= 3, "camera_position must have 3 elements");
+    TORCH_CHECK(total_gaussians >= 0, "total_gaussians must be non-negative");
+    const int64_t n = total_gaussians;
+    check_numel(mu_world, 3 * n, "mu_world must hold N x 3 values");
+    check_numel(albedo_coeff, 3 * n, "albedo_coeff must hold N x 3 values");
+    check_numel(illumination_coeff, 45 * n, "illumination_coeff must hold N x 15 x 3 values");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(mu_world.device());
+    auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mu_world.device());
+    Tensor colors = torch::empty({n, 3}, options);
+    check_rc(gsr_sh(total_gaussians, cfp(camera_position), cfp(mu_world), cfp(albedo_coeff),
+                    cfp(illumination_coeff), fp(colors), current_stream()),
+             "SH");
+    return colors;
+}
+
+// ---- rasterize (bindings.cpp:50-70 / rasterize.cu:284-487) ----
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_impl(
+    int num_gaussians, const Tensor& depths, const Tensor& mean_2d, const Tensor& cov_2d,
+    const Tensor& colors, const Tensor& alpha, int height, int width, bool want_keys) {
+    TORCH_CHECK(height >= 0 && width >= 0, "height and width must be non-negative");
+    auto device = mean_2d.device();
+    auto float_options = torch::TensorOptions().dtype(torch::kFloat32).device(device);
+    auto int_options = torch::TensorOptions().dtype(torch::kInt32).device(device);
+    auto key_options = torch::TensorOptions().dtype(torch::kInt64).device(device);
+    const int64_t tiles = (int64_t)((width + 15) / 16) * ((height + 15) / 16);
+    auto empty_buffers = [&]() {
+        return std::make_tuple(torch::zeros({height, width, 3}, float_options),
+                               torch::empty({0}, int_options),
+                               torch::zeros({tiles, 2}, int_options),
+                               torch::ones({height, width}, float_options),
+                               torch::zeros({height, width}, int_options),
+                               torch::empty({0}, key_options));
+    };
+    if (num_gaussians == 0) return empty_buffers();
+
+    CHECK_INPUT_FP32(depths);
+    CHECK_INPUT_FP32(mean_2d);
+    CHECK_INPUT_FP32(cov_2d);
+    CHECK_INPUT_FP32(colors);
+    CHECK_INPUT_FP32(alpha);
+    TORCH_CHECK(num_gaussians > 0, "num_gaussians must be non-negative");
+    TORCH_CHECK(mean_2d.dim() == 2 && mean_2d.size(0) == num_gaussians && mean_2d.size(1) == 2,
+                "mean_2d must have shape (N, 2)");
+    TORCH_CHECK(cov_2d.dim() == 2 && cov_2d.size(0) == num_gaussians && cov_2d.size(1) == 3,
+                "cov_2d must have shape (N, 3) upper-triangular [a, b, c]");
+    TORCH_CHECK(colors.dim() == 2 && colors.size(0) == num_gaussians && colors.size(1) == 3,
+                "colors must have shape (N, 3)");
+    TORCH_CHECK(depths.numel() == num_gaussians, "depths must have N elements");
+    TORCH_CHECK(alpha.numel() == num_gaussians, "alpha must have N elements");
+
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
+    void* st = current_stream();
+    Tensor bin_ws = workspace((int64_t)gsr_bin_workspace_bytes(num_gaussians, height, width),
+                              mean_2d);
+    int64_t m = 0;
+    check_rc(gsr_rasterize_bin(num_gaussians, cfp(depths), cfp(mean_2d), cfp(cov_2d), height,
+                               width, bin_ws.data_ptr(), (size_t)bin_ws.numel(), &m, st),
+             "rasterize");
+    if (m == 0) return empty_buffers();
+
+    Tensor sort_ws = workspace(
+        (int64_t)gsr_sort_workspace_bytes(m, num_gaussians, height, width), mean_2d);
+    Tensor sorted_ids = torch::empty({m}, int_options);
+    Tensor tile_ranges = torch::empty({tiles, 2}, int_options);
+    Tensor rendered_img = torch::empty({height, width, 3}, float_options);
+    Tensor final_T = torch::empty({height, width}, float_options);
+    Tensor n_contrib = torch::empty({height, width}, int_options);
+    Tensor sorted_keys = want_keys ? torch::empty({m}, key_options) : torch::empty({0}, key_options);
+    check_rc(gsr_rasterize_render(
+                 num_gaussians, cfp(depths), cfp(mean_2d), cfp(cov_2d), cfp(colors), cfp(alpha),
+                 height, width, bin_ws.data_ptr(), (size_t)bin_ws.numel(), m,
+                 sort_ws.data_ptr(), (size_t)sort_ws.numel(), sorted_ids.data_ptr<int32_t>(),
+                 tile_ranges.data_ptr<int32_t>(), fp(rendered_img), fp(final_T),
+                 n_contrib.data_ptr<int32_t>(),
+                 want_keys ? reinterpret_cast<uint64_t*>(sorted_keys.data_ptr<int64_t>()) : nullptr,
+                 st),
+             "rasterize");
+    return {rendered_img, sorted_ids, tile_ranges, final_T, n_contrib, sorted_keys};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> rasterize(int num_gaussians,
+                                                             const Tensor depths,
+                                                             const Tensor mean_2d,
+                                                             const Tensor cov_2d,
+                                                             const Tensor colors,
+                                                             const Tensor alpha, int height,
+                                                             int width) {
+    auto r = rasterize_impl(num_gaussians, depths, mean_2d, cov_2d, colors, alpha, height, width,
+                            false);
+    return {std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<3>(r), std::get<4>(r)};
+}
+
+// Not in the reference surface: `rasterize` plus the 64-bit sorted keys
+// (tile << 32 | depth bits) the reference sorts internally, for bit-exact
+// parity checks of the sort.
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_with_keys(
+    int num_gaussians, const Tensor depths, const Tensor mean_2d, const Tensor cov_2d,
+    const Tensor colors, const Tensor alpha, int height, int width) {
+    return rasterize_impl(num_gaussians, depths, mean_2d, cov_2d, colors, alpha, height, width,
+                          true);
+}
+
+// ---- backwards_rasterization (bindings.cpp:72-100 / rasterize_backward.cu:239-309) ----
+std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization(
+    const Tensor grad_output, const Tensor mean_2d, const Tensor cov_2d, const Tensor colors,
+    const Tensor alpha, const Tensor sorted_ids, const Tensor tile_ranges, const Tensor final_T,
+    const Tensor n_contrib, int num_gaussians, int height, int width) {
+    CHECK_INPUT_FP32(grad_output);
+    CHECK_INPUT_FP32(mean_2d);
+    CHECK_INPUT_FP32(cov_2d);
+    CHECK_INPUT_FP32(colors);
+    CHECK_INPUT_FP32(alpha);
+    CHECK_INPUT_FP32(final_T);
+    CHECK_INPUT_INT32(sorted_ids);
+    CHECK_INPUT_INT32(tile_ranges);
+    CHECK_INPUT_INT32(n_contrib);
+    TORCH_CHECK(mean_2d.dim() == 2 && mean_2d.size(0) == num_gaussians && mean_2d.size(1) == 2,
+                "mean_2d must have shape (N, 2)");
+    TORCH_CHECK(cov_2d.dim() == 2 && cov_2d.size(0) == num_gaussians && cov_2d.size(1) == 3,
+                "cov_2d must have shape (N, 3)");
+    TORCH_CHECK(colors.dim() == 2 && colors.size(0) == num_gaussians && colors.size(1) == 3,
+                "colors must have shape (N, 3)");
+    TORCH_CHECK(alpha.numel() == num_gaussians, "alpha must have N elements");
+    TORCH_CHECK(final_T.numel() == (int64_t)height * width, "final_T must have H*W elements");
+    TORCH_CHECK(n_contrib.numel() == (int64_t)height * width, "n_contrib must have H*W elements");
+    TORCH_CHECK(grad_output.numel() == (int64_t)height * width * 3,
+                "grad_output must have H*W*3 elements");
+    const int64_t tiles = (int64_t)((width + 15) / 16) * ((height + 15) / 16);
+    TORCH_CHECK(tile_ranges.numel() >= 2 * tiles, "tile_ranges must have T x 2 elements");
+
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(mean_2d.device());
+    auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mean_2d.device());
+    Tensor grad_mean_2d = torch::empty({num_gaussians, 2}, options);
+    Tensor grad_cov_2d = torch::empty({num_gaussians, 3}, options);
+    Tensor grad_colors = torch::empty({num_gaussians, 3}, options);
+    Tensor grad_alpha = torch::empty({num_gaussians, 1}, options);
+    Tensor ws = workspace((int64_t)gsr_backward_workspace_bytes(num_gaussians), mean_2d);
+    check_rc(gsr_rasterize_backward(
+                 num_gaussians, height, width, cfp(grad_output), cfp(mean_2d), cfp(cov_2d),
+                 cfp(colors), cfp(alpha), sorted_ids.data_ptr<int32_t>(), sorted_ids.numel(),
+                 tile_ranges.data_ptr<int32_t>(), cfp(final_T), n_contrib.data_ptr<int32_t>(),
+                 ws.data_ptr(), (size_t)ws.numel(), fp(grad_mean_2d), fp(grad_cov_2d),
+                 fp(grad_colors), fp(grad_alpha), current_stream()),
+             "backwards_rasterization");
+    return {grad_mean_2d, grad_cov_2d, grad_colors, grad_alpha};
+}
+
+// ---- backwards_SH (bindings.cpp:102-116 / delight_backward.cu:176-218) ----
+std::tuple<Tensor, Tensor, Tensor> backwards_SH(const Tensor colors_grad, const Tensor mu,
+                                                const Tensor albedo, const Tensor k_j,
+                                                const Tensor camera_position) {
+    CHECK_INPUT_FP32(colors_grad);
+    CHECK_INPUT_FP32(mu);
+    CHECK_INPUT_FP32(albedo);
+    CHECK_INPUT_FP32(k_j);
+    CHECK_INPUT_FP32(camera_position);
+    TORCH_CHECK(camera_position.numel() >= 3, "camera_position must have 3 elements");
+    const int64_t n = mu.size(0);
+    check_numel(colors_grad, 3 * n, "colors_grad must hold N x 3 values");
+    check_numel(albedo, 3 * n, "albedo must hold N x 3 values");
+    check_numel(k_j, 45 * n, "k_j must hold N x 15 x 3 values");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(mu.device());
+    auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mu.device());
+    Tensor albedo_grad = torch::empty({n, 3}, options);
+    Tensor k_j_grad = torch::empty({n, 15, 3}, options);
+    Tensor mu_grad = torch::empty({n, 3}, options);
+    check_rc(gsr_sh_backward((int)n, cfp(colors_grad), cfp(mu), cfp(albedo), cfp(k_j),
+                             cfp(camera_position), fp(albedo_grad), fp(k_j_grad), fp(mu_grad),
+                             current_stream()),
+             "backwards_SH");
+    return {albedo_grad, k_j_grad, mu_grad};
+}
+
+// ---- backwards_projection (bindings.cpp:118-138 / projection_backward.cu:142-187) ----
+std::tuple<Tensor, Tensor, Tensor> backwards_projection(
+    const Tensor mean_2d_grad, const Tensor cov_2d_grad, const Tensor mu, const Tensor q,
+    const Tensor s, const Tensor camera_rotation, const Tensor camera_translation, float fx,
+    float fy, float cx, float cy) {
+    CHECK_INPUT_FP32(mean_2d_grad);
+    CHECK_INPUT_FP32(cov_2d_grad);
+    CHECK_INPUT_FP32(mu);
+    CHECK_INPUT_FP32(q);
+    CHECK_INPUT_FP32(s);
+    CHECK_INPUT_FP32(camera_rotation);
+    CHECK_INPUT_FP32(camera_translation);
+    const int64_t n = mu.size(0);
+    check_numel(mean_2d_grad, 2 * n, "mean_2d_grad must hold N x 2 values");
+    check_numel(cov_2d_grad, 3 * n, "cov_2d_grad must hold N x 3 values");
+    check_numel(q, 4 * n, "q must hold N x 4 values");
+    check_numel(s, 3 * n, "s must hold N x 3 values");
+    check_numel(camera_rotation, 9, "camera_rotation must hold 3 x 3 values");
+    check_numel(camera_translation, 3, "camera_translation must hold 3 values");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(mu.device());
+    auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mu.device());
+    Tensor mu_grad = torch::empty({n, 3}, options);
+    Tensor q_grad = torch::empty({n, 4}, options);
+    Tensor s_grad = torch::empty({n, 3}, options);
+    check_rc(gsr_project_backward((int)n, cfp(mean_2d_grad), cfp(cov_2d_grad), cfp(mu), cfp(q),
+                                  cfp(s), cfp(camera_rotation), cfp(camera_translation), fx, fy,
+                                  cx, cy, fp(mu_grad), fp(q_grad), fp(s_grad), current_stream()),
+             "backwards_projection");
+    return {mu_grad, q_grad, s_grad};
+}
+
+}  // namespace
+
+PYBIND11_MODULE(custom_rasterizer_cuda, m) {
+    m.doc() = "MI355X (gfx950) Gaussian-splatting rasterizer behind the custom_rasterizer_cuda "
+              "surface";
+    m.def("project", &project, "3DGS projection (HIP, gfx950)");
+    m.def("SH", &spherical_harmonics, "3DGS spherical harmonics (HIP, gfx950)");
+    m.def("rasterize", &rasterize, "3DGS tile rasterization (HIP, gfx950)");
+    m.def("backwards_rasterization", &backwards_rasterization,
+          "3DGS backward rasterization (HIP, gfx950)");
+    m.def("backwards_SH", &backwards_SH, "3DGS backward spherical harmonics (HIP, gfx950)");
+    m.def("backwards_projection", &backwards_projection,
+          "3DGS backward projection (HIP, gfx950)");
+    m.def("rasterize_with_keys", &rasterize_with_keys,
+          "rasterize, also returning the sorted 64-bit keys (tile << 32 | depth bits)");
+    m.def("library_version", []() { return std::string(gsr_version()); });
+    // Stage timing of libgsraster (HIP events on the launch stream); not part of
+    // the reference surface.
+    m.def("profile_enable", [](bool on) { gsr_profile_enable(on ? 1 : 0); });
+    m.def("profile_reset", []() { gsr_profile_reset(); });
+    m.def("profile_collect", []() {
+        check_rc(gsr_profile_collect(), "profile_collect");
+        py::dict out;
+        for (const char* st : {"project", "sh", "bin_count", "depth_sort", "scan", "records",
+                               "emit", "tile_sort", "ranges", "blend_fwd", "blend_bwd", "sh_bwd",
+                               "project_bwd"}) {
+            int64_t c = 0;
+            double ms = 0.0;
+            gsr_profile_get(st, &c, &ms);
+            if (c) out[st] = py::make_tuple(c, ms);
+        }
+        return out;
+    });
+}

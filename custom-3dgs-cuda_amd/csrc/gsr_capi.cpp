@@ -1,0 +1,489 @@
+// gsr_capi.cpp — the extern "C" entry points of libgsraster.so
+// (declared in include/gsraster.h): argument checks, workspace carving and
+// the launch sequence of each stage.  No allocation happens here; every
+// buffer comes from the caller.
+#include <hip/hip_runtime.h>
+
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "gsr_internal.h"
+#include "../../include/gsraster.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(GSR_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define GSR_HIP(expr, what)                          \
+    do {                                             \
+        hipError_t gsr_e_ = (expr);                  \
+        if (gsr_e_ != hipSuccess) return hip_fail(gsr_e_, what); \
+    } while (0)
+
+#define GSR_REQUIRE(cond, msg) \
+    do {                       \
+        if (!(cond)) return fail(GSR_ERR_INVALID_ARGUMENT, msg); \
+    } while (0)
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+constexpr int kDepthPasses = 4;         // 32-bit depth keys, 8-bit digits
+constexpr int64_t kMaxPairs = 2147483647;  // sorted_ids and offsets are int32
+constexpr size_t kRecBytes = 48;
+
+int tiles_x_of(int W) { return (W + 15) / 16; }
+int tiles_y_of(int H) { return (H + 15) / 16; }
+
+// Digit passes needed to sort tile ids in [0, T).
+int tile_passes(int64_t T) {
+    if (T <= 1) return 0;
+    int bits = 0;
+    uint64_t v = (uint64_t)(T - 1);
+    while (v) {
+        ++bits;
+        v >>= 1;
+    }
+    return (bits + 7) / 8;
+}
+
+// Misc block at the head of the bin workspace.
+struct Misc {
+    uint64_t total;  // pair count written by the scan
+    int err;         // set by a kernel that hit its look-back spin bound
+    int pad;
+};
+
+struct BinLayout {
+    size_t misc, sortctl, scanctl, ctl_end;
+    size_t counts, rects, dk0, dv0, dk1, dv1, offsets, recs, end;
+};
+
+BinLayout bin_layout(int n) {
+    BinLayout L;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align_up(off + bytes, 256);
+        return o;
+    };
+    const size_t un = (size_t)(n > 0 ? n : 0);
+    L.misc = take(sizeof(Misc));
+    L.sortctl = take(gsr::sort_control_bytes(un, kDepthPasses));
+    L.scanctl = take(gsr::scan_control_bytes(n));
+    L.ctl_end = off;
+    L.counts = take(4 * un);
+    L.rects = take(8 * un);
+    L.dk0 = take(4 * un);
+    L.dv0 = take(4 * un);
+    L.dk1 = take(4 * un);
+    L.dv1 = take(4 * un);
+    L.offsets = take(4 * un);
+    L.recs = take(kRecBytes * un);
+    L.end = off;
+    return L;
+}
+
+struct SortLayout {
+    size_t ctl, ctl_end, tk0, tk1, vbuf, end;
+};
+
+SortLayout sort_layout(int64_t m, int passes) {
+    SortLayout L;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align_up(off + bytes, 256);
+        return o;
+    };
+    const size_t um = (size_t)(m > 0 ? m : 0);
+    L.ctl = take(passes > 0 ? gsr::sort_control_bytes(um, passes) : 0);
+    L.ctl_end = off;
+    L.tk0 = take(4 * um);
+    L.tk1 = take(4 * um);
+    L.vbuf = take(4 * um);
+    L.end = off;
+    return L;
+}
+
+template <typename T>
+T* at(void* base, size_t off) {
+    return reinterpret_cast<T*>(static_cast<char*>(base) + off);
+}
+
+// Pinned host slot for the one device-to-host read of the forward.
+Misc* pinned_misc() {
+    thread_local Misc* p = nullptr;
+    if (!p) {
+        void* h = nullptr;
+        if (hipHostMalloc(&h, sizeof(Misc), hipHostMallocDefault) != hipSuccess) return nullptr;
+        p = static_cast<Misc*>(h);
+    }
+    return p;
+}
+
+int ref_quat_mode() {
+    static const int mode = [] {
+        const char* v = std::getenv("GSR_REFERENCE_QUAT_GRAD");
+        return (v && v[0] == '1') ? 1 : 0;
+    }();
+    return mode;
+}
+
+// ---- optional per-stage timing (gsr_profile_*): a pair of HIP events on the
+// launch stream around each stage, collected after a synchronize ----
+struct ProfState {
+    std::mutex mu;
+    bool on = false;
+    std::vector<hipEvent_t> pool;
+    struct Pending {
+        const char* name;
+        hipEvent_t a, b;
+    };
+    std::vector<Pending> pending;
+    std::map<std::string, std::pair<int64_t, double>> acc;
+};
+ProfState& prof() {
+    static ProfState* p = new ProfState();
+    return *p;
+}
+
+class StageTimer {
+  public:
+    StageTimer(const char* name, hipStream_t st) : name_(name), st_(st) {
+        ProfState& P = prof();
+        std::lock_guard<std::mutex> lk(P.mu);
+        if (!P.on) return;
+        for (int i = 0; i < 2; ++i) {
+            hipEvent_t e = nullptr;
+            if (!P.pool.empty()) {
+                e = P.pool.back();
+                P.pool.pop_back();
+            } else if (hipEventCreate(&e) != hipSuccess) {
+                return;
+            }
+            (i == 0 ? a_ : b_) = e;
+        }
+        active_ = hipEventRecord(a_, st_) == hipSuccess;
+    }
+    ~StageTimer() {
+        if (!active_) return;
+        ProfState& P = prof();
+        std::lock_guard<std::mutex> lk(P.mu);
+        if (hipEventRecord(b_, st_) == hipSuccess) P.pending.push_back({name_, a_, b_});
+    }
+
+  private:
+    const char* name_;
+    hipStream_t st_;
+    hipEvent_t a_ = nullptr, b_ = nullptr;
+    bool active_ = false;
+};
+
+int check_screen(int height, int width) {
+    GSR_REQUIRE(height >= 0 && width >= 0, "height and width must be non-negative");
+    GSR_REQUIRE(tiles_x_of(width) < 65536 && tiles_y_of(height) < 65536,
+                "screen too large: at most 65535 tiles per axis");
+    return GSR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* gsr_last_error(void) { return g_err.c_str(); }
+
+const char* gsr_version(void) { return "gsraster 0.1 (gfx950)"; }
+
+int gsr_project(int n, const float* mu, const float* q, const float* s, const float* rot,
+                const float* trans, float fx, float fy, float cx, float cy, float* mean2d,
+                float* cov2d, float* depth, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(mu && q && s && rot && trans && mean2d && cov2d && depth, "null pointer");
+    GSR_REQUIRE(((uintptr_t)q & 15) == 0, "q must be 16-byte aligned");
+    StageTimer timer("project", as_stream(stream));
+    GSR_HIP(gsr::launch_project_fwd(n, mu, q, s, rot, trans, fx, fy, cx, cy, mean2d, cov2d, depth,
+                                    as_stream(stream)),
+            "project");
+    return GSR_OK;
+}
+
+int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, const float* k_j,
+           float* colors, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(cam_pos && mu && albedo && k_j && colors, "null pointer");
+    StageTimer timer("sh", as_stream(stream));
+    GSR_HIP(gsr::launch_sh_fwd(n, cam_pos, mu, albedo, k_j, colors, as_stream(stream)), "SH");
+    return GSR_OK;
+}
+
+size_t gsr_bin_workspace_bytes(int n, int height, int width) {
+    (void)height;
+    (void)width;
+    return bin_layout(n).end;
+}
+
+int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const float* cov2d,
+                      int height, int width, void* bin_ws, size_t bin_ws_bytes,
+                      int64_t* num_pairs, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    GSR_REQUIRE(num_pairs, "num_pairs must not be null");
+    if (int rc = check_screen(height, width)) return rc;
+    *num_pairs = 0;
+    const BinLayout L = bin_layout(n);
+    GSR_REQUIRE(bin_ws, "bin workspace must not be null");
+    if (bin_ws_bytes < L.end) return fail(GSR_ERR_WORKSPACE, "bin workspace too small");
+    hipStream_t st = as_stream(stream);
+    GSR_HIP(gsr::zero_fill(bin_ws, L.ctl_end, st), "rasterize: clear");
+    if (n == 0 || height == 0 || width == 0) return GSR_OK;
+    GSR_REQUIRE(depth && mean2d && cov2d, "null pointer");
+    Misc* misc = at<Misc>(bin_ws, L.misc);
+    int* err = &misc->err;
+    uint32_t* counts = at<uint32_t>(bin_ws, L.counts);
+    uint32_t* dk0 = at<uint32_t>(bin_ws, L.dk0);
+    uint32_t* dv0 = at<uint32_t>(bin_ws, L.dv0);
+    {
+        StageTimer timer("bin_count", st);
+        GSR_HIP(gsr::launch_bin_count(n, mean2d, cov2d, depth, height, width, counts,
+                                      at<uint2>(bin_ws, L.rects), dk0, dv0, st),
+                "rasterize: count");
+    }
+    {
+        StageTimer timer("depth_sort", st);
+        GSR_HIP(gsr::launch_radix_sort(dk0, dv0, at<uint32_t>(bin_ws, L.dk1),
+                                       at<uint32_t>(bin_ws, L.dv1), (uint64_t)n, 0, kDepthPasses,
+                                       at<void>(bin_ws, L.sortctl), err, st),
+                "rasterize: depth sort");
+    }
+    {
+        StageTimer timer("scan", st);
+        GSR_HIP(gsr::launch_scan_counts(n, dv0, counts, at<uint32_t>(bin_ws, L.offsets),
+                                        &misc->total, at<void>(bin_ws, L.scanctl), err, st),
+                "rasterize: scan");
+    }
+    Misc* host = pinned_misc();
+    if (!host) return fail(GSR_ERR_HIP, "rasterize: pinned host buffer allocation failed");
+    GSR_HIP(hipMemcpyAsync(host, misc, sizeof(Misc), hipMemcpyDeviceToHost, st),
+            "rasterize: read pair count");
+    GSR_HIP(hipStreamSynchronize(st), "rasterize: synchronize");
+    if (host->err) return fail(GSR_ERR_DEVICE, "rasterize: look-back spin bound reached");
+    if (host->total > (uint64_t)kMaxPairs)
+        return fail(GSR_ERR_TOO_MANY_PAIRS,
+                    "rasterize: " + std::to_string(host->total) +
+                        " (Gaussian, tile) pairs exceed the int32 limit; render in screen bands");
+    *num_pairs = (int64_t)host->total;
+    return GSR_OK;
+}
+
+size_t gsr_sort_workspace_bytes(int64_t num_pairs, int n, int height, int width) {
+    (void)n;
+    const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
+    return sort_layout(num_pairs, tile_passes(T)).end;
+}
+
+int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const float* cov2d,
+                         const float* colors, const float* alpha, int height, int width,
+                         void* bin_ws, size_t bin_ws_bytes, int64_t num_pairs, void* sort_ws,
+                         size_t sort_ws_bytes, int32_t* sorted_ids, int32_t* tile_ranges,
+                         float* img, float* final_T, int32_t* n_contrib, uint64_t* sorted_keys,
+                         void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (int rc = check_screen(height, width)) return rc;
+    GSR_REQUIRE(num_pairs >= 0 && num_pairs <= kMaxPairs, "num_pairs out of range");
+    const int tiles_x = tiles_x_of(width);
+    const int64_t T = (int64_t)tiles_x * tiles_y_of(height);
+    if (T == 0) return GSR_OK;
+    GSR_REQUIRE(tile_ranges && img && final_T && n_contrib, "null output pointer");
+    const BinLayout BL = bin_layout(n);
+    GSR_REQUIRE(bin_ws, "bin workspace must not be null");
+    if (bin_ws_bytes < BL.end) return fail(GSR_ERR_WORKSPACE, "bin workspace too small");
+    const int passes = tile_passes(T);
+    const SortLayout SL = sort_layout(num_pairs, passes);
+    hipStream_t st = as_stream(stream);
+    GSR_HIP(gsr::zero_fill(tile_ranges, (size_t)T * 8, st), "rasterize: clear ranges");
+    const uint64_t m = (uint64_t)num_pairs;
+    void* recs = at<void>(bin_ws, BL.recs);
+    if (m > 0) {
+        GSR_REQUIRE(sort_ws && sorted_ids, "null pointer");
+        if (sort_ws_bytes < SL.end) return fail(GSR_ERR_WORKSPACE, "sort workspace too small");
+        GSR_REQUIRE(mean2d && cov2d && colors && alpha && depth, "null pointer");
+        Misc* misc = at<Misc>(bin_ws, BL.misc);
+        GSR_HIP(gsr::zero_fill(sort_ws, SL.ctl_end, st), "rasterize: clear sort state");
+        {
+            StageTimer timer("records", st);
+            GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, recs, st),
+                    "rasterize: records");
+        }
+        uint32_t* tk0 = at<uint32_t>(sort_ws, SL.tk0);
+        uint32_t* tk1 = at<uint32_t>(sort_ws, SL.tk1);
+        uint32_t* vbuf = at<uint32_t>(sort_ws, SL.vbuf);
+        uint32_t* ids = reinterpret_cast<uint32_t*>(sorted_ids);
+        uint32_t* v0 = (passes % 2 == 0) ? ids : vbuf;
+        uint32_t* v1 = (passes % 2 == 0) ? vbuf : ids;
+        {
+            StageTimer timer("emit", st);
+            GSR_HIP(gsr::launch_emit_pairs(n, at<uint32_t>(bin_ws, BL.dv0),
+                                           at<uint32_t>(bin_ws, BL.counts),
+                                           at<uint2>(bin_ws, BL.rects),
+                                           at<uint32_t>(bin_ws, BL.offsets), tiles_x, m, tk0, v0, st),
+                    "rasterize: emit");
+        }
+        {
+            StageTimer timer("tile_sort", st);
+            GSR_HIP(gsr::launch_radix_sort(tk0, v0, tk1, v1, m, 0, passes,
+                                           at<void>(sort_ws, SL.ctl), &misc->err, st),
+                    "rasterize: tile sort");
+        }
+        const uint32_t* ktiles = (passes % 2 == 0) ? tk0 : tk1;
+        {
+            StageTimer timer("ranges", st);
+            GSR_HIP(gsr::launch_tile_ranges(m, (uint32_t)T, ktiles, tile_ranges, st), "rasterize: ranges");
+        }
+        if (sorted_keys)
+            GSR_HIP(gsr::launch_full_keys(m, ktiles, sorted_ids, depth, n, sorted_keys, st),
+                    "rasterize: keys");
+    }
+    StageTimer timer("blend_fwd", st);
+    GSR_HIP(gsr::launch_blend_fwd(n, height, width, tile_ranges, sorted_ids, m, recs, img, final_T,
+                                  n_contrib, st),
+            "rasterize: blend");
+    return GSR_OK;
+}
+
+int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream) {
+    GSR_REQUIRE(bin_ws && bin_ws_bytes >= sizeof(Misc), "bin workspace must not be null");
+    hipStream_t st = as_stream(stream);
+    Misc* host = pinned_misc();
+    if (!host) return fail(GSR_ERR_HIP, "pinned host buffer allocation failed");
+    GSR_HIP(hipMemcpyAsync(host, at<Misc>(bin_ws, 0), sizeof(Misc), hipMemcpyDeviceToHost, st),
+            "status: read");
+    GSR_HIP(hipStreamSynchronize(st), "status: synchronize");
+    if (host->err) return fail(GSR_ERR_DEVICE, "a sort or scan kernel reached its spin bound");
+    return GSR_OK;
+}
+
+size_t gsr_backward_workspace_bytes(int n) {
+    return align_up(kRecBytes * (size_t)(n > 0 ? n : 0), 256);
+}
+
+int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
+                           const float* mean2d, const float* cov2d, const float* colors,
+                           const float* alpha, const int32_t* sorted_ids, int64_t num_pairs,
+                           const int32_t* tile_ranges, const float* final_T,
+                           const int32_t* n_contrib, void* ws, size_t ws_bytes, float* d_mean2d,
+                           float* d_cov2d, float* d_colors, float* d_alpha, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (int rc = check_screen(height, width)) return rc;
+    GSR_REQUIRE(num_pairs >= 0, "num_pairs must be non-negative");
+    hipStream_t st = as_stream(stream);
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(mean2d && cov2d && colors && alpha && d_mean2d && d_cov2d && d_colors && d_alpha,
+                "null pointer");
+    if (ws_bytes < gsr_backward_workspace_bytes(n) || !ws)
+        return fail(GSR_ERR_WORKSPACE, "backward workspace too small");
+    GSR_HIP(gsr::zero_fill(d_mean2d, 8 * (size_t)n, st), "backward: clear");
+    GSR_HIP(gsr::zero_fill(d_cov2d, 12 * (size_t)n, st), "backward: clear");
+    GSR_HIP(gsr::zero_fill(d_colors, 12 * (size_t)n, st), "backward: clear");
+    GSR_HIP(gsr::zero_fill(d_alpha, 4 * (size_t)n, st), "backward: clear");
+    const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
+    if (T == 0 || num_pairs == 0) return GSR_OK;
+    GSR_REQUIRE(grad_img && sorted_ids && tile_ranges && final_T && n_contrib, "null pointer");
+    GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, ws, st),
+            "backward: records");
+    StageTimer timer("blend_bwd", st);
+    GSR_HIP(gsr::launch_blend_bwd(n, height, width, grad_img, tile_ranges, sorted_ids,
+                                  (uint64_t)num_pairs, ws, final_T, n_contrib, d_mean2d, d_cov2d,
+                                  d_colors, d_alpha, st),
+            "backward: blend");
+    return GSR_OK;
+}
+
+int gsr_sh_backward(int n, const float* colors_grad, const float* mu, const float* albedo,
+                    const float* k_j, const float* cam_pos, float* d_albedo, float* d_k_j,
+                    float* d_mu, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(colors_grad && mu && albedo && k_j && cam_pos && d_albedo && d_k_j && d_mu,
+                "null pointer");
+    StageTimer timer("sh_bwd", as_stream(stream));
+    GSR_HIP(gsr::launch_sh_bwd(n, colors_grad, mu, albedo, k_j, cam_pos, d_albedo, d_k_j, d_mu,
+                               as_stream(stream)),
+            "backwards_SH");
+    return GSR_OK;
+}
+
+int gsr_project_backward(int n, const float* d_mean2d, const float* d_cov2d, const float* mu,
+                         const float* q, const float* s, const float* rot, const float* trans,
+                         float fx, float fy, float cx, float cy, float* d_mu, float* d_q,
+                         float* d_s, void* stream) {
+    (void)cx;
+    (void)cy;
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(d_mean2d && d_cov2d && mu && q && s && rot && trans && d_mu && d_q && d_s,
+                "null pointer");
+    GSR_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)d_q & 15) == 0,
+                "q and d_q must be 16-byte aligned");
+    StageTimer timer("project_bwd", as_stream(stream));
+    GSR_HIP(gsr::launch_project_bwd(n, d_mean2d, d_cov2d, mu, q, s, rot, trans, fx, fy, d_mu, d_q,
+                                    d_s, ref_quat_mode(), as_stream(stream)),
+            "backwards_projection");
+    return GSR_OK;
+}
+
+void gsr_profile_enable(int on) {
+    ProfState& P = prof();
+    std::lock_guard<std::mutex> lk(P.mu);
+    P.on = on != 0;
+}
+
+int gsr_profile_collect(void) {
+    ProfState& P = prof();
+    std::lock_guard<std::mutex> lk(P.mu);
+    for (auto& e : P.pending) {
+        GSR_HIP(hipEventSynchronize(e.b), "profile: synchronize");
+        float ms = 0.0f;
+        GSR_HIP(hipEventElapsedTime(&ms, e.a, e.b), "profile: elapsed");
+        auto& slot = P.acc[e.name];
+        slot.first += 1;
+        slot.second += ms;
+        P.pool.push_back(e.a);
+        P.pool.push_back(e.b);
+    }
+    P.pending.clear();
+    return GSR_OK;
+}
+
+int gsr_profile_get(const char* stage, int64_t* count, double* total_ms) {
+    GSR_REQUIRE(stage && count && total_ms, "null pointer");
+    ProfState& P = prof();
+    std::lock_guard<std::mutex> lk(P.mu);
+    auto it = P.acc.find(stage);
+    *count = it == P.acc.end() ? 0 : it->second.first;
+    *total_ms = it == P.acc.end() ? 0.0 : it->second.second;
+    return GSR_OK;
+}
+
+void gsr_profile_reset(void) {
+    ProfState& P = prof();
+    std::lock_guard<std::mutex> lk(P.mu);
+    P.acc.clear();
+}
+
+}  // extern "C"

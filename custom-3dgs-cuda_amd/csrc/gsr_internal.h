@@ -1,0 +1,91 @@
+// gsr_internal.h — launchers behind the C ABI (include/gsraster.h).  Each
+// returns hipSuccess or the first HIP error; argument validation happens in
+// gsr_capi.cpp before any launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace gsr {
+
+hipError_t launch_project_fwd(int n, const float* mu, const float* q, const float* s,
+                              const float* rot, const float* tr, float fx, float fy, float cx,
+                              float cy, float* mean2d, float* cov2d, float* depth,
+                              hipStream_t st);
+
+hipError_t launch_project_bwd(int n, const float* dmean, const float* dcov, const float* mu,
+                              const float* q, const float* s, const float* rot, const float* tr,
+                              float fx, float fy, float* dmu, float* dq, float* ds, int ref_quat,
+                              hipStream_t st);
+
+hipError_t launch_sh_fwd(int n, const float* cam, const float* mu, const float* albedo,
+                         const float* kj, float* colors, hipStream_t st);
+
+hipError_t launch_sh_bwd(int n, const float* cgrad, const float* mu, const float* albedo,
+                         const float* kj, const float* cam, float* dA, float* dkj, float* dmu,
+                         hipStream_t st);
+
+// ---- radix sort (u32 keys, u32 values), LSD onesweep with 8-bit digits ----
+// Partition size of one onesweep work-group.
+constexpr int kSortThreads = 256;
+constexpr int kSortItems = 16;
+constexpr int kSortPartition = kSortThreads * kSortItems;
+constexpr int kRadixBins = 256;
+
+// Device control block of one sort: per-pass global digit histograms,
+// partition counters and look-back status words.  All of it must be zero
+// before the histogram kernel runs (sort_control_bytes / the fill kernel).
+size_t sort_control_bytes(uint64_t n, int passes);
+// Sorts keys[0..n) by bits [begin_bit, begin_bit + 8*passes), carrying vals.
+// Ping-pongs between (k0,v0) and (k1,v1); the result lands in (k0,v0) for an
+// even pass count and in (k1,v1) for an odd one.  `control` must be zeroed
+// on the stream first (zero_fill).  err (device int) is set when a look-back
+// exceeds kSpinLimit.
+hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
+                             int begin_bit, int passes, void* control, int* err, hipStream_t st);
+
+hipError_t zero_fill(void* p, size_t bytes, hipStream_t st);
+
+// ---- binning ----
+// counts[g], packed tile rect, depth key (float bits or 0xffffffff when the
+// Gaussian touches no tile) and identity values.
+hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
+                            int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
+                            uint32_t* dvals, hipStream_t st);
+
+// Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r]; the total
+// (u64) is written to *total.
+size_t scan_control_bytes(int n);
+hipError_t launch_scan_counts(int n, const uint32_t* perm, const uint32_t* counts,
+                              uint32_t* offsets, uint64_t* total, void* control, int* err,
+                              hipStream_t st);
+
+// Pair emission in depth order: tile keys + Gaussian ids.
+hipError_t launch_emit_pairs(int n, const uint32_t* perm, const uint32_t* counts,
+                             const uint2* rects, const uint32_t* offsets, int tiles_x, uint64_t m,
+                             uint32_t* tile_keys, uint32_t* ids, hipStream_t st);
+
+// [start, end) per tile from sorted tile keys; ranges must be zeroed.
+hipError_t launch_tile_ranges(uint64_t m, uint32_t T, const uint32_t* sorted_tiles,
+                              int32_t* ranges, hipStream_t st);
+
+// Optional debug output: (tile << 32) | float_bits(depth[id]).
+hipError_t launch_full_keys(uint64_t m, const uint32_t* sorted_tiles, const int32_t* ids,
+                            const float* depth, int n, uint64_t* keys, hipStream_t st);
+
+// ---- blend ----
+hipError_t launch_blend_records(int n, const float* mean2d, const float* cov2d,
+                                const float* colors, const float* alpha, void* recs,
+                                hipStream_t st);
+
+hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
+                            uint64_t m, const void* recs, float* img, float* finalT,
+                            int32_t* ncontrib, hipStream_t st);
+
+hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_t* ranges,
+                            const int32_t* ids, uint64_t num_pairs, const void* recs,
+                            const float* finalT, const int32_t* ncontrib, float* dmean,
+                            float* dcov, float* dcol, float* dalpha, hipStream_t st);
+
+}  // namespace gsr

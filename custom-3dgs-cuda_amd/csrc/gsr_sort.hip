@@ -1,0 +1,357 @@
+// gsr_sort.hip — LSD onesweep radix sort (u32 keys carrying u32 values) and
+// the decoupled look-back scan of per-Gaussian tile counts.
+//
+// Sort design (one kernel per 8-bit digit pass, plus one histogram kernel):
+//   * A work-group owns a partition of 4096 consecutive elements, claimed in
+//     launch order through an atomic counter so that every partition it waits
+//     on belongs to a work-group that is already resident.
+//   * Items are loaded wave-striped (item i of lane l in wave w is element
+//     w*1024 + i*64 + l), so each wave load is one contiguous 256 B access.
+//   * Stable in-partition ranks come from 8 ballots per item (lanes sharing a
+//     digit) plus per-wave running digit counters in LDS.
+//   * Each partition publishes its 256 digit counts, looks back over earlier
+//     partitions' published counts (decoupled look-back) and scatters its
+//     elements, first reordered in LDS so each digit's run is written with
+//     consecutive addresses.
+//   * Look-back spins are bounded by kSpinLimit; a partition that reaches it
+//     raises the error flag and finishes, so every wave exits.
+// HBM traffic per pass: 8 B read + 8 B written per element (+ 8 B per
+// partition and digit of status words).
+#include <algorithm>
+
+#include "gsr_internal.h"
+#include "gsr_common.h"
+
+namespace gsr {
+
+namespace {
+
+constexpr int kHistMaxPasses = 4;
+static_assert(kSortThreads == kRadixBins, "one thread per digit in the onesweep kernel");
+static_assert(kSortThreads == 256, "four waves per onesweep work-group");
+
+inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+struct SortCtl {
+    uint32_t* hist;      // [passes][256]
+    uint32_t* counters;  // [passes] (one per 64 B line)
+    uint64_t* status;    // [passes][parts][256]
+};
+
+inline uint64_t parts_for(uint64_t n) { return (n + kSortPartition - 1) / kSortPartition; }
+
+SortCtl carve(void* control, uint64_t n, int passes) {
+    char* p = static_cast<char*>(control);
+    SortCtl c;
+    c.hist = reinterpret_cast<uint32_t*>(p);
+    p += align_up((size_t)passes * kRadixBins * 4, 256);
+    c.counters = reinterpret_cast<uint32_t*>(p);
+    p += align_up((size_t)passes * 64, 256);
+    c.status = reinterpret_cast<uint64_t*>(p);
+    return c;
+}
+
+// Lanes of `active` whose 8-bit digit equals this lane's.
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active) {
+    uint64_t m = active;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+        const bool bit = (d >> b) & 1u;
+        const uint64_t t = ballot(bit);
+        m &= bit ? t : ~t;
+    }
+    return m;
+}
+
+__global__ __launch_bounds__(256) void fill_zero_kernel(uint4* __restrict__ p, size_t n16,
+                                                        uint8_t* __restrict__ tail,
+                                                        int tail_bytes) {
+    const size_t stride = (size_t)gridDim.x * 256;
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
+        p[i] = make_uint4(0u, 0u, 0u, 0u);
+    if (blockIdx.x == 0 && (int)threadIdx.x < tail_bytes) tail[threadIdx.x] = 0;
+}
+
+// Global digit histograms of every pass in one read of the keys.  Digit
+// counts are aggregated per wave (ballot match) before the LDS atomics, and
+// per work-group before the global atomics.
+__global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restrict__ keys,
+                                                         uint64_t n, int begin_bit, int passes,
+                                                         uint32_t* __restrict__ hist) {
+    __shared__ uint32_t s_h[kHistMaxPasses][kRadixBins];
+    for (int j = threadIdx.x; j < kHistMaxPasses * kRadixBins; j += 256) (&s_h[0][0])[j] = 0;
+    __syncthreads();
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    const uint64_t nround = (n + 255) / 256 * 256;  // keep whole waves in the loop
+    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < nround; i += stride) {
+        const bool valid = i < n;
+        const uint32_t k = valid ? keys[i] : 0u;
+        const uint64_t act = ballot(valid);
+        for (int p = 0; p < passes; ++p) {
+            const uint32_t d = (k >> (begin_bit + 8 * p)) & 0xffu;
+            const uint64_t peers = match_digit(d, act);
+            if (valid && (peers & lanemask_lt()) == 0)
+                atomicAdd(&s_h[p][d], (uint32_t)popc64(peers));
+        }
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < passes * kRadixBins; j += 256) {
+        const uint32_t v = (&s_h[0][0])[j];
+        if (v) atomicAdd(&hist[j], v);
+    }
+}
+
+__global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
+    const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
+    uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n, int shift,
+    const uint32_t* __restrict__ hist, uint64_t* __restrict__ status,
+    uint32_t* __restrict__ counter, int* __restrict__ err) {
+    __shared__ uint32_t s_keys[kSortPartition];
+    __shared__ uint32_t s_vals[kSortPartition];
+    __shared__ uint32_t s_wcnt[4][kRadixBins];
+    __shared__ uint32_t s_dstart[kRadixBins];
+    __shared__ uint64_t s_gbase[kRadixBins];
+    __shared__ uint32_t s_scan[4];
+    __shared__ uint32_t s_hscan[4];
+    __shared__ uint32_t s_part;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_part = atomicAdd(counter, 1u);
+    for (int j = tid; j < 4 * kRadixBins; j += kSortThreads) (&s_wcnt[0][0])[j] = 0;
+    __syncthreads();
+    const uint64_t part = s_part;
+    const uint64_t base = part * kSortPartition;
+    const int nvalid = (int)min((uint64_t)kSortPartition, n - base);
+
+    uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        const int e = wave * (kSortItems * 64) + i * 64 + lane;
+        const bool v = e < nvalid;
+        key[i] = v ? kin[base + e] : 0u;
+        val[i] = v ? vin[base + e] : 0u;
+    }
+    // Stable ranks within the wave's slice, in element order.
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        const int e = wave * (kSortItems * 64) + i * 64 + lane;
+        const bool v = e < nvalid;
+        const uint32_t d = (key[i] >> shift) & 0xffu;
+        const uint64_t peers = match_digit(d, ballot(v));
+        rank[i] = 0;
+        if (v) {
+            const uint32_t before = s_wcnt[wave][d];
+            const uint64_t lower = peers & lanemask_lt();
+            rank[i] = before + (uint32_t)popc64(lower);
+            if (lower == 0) s_wcnt[wave][d] = before + (uint32_t)popc64(peers);
+        }
+    }
+    __syncthreads();
+
+    // One thread per digit: partition total, publish, prefixes.
+    const int d = tid;
+    const uint32_t c0 = s_wcnt[0][d], c1 = s_wcnt[1][d], c2 = s_wcnt[2][d], c3 = s_wcnt[3][d];
+    const uint32_t total = c0 + c1 + c2 + c3;
+    uint64_t* my_status = status + part * kRadixBins + d;
+    store_agent(my_status, (part == 0 ? kFlagInclusive : kFlagAggregate) | (uint64_t)total);
+    s_wcnt[0][d] = 0;
+    s_wcnt[1][d] = c0;
+    s_wcnt[2][d] = c0 + c1;
+    s_wcnt[3][d] = c0 + c1 + c2;
+    const uint32_t inc = wave_inclusive_scan(total);
+    const uint32_t h = hist[d];
+    const uint32_t hinc = wave_inclusive_scan(h);
+    if (lane == 63) {
+        s_scan[wave] = inc;
+        s_hscan[wave] = hinc;
+    }
+    __syncthreads();
+    uint32_t wpre = 0, hpre = 0;
+    for (int w = 0; w < wave; ++w) {
+        wpre += s_scan[w];
+        hpre += s_hscan[w];
+    }
+    const uint32_t dstart = wpre + inc - total;
+    const uint64_t hexcl = (uint64_t)(hpre + hinc - h);
+    s_dstart[d] = dstart;
+    __syncthreads();
+
+    // Reorder the partition in LDS by digit (stable).
+#pragma unroll
+    for (int i = 0; i < kSortItems; ++i) {
+        const int e = wave * (kSortItems * 64) + i * 64 + lane;
+        if (e < nvalid) {
+            const uint32_t dd = (key[i] >> shift) & 0xffu;
+            const uint32_t pos = s_dstart[dd] + s_wcnt[wave][dd] + rank[i];
+            s_keys[pos] = key[i];
+            s_vals[pos] = val[i];
+        }
+    }
+
+    // Decoupled look-back for digit d over earlier partitions.
+    uint64_t excl = 0;
+    if (part > 0) {
+        uint64_t p = part - 1;
+        uint32_t spins = 0;
+        while (true) {
+            const uint64_t s = load_agent(status + p * kRadixBins + d);
+            const uint64_t flag = s & ~kValueMask;
+            if (flag == 0) {
+                if (++spins > kSpinLimit) {
+                    atomicOr(err, 1);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                continue;
+            }
+            excl += s & kValueMask;
+            if (flag == kFlagInclusive || p == 0) break;
+            --p;
+        }
+        store_agent(my_status, kFlagInclusive | (excl + total));
+    }
+    s_gbase[d] = hexcl + excl - (uint64_t)dstart;
+    __syncthreads();
+
+    for (int j = tid; j < nvalid; j += kSortThreads) {
+        const uint32_t k = s_keys[j];
+        const uint64_t o = s_gbase[(k >> shift) & 0xffu] + (uint64_t)j;
+        if (o < n) {  // always true for consistent histograms; guards the stores
+            kout[o] = k;
+            vout[o] = s_vals[j];
+        }
+    }
+}
+
+// ---- exclusive scan of counts[perm[r]] (decoupled look-back) -------------
+constexpr int kScanThreads = 256;
+constexpr int kScanItems = 16;
+constexpr int kScanPartition = kScanThreads * kScanItems;
+
+__global__ __launch_bounds__(kScanThreads) void scan_counts_kernel(
+    int n, const uint32_t* __restrict__ perm, const uint32_t* __restrict__ counts,
+    uint32_t* __restrict__ offsets, uint64_t* __restrict__ total, uint64_t* __restrict__ status,
+    uint32_t* __restrict__ counter, int* __restrict__ err) {
+    __shared__ uint32_t s_part;
+    __shared__ uint32_t s_wsum[4];
+    __shared__ uint64_t s_base;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_part = atomicAdd(counter, 1u);
+    __syncthreads();
+    const uint64_t part = s_part;
+    const int64_t first = (int64_t)part * kScanPartition + (int64_t)tid * kScanItems;
+    uint32_t c[kScanItems];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int i = 0; i < kScanItems; ++i) {
+        const int64_t r = first + i;
+        const uint32_t g = (r < n) ? perm[r] : 0xffffffffu;
+        c[i] = (g < (uint32_t)n) ? counts[g] : 0u;
+        sum += c[i];
+    }
+    const uint32_t inc = wave_inclusive_scan(sum);
+    if (lane == 63) s_wsum[wave] = inc;
+    __syncthreads();
+    uint32_t wpre = 0, btot = 0;
+    for (int w = 0; w < 4; ++w) {
+        if (w < wave) wpre += s_wsum[w];
+        btot += s_wsum[w];
+    }
+    if (tid == 0) {
+        uint64_t* mine = status + part;
+        store_agent(mine, (part == 0 ? kFlagInclusive : kFlagAggregate) | (uint64_t)btot);
+        uint64_t excl = 0;
+        if (part > 0) {
+            uint64_t p = part - 1;
+            uint32_t spins = 0;
+            while (true) {
+                const uint64_t s = load_agent(status + p);
+                const uint64_t flag = s & ~kValueMask;
+                if (flag == 0) {
+                    if (++spins > kSpinLimit) {
+                        atomicOr(err, 1);
+                        break;
+                    }
+                    __builtin_amdgcn_s_sleep(1);
+                    continue;
+                }
+                excl += s & kValueMask;
+                if (flag == kFlagInclusive || p == 0) break;
+                --p;
+            }
+            store_agent(mine, kFlagInclusive | (excl + btot));
+        }
+        s_base = excl;
+        const uint64_t pbeg = part * kScanPartition;
+        if (pbeg + kScanPartition >= (uint64_t)n) *total = excl + btot;
+    }
+    __syncthreads();
+    uint64_t run = s_base + wpre + inc - sum;
+#pragma unroll
+    for (int i = 0; i < kScanItems; ++i) {
+        const int64_t r = first + i;
+        if (r < n) offsets[r] = (uint32_t)run;
+        run += c[i];
+    }
+}
+
+}  // namespace
+
+hipError_t zero_fill(void* p, size_t bytes, hipStream_t st) {
+    if (bytes == 0) return hipSuccess;
+    const size_t n16 = bytes / 16;
+    const int tail = (int)(bytes - n16 * 16);
+    uint8_t* tailp = static_cast<uint8_t*>(p) + n16 * 16;
+    const size_t blocks = std::min<size_t>(std::max<size_t>((n16 + 255) / 256, 1), 2048);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       static_cast<uint4*>(p), n16, tailp, tail);
+    return hipGetLastError();
+}
+
+size_t sort_control_bytes(uint64_t n, int passes) {
+    return align_up((size_t)passes * kRadixBins * 4, 256) + align_up((size_t)passes * 64, 256) +
+           (size_t)passes * parts_for(n) * kRadixBins * 8;
+}
+
+hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
+                             int begin_bit, int passes, void* control, int* err, hipStream_t st) {
+    if (n == 0 || passes <= 0) return hipSuccess;
+    if (passes > kHistMaxPasses) return hipErrorInvalidValue;
+    const uint64_t parts = parts_for(n);
+    SortCtl c = carve(control, n, passes);
+    const unsigned hblocks = (unsigned)std::min<uint64_t>(parts, 512);
+    hipLaunchKernelGGL(radix_hist_kernel, dim3(hblocks), dim3(256), 0, st, k0, n, begin_bit,
+                       passes, c.hist);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    uint32_t *ki = k0, *vi = v0, *ko = k1, *vo = v1;
+    for (int p = 0; p < passes; ++p) {
+        hipLaunchKernelGGL(onesweep_kernel, dim3((unsigned)parts), dim3(kSortThreads), 0, st, ki,
+                           vi, ko, vo, n, begin_bit + 8 * p, c.hist + p * kRadixBins,
+                           c.status + (size_t)p * parts * kRadixBins, c.counters + p * 16, err);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+        std::swap(ki, ko);
+        std::swap(vi, vo);
+    }
+    return hipSuccess;
+}
+
+size_t scan_control_bytes(int n) {
+    const size_t parts = ((size_t)std::max(n, 1) + kScanPartition - 1) / kScanPartition;
+    return 256 + parts * 8;
+}
+
+hipError_t launch_scan_counts(int n, const uint32_t* perm, const uint32_t* counts,
+                              uint32_t* offsets, uint64_t* total, void* control, int* err,
+                              hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const unsigned parts = (unsigned)(((size_t)n + kScanPartition - 1) / kScanPartition);
+    uint32_t* counter = static_cast<uint32_t*>(control);
+    uint64_t* status = reinterpret_cast<uint64_t*>(static_cast<char*>(control) + 256);
+    hipLaunchKernelGGL(scan_counts_kernel, dim3(parts), dim3(kScanThreads), 0, st, n, perm, counts,
+                       offsets, total, status, counter, err);
+    return hipGetLastError();
+}
+
+}  // namespace gsr

@@ -1,0 +1,153 @@
+"""Autograd glue over ``custom_rasterizer_cuda`` — the counterpart of the reference's
+gaussian_splatting/rasterizer/rasterize.py:10-160, same call order and semantics:
+
+forward:  cam_position = -R^T t; project -> (mean2d, cov2d, depth); approximate screen
+          radii for densification; SH colours; rasterize -> image.
+backward: backwards_rasterization -> (d mean2d, d cov2d, d colours, d alpha);
+          backwards_SH -> (d albedo, d k_j, d mu via view direction);
+          backwards_projection -> (d mu, d q, d log-scale); d mu = sum of both paths.
+
+The extension is the MI355X HIP build (libgsraster.so); there is no fallback path.
+"""
+
+from __future__ import annotations
+
+import sys
+from pathlib import Path
+
+import torch as t
+
+from gaussian_splatting.scene.gaussian import gaussian
+
+try:
+    import custom_rasterizer_cuda as crc
+except ImportError:  # the built module sits beside this package
+    _root = str(Path(__file__).resolve().parents[2])
+    if _root not in sys.path:
+        sys.path.insert(0, _root)
+    try:
+        import custom_rasterizer_cuda as crc
+    except ImportError:
+        crc = None
+
+
+class RasterizeFunction(t.autograd.Function):
+    """Full rasterization pipeline. Returns the rendered image [H, W, 3].
+
+    After forward, ``last_radii2d`` holds approximate screen radii (N,).
+    After backward, ``last_mean2d_grad`` holds dL/d mean2d (N, 2) for densification.
+    """
+
+    last_mean2d_grad: t.Tensor | None = None
+    last_radii2d: t.Tensor | None = None
+
+    @staticmethod
+    def forward(ctx, mu, q, s, alpha, albedo, k_j, cam_rotation, cam_translation, fx, fy, cx, cy,
+                height, width):
+        if crc is None:
+            raise ImportError(
+                "custom_rasterizer_cuda is not built. "
+                "Build it with: python custom-3dgs-cuda_amd/build.py"
+            )
+
+        num_gaussians = mu.shape[0]
+        mu = mu.contiguous()
+        q = q.contiguous()
+        s = s.contiguous()
+        alpha = alpha.contiguous()
+        albedo = albedo.contiguous()
+        k_j = k_j.contiguous()
+        cam_rotation = cam_rotation.contiguous()
+        cam_translation = cam_translation.contiguous()
+
+        fx_f, fy_f = float(fx), float(fy)
+        cx_f, cy_f = float(cx), float(cy)
+        img_h, img_w = int(height), int(width)
+
+        cam_position = -t.matmul(cam_rotation.T, cam_translation)
+        cam_position = cam_position.reshape(3).contiguous()
+
+        mean_2d, cov_2d, depths = crc.project(
+            num_gaussians, mu, q, s, cam_rotation, cam_translation, fx_f, fy_f, cx_f, cy_f
+        )
+        # Screen radius ~ 3 * sqrt(max eigenvalue of [[a, b], [b, c]]) (rasterize.py:49-53).
+        a, b, c = cov_2d[:, 0], cov_2d[:, 1], cov_2d[:, 2]
+        mid = 0.5 * (a + c)
+        radius = mid + t.sqrt(t.clamp((0.5 * (a - c)) ** 2 + b * b, min=0.1))
+        RasterizeFunction.last_radii2d = (3.0 * t.sqrt(t.clamp(radius, min=0.0))).detach()
+
+        colors = crc.SH(num_gaussians, cam_position, mu, albedo, k_j)
+        rendered_img, sorted_ids, tile_ranges, final_T, n_contrib = crc.rasterize(
+            num_gaussians, depths, mean_2d, cov_2d, colors, alpha, img_h, img_w
+        )
+
+        ctx.save_for_backward(
+            mean_2d, cov_2d, colors, alpha,
+            sorted_ids, tile_ranges, final_T, n_contrib,
+            mu, q, s, albedo, k_j,
+            cam_rotation, cam_translation, cam_position,
+        )
+        ctx.num_gaussians = num_gaussians
+        ctx.height = img_h
+        ctx.width = img_w
+        ctx.fx = fx_f
+        ctx.fy = fy_f
+        ctx.cx = cx_f
+        ctx.cy = cy_f
+        return rendered_img
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        (
+            mean_2d, cov_2d, colors, alpha,
+            sorted_ids, tile_ranges, final_T, n_contrib,
+            mu, q, s, albedo, k_j,
+            cam_rotation, cam_translation, cam_position,
+        ) = ctx.saved_tensors
+
+        mean_2d_grad, cov_2d_grad, colors_grad, alpha_grad = crc.backwards_rasterization(
+            grad_output.contiguous(), mean_2d, cov_2d, colors, alpha,
+            sorted_ids, tile_ranges, final_T, n_contrib,
+            ctx.num_gaussians, ctx.height, ctx.width,
+        )
+        RasterizeFunction.last_mean2d_grad = mean_2d_grad.detach()
+
+        albedo_grad, k_j_grad, mu_sh_grad = crc.backwards_SH(
+            colors_grad, mu, albedo, k_j, cam_position
+        )
+        mu_grad, q_grad, s_grad = crc.backwards_projection(
+            mean_2d_grad, cov_2d_grad, mu, q, s, cam_rotation, cam_translation,
+            ctx.fx, ctx.fy, ctx.cx, ctx.cy,
+        )
+        mu_grad = mu_grad + mu_sh_grad
+        # alpha arrives as [N] or [N, 1]; hand back a gradient of the same shape
+        alpha_grad = alpha_grad.reshape(alpha.shape)
+
+        return (mu_grad, q_grad, s_grad, alpha_grad, albedo_grad, k_j_grad,
+                None, None, None, None, None, None, None, None)
+
+
+def rasterize(gaussians: gaussian, image: dict) -> t.Tensor:
+    """Training-loop entry point (rasterize.py:137-160).
+
+    Opacity is stored as logits; the sigmoid is applied here so the rasterizer
+    receives opacity in (0, 1) while gradients still flow to ``gaussians.alpha``.
+    """
+    RasterizeFunction.last_mean2d_grad = None
+    RasterizeFunction.last_radii2d = None
+    return RasterizeFunction.apply(
+        gaussians.mu,
+        gaussians.q,
+        gaussians.s,
+        t.sigmoid(gaussians.alpha),
+        gaussians.A,
+        gaussians.k_j,
+        image["R"],
+        image["T"],
+        image["fx"],
+        image["fy"],
+        image["cx"],
+        image["cy"],
+        image["height"],
+        image["width"],
+    )

@@ -1,0 +1,129 @@
+/* gsraster.h — C ABI of the MI355X (gfx950) differentiable Gaussian-splatting
+ * rasterizer, libgsraster.so.
+ *
+ * Plain pointers and sizes only.  Every tensor argument is a DEVICE pointer
+ * to contiguous fp32 / int32 data in the layouts of the reference's
+ * custom_rasterizer_cuda extension (kmurungi/custom-3dgs-cuda):
+ *   mu [N,3], q [N,4] (w,x,y,z; 16-byte aligned), s [N,3] log-scales,
+ *   rot [3,3] row-major world-to-camera rows, trans [3],
+ *   mean2d [N,2], cov2d [N,3] = (a, b, c) of [[a, b], [b, c]], depth [N],
+ *   albedo [N,3], k_j [N,15,3], colors [N,3], alpha [N] post-sigmoid,
+ *   img [H,W,3], final_T [H,W], n_contrib [H,W] int32,
+ *   sorted_ids [M] int32, tile_ranges [T,2] int32, T = ceil(W/16)*ceil(H/16).
+ * `stream` is a hipStream_t (NULL = the null stream); all work is enqueued
+ * on it.  Only gsr_rasterize_bin and gsr_rasterize_status synchronize it.
+ *
+ * Every entry point returns GSR_OK or an error code; gsr_last_error() gives
+ * the calling thread's message for the last failure.  Outputs are fully
+ * written by the call (no zero-initialisation by the caller is needed).
+ */
+#ifndef GSRASTER_H
+#define GSRASTER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GSR_OK 0
+#define GSR_ERR_INVALID_ARGUMENT 1 /* null pointer, bad size, misaligned q */
+#define GSR_ERR_HIP 2              /* a HIP runtime call or launch failed */
+#define GSR_ERR_WORKSPACE 3        /* workspace smaller than the size query */
+#define GSR_ERR_TOO_MANY_PAIRS 4   /* M >= 2^31 (the int32 sorted_ids limit) */
+#define GSR_ERR_DEVICE 5           /* a kernel reported an error (look-back spin limit) */
+
+const char* gsr_last_error(void);
+const char* gsr_version(void);
+
+/* Replaces project_gaussians_to_2d (csrc/forward/projection.h:5,
+ * launcher csrc/forward/projection.cu:109-153; bound as `project` at
+ * csrc/bindings.cpp:12-29,142).  Culled Gaussians (camera z <= 0.2) get zero
+ * mean, covariance and depth. */
+int gsr_project(int n, const float* mu, const float* q, const float* s, const float* rot,
+                const float* trans, float fx, float fy, float cx, float cy, float* mean2d,
+                float* cov2d, float* depth, void* stream);
+
+/* Replaces launch_spherical_harmonics_kernel (csrc/forward/SH.h:4,
+ * csrc/forward/SH.cu:95-131; bound as `SH` at csrc/bindings.cpp:32-46,143).
+ * cam_pos is a device pointer to 3 floats (the reference copies it to the
+ * host first). */
+int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, const float* k_j,
+           float* colors, void* stream);
+
+/* Replaces launch_rasterization (csrc/forward/rasterize.h:11,
+ * csrc/forward/rasterize.cu:284-487; bound as `rasterize` at
+ * csrc/bindings.cpp:50-70,144), split where the reference itself reads the
+ * pair count back to the host (rasterize.cu:382-390):
+ *   1. gsr_rasterize_bin: per-Gaussian tile counts, depth order, pair
+ *      offsets; writes M to *num_pairs (synchronizes `stream`).
+ *   2. gsr_rasterize_render: pair emission, tile sort, tile ranges, blend.
+ * bin_ws (gsr_bin_workspace_bytes) must stay untouched between the calls;
+ * sort_ws is sized by gsr_sort_workspace_bytes(M, ...).  sorted_keys
+ * (optional, may be NULL) receives the reference's 64-bit sort keys
+ * (tile << 32 | float bits of depth) in sorted order. */
+size_t gsr_bin_workspace_bytes(int n, int height, int width);
+int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const float* cov2d,
+                      int height, int width, void* bin_ws, size_t bin_ws_bytes,
+                      int64_t* num_pairs, void* stream);
+size_t gsr_sort_workspace_bytes(int64_t num_pairs, int n, int height, int width);
+int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const float* cov2d,
+                         const float* colors, const float* alpha, int height, int width,
+                         void* bin_ws, size_t bin_ws_bytes, int64_t num_pairs, void* sort_ws,
+                         size_t sort_ws_bytes, int32_t* sorted_ids, int32_t* tile_ranges,
+                         float* img, float* final_T, int32_t* n_contrib, uint64_t* sorted_keys,
+                         void* stream);
+/* Synchronizes `stream` and reports GSR_ERR_DEVICE if a sort or scan kernel of
+ * the last bin/render calls on this bin_ws hit its look-back spin bound. */
+int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream);
+
+/* Replaces launch_backward_rasterization (csrc/backward/rasterize_backward.h:5,
+ * csrc/backward/rasterize_backward.cu:239-309; bound as
+ * `backwards_rasterization` at csrc/bindings.cpp:72-100,147).  num_pairs is
+ * the length of sorted_ids (tile ranges are clamped to it); ids outside
+ * [0, n) are skipped as in the reference.  Outputs: d_mean2d [N,2],
+ * d_cov2d [N,3] (dL/d(a,b,c)), d_colors [N,3], d_alpha [N]. */
+size_t gsr_backward_workspace_bytes(int n);
+int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
+                           const float* mean2d, const float* cov2d, const float* colors,
+                           const float* alpha, const int32_t* sorted_ids, int64_t num_pairs,
+                           const int32_t* tile_ranges, const float* final_T,
+                           const int32_t* n_contrib, void* ws, size_t ws_bytes, float* d_mean2d,
+                           float* d_cov2d, float* d_colors, float* d_alpha, void* stream);
+
+/* Replaces launch_backward_SH (csrc/backward/delight_backward.h:5,
+ * csrc/backward/delight_backward.cu:176-218; bound as `backwards_SH` at
+ * csrc/bindings.cpp:102-116,148).  cam_pos is a device pointer. */
+int gsr_sh_backward(int n, const float* colors_grad, const float* mu, const float* albedo,
+                    const float* k_j, const float* cam_pos, float* d_albedo, float* d_k_j,
+                    float* d_mu, void* stream);
+
+/* Replaces launch_backward_projection (csrc/backward/projection_backward.h:5,
+ * csrc/backward/projection_backward.cu:142-187; bound as
+ * `backwards_projection` at csrc/bindings.cpp:118-138,149).  cx, cy are
+ * accepted and unused, as in the reference.  The quaternion gradient is the
+ * derivative of the rotation the forward builds; set the environment
+ * variable GSR_REFERENCE_QUAT_GRAD=1 before the first call to get the
+ * reference's literal formula (projection_backward.cu:334-344) instead. */
+int gsr_project_backward(int n, const float* d_mean2d, const float* d_cov2d, const float* mu,
+                         const float* q, const float* s, const float* rot, const float* trans,
+                         float fx, float fy, float cx, float cy, float* d_mu, float* d_q,
+                         float* d_s, void* stream);
+
+/* Stage timing (no counterpart in the reference; for benchmarks).  While
+ * enabled, each entry point records a pair of HIP events on its stream around
+ * its stage's kernels: "project", "sh", "bin_count", "depth_sort", "scan",
+ * "records", "emit", "tile_sort", "ranges", "blend_fwd", "blend_bwd",
+ * "sh_bwd", "project_bwd".  gsr_profile_collect waits for the recorded events
+ * and adds their durations to per-stage totals read by gsr_profile_get. */
+void gsr_profile_enable(int on);
+int gsr_profile_collect(void);
+int gsr_profile_get(const char* stage, int64_t* count, double* total_ms);
+void gsr_profile_reset(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GSRASTER_H */

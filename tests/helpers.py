@@ -1,0 +1,79 @@
+"""Shared test helpers: run a scene through the CPU oracle, compare arrays."""
+
+from __future__ import annotations
+
+import numpy as np
+
+from oracle import oracle as orc
+
+
+def scene_arrays(scene) -> dict:
+    """numpy copies of a synthetic Scene's parameters and camera (opacity post-sigmoid)."""
+    g, v = scene.gaussians, scene.view
+    import torch
+
+    f = lambda x: x.detach().cpu().numpy().astype(np.float32)
+    R, T = f(v["R"]), f(v["T"])
+    return dict(
+        mu=f(g.mu), q=f(g.q), s=f(g.s), alpha=f(torch.sigmoid(g.alpha.detach().cpu())),
+        A=f(g.A), kj=f(g.k_j), R=R, t=T, cam=(-(R.T @ T)).astype(np.float32).reshape(3),
+        fx=float(v["fx"]), fy=float(v["fy"]), cx=float(v["cx"]), cy=float(v["cy"]),
+        H=int(v["height"]), W=int(v["width"]))
+
+
+def oracle_forward(a: dict) -> dict:
+    mean2d, cov2d, depth = orc.project(a["mu"], a["q"], a["s"], a["R"], a["t"], a["fx"], a["fy"],
+                                       a["cx"], a["cy"])
+    colors = orc.sh(a["cam"], a["mu"], a["A"], a["kj"])
+    img, ids, ranges, fT, nc, keys = orc.rasterize(depth, mean2d, cov2d, colors, a["alpha"],
+                                                   a["H"], a["W"])
+    return dict(mean2d=mean2d, cov2d=cov2d, depth=depth, colors=colors, img=img, ids=ids,
+                ranges=ranges, final_T=fT, n_contrib=nc, keys=keys)
+
+
+def bits(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x)
+    return x.view(np.uint32) if x.dtype == np.float32 else x.view(np.uint64)
+
+
+def assert_bitwise(got, want, what: str) -> None:
+    got, want = np.asarray(got), np.asarray(want)
+    assert got.shape == want.shape, f"{what}: shape {got.shape} != {want.shape}"
+    if got.dtype in (np.float32, np.float64):
+        same = bits(got) == bits(want)
+        # +0 and -0 are the same value; the bar is the value bits otherwise
+        same |= (got == 0) & (want == 0)
+    else:
+        same = got == want
+    if not np.all(same):
+        idx = np.argwhere(~same)
+        first = tuple(idx[0])
+        raise AssertionError(
+            f"{what}: {idx.shape[0]} of {got.size} elements differ; first at {first}: "
+            f"got {got[first]!r} want {want[first]!r}")
+
+
+def assert_grad_close(got, want, absum, what: str, rel: float = 1e-4) -> None:
+    """fp32 gradient vs float64 oracle sum.
+
+    Bar: |got - want| <= rel * max(|want|, absum_floor) per element, where the
+    floor is rel-scaled by the sum of |terms| (absum) that formed the element:
+    an fp32 sum of k terms in any order is accurate to ~k*eps*sum|terms|, so
+    elements whose terms cancel are held to the conditioning of their sum, and
+    every other element to 1e-4 relative.
+    """
+    got = np.asarray(got, dtype=np.float64).reshape(np.shape(want))
+    want = np.asarray(want, dtype=np.float64)
+    absum = np.asarray(absum, dtype=np.float64).reshape(want.shape)
+    scale = np.maximum(np.abs(want), 0.05 * absum)
+    scale = np.maximum(scale, 1e-30)
+    err = np.abs(got - want) / scale
+    worst = np.unravel_index(np.argmax(err), err.shape) if err.size else None
+    assert err.size == 0 or err.max() <= rel, (
+        f"{what}: max scaled error {err.max():.3e} > {rel} at {worst}: got {got[worst]!r} "
+        f"want {want[worst]!r} absum {absum[worst]!r}")
+    # tensor-level relative error, the plain 1e-4 rel bar
+    den = np.linalg.norm(want.ravel())
+    if den > 0:
+        tot = np.linalg.norm((got - want).ravel()) / den
+        assert tot <= rel, f"{what}: tensor relative error {tot:.3e} > {rel}"

@@ -1,0 +1,222 @@
+"""GPU parity: the HIP library (through custom_rasterizer_cuda) against the CPU oracle.
+
+Bars (rasterizer baseline): sorted keys, sorted ids, tile ranges and n_contrib
+bit-exact; fp32 images and final transmittance within 1e-5 absolute; gradients
+within 1e-4 relative (helpers.assert_grad_close: 1e-4 of |oracle|, floored at
+5e-6 of the sum of |terms| for sums that cancel).  Projection, SH, images and
+transmittance are also checked bit for bit, which the shared operation order
+makes the expected outcome.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from gaussian_splatting import synthetic
+from helpers import assert_bitwise, assert_grad_close, oracle_forward, scene_arrays
+from oracle import oracle as orc
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, device, dtype=torch.float32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(device=device, dtype=dtype)
+
+
+def _np(t):
+    return t.detach().cpu().numpy()
+
+
+def gpu_forward(crc, a: dict, device) -> dict:
+    n = a["mu"].shape[0]
+    mu, q, s = _dev(a["mu"], device), _dev(a["q"], device), _dev(a["s"], device)
+    R, T = _dev(a["R"], device), _dev(a["t"], device)
+    mean2d, cov2d, depth = crc.project(n, mu, q, s, R, T, a["fx"], a["fy"], a["cx"], a["cy"])
+    colors = crc.SH(n, _dev(a["cam"], device), mu, _dev(a["A"], device), _dev(a["kj"], device))
+    alpha = _dev(a["alpha"], device)
+    img, ids, ranges, fT, nc, keys = crc.rasterize_with_keys(n, depth, mean2d, cov2d, colors,
+                                                             alpha, a["H"], a["W"])
+    torch.cuda.synchronize()
+    return dict(mean2d=_np(mean2d), cov2d=_np(cov2d), depth=_np(depth), colors=_np(colors),
+                img=_np(img), ids=_np(ids), ranges=_np(ranges), final_T=_np(fT),
+                n_contrib=_np(nc), keys=_np(keys).view(np.uint64), tensors=dict(
+                    mean2d=mean2d, cov2d=cov2d, colors=colors, alpha=alpha, ids=ids,
+                    ranges=ranges, final_T=fT, n_contrib=nc))
+
+
+def _check_forward(got, want, images_bitwise=True):
+    assert_bitwise(got["mean2d"], want["mean2d"], "mean2d")
+    assert_bitwise(got["cov2d"], want["cov2d"], "cov2d")
+    assert_bitwise(got["depth"], want["depth"], "depth")
+    assert_bitwise(got["colors"], want["colors"], "colors")
+    assert_bitwise(got["keys"], want["keys"], "sorted keys")
+    assert_bitwise(got["ids"], want["ids"], "sorted_ids")
+    assert_bitwise(got["ranges"], want["ranges"], "tile_ranges")
+    assert_bitwise(got["n_contrib"], want["n_contrib"], "n_contrib")
+    assert np.abs(got["img"] - want["img"]).max() <= 1e-5
+    assert np.abs(got["final_T"] - want["final_T"]).max() <= 1e-5
+    if images_bitwise:
+        assert_bitwise(got["img"], want["img"], "img")
+        assert_bitwise(got["final_T"], want["final_T"], "final_T")
+
+
+SCENES = [
+    ("c1", dict()),
+    ("c2", dict(n=20_000, width=640, height=360)),
+    ("c3", dict(n=20_000, width=480, height=270)),
+    ("c4", dict(n=50_000, width=480, height=272)),
+    ("c5", dict(n=30_000, width=400, height=224)),
+]
+
+
+@pytest.mark.parametrize("name,kw", SCENES, ids=[s[0] for s in SCENES])
+def test_forward_parity_configs(crc, device, name, kw):
+    print(f"[gpu] forward parity {name} {kw}", flush=True)
+    sc = synthetic.config_scene(name, requires_grad=False, **kw)
+    a = scene_arrays(sc)
+    _check_forward(gpu_forward(crc, a, device), oracle_forward(a))
+
+
+def test_forward_parity_bench_scene(crc, device):
+    sc = synthetic.bench_scene(n=30_000, width=640, height=360, requires_grad=False)
+    a = scene_arrays(sc)
+    _check_forward(gpu_forward(crc, a, device), oracle_forward(a))
+
+
+@pytest.mark.parametrize("H,W", [(16, 16), (17, 33), (1, 1), (100, 7), (240, 321)])
+def test_forward_parity_odd_screens(crc, device, H, W):
+    sc = synthetic.config_scene("c1", requires_grad=False, n=3000, width=W, height=H)
+    a = scene_arrays(sc)
+    _check_forward(gpu_forward(crc, a, device), oracle_forward(a))
+
+
+def test_projection_wide_ranges_bitwise(crc, device):
+    """Random poses, log-scales over [-12, 4] (exp over a wide range), culled points."""
+    rng = np.random.default_rng(5)
+    n = 200_000
+    mu = np.c_[rng.uniform(-3, 3, (n, 2)), rng.uniform(-1, 8, n)].astype(np.float32)
+    q = rng.normal(size=(n, 4)).astype(np.float32)
+    q[::97] = 0.0
+    s = rng.uniform(-12, 4, (n, 3)).astype(np.float32)
+    ang = rng.normal(size=4)
+    w, x, y, z = ang / np.linalg.norm(ang)
+    R = np.array([[1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)],
+                  [2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)],
+                  [2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)]], np.float32)
+    t = np.array([0.1, -0.2, 0.5], np.float32)
+    want = orc.project(mu, q, s, R, t, 811.0, 799.5, 640.0, 360.0)
+    got = crc.project(n, _dev(mu, device), _dev(q, device), _dev(s, device), _dev(R, device),
+                      _dev(t, device), 811.0, 799.5, 640.0, 360.0)
+    for g, w_, nm in zip(got, want, ("mean2d", "cov2d", "depth")):
+        assert_bitwise(_np(g), w_, nm)
+
+
+def test_sh_bitwise(crc, device):
+    rng = np.random.default_rng(6)
+    n = 100_000
+    mu = rng.normal(size=(n, 3)).astype(np.float32) * 3
+    A = rng.uniform(-2, 2, (n, 3)).astype(np.float32)
+    kj = rng.normal(0, 0.3, (n, 15, 3)).astype(np.float32)
+    cam = np.array([0.3, -0.1, -2.0], np.float32)
+    want = orc.sh(cam, mu, A, kj)
+    got = crc.SH(n, _dev(cam, device), _dev(mu, device), _dev(A, device), _dev(kj, device))
+    assert_bitwise(_np(got), want, "colors")
+
+
+def test_empty_frames(crc, device):
+    f = lambda *s: torch.zeros(*s, device=device)
+    img, ids, ranges, fT, nc = crc.rasterize(0, f(0), f(0, 2), f(0, 3), f(0, 3), f(0), 40, 50)
+    assert img.shape == (40, 50, 3) and float(img.abs().sum()) == 0
+    assert ids.numel() == 0 and ranges.shape == (12, 2) and int(ranges.abs().sum()) == 0
+    assert bool((fT == 1).all()) and int(nc.abs().sum()) == 0
+    # every Gaussian culled (zero covariance -> det <= 0 -> no tiles)
+    n = 10
+    img, ids, ranges, fT, nc = crc.rasterize(n, f(n) + 1, f(n, 2) + 5, f(n, 3), f(n, 3),
+                                             f(n) + 0.5, 32, 32)
+    assert ids.numel() == 0 and bool((fT == 1).all()) and float(img.abs().sum()) == 0
+    assert ranges.dtype == torch.int32 and nc.dtype == torch.int32
+
+
+def test_input_checks(crc, device):
+    n = 4
+    good = lambda *s: torch.zeros(*s, device=device)
+    with pytest.raises(RuntimeError, match="mean_2d must have shape"):
+        crc.rasterize(n, good(n), good(n, 3), good(n, 3), good(n, 3), good(n), 16, 16)
+    with pytest.raises(RuntimeError, match="must be contiguous"):
+        crc.rasterize(n, good(n), good(2, n).t(), good(n, 3), good(n, 3), good(n), 16, 16)
+    with pytest.raises(RuntimeError, match="must be FP32"):
+        crc.rasterize(n, good(n), good(n, 2).double(), good(n, 3), good(n, 3), good(n), 16, 16)
+    with pytest.raises(RuntimeError, match="must be a CUDA tensor"):
+        crc.rasterize(n, good(n).cpu(), good(n, 2), good(n, 3), good(n, 3), good(n), 16, 16)
+
+
+def _backward_case(crc, device, a, seed=3, corrupt=False):
+    fw = gpu_forward(crc, a, device)
+    want = oracle_forward(a)
+    assert_bitwise(fw["n_contrib"], want["n_contrib"], "n_contrib")
+    H, W = a["H"], a["W"]
+    G = synthetic.grad_image(H, W, seed=seed).numpy()
+    t = fw["tensors"]
+    ids = t["ids"]
+    ids_np = want["ids"].copy()
+    if corrupt and ids_np.size > 10:
+        pos = np.random.default_rng(0).choice(ids_np.size, 8, replace=False)
+        ids_np[pos[:4]] = -1
+        ids_np[pos[4:]] = a["mu"].shape[0] + 5
+        ids = _dev(ids_np, device, torch.int32)
+    n = a["mu"].shape[0]
+    dm, dc, dcol, dal = crc.backwards_rasterization(
+        _dev(G, device), t["mean2d"], t["cov2d"], t["colors"], t["alpha"], ids, t["ranges"],
+        t["final_T"], t["n_contrib"], n, H, W)
+    torch.cuda.synchronize()
+    ref = orc.blend_bwd(G, want["mean2d"], want["cov2d"], want["colors"], a["alpha"], ids_np,
+                        want["ranges"], want["final_T"], want["n_contrib"], H, W, with_abs=True)
+    for got_t, r, ab, nm in zip((dm, dc, dcol, dal), ref[:4], ref[4:], ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")):
+        assert_grad_close(_np(got_t), r, ab, nm)
+    assert dal.shape == (n, 1)
+    return fw, want, G, (dm, dc, dcol, dal)
+
+
+@pytest.mark.parametrize("name,kw", [("c1", dict()), ("c3", dict(n=20_000, width=480, height=270)),
+                                     ("c5", dict(n=20_000, width=320, height=192))],
+                         ids=["c1", "c3", "c5"])
+def test_rasterize_backward_parity(crc, device, name, kw):
+    print(f"[gpu] backward parity {name} {kw}", flush=True)
+    a = scene_arrays(synthetic.config_scene(name, requires_grad=False, **kw))
+    _backward_case(crc, device, a)
+
+
+def test_rasterize_backward_skips_corrupt_ids(crc, device):
+    a = scene_arrays(synthetic.config_scene("c1", requires_grad=False, n=2000, width=64, height=48))
+    _backward_case(crc, device, a, corrupt=True)
+
+
+def test_sh_and_projection_backward_parity(crc, device):
+    rng = np.random.default_rng(9)
+    n = 50_000
+    a = scene_arrays(synthetic.config_scene("c3", requires_grad=False, n=n))
+    cg = rng.normal(size=(n, 3)).astype(np.float32)
+    want = orc.sh_bwd(cg, a["mu"], a["A"], a["kj"], a["cam"])
+    got = crc.backwards_SH(_dev(cg, device), _dev(a["mu"], device), _dev(a["A"], device),
+                           _dev(a["kj"], device), _dev(a["cam"], device))
+    for g, w, nm in zip(got, want, ("d_albedo", "d_k_j", "d_mu_sh")):
+        assert_bitwise(_np(g), w, nm)
+    dm = rng.normal(size=(n, 2)).astype(np.float32)
+    dc = rng.normal(size=(n, 3)).astype(np.float32)
+    want = orc.project_bwd(dm, dc, a["mu"], a["q"], a["s"], a["R"], a["t"], a["fx"], a["fy"],
+                           a["cx"], a["cy"])
+    got = crc.backwards_projection(_dev(dm, device), _dev(dc, device), _dev(a["mu"], device),
+                                   _dev(a["q"], device), _dev(a["s"], device), _dev(a["R"], device),
+                                   _dev(a["t"], device), a["fx"], a["fy"], a["cx"], a["cy"])
+    for g, w, nm in zip(got, want, ("d_mu", "d_q", "d_s")):
+        assert_bitwise(_np(g), w, nm)
+
+
+def test_forward_is_deterministic(crc, device):
+    a = scene_arrays(synthetic.config_scene("c2", requires_grad=False, n=40_000))
+    r1 = gpu_forward(crc, a, device)
+    r2 = gpu_forward(crc, a, device)
+    for k in ("keys", "ids", "ranges", "n_contrib", "img", "final_T"):
+        assert_bitwise(r1[k], r2[k], k)
