@@ -48,7 +48,38 @@ def test_projection_backward_matches_finite_differences(crc, device):
     m2, c2 = Project.apply(mu, q, s)
     assert torch.isfinite(m2).all() and torch.isfinite(c2).all()
     assert float(m2.detach().abs().sum()) > 1.0 and float(c2.detach().abs().sum()) > 0.1
-    assert gradcheck(Project.apply, (mu, q, s), **GRADCHECK)
+    # fp32 central differences at eps 1e-3 of outputs near 43 px^2 carry ~ulp(43)/eps
+    # ~ 2e-3 of rounding noise, above atol; the numerical Jacobian is therefore taken
+    # from the float64 forward (the CPU oracle, whose fp32 forward the GPU matches bit
+    # for bit) at the same fp32 inputs, and the GPU's analytical Jacobian is held to
+    # the reference's tolerances against it.
+    import numpy as np
+    from oracle import oracle as orc
+
+    inputs = {"mu": mu, "q": q, "s": s}
+    n_out = 10
+    for name, x in inputs.items():
+        ana = np.zeros((n_out, x.numel()))
+        for o in range(n_out):
+            gm = torch.zeros(2, 2, device=device)
+            gc = torch.zeros(2, 3, device=device)
+            (gm if o < 4 else gc).view(-1)[o if o < 4 else o - 4] = 1.0
+            grads = crc.backwards_projection(gm, gc, mu.detach(), q.detach(), s.detach(),
+                                             rotation, translation, fx, fy, cx, cy)
+            ana[o] = grads[list(inputs).index(name)].detach().cpu().numpy().reshape(-1)
+        num = np.zeros_like(ana)
+        base = {k: v.detach().cpu().numpy().astype(np.float64) for k, v in inputs.items()}
+        for j in range(x.numel()):
+            outs = []
+            for sgn in (1, -1):
+                p = {k: v.copy() for k, v in base.items()}
+                p[name].reshape(-1)[j] += sgn * GRADCHECK["eps"]
+                a2, b2, _ = orc.project(p["mu"], p["q"], p["s"], np.eye(3), np.zeros(3), fx, fy, cx,
+                                        cy, dtype=np.float64)
+                outs.append(np.concatenate([a2.reshape(-1), b2.reshape(-1)]))
+            num[:, j] = (outs[0] - outs[1]) / (2 * GRADCHECK["eps"])
+        bad = np.abs(ana - num) > GRADCHECK["atol"] + GRADCHECK["rtol"] * np.abs(num)
+        assert not bad.any(), (name, np.argwhere(bad)[:4], ana[bad][:4], num[bad][:4])
 
 
 def test_sh_backward_matches_finite_differences(crc, device):
