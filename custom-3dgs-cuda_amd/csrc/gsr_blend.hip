@@ -11,9 +11,9 @@
 // when its ballot of live lanes is empty; the tile stops when all 256 are done.
 // Backward: the tile walks only entries [0, max n_contrib) of its list, back
 // to front (the reference walks all K entries and skips the tail per pixel);
-// each entry's 9 per-pixel gradient terms are summed across the wave (64 -> 1),
-// across the four waves through LDS, and then added to HBM with one set of 9
-// float atomics per (tile, entry).
+// each entry's 9 per-pixel gradient terms are summed across the wave (64 -> 1,
+// one transposed permlane/DPP reduction), across the four waves through LDS,
+// and then added to HBM with one set of 9 float atomics per (tile, entry).
 #include "gsr_internal.h"
 #include "gsr_common.h"
 
@@ -152,6 +152,7 @@ __global__ __launch_bounds__(kThreads) void blend_bwd_kernel(
     const int maxc = min((int)max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3])), end - start);
 
     float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f;
+    const int my_value = reduce9_value_of_lane(lane);
     for (int hi = maxc; hi > 0; hi -= kBatch) {
         const int lo = max(0, hi - kBatch);
         const int cnt = hi - lo;
@@ -173,58 +174,50 @@ __global__ __launch_bounds__(kThreads) void blend_bwd_kernel(
         __syncthreads();
         for (int j = cnt - 1; j >= 0; --j) {
             const int contributor = lo + j + 1;
+            // Branch-free form of the reference's per-pixel skips: an entry the
+            // pixel did not blend (beyond n_contrib, power > 0, alpha < 1/255,
+            // corrupt id) contributes zero terms and leaves T and the
+            // background colour unchanged.
+            const float4 A = s_a[j];
+            const float4 B = s_b[j];
+            const float4 Cc = s_c[j];
+            const float dx = fpx - A.x;
+            const float dy = fpy - A.y;
+            const float power = -0.5f * (A.z * dx * dx + A.w * dx * dy + B.x * dy * dy);
+            const float G = exp_gs(power);
+            const float araw = B.y * G;
+            const float alpha = fminf(kAlphaMax, araw);
+            const bool id_ok = s_id[j] >= 0;
+            const bool act = (contributor <= last) & id_ok & !(power > 0.0f) &
+                             !(alpha < kAlphaMin);
+            const float om = 1.0f - alpha;
+            const float Tb = T / fmaxf(om, 1e-4f);
+            const float aT = act ? alpha * Tb : 0.0f;
+            const float dal =
+                act ? ((B.z - acc0) * g0 + (B.w - acc1) * g1 + (Cc.x - acc2) * g2) * Tb : 0.0f;
+            // alpha = min(0.99, o G): a clamped alpha passes no gradient to o or G
+            const bool unclamped = araw < kAlphaMax;
+            const float dop = unclamped ? G * dal : 0.0f;
+            const float dpw = unclamped ? alpha * dal : 0.0f;
+            const float cy = Cc.y;
             float v[9];
-#pragma unroll
-            for (int k = 0; k < 9; ++k) v[k] = 0.0f;
-            bool act = false;
-            if (contributor <= last && s_id[j] >= 0) {
-                const float4 A = s_a[j];
-                const float4 B = s_b[j];
-                const float dx = fpx - A.x;
-                const float dy = fpy - A.y;
-                const float power = -0.5f * (A.z * dx * dx + A.w * dx * dy + B.x * dy * dy);
-                if (!(power > 0.0f)) {
-                    const float G = exp_gs(power);
-                    const float araw = B.y * G;
-                    const float alpha = fminf(kAlphaMax, araw);
-                    if (!(alpha < kAlphaMin)) {
-                        act = true;
-                        const float4 Cc = s_c[j];
-                        const float om = 1.0f - alpha;
-                        const float Tb = T / fmaxf(om, 1e-4f);
-                        const float aT = alpha * Tb;
-                        v[5] = aT * g0;
-                        v[6] = aT * g1;
-                        v[7] = aT * g2;
-                        const float dal =
-                            ((B.z - acc0) * g0 + (B.w - acc1) * g1 + (Cc.x - acc2) * g2) * Tb;
-                        float dop = 0.0f, dpw = 0.0f;
-                        if (araw < kAlphaMax) {
-                            dop = G * dal;
-                            dpw = alpha * dal;
-                        }
-                        const float cy = Cc.y;
-                        v[0] = dpw * (A.z * dx + cy * dy);
-                        v[1] = dpw * (cy * dx + B.x * dy);
-                        v[2] = -0.5f * dpw * dx * dx;
-                        v[3] = -dpw * dx * dy;
-                        v[4] = -0.5f * dpw * dy * dy;
-                        v[8] = dop;
-                        acc0 = alpha * B.z + om * acc0;
-                        acc1 = alpha * B.w + om * acc1;
-                        acc2 = alpha * Cc.x + om * acc2;
-                        T = Tb;
-                    }
-                }
-            }
-            if (ballot(act) != 0) {
-#pragma unroll
-                for (int k = 0; k < 9; ++k) v[k] = wave_sum(v[k]);
-            }
-            if (lane == 0) {
-#pragma unroll
-                for (int k = 0; k < 9; ++k) s_part[wave][k][j] = v[k];
-            }
+            v[0] = dpw * (A.z * dx + cy * dy);
+            v[1] = dpw * (cy * dx + B.x * dy);
+            v[2] = -0.5f * dpw * dx * dx;
+            v[3] = -dpw * dx * dy;
+            v[4] = -0.5f * dpw * dy * dy;
+            v[5] = aT * g0;
+            v[6] = aT * g1;
+            v[7] = aT * g2;
+            v[8] = dop;
+            acc0 = act ? alpha * B.z + om * acc0 : acc0;
+            acc1 = act ? alpha * B.w + om * acc1 : acc1;
+            acc2 = act ? alpha * Cc.x + om * acc2 : acc2;
+            T = act ? Tb : T;
+            // Wave totals of the nine terms: one transposed reduction, then the
+            // nine lanes that hold a total write it (zeros when no lane blended).
+            const float w9 = (ballot(act) != 0) ? wave_reduce9(v) : 0.0f;
+            if (my_value >= 0) s_part[wave][my_value][j] = w9;
         }
         __syncthreads();
         if (tid < cnt) {

@@ -27,11 +27,14 @@ constexpr float kTransmittanceMin = 1e-4f;  // rasterize.cu:265
 // Faithfully rounded (max 0.955 ulp over [-87.34, 88.72]); results below
 // FLT_MIN are flushed to +0.  Host and device evaluate the same IEEE
 // operations, so their results agree bit for bit.
+// Branch-free: the polynomial runs on x clamped to the finite range (bit-identical
+// for in-range x) and the out-of-range results are selected afterwards, so a
+// wave never diverges inside exp.
 __device__ __forceinline__ float exp_gs(float x) {
-    if (x > 88.72283935546875f) return __builtin_inff();
-    if (!(x >= -87.33654022216796875f)) return (x != x) ? x : 0.0f;
-    const float k = __builtin_rintf(x * 1.44269502162933349609375f);
-    float r = __builtin_fmaf(-k, 0.693145751953125f, x);
+    constexpr float kHi = 88.72283935546875f, kLo = -87.33654022216796875f;
+    const float xc = fminf(fmaxf(x, kLo), kHi);
+    const float k = __builtin_rintf(xc * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(-k, 0.693145751953125f, xc);
     r = __builtin_fmaf(-k, 1.428606765330187045e-06f, r);
     float p = 0.0013766406336799264f;
     p = __builtin_fmaf(p, r, 0.00837041437625885f);
@@ -40,7 +43,9 @@ __device__ __forceinline__ float exp_gs(float x) {
     p = __builtin_fmaf(p, r, 0.49999988079071045f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_ldexpf(p, (int)k);
+    const float e = __builtin_ldexpf(p, (int)k);
+    const float below = (x != x) ? x : 0.0f;
+    return (x > kHi) ? __builtin_inff() : ((x >= kLo) ? e : below);
 }
 
 // Saturating float -> int32 with NaN -> 0 (the GPU conversion the reference's
@@ -70,6 +75,76 @@ __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
     return v;
+}
+
+// DPP lane moves within a 16-lane row (gfx9 encodings).
+template <int Ctrl, int BankMask = 0xf>
+__device__ __forceinline__ float dpp_move(float x, float old = 0.0f) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(x), Ctrl,
+                                                      0xf, BankMask, false));
+}
+constexpr int kDppQuadXor1 = 0xB1;  // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;  // quad_perm [2,3,0,1]
+constexpr int kDppRowShl4 = 0x104;
+constexpr int kDppRowShr4 = 0x114;
+constexpr int kDppRowRor8 = 0x128;  // lane i <- lane i ^ 8 within the row
+
+// lane i <- lane i ^ 4 within the row: two bank-masked moves.
+__device__ __forceinline__ float lane_xor4(float x) {
+    const float t = dpp_move<kDppRowShr4, 0xa>(x);
+    return dpp_move<kDppRowShl4, 0x5>(x, t);
+}
+
+// a + b with their upper/lower 32-lane halves exchanged: lanes 0-31 get
+// a[l] + a[l+32], lanes 32-63 get b[l-32] + b[l] (v_permlane32_swap, gfx950).
+__device__ __forceinline__ float fold32(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+// Row-pair fold: rows 0,2 get a's (row0+row1, row2+row3), rows 1,3 get b's
+// (v_permlane16_swap, gfx950).
+__device__ __forceinline__ float fold16(float a, float b) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Sums nine per-lane values over the whole wave with a transposed reduction:
+// each level halves the number of live registers while doubling the lanes
+// summed (32: permlane32 swap, 16: permlane16 swap, 8: row_ror, 4: bank-masked
+// row shifts, 2 and 1: quad permutes), ~30 VALU instead of 9 x 6 shuffles.
+// Value k's wave total ends in lane kReduce9Lane[k] of the result.  All 64
+// lanes must be active.
+constexpr int kReduce9Lane[9] = {0, 32, 16, 48, 8, 40, 24, 56, 4};
+
+__device__ __forceinline__ float wave_reduce9(const float v[9]) {
+    const float r0 = fold32(v[0], v[1]);  // lanes 0-31: v0, 32-63: v1
+    const float r1 = fold32(v[2], v[3]);
+    const float r2 = fold32(v[4], v[5]);
+    const float r3 = fold32(v[6], v[7]);
+    const float r4 = fold32(v[8], v[8]);
+    const float s0 = fold16(r0, r1);      // rows: v0, v2, v1, v3
+    const float s1 = fold16(r2, r3);      // rows: v4, v6, v5, v7
+    const float s2 = fold16(r4, r4);      // rows: v8
+    const int l = lane_id();
+    const bool b3 = (l & 8) != 0;
+    const float u0 = (b3 ? s1 : s0) + dpp_move<kDppRowRor8>(b3 ? s0 : s1);
+    const float u1 = s2 + dpp_move<kDppRowRor8>(s2);
+    const bool b2 = (l & 4) != 0;
+    float w = (b2 ? u1 : u0) + lane_xor4(b2 ? u0 : u1);
+    w = w + dpp_move<kDppQuadXor2>(w);
+    w = w + dpp_move<kDppQuadXor1>(w);
+    return w;
+}
+
+// Which of the nine values lane l holds after wave_reduce9 (-1: a duplicate).
+__device__ __forceinline__ int reduce9_value_of_lane(int l) {
+    if (l & 3) return -1;
+    const int row = l >> 4, sub = (l >> 2) & 3;
+    if (sub == 0) return (row == 0) ? 0 : (row == 1) ? 2 : (row == 2) ? 1 : 3;
+    if (sub == 2) return (row == 0) ? 4 : (row == 1) ? 6 : (row == 2) ? 5 : 7;
+    return (l == 4) ? 8 : -1;
 }
 
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
