@@ -121,6 +121,24 @@ __global__ __launch_bounds__(kThreads) void full_keys_kernel(uint64_t m,
     keys[i] = ((uint64_t)tiles[i] << 32) | (uint64_t)dbits;
 }
 
+// Squared distance d^2 beyond which o * exp(-q/2) < 1/255 for every pixel, with
+// q = d^T C d >= lambda_min(C) |d|^2.  Computed in double from the fp32 conic and
+// opacity; lambda_min is lowered by 2e-5 (mid + |cy|) to cover the fp32
+// rounding of q in the per-pixel evaluation (~4e-7 of the same scale), and the
+// threshold raised by 0.1% + 1e-4 to cover exp and the o*G product, so an entry
+// is skipped only where the reference's per-pixel tests skip it too.
+__device__ __forceinline__ float alpha_cut_radius2(float cx, float cy, float cz, float o) {
+    if (!(o >= kAlphaMin)) return -1.0f;  // alpha <= o < 1/255 for every pixel
+    const double mid = 0.5 * ((double)cx + (double)cz);
+    const double det = (double)cx * cz - (double)cy * cy;
+    if (!(det > 0.0) || !(mid > 0.0)) return __builtin_inff();
+    const double lmax = mid + sqrt(fmax(0.0, mid * mid - det));
+    const double k = 0.5 * (det / lmax - 2e-5 * (mid + fabs((double)cy)));
+    if (!(k > 0.0)) return __builtin_inff();
+    const double r2 = (log(255.0 * (double)o) * 1.001 + 1e-4) / k;
+    return nextafterf((float)r2, __builtin_inff());
+}
+
 // Conic = cov^-1 with 1/det first (rasterize.cu:224-232), packed with mean,
 // opacity and colour so the blend loads one 48 B record per list entry.
 __global__ __launch_bounds__(kThreads) void blend_records_kernel(
@@ -136,7 +154,8 @@ __global__ __launch_bounds__(kThreads) void blend_records_kernel(
     BlendRec r;
     r.a = make_float4(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1], cx, 2.0f * cy);
     r.b = make_float4(cz, alpha[i], colors[3 * (size_t)i], colors[3 * (size_t)i + 1]);
-    r.c = make_float4(colors[3 * (size_t)i + 2], cy, 0.0f, 0.0f);
+    r.c = make_float4(colors[3 * (size_t)i + 2], cy, alpha_cut_radius2(cx, cy, cz, alpha[i]),
+                      0.0f);
     recs[i] = r;
 }
 

@@ -1,19 +1,32 @@
 // gsr_blend.hip — front-to-back alpha blend (a8) and its backward (a10).
 //
-// One work-group per 16x16 tile, four wave64s, each wave owning an 8x8 pixel
-// quadrant (compact quadrants let a whole wave finish together).  A batch of
-// 256 list entries is staged in LDS as 48 B blend records (one coalesced
-// record load per entry); every lane then walks the batch with broadcast LDS
+// One work-group per 16x16 tile.  Layout template kPix (pixels per lane):
+// 4 / kPix wave64s, each owning a 16 x (4 kPix) strip of the tile; lane l
+// holds column l & 15 and rows (l >> 4) + 4p, p < kPix, of its strip.  More
+// pixels per lane give each lane independent dependency chains and divide the
+// per-pixel share of the batch loads and of the backward's wave reductions;
+// more waves per tile shorten the longest tile's critical path.  A batch of
+// one list entry per thread is staged in LDS as 48 B blend records (one
+// coalesced record load per entry); lanes walk the batch with broadcast LDS
 // reads.  Per-pixel arithmetic is the reference's, operation for operation
 // (rasterize.cu:241-270, rasterize_backward.cu:113-200).
 //
-// Forward early exit: a lane is done once T < 1e-4; a wave leaves the batch
-// when its ballot of live lanes is empty; the tile stops when all 256 are done.
+// Exact strip culling: each record carries cut2, a squared distance beyond
+// which no pixel can reach alpha >= 1/255 (gsr_bin.hip).  When the batch is
+// staged, each entry gets one bit per strip: clear when the strip lies beyond
+// cut2 from the mean.  Every pixel of such a strip would skip the entry in the
+// reference's own tests, so the wave skips it without changing any result.
+//
+// Forward early exit: a pixel is done once T < 1e-4; a wave leaves the batch
+// when its ballot of live pixels is empty; the tile stops when all are done.
 // Backward: the tile walks only entries [0, max n_contrib) of its list, back
-// to front (the reference walks all K entries and skips the tail per pixel);
-// each entry's 9 per-pixel gradient terms are summed across the wave (64 -> 1,
-// one transposed permlane/DPP reduction), across the four waves through LDS,
-// and then added to HBM with one set of 9 float atomics per (tile, entry).
+// to front (the reference walks all K entries and skips the tail per pixel),
+// and each wave skips entries beyond its own max n_contrib; each entry's 9
+// per-pixel gradient terms are summed in the lane, across the wave (one
+// transposed permlane/DPP reduction) and across the waves through LDS, then
+// added to HBM with one set of 9 float atomics per (tile, entry).
+#include <cstdlib>
+
 #include "gsr_internal.h"
 #include "gsr_common.h"
 
@@ -21,21 +34,32 @@ namespace gsr {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kBatch = 256;
-
-struct PixelMap {
-    int px, py;
-    bool inside;
+template <int kPix>
+struct Layout {
+    static constexpr int kWaves = 4 / kPix;
+    static constexpr int kThreads = kWaves * kWave;
+    static constexpr int kBatch = kThreads;
+    static constexpr int kRows = 4 * kPix;  // rows per wave strip
 };
 
-__device__ __forceinline__ PixelMap pixel_of(int tile, int tiles_x, int W, int H) {
+template <int kPix>
+struct Pixels {
+    int px;
+    int py[kPix];
+    bool in[kPix];
+};
+
+template <int kPix>
+__device__ __forceinline__ Pixels<kPix> pixels_of(int tile, int tiles_x, int W, int H) {
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int tx = tile % tiles_x, ty = tile / tiles_x;
-    PixelMap p;
-    p.px = tx * kTileSize + (wave & 1) * 8 + (lane & 7);
-    p.py = ty * kTileSize + (wave >> 1) * 8 + (lane >> 3);
-    p.inside = p.px < W && p.py < H;
+    Pixels<kPix> p;
+    p.px = tx * kTileSize + (lane & 15);
+#pragma unroll
+    for (int k = 0; k < kPix; ++k) {
+        p.py[k] = ty * kTileSize + wave * Layout<kPix>::kRows + (lane >> 4) + 4 * k;
+        p.in[k] = p.px < W && p.py[k] < H;
+    }
     return p;
 }
 
@@ -46,188 +70,294 @@ __device__ __forceinline__ void clamp_range(int2 rg, uint64_t m, int& start, int
     end = (int)e;
 }
 
-__global__ __launch_bounds__(kThreads) void blend_fwd_kernel(
+// Bit w set: a pixel of strip w may lie within cut2 of the mean.  The fp32
+// distance carries ~3e-7 relative rounding; the 1e-6 slack keeps the test
+// conservative.
+template <int kPix>
+__device__ __forceinline__ uint32_t strip_bits(const BlendRec& r, int tile, int tiles_x) {
+    const float cut2 = r.c.z;
+    const int tx = tile % tiles_x, ty = tile / tiles_x;
+    const float x0 = (float)(tx * kTileSize), x1 = x0 + (float)(kTileSize - 1);
+    const float ddx = fmaxf(fmaxf(x0 - r.a.x, r.a.x - x1), 0.0f);
+    uint32_t bits = 0;
+#pragma unroll
+    for (int w = 0; w < Layout<kPix>::kWaves; ++w) {
+        const float y0 = (float)(ty * kTileSize + w * Layout<kPix>::kRows);
+        const float y1 = y0 + (float)(Layout<kPix>::kRows - 1);
+        const float ddy = fmaxf(fmaxf(y0 - r.a.y, r.a.y - y1), 0.0f);
+        const float d2 = ddx * ddx + ddy * ddy;
+        const bool skip = d2 * (1.0f - 1e-6f) > cut2;
+        bits |= skip ? 0u : (1u << w);
+    }
+    return bits;
+}
+
+template <int kPix>
+__device__ __forceinline__ void stage_entry(const BlendRec* __restrict__ recs, int g, int n,
+                                            int tile, int tiles_x, float4* s_a, float4* s_b,
+                                            float4* s_c, uint32_t* s_bits, int* s_id, int slot) {
+    BlendRec r;
+    const bool ok = g >= 0 && g < n;
+    if (ok) {
+        r = recs[g];
+    } else {  // corrupt id: skipped (rasterize_backward.cu:79-86)
+        r.a = r.b = r.c = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    s_a[slot] = r.a;
+    s_b[slot] = r.b;
+    s_c[slot] = r.c;
+    s_bits[slot] = ok ? strip_bits<kPix>(r, tile, tiles_x) : 0u;
+    if (s_id) s_id[slot] = ok ? g : -1;
+}
+
+struct FwdPixel {
+    float T, C0, C1, C2;
+    int last;
+    bool done;
+};
+
+// One pixel's forward step for one list entry (rasterize.cu:243-268), with the
+// reference's skips as selects: the same fp32 operations in the same order.
+__device__ __forceinline__ void fwd_step(FwdPixel& p, float fx, float fy, const float4& A,
+                                         const float4& B, float cb, int contributor) {
+    const float dx = fx - A.x;
+    const float dy = fy - A.y;
+    const float power = -0.5f * (A.z * dx * dx + A.w * dx * dy + B.x * dy * dy);
+    const float alpha = fminf(kAlphaMax, B.y * exp_gs(power));
+    const bool blend = !p.done & !(power > 0.0f) & !(alpha < kAlphaMin);
+    const float w = alpha * p.T;
+    const float Tn = p.T * (1.0f - alpha);
+    p.C0 = blend ? p.C0 + B.z * w : p.C0;
+    p.C1 = blend ? p.C1 + B.w * w : p.C1;
+    p.C2 = blend ? p.C2 + cb * w : p.C2;
+    p.T = blend ? Tn : p.T;
+    p.last = blend ? contributor : p.last;
+    p.done = p.done | (blend & (Tn < kTransmittanceMin));
+}
+
+template <int kPix>
+__device__ __forceinline__ bool all_done(const FwdPixel (&p)[kPix]) {
+    bool d = true;
+#pragma unroll
+    for (int k = 0; k < kPix; ++k) d &= p[k].done;
+    return d;
+}
+
+template <int kPix>
+__global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
     int n, int H, int W, int tiles_x, uint64_t m, const int2* __restrict__ ranges,
     const int32_t* __restrict__ ids, const BlendRec* __restrict__ recs, float* __restrict__ img,
     float* __restrict__ finalT, int32_t* __restrict__ ncontrib) {
+    constexpr int kBatch = Layout<kPix>::kBatch;
     __shared__ float4 s_a[kBatch];
     __shared__ float4 s_b[kBatch];
     __shared__ float4 s_c[kBatch];
+    __shared__ uint32_t s_bits[kBatch];
     const int tile = blockIdx.x;
-    const PixelMap pm = pixel_of(tile, tiles_x, W, H);
-    const float fpx = (float)pm.px, fpy = (float)pm.py;
+    const int tid = threadIdx.x, wave = tid >> 6;
+    const uint32_t my_bit = 1u << wave;
+    const Pixels<kPix> pp = pixels_of<kPix>(tile, tiles_x, W, H);
+    const float fx = (float)pp.px;
+    float fy[kPix];
+    FwdPixel p[kPix];
+#pragma unroll
+    for (int k = 0; k < kPix; ++k) {
+        fy[k] = (float)pp.py[k];
+        p[k] = FwdPixel{1.0f, 0.0f, 0.0f, 0.0f, 0, !pp.in[k]};
+    }
     int start, end;
     clamp_range(ranges[tile], m, start, end);
 
-    float T = 1.0f, C0 = 0.0f, C1 = 0.0f, C2 = 0.0f;
-    int last = 0;
-    bool done = !pm.inside;
-    const int tid = threadIdx.x;
     for (int b0 = start; b0 < end; b0 += kBatch) {
         const int cnt = min(kBatch, end - b0);
         __syncthreads();
-        if (tid < cnt) {
-            const int g = ids[b0 + tid];
-            BlendRec r;
-            if (g >= 0 && g < n) {
-                r = recs[g];
-            } else {  // ids come from the sort; a zero record is never blended
-                r.a = r.b = r.c = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            }
-            s_a[tid] = r.a;
-            s_b[tid] = r.b;
-            s_c[tid] = r.c;
-        }
+        if (tid < cnt)
+            stage_entry<kPix>(recs, ids[b0 + tid], n, tile, tiles_x, s_a, s_b, s_c, s_bits,
+                              nullptr, tid);
         __syncthreads();
-        if (ballot(!done) != 0) {
-            const int cbase = b0 - start;
+        if (ballot(!all_done(p)) != 0) {
+            const int cbase = b0 - start + 1;
             for (int j = 0; j < cnt; ++j) {
-                if (!done) {
-                    const float4 A = s_a[j];
-                    const float4 B = s_b[j];
-                    const float dx = fpx - A.x;
-                    const float dy = fpy - A.y;
-                    const float power = -0.5f * (A.z * dx * dx + A.w * dx * dy + B.x * dy * dy);
-                    if (!(power > 0.0f)) {
-                        const float alpha = fminf(kAlphaMax, B.y * exp_gs(power));
-                        if (!(alpha < kAlphaMin)) {
-                            const float w = alpha * T;
-                            C0 = C0 + B.z * w;
-                            C1 = C1 + B.w * w;
-                            C2 = C2 + s_c[j].x * w;
-                            T = T * (1.0f - alpha);
-                            last = cbase + j + 1;
-                            if (T < kTransmittanceMin) done = true;
-                        }
-                    }
-                }
-                if (ballot(!done) == 0) break;
+                if ((s_bits[j] & my_bit) == 0) continue;  // no pixel of this strip blends it
+                const float4 A = s_a[j];
+                const float4 B = s_b[j];
+                const float cb = s_c[j].x;
+#pragma unroll
+                for (int k = 0; k < kPix; ++k) fwd_step(p[k], fx, fy[k], A, B, cb, cbase + j);
+                if (ballot(!all_done(p)) == 0) break;
             }
         }
-        if (__syncthreads_and(done)) break;
+        if (__syncthreads_and(all_done(p))) break;
     }
-    if (pm.inside) {
-        const size_t p = (size_t)pm.py * W + pm.px;
-        img[3 * p] = C0;
-        img[3 * p + 1] = C1;
-        img[3 * p + 2] = C2;
-        finalT[p] = T;
-        ncontrib[p] = last;
+#pragma unroll
+    for (int k = 0; k < kPix; ++k) {
+        if (!pp.in[k]) continue;
+        const size_t q = (size_t)pp.py[k] * W + pp.px;
+        img[3 * q] = p[k].C0;
+        img[3 * q + 1] = p[k].C1;
+        img[3 * q + 2] = p[k].C2;
+        finalT[q] = p[k].T;
+        ncontrib[q] = p[k].last;
     }
 }
 
-__global__ __launch_bounds__(kThreads) void blend_bwd_kernel(
+struct BwdPixel {
+    float g0, g1, g2, T, acc0, acc1, acc2;
+    int last;
+};
+
+// One pixel's backward step for one list entry (rasterize_backward.cu:117-198):
+// writes its 9 terms to t and returns whether the pixel blended the entry.
+// The decision part (power, exp, alpha) is evaluated exactly as in the forward
+// so the skips (beyond n_contrib, power > 0, alpha < 1/255) match it; they are
+// selects, so a skipped entry gives zero terms and leaves T and the
+// background colour unchanged.  The gradient arithmetic after the decision
+// only has to meet the fp32 gradient tolerance and may use fused multiply-adds.
+__device__ __forceinline__ bool bwd_step(BwdPixel& p, float fx, float fy, const float4& A,
+                                         const float4& B, const float4& Cc, int contributor,
+                                         float t[9]) {
+    const float dx = fx - A.x;
+    const float dy = fy - A.y;
+    const float power = -0.5f * (A.z * dx * dx + A.w * dx * dy + B.x * dy * dy);
+    const float G = exp_gs(power);
+    const float araw = B.y * G;
+    const float alpha = fminf(kAlphaMax, araw);
+    const bool act = (contributor <= p.last) & !(power > 0.0f) & !(alpha < kAlphaMin);
+    {
+#pragma clang fp contract(fast)
+        const float om = 1.0f - alpha;
+        // T / max(1 - alpha, 1e-4): reciprocal refined by one Newton step (~1 ulp)
+        const float d = fmaxf(om, 1e-4f);
+        float r = __builtin_amdgcn_rcpf(d);
+        r = __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+        const float Tb = p.T * r;
+        const float aT = act ? alpha * Tb : 0.0f;
+        const float dal = act ? ((B.z - p.acc0) * p.g0 + (B.w - p.acc1) * p.g1 +
+                                 (Cc.x - p.acc2) * p.g2) * Tb
+                              : 0.0f;
+        // alpha = min(0.99, o G): a clamped alpha passes no gradient to o or G
+        const bool unclamped = araw < kAlphaMax;
+        const float dop = unclamped ? G * dal : 0.0f;
+        const float dpw = unclamped ? alpha * dal : 0.0f;
+        const float cy = Cc.y;
+        t[0] = dpw * (A.z * dx + cy * dy);
+        t[1] = dpw * (cy * dx + B.x * dy);
+        t[2] = -0.5f * dpw * dx * dx;
+        t[3] = -dpw * dx * dy;
+        t[4] = -0.5f * dpw * dy * dy;
+        t[5] = aT * p.g0;
+        t[6] = aT * p.g1;
+        t[7] = aT * p.g2;
+        t[8] = dop;
+        p.acc0 = act ? alpha * B.z + om * p.acc0 : p.acc0;
+        p.acc1 = act ? alpha * B.w + om * p.acc1 : p.acc1;
+        p.acc2 = act ? alpha * Cc.x + om * p.acc2 : p.acc2;
+        p.T = act ? Tb : p.T;
+    }
+    return act;
+}
+
+__device__ __forceinline__ BwdPixel load_bwd_pixel(bool in, int px, int py, int W,
+                                                   const float* __restrict__ grad,
+                                                   const float* __restrict__ finalT,
+                                                   const int32_t* __restrict__ ncontrib) {
+    BwdPixel p{0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0};
+    if (in) {
+        const size_t q = (size_t)py * W + px;
+        p.g0 = grad[3 * q];
+        p.g1 = grad[3 * q + 1];
+        p.g2 = grad[3 * q + 2];
+        p.T = finalT[q];
+        p.last = max(ncontrib[q], 0);
+    }
+    return p;
+}
+
+template <int kPix>
+__global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     int n, int H, int W, int tiles_x, uint64_t m, const float* __restrict__ grad,
     const int2* __restrict__ ranges, const int32_t* __restrict__ ids,
     const BlendRec* __restrict__ recs, const float* __restrict__ finalT,
     const int32_t* __restrict__ ncontrib, float* __restrict__ dmean, float* __restrict__ dcov,
     float* __restrict__ dcol, float* __restrict__ dalpha) {
+    constexpr int kWaves = Layout<kPix>::kWaves;
+    constexpr int kBatch = Layout<kPix>::kBatch;
     __shared__ float4 s_a[kBatch];
     __shared__ float4 s_b[kBatch];
     __shared__ float4 s_c[kBatch];
+    __shared__ uint32_t s_bits[kBatch];
     __shared__ int s_id[kBatch];
-    __shared__ float s_part[4][9][kBatch];
-    __shared__ uint32_t s_max[4];
+    __shared__ float s_part[kWaves][9][kBatch];
+    __shared__ uint32_t s_max[kWaves];
 
     const int tile = blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const PixelMap pm = pixel_of(tile, tiles_x, W, H);
-    const float fpx = (float)pm.px, fpy = (float)pm.py;
+    const uint32_t my_bit = 1u << wave;
+    const Pixels<kPix> pp = pixels_of<kPix>(tile, tiles_x, W, H);
+    const float fx = (float)pp.px;
+    float fy[kPix];
+    BwdPixel p[kPix];
+    int my_last = 0;
+#pragma unroll
+    for (int k = 0; k < kPix; ++k) {
+        fy[k] = (float)pp.py[k];
+        p[k] = load_bwd_pixel(pp.in[k], pp.px, pp.py[k], W, grad, finalT, ncontrib);
+        my_last = max(my_last, p[k].last);
+    }
     int start, end;
     clamp_range(ranges[tile], m, start, end);
-
-    float g0 = 0.0f, g1 = 0.0f, g2 = 0.0f, T = 0.0f;
-    int last = 0;
-    if (pm.inside) {
-        const size_t p = (size_t)pm.py * W + pm.px;
-        g0 = grad[3 * p];
-        g1 = grad[3 * p + 1];
-        g2 = grad[3 * p + 2];
-        T = finalT[p];
-        last = ncontrib[p];
-    }
-    const uint32_t wmax = wave_max_u32((uint32_t)max(last, 0));
-    if (lane == 0) s_max[wave] = wmax;
+    const int wave_last = (int)wave_max_u32((uint32_t)my_last);
+    if (lane == 0) s_max[wave] = (uint32_t)wave_last;
     __syncthreads();
-    const int maxc = min((int)max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3])), end - start);
-
-    float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f;
+    uint32_t tile_last = 0;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) tile_last = max(tile_last, s_max[w]);
+    const int maxc = min((int)tile_last, end - start);
     const int my_value = reduce9_value_of_lane(lane);
+
     for (int hi = maxc; hi > 0; hi -= kBatch) {
         const int lo = max(0, hi - kBatch);
         const int cnt = hi - lo;
         __syncthreads();
-        if (tid < cnt) {
-            const int g = ids[start + lo + tid];
-            const bool ok = g >= 0 && g < n;  // corrupt ids are skipped (rasterize_backward.cu:79-86)
-            s_id[tid] = ok ? g : -1;
-            BlendRec r;
-            if (ok) {
-                r = recs[g];
-            } else {
-                r.a = r.b = r.c = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            }
-            s_a[tid] = r.a;
-            s_b[tid] = r.b;
-            s_c[tid] = r.c;
-        }
+        if (tid < cnt)
+            stage_entry<kPix>(recs, ids[start + lo + tid], n, tile, tiles_x, s_a, s_b, s_c,
+                              s_bits, s_id, tid);
         __syncthreads();
         for (int j = cnt - 1; j >= 0; --j) {
             const int contributor = lo + j + 1;
-            // Branch-free form of the reference's per-pixel skips: an entry the
-            // pixel did not blend (beyond n_contrib, power > 0, alpha < 1/255,
-            // corrupt id) contributes zero terms and leaves T and the
-            // background colour unchanged.
-            const float4 A = s_a[j];
-            const float4 B = s_b[j];
-            const float4 Cc = s_c[j];
-            const float dx = fpx - A.x;
-            const float dy = fpy - A.y;
-            const float power = -0.5f * (A.z * dx * dx + A.w * dx * dy + B.x * dy * dy);
-            const float G = exp_gs(power);
-            const float araw = B.y * G;
-            const float alpha = fminf(kAlphaMax, araw);
-            const bool id_ok = s_id[j] >= 0;
-            const bool act = (contributor <= last) & id_ok & !(power > 0.0f) &
-                             !(alpha < kAlphaMin);
-            const float om = 1.0f - alpha;
-            const float Tb = T / fmaxf(om, 1e-4f);
-            const float aT = act ? alpha * Tb : 0.0f;
-            const float dal =
-                act ? ((B.z - acc0) * g0 + (B.w - acc1) * g1 + (Cc.x - acc2) * g2) * Tb : 0.0f;
-            // alpha = min(0.99, o G): a clamped alpha passes no gradient to o or G
-            const bool unclamped = araw < kAlphaMax;
-            const float dop = unclamped ? G * dal : 0.0f;
-            const float dpw = unclamped ? alpha * dal : 0.0f;
-            const float cy = Cc.y;
-            float v[9];
-            v[0] = dpw * (A.z * dx + cy * dy);
-            v[1] = dpw * (cy * dx + B.x * dy);
-            v[2] = -0.5f * dpw * dx * dx;
-            v[3] = -dpw * dx * dy;
-            v[4] = -0.5f * dpw * dy * dy;
-            v[5] = aT * g0;
-            v[6] = aT * g1;
-            v[7] = aT * g2;
-            v[8] = dop;
-            acc0 = act ? alpha * B.z + om * acc0 : acc0;
-            acc1 = act ? alpha * B.w + om * acc1 : acc1;
-            acc2 = act ? alpha * Cc.x + om * acc2 : acc2;
-            T = act ? Tb : T;
-            // Wave totals of the nine terms: one transposed reduction, then the
-            // nine lanes that hold a total write it (zeros when no lane blended).
-            const float w9 = (ballot(act) != 0) ? wave_reduce9(v) : 0.0f;
+            float w9 = 0.0f;
+            // wave-uniform skips: beyond every pixel's n_contrib, or culled
+            if (contributor <= wave_last && (s_bits[j] & my_bit) != 0) {
+                const float4 A = s_a[j];
+                const float4 B = s_b[j];
+                const float4 Cc = s_c[j];
+                float v[9];
+                bool act = bwd_step(p[0], fx, fy[0], A, B, Cc, contributor, v);
+#pragma unroll
+                for (int k = 1; k < kPix; ++k) {
+                    float t[9];
+                    act |= bwd_step(p[k], fx, fy[k], A, B, Cc, contributor, t);
+#pragma unroll
+                    for (int q = 0; q < 9; ++q) v[q] += t[q];
+                }
+                if (ballot(act) != 0) w9 = wave_reduce9(v);
+            }
             if (my_value >= 0) s_part[wave][my_value][j] = w9;
         }
         __syncthreads();
         if (tid < cnt) {
             const int g = s_id[tid];
-            if (g >= 0) {
-                float t[9];
+            float t[9];
+            bool any = false;
 #pragma unroll
-                for (int k = 0; k < 9; ++k)
-                    t[k] = s_part[0][k][tid] + s_part[1][k][tid] + s_part[2][k][tid] +
-                           s_part[3][k][tid];
+            for (int k = 0; k < 9; ++k) {
+                float acc = 0.0f;
+#pragma unroll
+                for (int w = 0; w < kWaves; ++w) acc += s_part[w][k][tid];
+                t[k] = acc;
+                any |= acc != 0.0f;
+            }
+            if (g >= 0 && any) {
                 // conic gradient -> covariance gradient (rasterize_backward.cu:211-221)
                 const float vx = s_a[tid].z, vy = s_c[tid].y, vz = s_b[tid].x;
                 const float gx = t[2], gy = 0.5f * t[3], gz = t[4];
@@ -248,6 +378,22 @@ __global__ __launch_bounds__(kThreads) void blend_bwd_kernel(
     }
 }
 
+// Pixels per lane for each kernel: the measured defaults, overridable for
+// tuning with GSR_BLEND_FWD_PIX / GSR_BLEND_BWD_PIX = 1 or 2.
+int pix_setting(const char* env, int dflt) {
+    const char* v = std::getenv(env);
+    if (v && (v[0] == '1' || v[0] == '2') && v[1] == '\0') return v[0] - '0';
+    return dflt;
+}
+int fwd_pix() {
+    static const int p = pix_setting("GSR_BLEND_FWD_PIX", 1);
+    return p;
+}
+int bwd_pix() {
+    static const int p = pix_setting("GSR_BLEND_BWD_PIX", 2);
+    return p;
+}
+
 }  // namespace
 
 hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
@@ -257,9 +403,14 @@ hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const in
     const int tiles_y = (H + kTileSize - 1) / kTileSize;
     const unsigned tiles = (unsigned)(tiles_x * tiles_y);
     if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(blend_fwd_kernel, dim3(tiles), dim3(kThreads), 0, st, n, H, W, tiles_x, m,
-                       reinterpret_cast<const int2*>(ranges), ids,
-                       static_cast<const BlendRec*>(recs), img, finalT, ncontrib);
+    const auto* r = reinterpret_cast<const int2*>(ranges);
+    const auto* rc = static_cast<const BlendRec*>(recs);
+    if (fwd_pix() == 2)
+        hipLaunchKernelGGL(blend_fwd_kernel<2>, dim3(tiles), dim3(Layout<2>::kThreads), 0, st, n,
+                           H, W, tiles_x, m, r, ids, rc, img, finalT, ncontrib);
+    else
+        hipLaunchKernelGGL(blend_fwd_kernel<1>, dim3(tiles), dim3(Layout<1>::kThreads), 0, st, n,
+                           H, W, tiles_x, m, r, ids, rc, img, finalT, ncontrib);
     return hipGetLastError();
 }
 
@@ -271,10 +422,16 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_
     const int tiles_y = (H + kTileSize - 1) / kTileSize;
     const unsigned tiles = (unsigned)(tiles_x * tiles_y);
     if (tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(blend_bwd_kernel, dim3(tiles), dim3(kThreads), 0, st, n, H, W, tiles_x,
-                       num_pairs, grad, reinterpret_cast<const int2*>(ranges), ids,
-                       static_cast<const BlendRec*>(recs), finalT, ncontrib, dmean, dcov, dcol,
-                       dalpha);
+    const auto* r = reinterpret_cast<const int2*>(ranges);
+    const auto* rc = static_cast<const BlendRec*>(recs);
+    if (bwd_pix() == 2)
+        hipLaunchKernelGGL(blend_bwd_kernel<2>, dim3(tiles), dim3(Layout<2>::kThreads), 0, st, n,
+                           H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib, dmean,
+                           dcov, dcol, dalpha);
+    else
+        hipLaunchKernelGGL(blend_bwd_kernel<1>, dim3(tiles), dim3(Layout<1>::kThreads), 0, st, n,
+                           H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib, dmean,
+                           dcov, dcol, dalpha);
     return hipGetLastError();
 }
 
