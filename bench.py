@@ -41,7 +41,7 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
     (N Gaussians, M pairs, P pixels, T tiles); the two sorts use this build's own
     algorithm (8 B read + 8 B written per element and pass, plus one 4 B histogram read)."""
     P, T = W * H, _tiles(W, H)
-    tile_passes = max(1, math.ceil(max(1, (T - 1).bit_length()) / 8)) if T > 1 else 0
+    tile_passes = max(1, math.ceil((T - 1).bit_length() / 8)) if T > 1 else 1
     return {
         "project": 64 * N,
         "sh": 216 * N,
@@ -49,8 +49,9 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
         "depth_sort": 4 * 16 * N + 4 * N,
         "scan": 12 * N,
         "records": 36 * N + 48 * N,
-        "emit": 8 * M + 24 * N,
-        "tile_sort": tile_passes * 16 * M + 4 * M,
+        # the first pass generates its pairs from per-Gaussian data (perm,
+        # offset, rect: 16 B) and writes 8 B per pair; later passes move 16 B
+        "tile_sort": (16 * tile_passes - 8) * M + 16 * N,
         "ranges": 4 * M + 8 * T,
         "blend_fwd": 40 * M + 20 * P + 8 * T,
         "blend_bwd": 76 * M + 20 * P + 8 * T,

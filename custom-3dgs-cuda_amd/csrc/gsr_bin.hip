@@ -1,15 +1,20 @@
-// gsr_bin.hip — tile binning (a3-a5), tile ranges (a7) and the per-Gaussian
-// blend records.
+// gsr_bin.hip — tile binning, tile ranges and the per-Gaussian blend records.
 //
 // Ordering design.  The reference emits 64-bit (tile << 32 | depth bits) keys
 // in Gaussian-major order and stable-sorts all of them (rasterize.cu:124-135,
 // :423-435), which orders pairs by (tile, depth bits, Gaussian id).  Here the
 // Gaussians are first stable-sorted by depth bits (N keys, 32 bits), pairs are
-// emitted in that depth order carrying only the tile id, and the pairs are
+// laid out in that depth order carrying only the tile id, and the pairs are
 // then stable-sorted by the tile id's significant bits.  Stability makes the
 // result the same (tile, depth bits, Gaussian id) order, bit for bit, while
 // the M-sized sort moves 8 B per pair per pass over ceil(log2 T / 8) passes
-// instead of 12 B over ceil((32 + log2 T) / 8).
+// instead of 12 B over ceil((32 + log2 T) / 8).  The pairs are never written
+// in depth order: the first tile-sort pass generates them per partition from
+// the depth order, the per-Gaussian offsets and tile rectangles, and the
+// passes' digit histograms come from the rectangles here, so no pass reads
+// the keys only to count them.
+#include <algorithm>
+
 #include "gsr_internal.h"
 #include "gsr_common.h"
 
@@ -47,45 +52,109 @@ __device__ __forceinline__ TileRect tile_rect(float mx, float my, float a, float
     return r;
 }
 
+// Adds the digit counts of the tile ids in the row range [a, a + w) to the
+// work-group histograms: digit 0 through a difference array over the 256 bins
+// (w >> 8 full cycles are counted once per row in *full), digits 1..passes-1
+// per aligned block of 256^p ids the range meets.
+__device__ __forceinline__ void hist_row(uint32_t a, uint32_t w, int passes, int* s_d0,
+                                         uint32_t (*s_h)[kRadixBins], uint32_t* full) {
+    *full += w >> 8;
+    const uint32_t rem = w & 255u;
+    if (rem) {
+        const uint32_t st = a & 255u, en = st + rem;
+        atomicAdd(&s_d0[st], 1);
+        if (en <= 256u) {
+            atomicSub(&s_d0[en], 1);
+        } else {
+            atomicAdd(&s_d0[0], 1);
+            atomicSub(&s_d0[en - 256u], 1);
+        }
+    }
+    for (int p = 1; p < passes; ++p) {
+        const int sh = 8 * p;
+        const uint64_t lo = a, hi = (uint64_t)a + w;
+        for (uint64_t b = lo >> sh; b <= (hi - 1) >> sh; ++b) {
+            const uint64_t bl = max(lo, b << sh), bh = min(hi, (b + 1) << sh);
+            atomicAdd(&s_h[p - 1][b & 255u], (uint32_t)(bh - bl));
+        }
+    }
+}
+
+// Per Gaussian: tile rectangle and count (rasterize.cu:19-59, :98-105), the
+// depth sort's key and value, and the Gaussian's share of the tile sort's
+// global digit histograms (tile_hist[p][d] counts the pairs whose tile id has
+// digit d in pass p), accumulated per work-group and flushed with one global
+// atomic per non-zero bin.
 __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     int n, const float* __restrict__ mean2d, const float* __restrict__ cov2d,
     const float* __restrict__ depth, int H, int W, uint32_t* __restrict__ counts,
-    uint2* __restrict__ rects, uint32_t* __restrict__ dkeys, uint32_t* __restrict__ dvals) {
-    const int i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const TileRect r = tile_rect(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1],
-                                 cov2d[3 * (size_t)i], cov2d[3 * (size_t)i + 1],
-                                 cov2d[3 * (size_t)i + 2], W, H);
-    const uint32_t cnt = r.ok ? (uint32_t)(max(0, r.x1 - r.x0) * max(0, r.y1 - r.y0)) : 0u;
-    counts[i] = cnt;
-    rects[i] = make_uint2((uint32_t)r.x0 | ((uint32_t)r.x1 << 16),
-                          (uint32_t)r.y0 | ((uint32_t)r.y1 << 16));
-    // Gaussians without tiles sort last; they emit nothing, so their place
-    // in the depth order never shows.
-    dkeys[i] = cnt ? __float_as_uint(depth[i]) : 0xffffffffu;
-    dvals[i] = (uint32_t)i;
+    uint2* __restrict__ rects, uint32_t* __restrict__ dkeys, uint32_t* __restrict__ dvals,
+    int passes, uint32_t* __restrict__ tile_hist) {
+    __shared__ int s_d0[kRadixBins + 1];
+    __shared__ uint32_t s_h[3][kRadixBins];
+    __shared__ uint32_t s_full[kThreads / kWave];
+    __shared__ uint32_t s_scan[kThreads / kWave];
+    const int tid = threadIdx.x;
+    for (int j = tid; j <= kRadixBins; j += kThreads) s_d0[j] = 0;
+    for (int j = tid; j < 3 * kRadixBins; j += kThreads) (&s_h[0][0])[j] = 0;
+    __syncthreads();
+    const int tiles_x = (W + 15) / 16;
+    uint32_t full = 0;
+    for (int i = blockIdx.x * kThreads + tid; i < n; i += gridDim.x * kThreads) {
+        const TileRect r = tile_rect(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1],
+                                     cov2d[3 * (size_t)i], cov2d[3 * (size_t)i + 1],
+                                     cov2d[3 * (size_t)i + 2], W, H);
+        const uint32_t cnt = r.ok ? (uint32_t)(max(0, r.x1 - r.x0) * max(0, r.y1 - r.y0)) : 0u;
+        counts[i] = cnt;
+        rects[i] = make_uint2((uint32_t)r.x0 | ((uint32_t)r.x1 << 16),
+                              (uint32_t)r.y0 | ((uint32_t)r.y1 << 16));
+        // Gaussians without tiles sort last; they emit nothing, so their place
+        // in the depth order never shows.
+        dkeys[i] = cnt ? __float_as_uint(depth[i]) : 0xffffffffu;
+        dvals[i] = (uint32_t)i;
+        if (cnt) {
+            const uint32_t w = (uint32_t)(r.x1 - r.x0);
+            for (int y = r.y0; y < r.y1; ++y)
+                hist_row((uint32_t)y * (uint32_t)tiles_x + (uint32_t)r.x0, w, passes, s_d0, s_h,
+                         &full);
+        }
+    }
+    const uint32_t wfull = (uint32_t)wave_sum_u32(full);
+    if ((tid & 63) == 0) s_full[tid >> 6] = wfull;
+    __syncthreads();
+    // digit-0 bin d = full cycles + prefix of the difference array
+    const uint32_t all = s_full[0] + s_full[1] + s_full[2] + s_full[3];
+    const uint32_t inc = wave_inclusive_scan((uint32_t)s_d0[tid]);
+    if ((tid & 63) == 63) s_scan[tid >> 6] = inc;
+    __syncthreads();
+    uint32_t pre = 0;
+    for (int w = 0; w < (tid >> 6); ++w) pre += s_scan[w];
+    const uint32_t d0 = all + pre + inc;
+    if (d0) atomicAdd(&tile_hist[tid], d0);
+    for (int p = 1; p < passes; ++p) {
+        const uint32_t v = s_h[p - 1][tid];
+        if (v) atomicAdd(&tile_hist[p * kRadixBins + tid], v);
+    }
 }
 
-// One thread per depth rank: write the Gaussian's tiles, ty outer, tx inner.
-__global__ __launch_bounds__(kThreads) void emit_pairs_kernel(
+// part_rank[p] = the depth rank whose pairs include sort slot p * kSortPartition;
+// part_rank[nparts] = one past the last rank with pairs.
+__global__ __launch_bounds__(kThreads) void partition_starts_kernel(
     int n, const uint32_t* __restrict__ perm, const uint32_t* __restrict__ counts,
-    const uint2* __restrict__ rects, const uint32_t* __restrict__ offsets, int tiles_x,
-    uint64_t m, uint32_t* __restrict__ tile_keys, uint32_t* __restrict__ ids) {
+    const uint32_t* __restrict__ offsets, uint64_t m, uint32_t nparts,
+    uint32_t* __restrict__ part_rank) {
     const int r = blockIdx.x * kThreads + threadIdx.x;
     if (r >= n) return;
     const uint32_t g = perm[r];
-    if (g >= (uint32_t)n || counts[g] == 0) return;
-    if ((uint64_t)offsets[r] + counts[g] > m) return;  // inconsistent scan: write nothing
-    const uint2 rc = rects[g];
-    const int x0 = rc.x & 0xffff, x1 = rc.x >> 16, y0 = rc.y & 0xffff, y1 = rc.y >> 16;
-    size_t o = offsets[r];
-    for (int ty = y0; ty < y1; ++ty) {
-        const uint32_t row = (uint32_t)(ty * tiles_x);
-        for (int tx = x0; tx < x1; ++tx, ++o) {
-            tile_keys[o] = row + (uint32_t)tx;
-            ids[o] = g;
-        }
-    }
+    if (g >= (uint32_t)n) return;
+    const uint64_t c = counts[g];
+    if (c == 0) return;
+    const uint64_t off = offsets[r], end = off + c;
+    if (end > m) return;  // inconsistent scan: write nothing
+    for (uint64_t p = (off + kSortPartition - 1) / kSortPartition; p <= (end - 1) / kSortPartition;
+         ++p)
+        part_rank[p] = (uint32_t)r;
+    if (end == m) part_rank[nparts] = (uint32_t)r + 1;
 }
 
 // identify_tile_ranges_kernel (rasterize.cu:140-166): tile boundaries in the
@@ -165,19 +234,25 @@ inline unsigned blocks_for(uint64_t n) { return (unsigned)((n + kThreads - 1) / 
 
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
-                            uint32_t* dvals, hipStream_t st) {
+                            uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
+                            hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(bin_count_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, n, mean2d,
-                       cov2d, depth, H, W, counts, rects, dkeys, dvals);
+    if (tile_passes < 1 || tile_passes > 4) return hipErrorInvalidValue;
+    // at most one work-group per CU: the histogram flush costs one global
+    // atomic per bin and work-group
+    const unsigned blocks = std::min(blocks_for(n), 256u);
+    hipLaunchKernelGGL(bin_count_kernel, dim3(blocks), dim3(kThreads), 0, st, n, mean2d, cov2d,
+                       depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist);
     return hipGetLastError();
 }
 
-hipError_t launch_emit_pairs(int n, const uint32_t* perm, const uint32_t* counts,
-                             const uint2* rects, const uint32_t* offsets, int tiles_x, uint64_t m,
-                             uint32_t* tile_keys, uint32_t* ids, hipStream_t st) {
-    if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(emit_pairs_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, n, perm,
-                       counts, rects, offsets, tiles_x, m, tile_keys, ids);
+hipError_t launch_partition_starts(int n, const uint32_t* perm, const uint32_t* counts,
+                                   const uint32_t* offsets, uint64_t m, uint32_t* part_rank,
+                                   hipStream_t st) {
+    if (n <= 0 || m == 0) return hipSuccess;
+    const uint32_t nparts = (uint32_t)((m + kSortPartition - 1) / kSortPartition);
+    hipLaunchKernelGGL(partition_starts_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, n,
+                       perm, counts, offsets, m, nparts, part_rank);
     return hipGetLastError();
 }
 

@@ -49,17 +49,18 @@ constexpr size_t kRecBytes = 48;
 int tiles_x_of(int W) { return (W + 15) / 16; }
 int tiles_y_of(int H) { return (H + 15) / 16; }
 
-// Digit passes needed to sort tile ids in [0, T).
+// Digit passes of the tile sort for tile ids in [0, T): ceil(bits / 8), at
+// least one (the pass that generates the pairs).
 int tile_passes(int64_t T) {
-    if (T <= 1) return 0;
     int bits = 0;
-    uint64_t v = (uint64_t)(T - 1);
+    uint64_t v = (uint64_t)(T > 1 ? T - 1 : 0);
     while (v) {
         ++bits;
         v >>= 1;
     }
-    return (bits + 7) / 8;
+    return bits > 8 ? (bits + 7) / 8 : 1;
 }
+constexpr int kMaxTilePasses = 4;
 
 // Misc block at the head of the bin workspace.
 struct Misc {
@@ -69,7 +70,7 @@ struct Misc {
 };
 
 struct BinLayout {
-    size_t misc, sortctl, scanctl, ctl_end;
+    size_t misc, sortctl, scanctl, tilehist, ctl_end;
     size_t counts, rects, dk0, dv0, dk1, dv1, offsets, recs, end;
 };
 
@@ -85,6 +86,7 @@ BinLayout bin_layout(int n) {
     L.misc = take(sizeof(Misc));
     L.sortctl = take(gsr::sort_control_bytes(un, kDepthPasses));
     L.scanctl = take(gsr::scan_control_bytes(n));
+    L.tilehist = take((size_t)kMaxTilePasses * 256 * 4);
     L.ctl_end = off;
     L.counts = take(4 * un);
     L.rects = take(8 * un);
@@ -99,7 +101,7 @@ BinLayout bin_layout(int n) {
 }
 
 struct SortLayout {
-    size_t ctl, ctl_end, tk0, tk1, vbuf, end;
+    size_t ctl, part_rank, ctl_end, tk0, tk1, vbuf, end;
 };
 
 SortLayout sort_layout(int64_t m, int passes) {
@@ -111,7 +113,8 @@ SortLayout sort_layout(int64_t m, int passes) {
         return o;
     };
     const size_t um = (size_t)(m > 0 ? m : 0);
-    L.ctl = take(passes > 0 ? gsr::sort_control_bytes(um, passes) : 0);
+    L.ctl = take(gsr::onesweep_state_bytes(um, passes));
+    L.part_rank = take(4 * ((um + gsr::kSortPartition - 1) / gsr::kSortPartition + 1));
     L.ctl_end = off;
     L.tk0 = take(4 * um);
     L.tk1 = take(4 * um);
@@ -260,8 +263,10 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
     uint32_t* dv0 = at<uint32_t>(bin_ws, L.dv0);
     {
         StageTimer timer("bin_count", st);
+        const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
         GSR_HIP(gsr::launch_bin_count(n, mean2d, cov2d, depth, height, width, counts,
-                                      at<uint2>(bin_ws, L.rects), dk0, dv0, st),
+                                      at<uint2>(bin_ws, L.rects), dk0, dv0, tile_passes(T),
+                                      at<uint32_t>(bin_ws, L.tilehist), st),
                 "rasterize: count");
     }
     {
@@ -332,28 +337,32 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
         }
         uint32_t* tk0 = at<uint32_t>(sort_ws, SL.tk0);
         uint32_t* tk1 = at<uint32_t>(sort_ws, SL.tk1);
-        uint32_t* vbuf = at<uint32_t>(sort_ws, SL.vbuf);
         uint32_t* ids = reinterpret_cast<uint32_t*>(sorted_ids);
-        uint32_t* v0 = (passes % 2 == 0) ? ids : vbuf;
-        uint32_t* v1 = (passes % 2 == 0) ? vbuf : ids;
-        {
-            StageTimer timer("emit", st);
-            GSR_HIP(gsr::launch_emit_pairs(n, at<uint32_t>(bin_ws, BL.dv0),
-                                           at<uint32_t>(bin_ws, BL.counts),
-                                           at<uint2>(bin_ws, BL.rects),
-                                           at<uint32_t>(bin_ws, BL.offsets), tiles_x, m, tk0, v0, st),
-                    "rasterize: emit");
-        }
+        uint32_t* ktiles = ((passes - 1) % 2 == 0) ? tk0 : tk1;  // the last pass's keys
         {
             StageTimer timer("tile_sort", st);
-            GSR_HIP(gsr::launch_radix_sort(tk0, v0, tk1, v1, m, 0, passes,
-                                           at<void>(sort_ws, SL.ctl), &misc->err, st),
+            uint32_t* part_rank = at<uint32_t>(sort_ws, SL.part_rank);
+            gsr::EmitSource es;
+            es.perm = at<uint32_t>(bin_ws, BL.dv0);
+            es.counts = at<uint32_t>(bin_ws, BL.counts);
+            es.rects = at<uint2>(bin_ws, BL.rects);
+            es.offsets = at<uint32_t>(bin_ws, BL.offsets);
+            es.part_rank = part_rank;
+            es.nparts = (uint32_t)((m + gsr::kSortPartition - 1) / gsr::kSortPartition);
+            es.tiles_x = tiles_x;
+            GSR_HIP(gsr::launch_partition_starts(n, es.perm, es.counts, es.offsets, m, part_rank,
+                                                 st),
+                    "rasterize: partition starts");
+            GSR_HIP(gsr::launch_tile_sort(es, m, passes, at<uint32_t>(bin_ws, BL.tilehist),
+                                          at<void>(sort_ws, SL.ctl), tk0, tk1,
+                                          at<uint32_t>(sort_ws, SL.vbuf), ids, ktiles,
+                                          &misc->err, st),
                     "rasterize: tile sort");
         }
-        const uint32_t* ktiles = (passes % 2 == 0) ? tk0 : tk1;
         {
             StageTimer timer("ranges", st);
-            GSR_HIP(gsr::launch_tile_ranges(m, (uint32_t)T, ktiles, tile_ranges, st), "rasterize: ranges");
+            GSR_HIP(gsr::launch_tile_ranges(m, (uint32_t)T, ktiles, tile_ranges, st),
+                    "rasterize: ranges");
         }
         if (sorted_keys)
             GSR_HIP(gsr::launch_full_keys(m, ktiles, sorted_ids, depth, n, sorted_keys, st),

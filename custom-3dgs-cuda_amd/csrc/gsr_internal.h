@@ -47,12 +47,38 @@ hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t*
 
 hipError_t zero_fill(void* p, size_t bytes, hipStream_t st);
 
+// Where the first tile-sort pass generates its (tile, Gaussian) pairs: depth
+// order perm, per-Gaussian counts and packed tile rectangles, per-rank pair
+// offsets, and part_rank[p] = the rank holding pair slot p * kSortPartition
+// (nparts + 1 entries; the last is one past the last rank with pairs).
+struct EmitSource {
+    const uint32_t* perm = nullptr;
+    const uint32_t* counts = nullptr;
+    const uint2* rects = nullptr;
+    const uint32_t* offsets = nullptr;
+    const uint32_t* part_rank = nullptr;
+    uint32_t nparts = 0;
+    int tiles_x = 0;
+};
+
+// Status words and partition counters of `passes` onesweep passes over n
+// elements (zero before use).
+size_t onesweep_state_bytes(uint64_t n, int passes);
+// Stable LSD sort of the m pairs described by es on tile-id digits 0..passes-1.
+// hist holds the passes' global digit histograms ([passes][256], from the
+// tile rectangles).  Values (Gaussian ids) end in out_vals; keys (tile ids)
+// in out_keys when it is not null.  k0/k1/vbuf are m-element scratch.
+hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, const uint32_t* hist,
+                            void* state, uint32_t* k0, uint32_t* k1, uint32_t* vbuf,
+                            uint32_t* out_vals, uint32_t* out_keys, int* err, hipStream_t st);
+
 // ---- binning ----
 // counts[g], packed tile rect, depth key (float bits or 0xffffffff when the
 // Gaussian touches no tile) and identity values.
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
-                            uint32_t* dvals, hipStream_t st);
+                            uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
+                            hipStream_t st);
 
 // Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r]; the total
 // (u64) is written to *total.
@@ -61,10 +87,11 @@ hipError_t launch_scan_counts(int n, const uint32_t* perm, const uint32_t* count
                               uint32_t* offsets, uint64_t* total, void* control, int* err,
                               hipStream_t st);
 
-// Pair emission in depth order: tile keys + Gaussian ids.
-hipError_t launch_emit_pairs(int n, const uint32_t* perm, const uint32_t* counts,
-                             const uint2* rects, const uint32_t* offsets, int tiles_x, uint64_t m,
-                             uint32_t* tile_keys, uint32_t* ids, hipStream_t st);
+// part_rank[p] for the fused emission of the first tile-sort pass (nparts + 1
+// entries, nparts = ceil(m / kSortPartition)).
+hipError_t launch_partition_starts(int n, const uint32_t* perm, const uint32_t* counts,
+                                   const uint32_t* offsets, uint64_t m, uint32_t* part_rank,
+                                   hipStream_t st);
 
 // [start, end) per tile from sorted tile keys; ranges must be zeroed.
 hipError_t launch_tile_ranges(uint64_t m, uint32_t T, const uint32_t* sorted_tiles,

@@ -101,36 +101,121 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restr
     }
 }
 
+// Expands the (tile, Gaussian) pairs of sort slots [base, base + nvalid) into
+// s_keys / s_vals, slot order.  Pair slots are laid out by depth rank r at
+// offsets[r] (ty outer, tx inner over the rank's tile rectangle), the order in
+// which the reference emits keys per Gaussian (rasterize.cu:124-135).  Ranks
+// r_lo..r_lo+nr-1 overlap the partition; the first kSortPartition of their
+// offsets are staged in s_off (more only occur when ranks without pairs sit
+// between ranks with pairs, and are then read from global memory).  Each
+// thread expands 16 consecutive slots: one binary search, then a linear walk.
+__device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base, int nvalid,
+                                             uint32_t* s_keys, uint32_t* s_vals,
+                                             uint32_t* s_off) {
+    const int tid = threadIdx.x;
+    const uint32_t part = (uint32_t)(base / kSortPartition);
+    const uint32_t r_lo = es.part_rank[part];
+    const uint32_t r_next = es.part_rank[part + 1];
+    // last rank holding a slot of this partition
+    const uint64_t next_base = base + (uint64_t)nvalid;
+    const uint32_t r_last =
+        (part + 1 < es.nparts && (uint64_t)es.offsets[r_next] < next_base) ? r_next : r_next - 1;
+    const uint32_t nr = (r_last >= r_lo) ? r_last - r_lo + 1 : 1u;
+    const uint32_t nstage = min(nr, (uint32_t)kSortPartition);
+    for (uint32_t j = tid; j < nstage; j += kSortThreads) s_off[j] = es.offsets[r_lo + j];
+    __syncthreads();
+    auto off_of = [&](uint32_t j) -> uint64_t {
+        return (j < (uint32_t)kSortPartition) ? s_off[j] : es.offsets[r_lo + j];
+    };
+    const int first = tid * kSortItems;
+    if (first < nvalid) {
+        const uint64_t s0 = base + (uint64_t)first;
+        uint32_t lo = 0, hi = nr - 1;  // last j with offset <= s0
+        while (lo < hi) {
+            const uint32_t mid = (lo + hi + 1) >> 1;
+            if (off_of(mid) <= s0) lo = mid; else hi = mid - 1;
+        }
+        uint32_t j = lo;
+        uint32_t g = es.perm[r_lo + j];
+        uint2 rc = es.rects[g];
+        uint32_t x0 = rc.x & 0xffffu, w = (rc.x >> 16) - x0, y0 = rc.y & 0xffffu;
+        uint64_t kbase = off_of(j);
+        uint64_t next = (j + 1 < nr) ? off_of(j + 1) : ~0ull;
+        for (int i = 0; i < kSortItems; ++i) {
+            const int slot = first + i;
+            if (slot >= nvalid) break;
+            const uint64_t sg = base + (uint64_t)slot;
+            while (sg >= next) {
+                ++j;
+                g = es.perm[r_lo + j];
+                rc = es.rects[g];
+                x0 = rc.x & 0xffffu;
+                w = (rc.x >> 16) - x0;
+                y0 = rc.y & 0xffffu;
+                kbase = next;
+                next = (j + 1 < nr) ? off_of(j + 1) : ~0ull;
+            }
+            const uint32_t k = (uint32_t)(sg - kbase);
+            const uint32_t row = w ? k / w : 0u;
+            const uint32_t col = k - row * w;
+            s_keys[slot] = (y0 + row) * (uint32_t)es.tiles_x + x0 + col;
+            s_vals[slot] = g;
+        }
+    }
+    __syncthreads();
+}
+
+// One LSD pass over 8-bit digit (key >> shift) & 0xff.  kEmit: the partition's
+// (tile, Gaussian) pairs are generated from the depth order instead of being
+// read (the first tile pass).  kWriteKeys: store keys as well as values (the
+// final pass only needs the values unless a caller asked for the keys).
+template <bool kEmit, bool kWriteKeys>
 __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n, int shift,
     const uint32_t* __restrict__ hist, uint64_t* __restrict__ status,
-    uint32_t* __restrict__ counter, int* __restrict__ err) {
+    uint32_t* __restrict__ counter, int* __restrict__ err, EmitSource es) {
+    // s_aux holds the emission's staged offsets first, then the digit counters,
+    // digit starts and global bases (7 KB).
+    constexpr int kAuxWords = kEmit ? kSortPartition : 7 * kRadixBins;
     __shared__ uint32_t s_keys[kSortPartition];
     __shared__ uint32_t s_vals[kSortPartition];
-    __shared__ uint32_t s_wcnt[4][kRadixBins];
-    __shared__ uint32_t s_dstart[kRadixBins];
-    __shared__ uint64_t s_gbase[kRadixBins];
+    __shared__ __align__(16) uint32_t s_aux[kAuxWords];
     __shared__ uint32_t s_scan[4];
     __shared__ uint32_t s_hscan[4];
     __shared__ uint32_t s_part;
+    uint32_t (*s_wcnt)[kRadixBins] = reinterpret_cast<uint32_t (*)[kRadixBins]>(s_aux);
+    uint32_t* s_dstart = s_aux + 4 * kRadixBins;
+    uint64_t* s_gbase = reinterpret_cast<uint64_t*>(s_aux + 5 * kRadixBins);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid == 0) s_part = atomicAdd(counter, 1u);
-    for (int j = tid; j < 4 * kRadixBins; j += kSortThreads) (&s_wcnt[0][0])[j] = 0;
     __syncthreads();
     const uint64_t part = s_part;
     const uint64_t base = part * kSortPartition;
     const int nvalid = (int)min((uint64_t)kSortPartition, n - base);
 
     uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
+    if constexpr (kEmit) {
+        expand_pairs(es, base, nvalid, s_keys, s_vals, s_aux);  // ends with a barrier
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-        const int e = wave * (kSortItems * 64) + i * 64 + lane;
-        const bool v = e < nvalid;
-        key[i] = v ? kin[base + e] : 0u;
-        val[i] = v ? vin[base + e] : 0u;
+        for (int i = 0; i < kSortItems; ++i) {
+            const int e = wave * (kSortItems * 64) + i * 64 + lane;
+            const bool v = e < nvalid;
+            key[i] = v ? s_keys[e] : 0u;
+            val[i] = v ? s_vals[e] : 0u;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < kSortItems; ++i) {
+            const int e = wave * (kSortItems * 64) + i * 64 + lane;
+            const bool v = e < nvalid;
+            key[i] = v ? kin[base + e] : 0u;
+            val[i] = v ? vin[base + e] : 0u;
+        }
     }
+    for (int j = tid; j < 4 * kRadixBins; j += kSortThreads) (&s_wcnt[0][0])[j] = 0;
+    __syncthreads();
     // Stable ranks within the wave's slice, in element order.
 #pragma unroll
     for (int i = 0; i < kSortItems; ++i) {
@@ -217,7 +302,7 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
         const uint32_t k = s_keys[j];
         const uint64_t o = s_gbase[(k >> shift) & 0xffu] + (uint64_t)j;
         if (o < n) {  // always true for consistent histograms; guards the stores
-            kout[o] = k;
+            if constexpr (kWriteKeys) kout[o] = k;
             vout[o] = s_vals[j];
         }
     }
@@ -326,13 +411,62 @@ hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t*
     if (e != hipSuccess) return e;
     uint32_t *ki = k0, *vi = v0, *ko = k1, *vo = v1;
     for (int p = 0; p < passes; ++p) {
-        hipLaunchKernelGGL(onesweep_kernel, dim3((unsigned)parts), dim3(kSortThreads), 0, st, ki,
-                           vi, ko, vo, n, begin_bit + 8 * p, c.hist + p * kRadixBins,
-                           c.status + (size_t)p * parts * kRadixBins, c.counters + p * 16, err);
+        hipLaunchKernelGGL((onesweep_kernel<false, true>), dim3((unsigned)parts),
+                           dim3(kSortThreads), 0, st, ki, vi, ko, vo, n, begin_bit + 8 * p,
+                           c.hist + p * kRadixBins, c.status + (size_t)p * parts * kRadixBins,
+                           c.counters + p * 16, err, EmitSource{});
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         std::swap(ki, ko);
         std::swap(vi, vo);
+    }
+    return hipSuccess;
+}
+
+size_t onesweep_state_bytes(uint64_t n, int passes) {
+    return align_up((size_t)passes * 64, 256) + (size_t)passes * parts_for(n) * kRadixBins * 8;
+}
+
+hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, const uint32_t* hist,
+                            void* state, uint32_t* k0, uint32_t* k1, uint32_t* vbuf,
+                            uint32_t* out_vals, uint32_t* out_keys, int* err, hipStream_t st) {
+    if (m == 0) return hipSuccess;
+    if (passes < 1 || passes > 4) return hipErrorInvalidValue;
+    const uint64_t parts = parts_for(m);
+    uint32_t* counters = static_cast<uint32_t*>(state);
+    uint64_t* status = reinterpret_cast<uint64_t*>(static_cast<char*>(state) +
+                                                   align_up((size_t)passes * 64, 256));
+    // values: the last pass writes out_vals; earlier passes alternate back from it
+    // keys: pass p writes keys[p & 1] and the next pass reads them
+    uint32_t* kbuf[2] = {k0, k1};
+    uint32_t* vdst[4];
+    for (int p = passes - 1, flip = 0; p >= 0; --p, flip ^= 1) vdst[p] = flip ? vbuf : out_vals;
+    for (int p = 0; p < passes; ++p) {
+        const bool last = p == passes - 1;
+        uint32_t* ko = last ? out_keys : kbuf[p & 1];
+        const uint32_t* ki = p == 0 ? nullptr : kbuf[(p - 1) & 1];
+        const uint32_t* vi = p == 0 ? nullptr : vdst[p - 1];
+        const dim3 grid((unsigned)parts), block(kSortThreads);
+        uint64_t* stat = status + (size_t)p * parts * kRadixBins;
+        const uint32_t* h = hist + p * kRadixBins;
+        uint32_t* ctr = counters + p * 16;
+        if (p == 0) {
+            if (ko)
+                hipLaunchKernelGGL((onesweep_kernel<true, true>), grid, block, 0, st, ki, vi, ko,
+                                   vdst[p], m, 8 * p, h, stat, ctr, err, es);
+            else
+                hipLaunchKernelGGL((onesweep_kernel<true, false>), grid, block, 0, st, ki, vi, ko,
+                                   vdst[p], m, 8 * p, h, stat, ctr, err, es);
+        } else {
+            if (ko)
+                hipLaunchKernelGGL((onesweep_kernel<false, true>), grid, block, 0, st, ki, vi, ko,
+                                   vdst[p], m, 8 * p, h, stat, ctr, err, es);
+            else
+                hipLaunchKernelGGL((onesweep_kernel<false, false>), grid, block, 0, st, ki, vi,
+                                   ko, vdst[p], m, 8 * p, h, stat, ctr, err, es);
+        }
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
     }
     return hipSuccess;
 }
