@@ -147,13 +147,14 @@ template <int kPix>
 __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
     int n, int H, int W, int tiles_x, uint64_t m, const int2* __restrict__ ranges,
     const int32_t* __restrict__ ids, const BlendRec* __restrict__ recs, float* __restrict__ img,
-    float* __restrict__ finalT, int32_t* __restrict__ ncontrib) {
+    float* __restrict__ finalT, int32_t* __restrict__ ncontrib,
+    const uint32_t* __restrict__ order) {
     constexpr int kBatch = Layout<kPix>::kBatch;
     __shared__ float4 s_a[kBatch];
     __shared__ float4 s_b[kBatch];
     __shared__ float4 s_c[kBatch];
     __shared__ uint32_t s_bits[kBatch];
-    const int tile = blockIdx.x;
+    const int tile = order ? (int)order[blockIdx.x] : (int)blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6;
     const uint32_t my_bit = 1u << wave;
     const Pixels<kPix> pp = pixels_of<kPix>(tile, tiles_x, W, H);
@@ -279,7 +280,7 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     const int2* __restrict__ ranges, const int32_t* __restrict__ ids,
     const BlendRec* __restrict__ recs, const float* __restrict__ finalT,
     const int32_t* __restrict__ ncontrib, float* __restrict__ dmean, float* __restrict__ dcov,
-    float* __restrict__ dcol, float* __restrict__ dalpha) {
+    float* __restrict__ dcol, float* __restrict__ dalpha, const uint32_t* __restrict__ order) {
     constexpr int kWaves = Layout<kPix>::kWaves;
     constexpr int kBatch = Layout<kPix>::kBatch;
     __shared__ float4 s_a[kBatch];
@@ -290,7 +291,7 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     __shared__ float s_part[kWaves][9][kBatch];
     __shared__ uint32_t s_max[kWaves];
 
-    const int tile = blockIdx.x;
+    const int tile = order ? (int)order[blockIdx.x] : (int)blockIdx.x;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const uint32_t my_bit = 1u << wave;
     const Pixels<kPix> pp = pixels_of<kPix>(tile, tiles_x, W, H);
@@ -378,6 +379,92 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     }
 }
 
+// ---- tile scheduling: work-groups start in descending order of estimated
+// work, so the longest tiles do not start last and set the kernel's tail.
+// The order changes no result: every tile's pixels are computed by one
+// work-group on their own. ----
+
+// Backward work of a tile: its list entries up to the largest n_contrib.
+__global__ __launch_bounds__(kTilePixels) void tile_work_bwd_kernel(
+    int H, int W, int tiles_x, uint64_t m, const int2* __restrict__ ranges,
+    const int32_t* __restrict__ ncontrib, uint32_t* __restrict__ work) {
+    __shared__ uint32_t s_max[kTilePixels / kWave];
+    const int tile = blockIdx.x, tid = threadIdx.x;
+    const int px = (tile % tiles_x) * kTileSize + (tid & 15);
+    const int py = (tile / tiles_x) * kTileSize + (tid >> 4);
+    const uint32_t c =
+        (px < W && py < H) ? (uint32_t)max(ncontrib[(size_t)py * W + px], 0) : 0u;
+    const uint32_t wm = wave_max_u32(c);
+    if ((tid & 63) == 0) s_max[tid >> 6] = wm;
+    __syncthreads();
+    if (tid == 0) {
+        int start, end;
+        clamp_range(ranges[tile], m, start, end);
+        const uint32_t mx = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
+        work[tile] = min(mx, (uint32_t)(end - start));
+    }
+}
+
+// 256 buckets, ordered like the value: 5-bit exponent, 3-bit mantissa.
+__device__ __forceinline__ uint32_t work_bucket(uint32_t w) {
+    if (w == 0) return 0;
+    const uint32_t e = 31u - (uint32_t)__builtin_clz(w);
+    const uint32_t mant = (e >= 3) ? (w >> (e - 3)) & 7u : (w << (3 - e)) & 7u;
+    return min(255u, e * 8u + mant + 1u);
+}
+
+constexpr int kOrderThreads = 1024;
+
+// order[i] = tiles by descending work bucket (one work-group).  work == null:
+// the forward's estimate, the tile's list length.
+__global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
+    int T, uint64_t m, const int2* __restrict__ ranges, const uint32_t* __restrict__ work,
+    uint32_t* __restrict__ order) {
+    __shared__ uint32_t s_cnt[256];
+    __shared__ uint32_t s_scan[4];
+    const int tid = threadIdx.x;
+    auto bucket_of = [&](int t) -> uint32_t {
+        uint32_t w;
+        if (work) {
+            w = work[t];
+        } else {
+            int start, end;
+            clamp_range(ranges[t], m, start, end);
+            w = (uint32_t)(end - start);
+        }
+        return 255u - work_bucket(w);  // descending work
+    };
+    if (tid < 256) s_cnt[tid] = 0;
+    __syncthreads();
+    for (int t = tid; t < T; t += kOrderThreads) atomicAdd(&s_cnt[bucket_of(t)], 1u);
+    __syncthreads();
+    uint32_t c = 0, inc = 0;
+    if (tid < 256) {
+        c = s_cnt[tid];
+        inc = wave_inclusive_scan(c);
+        if ((tid & 63) == 63) s_scan[tid >> 6] = inc;
+    }
+    __syncthreads();
+    if (tid < 256) {
+        uint32_t pre = 0;
+        for (int w = 0; w < (tid >> 6); ++w) pre += s_scan[w];
+        s_cnt[tid] = pre + inc - c;  // first slot of the bucket
+    }
+    __syncthreads();
+    for (int t = tid; t < T; t += kOrderThreads) {
+        const uint32_t pos = atomicAdd(&s_cnt[bucket_of(t)], 1u);
+        if (pos < (uint32_t)T) order[pos] = (uint32_t)t;
+    }
+}
+
+bool tile_order_enabled() {
+    static const bool on = [] {
+        const char* v = std::getenv("GSR_TILE_ORDER");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
 // Pixels per lane for each kernel: the measured defaults, overridable for
 // tuning with GSR_BLEND_FWD_PIX / GSR_BLEND_BWD_PIX = 1 or 2.
 int pix_setting(const char* env, int dflt) {
@@ -398,40 +485,57 @@ int bwd_pix() {
 
 hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
                             uint64_t m, const void* recs, float* img, float* finalT,
-                            int32_t* ncontrib, hipStream_t st) {
+                            int32_t* ncontrib, uint32_t* order, hipStream_t st) {
     const int tiles_x = (W + kTileSize - 1) / kTileSize;
     const int tiles_y = (H + kTileSize - 1) / kTileSize;
     const unsigned tiles = (unsigned)(tiles_x * tiles_y);
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
     const auto* rc = static_cast<const BlendRec*>(recs);
+    if (!tile_order_enabled()) order = nullptr;
+    if (order) {
+        hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles, m,
+                           r, nullptr, order);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     if (fwd_pix() == 2)
         hipLaunchKernelGGL(blend_fwd_kernel<2>, dim3(tiles), dim3(Layout<2>::kThreads), 0, st, n,
-                           H, W, tiles_x, m, r, ids, rc, img, finalT, ncontrib);
+                           H, W, tiles_x, m, r, ids, rc, img, finalT, ncontrib, order);
     else
         hipLaunchKernelGGL(blend_fwd_kernel<1>, dim3(tiles), dim3(Layout<1>::kThreads), 0, st, n,
-                           H, W, tiles_x, m, r, ids, rc, img, finalT, ncontrib);
+                           H, W, tiles_x, m, r, ids, rc, img, finalT, ncontrib, order);
     return hipGetLastError();
 }
 
 hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_t* ranges,
                             const int32_t* ids, uint64_t num_pairs, const void* recs,
                             const float* finalT, const int32_t* ncontrib, float* dmean,
-                            float* dcov, float* dcol, float* dalpha, hipStream_t st) {
+                            float* dcov, float* dcol, float* dalpha, uint32_t* work,
+                            uint32_t* order, hipStream_t st) {
     const int tiles_x = (W + kTileSize - 1) / kTileSize;
     const int tiles_y = (H + kTileSize - 1) / kTileSize;
     const unsigned tiles = (unsigned)(tiles_x * tiles_y);
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
     const auto* rc = static_cast<const BlendRec*>(recs);
+    if (!tile_order_enabled() || !work) order = nullptr;
+    if (order) {
+        hipLaunchKernelGGL(tile_work_bwd_kernel, dim3(tiles), dim3(kTilePixels), 0, st, H, W,
+                           tiles_x, num_pairs, r, ncontrib, work);
+        hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles,
+                           num_pairs, r, work, order);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     if (bwd_pix() == 2)
         hipLaunchKernelGGL(blend_bwd_kernel<2>, dim3(tiles), dim3(Layout<2>::kThreads), 0, st, n,
                            H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib, dmean,
-                           dcov, dcol, dalpha);
+                           dcov, dcol, dalpha, order);
     else
         hipLaunchKernelGGL(blend_bwd_kernel<1>, dim3(tiles), dim3(Layout<1>::kThreads), 0, st, n,
                            H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib, dmean,
-                           dcov, dcol, dalpha);
+                           dcov, dcol, dalpha, order);
     return hipGetLastError();
 }
 

@@ -101,10 +101,10 @@ BinLayout bin_layout(int n) {
 }
 
 struct SortLayout {
-    size_t ctl, part_rank, ctl_end, tk0, tk1, vbuf, end;
+    size_t ctl, part_rank, ctl_end, tk0, tk1, vbuf, order, end;
 };
 
-SortLayout sort_layout(int64_t m, int passes) {
+SortLayout sort_layout(int64_t m, int passes, int64_t T) {
     SortLayout L;
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -119,6 +119,7 @@ SortLayout sort_layout(int64_t m, int passes) {
     L.tk0 = take(4 * um);
     L.tk1 = take(4 * um);
     L.vbuf = take(4 * um);
+    L.order = take(4 * (size_t)(T > 0 ? T : 0));
     L.end = off;
     return L;
 }
@@ -299,7 +300,7 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
 size_t gsr_sort_workspace_bytes(int64_t num_pairs, int n, int height, int width) {
     (void)n;
     const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
-    return sort_layout(num_pairs, tile_passes(T)).end;
+    return sort_layout(num_pairs, tile_passes(T), T).end;
 }
 
 int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const float* cov2d,
@@ -319,7 +320,7 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
     GSR_REQUIRE(bin_ws, "bin workspace must not be null");
     if (bin_ws_bytes < BL.end) return fail(GSR_ERR_WORKSPACE, "bin workspace too small");
     const int passes = tile_passes(T);
-    const SortLayout SL = sort_layout(num_pairs, passes);
+    const SortLayout SL = sort_layout(num_pairs, passes, T);
     hipStream_t st = as_stream(stream);
     GSR_HIP(gsr::zero_fill(tile_ranges, (size_t)T * 8, st), "rasterize: clear ranges");
     const uint64_t m = (uint64_t)num_pairs;
@@ -369,8 +370,9 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                     "rasterize: keys");
     }
     StageTimer timer("blend_fwd", st);
+    uint32_t* order = m > 0 ? at<uint32_t>(sort_ws, SL.order) : nullptr;
     GSR_HIP(gsr::launch_blend_fwd(n, height, width, tile_ranges, sorted_ids, m, recs, img, final_T,
-                                  n_contrib, st),
+                                  n_contrib, order, st),
             "rasterize: blend");
     return GSR_OK;
 }
@@ -387,8 +389,11 @@ int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream) {
     return GSR_OK;
 }
 
-size_t gsr_backward_workspace_bytes(int n) {
-    return align_up(kRecBytes * (size_t)(n > 0 ? n : 0), 256);
+size_t gsr_backward_workspace_bytes(int n, int height, int width) {
+    const size_t T = (height > 0 && width > 0)
+                         ? (size_t)tiles_x_of(width) * (size_t)tiles_y_of(height)
+                         : 0;
+    return align_up(kRecBytes * (size_t)(n > 0 ? n : 0), 256) + 2 * align_up(4 * T, 256);
 }
 
 int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
@@ -404,7 +409,7 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
     if (n == 0) return GSR_OK;
     GSR_REQUIRE(mean2d && cov2d && colors && alpha && d_mean2d && d_cov2d && d_colors && d_alpha,
                 "null pointer");
-    if (ws_bytes < gsr_backward_workspace_bytes(n) || !ws)
+    if (ws_bytes < gsr_backward_workspace_bytes(n, height, width) || !ws)
         return fail(GSR_ERR_WORKSPACE, "backward workspace too small");
     GSR_HIP(gsr::zero_fill(d_mean2d, 8 * (size_t)n, st), "backward: clear");
     GSR_HIP(gsr::zero_fill(d_cov2d, 12 * (size_t)n, st), "backward: clear");
@@ -415,10 +420,13 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
     GSR_REQUIRE(grad_img && sorted_ids && tile_ranges && final_T && n_contrib, "null pointer");
     GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, ws, st),
             "backward: records");
+    const size_t rec_end = align_up(kRecBytes * (size_t)n, 256);
+    uint32_t* work = at<uint32_t>(ws, rec_end);
+    uint32_t* order = at<uint32_t>(ws, rec_end + align_up(4 * (size_t)T, 256));
     StageTimer timer("blend_bwd", st);
     GSR_HIP(gsr::launch_blend_bwd(n, height, width, grad_img, tile_ranges, sorted_ids,
                                   (uint64_t)num_pairs, ws, final_T, n_contrib, d_mean2d, d_cov2d,
-                                  d_colors, d_alpha, st),
+                                  d_colors, d_alpha, work, order, st),
             "backward: blend");
     return GSR_OK;
 }
