@@ -175,6 +175,9 @@ def main() -> int:
     ap.add_argument("--height", type=int, default=1080)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the 720p and c3 side runs")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="only run a plain 256 MiB device copy 5 times (the reference kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the rasterizer path here runs on a single MI355X "
@@ -189,6 +192,15 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 1
     dev = torch.device("cuda")
+    if args.calibrate_copy:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4,
+                          "launches": 5}), flush=True)
+        return 0
     W, H, N = args.width, args.height, args.gaussians
     sc = synthetic.bench_scene(n=N, width=W, height=H, device=dev)
     workload = f"bench_{N // 1000}k_{W}x{H}"

@@ -1,4 +1,4 @@
-// gsr_blend.hip — front-to-back alpha blend (a8) and its backward (a10).
+// gsr_blend.hip — front-to-back alpha blend and its backward.
 //
 // One work-group per 16x16 tile.  Layout template kPix (pixels per lane):
 // 4 / kPix wave64s, each owning a 16 x (4 kPix) strip of the tile; lane l
@@ -8,8 +8,9 @@
 // more waves per tile shorten the longest tile's critical path.  A batch of
 // one list entry per thread is staged in LDS as 48 B blend records (one
 // coalesced record load per entry); lanes walk the batch with broadcast LDS
-// reads.  Per-pixel arithmetic is the reference's, operation for operation
-// (rasterize.cu:241-270, rasterize_backward.cu:113-200).
+// reads.  The forward's per-pixel arithmetic is the reference's, operation
+// for operation (rasterize.cu:241-270); the backward's decisions are too
+// (rasterize_backward.cu:113-200).
 //
 // Exact strip culling: each record carries cut2, a squared distance beyond
 // which no pixel can reach alpha >= 1/255 (gsr_bin.hip).  When the batch is
@@ -18,13 +19,16 @@
 // reference's own tests, so the wave skips it without changing any result.
 //
 // Forward early exit: a pixel is done once T < 1e-4; a wave leaves the batch
-// when its ballot of live pixels is empty; the tile stops when all are done.
+// when none of its pixels is live; the tile stops when all are done.
 // Backward: the tile walks only entries [0, max n_contrib) of its list, back
 // to front (the reference walks all K entries and skips the tail per pixel),
-// and each wave skips entries beyond its own max n_contrib; each entry's 9
-// per-pixel gradient terms are summed in the lane, across the wave (one
+// and each wave skips entries beyond its own max n_contrib; each entry's nine
+// gradient sums are formed in the lane, summed across the wave (one
 // transposed permlane/DPP reduction) and across the waves through LDS, then
 // added to HBM with one set of 9 float atomics per (tile, entry).
+//
+// Work-groups take their tile from a launch order, longest estimated work
+// first (tile_order_kernel), so long tiles do not start last.
 #include <cstdlib>
 
 #include "gsr_internal.h"
@@ -110,11 +114,15 @@ __device__ __forceinline__ void stage_entry(const BlendRec* __restrict__ recs, i
     if (s_id) s_id[slot] = ok ? g : -1;
 }
 
+// Forward pixel state.  A pixel is done once a blend takes T below 1e-4
+// (rasterize.cu:264-267); T only changes on a blend, so "done" is T < 1e-4
+// and needs no flag (pixels off the screen start with T = 0).
 struct FwdPixel {
     float T, C0, C1, C2;
     int last;
-    bool done;
 };
+
+__device__ __forceinline__ bool live(const FwdPixel& p) { return p.T >= kTransmittanceMin; }
 
 // One pixel's forward step for one list entry (rasterize.cu:243-268), with the
 // reference's skips as selects: the same fp32 operations in the same order.
@@ -123,8 +131,8 @@ __device__ __forceinline__ void fwd_step(FwdPixel& p, float fx, float fy, const 
     const float dx = fx - A.x;
     const float dy = fy - A.y;
     const float power = -0.5f * (A.z * dx * dx + A.w * dx * dy + B.x * dy * dy);
-    const float alpha = fminf(kAlphaMax, B.y * exp_gs(power));
-    const bool blend = !p.done & !(power > 0.0f) & !(alpha < kAlphaMin);
+    const float alpha = fminf(kAlphaMax, B.y * exp_blend(power));
+    const bool blend = live(p) & !(power > 0.0f) & !(alpha < kAlphaMin);
     const float w = alpha * p.T;
     const float Tn = p.T * (1.0f - alpha);
     p.C0 = blend ? p.C0 + B.z * w : p.C0;
@@ -132,15 +140,19 @@ __device__ __forceinline__ void fwd_step(FwdPixel& p, float fx, float fy, const 
     p.C2 = blend ? p.C2 + cb * w : p.C2;
     p.T = blend ? Tn : p.T;
     p.last = blend ? contributor : p.last;
-    p.done = p.done | (blend & (Tn < kTransmittanceMin));
 }
 
 template <int kPix>
-__device__ __forceinline__ bool all_done(const FwdPixel (&p)[kPix]) {
-    bool d = true;
+__device__ __forceinline__ bool any_live(const FwdPixel (&p)[kPix]) {
+    bool l = false;
 #pragma unroll
-    for (int k = 0; k < kPix; ++k) d &= p[k].done;
-    return d;
+    for (int k = 0; k < kPix; ++k) l |= live(p[k]);
+    return l;
+}
+
+// Entry j's strip bits as a wave-uniform (scalar) value.
+__device__ __forceinline__ uint32_t uniform_bits(const uint32_t* s_bits, int j) {
+    return __builtin_amdgcn_readfirstlane(s_bits[j]);
 }
 
 template <int kPix>
@@ -155,7 +167,8 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
     __shared__ float4 s_c[kBatch];
     __shared__ uint32_t s_bits[kBatch];
     const int tile = order ? (int)order[blockIdx.x] : (int)blockIdx.x;
-    const int tid = threadIdx.x, wave = tid >> 6;
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: uniform branches
     const uint32_t my_bit = 1u << wave;
     const Pixels<kPix> pp = pixels_of<kPix>(tile, tiles_x, W, H);
     const float fx = (float)pp.px;
@@ -164,7 +177,7 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
 #pragma unroll
     for (int k = 0; k < kPix; ++k) {
         fy[k] = (float)pp.py[k];
-        p[k] = FwdPixel{1.0f, 0.0f, 0.0f, 0.0f, 0, !pp.in[k]};
+        p[k] = FwdPixel{pp.in[k] ? 1.0f : 0.0f, 0.0f, 0.0f, 0.0f, 0};
     }
     int start, end;
     clamp_range(ranges[tile], m, start, end);
@@ -176,19 +189,19 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
             stage_entry<kPix>(recs, ids[b0 + tid], n, tile, tiles_x, s_a, s_b, s_c, s_bits,
                               nullptr, tid);
         __syncthreads();
-        if (ballot(!all_done(p)) != 0) {
+        if (ballot(any_live(p)) != 0) {
             const int cbase = b0 - start + 1;
             for (int j = 0; j < cnt; ++j) {
-                if ((s_bits[j] & my_bit) == 0) continue;  // no pixel of this strip blends it
+                if ((uniform_bits(s_bits, j) & my_bit) == 0) continue;  // strip culled
                 const float4 A = s_a[j];
                 const float4 B = s_b[j];
                 const float cb = s_c[j].x;
 #pragma unroll
                 for (int k = 0; k < kPix; ++k) fwd_step(p[k], fx, fy[k], A, B, cb, cbase + j);
-                if (ballot(!all_done(p)) == 0) break;
+                if (ballot(any_live(p)) == 0) break;
             }
         }
-        if (__syncthreads_and(all_done(p))) break;
+        if (__syncthreads_and(!any_live(p))) break;
     }
 #pragma unroll
     for (int k = 0; k < kPix; ++k) {
@@ -202,67 +215,70 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
     }
 }
 
+// Backward pixel state: dL/dpixel, T (unwound back to front from final_T),
+// accg = sum over channels of dL/dpixel * the reconstructed colour of what lies
+// behind (the reference keeps the colour, accum_rec, and only ever uses its
+// dot product with dL/dpixel), and n_contrib.
 struct BwdPixel {
-    float g0, g1, g2, T, acc0, acc1, acc2;
+    float g0, g1, g2, T, accg;
     int last;
 };
 
-// One pixel's backward step for one list entry (rasterize_backward.cu:117-198):
-// writes its 9 terms to t and returns whether the pixel blended the entry.
+struct BwdTerms {
+    float aT;   // alpha * T_before: dL/dcolour = aT * dL/dpixel
+    float dpw;  // dL/dpower
+    float dop;  // dL/dopacity
+    float dy;   // pixel y - mean.y
+    bool act;
+};
+
+// One pixel's backward step for one list entry (rasterize_backward.cu:117-198).
 // The decision part (power, exp, alpha) is evaluated exactly as in the forward
-// so the skips (beyond n_contrib, power > 0, alpha < 1/255) match it; they are
-// selects, so a skipped entry gives zero terms and leaves T and the
-// background colour unchanged.  The gradient arithmetic after the decision
-// only has to meet the fp32 gradient tolerance and may use fused multiply-adds.
-__device__ __forceinline__ bool bwd_step(BwdPixel& p, float fx, float fy, const float4& A,
-                                         const float4& B, const float4& Cc, int contributor,
-                                         float t[9]) {
-    const float dx = fx - A.x;
+// so the skips (beyond n_contrib, power > 0, alpha < 1/255) match it.  A
+// skipped entry enters the update with alpha 0, which leaves T (x / 1) and
+// accg unchanged and gives zero terms.  The gradient arithmetic after the
+// decision only has to meet the fp32 gradient tolerance and may use fused
+// multiply-adds.  dxdx = (conic.x * dx) * dx and wdx = (2 conic.y) * dx are
+// shared by the lane's pixels, which have the same column.
+__device__ __forceinline__ BwdTerms bwd_step(BwdPixel& p, float dxdx, float wdx, float fy,
+                                             const float4& A, const float4& B, float cb,
+                                             int contributor) {
     const float dy = fy - A.y;
-    const float power = -0.5f * (A.z * dx * dx + A.w * dx * dy + B.x * dy * dy);
-    const float G = exp_gs(power);
+    const float power = -0.5f * (dxdx + wdx * dy + B.x * dy * dy);
+    const float G = exp_blend(power);
     const float araw = B.y * G;
     const float alpha = fminf(kAlphaMax, araw);
     const bool act = (contributor <= p.last) & !(power > 0.0f) & !(alpha < kAlphaMin);
+    // alpha = min(0.99, o G): a clamped alpha passes no gradient to o or G
+    const bool unc = act & (araw < kAlphaMax);
+    BwdTerms t;
+    t.act = act;
+    t.dy = dy;
     {
 #pragma clang fp contract(fast)
-        const float om = 1.0f - alpha;
+        const float ae = act ? alpha : 0.0f;
         // T / max(1 - alpha, 1e-4): reciprocal refined by one Newton step (~1 ulp)
-        const float d = fmaxf(om, 1e-4f);
+        const float d = fmaxf(1.0f - ae, 1e-4f);
         float r = __builtin_amdgcn_rcpf(d);
         r = __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
         const float Tb = p.T * r;
-        const float aT = act ? alpha * Tb : 0.0f;
-        const float dal = act ? ((B.z - p.acc0) * p.g0 + (B.w - p.acc1) * p.g1 +
-                                 (Cc.x - p.acc2) * p.g2) * Tb
-                              : 0.0f;
-        // alpha = min(0.99, o G): a clamped alpha passes no gradient to o or G
-        const bool unclamped = araw < kAlphaMax;
-        const float dop = unclamped ? G * dal : 0.0f;
-        const float dpw = unclamped ? alpha * dal : 0.0f;
-        const float cy = Cc.y;
-        t[0] = dpw * (A.z * dx + cy * dy);
-        t[1] = dpw * (cy * dx + B.x * dy);
-        t[2] = -0.5f * dpw * dx * dx;
-        t[3] = -dpw * dx * dy;
-        t[4] = -0.5f * dpw * dy * dy;
-        t[5] = aT * p.g0;
-        t[6] = aT * p.g1;
-        t[7] = aT * p.g2;
-        t[8] = dop;
-        p.acc0 = act ? alpha * B.z + om * p.acc0 : p.acc0;
-        p.acc1 = act ? alpha * B.w + om * p.acc1 : p.acc1;
-        p.acc2 = act ? alpha * Cc.x + om * p.acc2 : p.acc2;
-        p.T = act ? Tb : p.T;
+        const float cg = B.z * p.g0 + B.w * p.g1 + cb * p.g2;
+        const float diff = cg - p.accg;
+        const float dal = diff * Tb;
+        t.aT = ae * Tb;
+        t.dpw = (unc ? alpha : 0.0f) * dal;
+        t.dop = (unc ? G : 0.0f) * dal;
+        p.accg = __builtin_fmaf(ae, diff, p.accg);
+        p.T = Tb;
     }
-    return act;
+    return t;
 }
 
 __device__ __forceinline__ BwdPixel load_bwd_pixel(bool in, int px, int py, int W,
                                                    const float* __restrict__ grad,
                                                    const float* __restrict__ finalT,
                                                    const int32_t* __restrict__ ncontrib) {
-    BwdPixel p{0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0};
+    BwdPixel p{0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0};
     if (in) {
         const size_t q = (size_t)py * W + px;
         p.g0 = grad[3 * q];
@@ -273,6 +289,13 @@ __device__ __forceinline__ BwdPixel load_bwd_pixel(bool in, int px, int py, int 
     }
     return p;
 }
+
+// Per (tile, entry) the wave sums nine values.  A lane's pixels share dx, so
+// the reference's per-pixel mean and conic terms (rasterize_backward.cu:
+// 163-176) summed over the lane follow from P1 = sum dpw dx, P2 = sum dpw dy
+// and P5 = sum dpw dy^2: dL/dmean = (cx P1 + cy P2, cy P1 + cz P2), dL/dconic
+// = (-P1 dx / 2, -P2 dx, -P5 / 2); then dL/dcolour (3) and dL/dopacity.
+constexpr int kTerms = 9;
 
 template <int kPix>
 __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
@@ -288,11 +311,12 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     __shared__ float4 s_c[kBatch];
     __shared__ uint32_t s_bits[kBatch];
     __shared__ int s_id[kBatch];
-    __shared__ float s_part[kWaves][9][kBatch];
+    __shared__ float s_part[kWaves][kTerms][kBatch + 1];  // +1: the 9 writers hit 9 banks
     __shared__ uint32_t s_max[kWaves];
 
     const int tile = order ? (int)order[blockIdx.x] : (int)blockIdx.x;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: uniform branches
     const uint32_t my_bit = 1u << wave;
     const Pixels<kPix> pp = pixels_of<kPix>(tile, tiles_x, W, H);
     const float fx = (float)pp.px;
@@ -307,7 +331,7 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     }
     int start, end;
     clamp_range(ranges[tile], m, start, end);
-    const int wave_last = (int)wave_max_u32((uint32_t)my_last);
+    const int wave_last = __builtin_amdgcn_readfirstlane((int)wave_max_u32((uint32_t)my_last));
     if (lane == 0) s_max[wave] = (uint32_t)wave_last;
     __syncthreads();
     uint32_t tile_last = 0;
@@ -328,52 +352,91 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
             const int contributor = lo + j + 1;
             float w9 = 0.0f;
             // wave-uniform skips: beyond every pixel's n_contrib, or culled
-            if (contributor <= wave_last && (s_bits[j] & my_bit) != 0) {
+            if (contributor <= wave_last && (uniform_bits(s_bits, j) & my_bit) != 0) {
                 const float4 A = s_a[j];
                 const float4 B = s_b[j];
-                const float4 Cc = s_c[j];
-                float v[9];
-                bool act = bwd_step(p[0], fx, fy[0], A, B, Cc, contributor, v);
+                const float2 Cc = *reinterpret_cast<const float2*>(&s_c[j]);  // (b, conic.y)
+                const float dx = fx - A.x;
+                const float dxdx = A.z * dx * dx;
+                const float wdx = A.w * dx;
+                // per-lane sums over its pixels, started from the first pixel's terms
+                float S0, P2, P5, c0, c1, c2, dop;
+                bool act;
+                {
+                    const BwdTerms t = bwd_step(p[0], dxdx, wdx, fy[0], A, B, Cc.x, contributor);
+                    const float e = t.dpw * t.dy;
+                    S0 = t.dpw;
+                    P2 = e;
+                    P5 = e * t.dy;
+                    c0 = t.aT * p[0].g0;
+                    c1 = t.aT * p[0].g1;
+                    c2 = t.aT * p[0].g2;
+                    dop = t.dop;
+                    act = t.act;
+                }
 #pragma unroll
                 for (int k = 1; k < kPix; ++k) {
-                    float t[9];
-                    act |= bwd_step(p[k], fx, fy[k], A, B, Cc, contributor, t);
-#pragma unroll
-                    for (int q = 0; q < 9; ++q) v[q] += t[q];
+                    const BwdTerms t = bwd_step(p[k], dxdx, wdx, fy[k], A, B, Cc.x, contributor);
+                    {
+#pragma clang fp contract(fast)
+                        const float e = t.dpw * t.dy;
+                        S0 += t.dpw;
+                        P2 += e;
+                        P5 += e * t.dy;
+                        c0 += t.aT * p[k].g0;
+                        c1 += t.aT * p[k].g1;
+                        c2 += t.aT * p[k].g2;
+                        dop += t.dop;
+                    }
+                    act |= t.act;
                 }
-                if (ballot(act) != 0) w9 = wave_reduce9(v);
+                if (ballot(act) != 0) {
+                    const float P1 = dx * S0;
+                    // mean terms formed in the lane, before the wide sum, as the
+                    // per-pixel dpw (conic.x dx + conic.y dy) is
+                    const float cy = Cc.y;
+                    const float vals[kTerms] = {A.z * P1 + cy * P2, cy * P1 + B.x * P2, dx * P1,
+                                                dx * P2, P5, c0, c1, c2, dop};
+                    w9 = wave_reduce9(vals);
+                }
             }
             if (my_value >= 0) s_part[wave][my_value][j] = w9;
         }
         __syncthreads();
         if (tid < cnt) {
             const int g = s_id[tid];
-            float t[9];
+            float tot[kTerms];
             bool any = false;
 #pragma unroll
-            for (int k = 0; k < 9; ++k) {
+            for (int k = 0; k < kTerms; ++k) {
                 float acc = 0.0f;
 #pragma unroll
                 for (int w = 0; w < kWaves; ++w) acc += s_part[w][k][tid];
-                t[k] = acc;
+                tot[k] = acc;
                 any |= acc != 0.0f;
             }
             if (g >= 0 && any) {
+                const float cx = s_a[tid].z, cy = s_c[tid].y, cz = s_b[tid].x;
+                float t[5];
+                t[0] = tot[0];                     // dL/dmean.x
+                t[1] = tot[1];                     // dL/dmean.y
+                t[2] = -0.5f * tot[2];             // dL/dconic.x
+                t[3] = -tot[3];                    // dL/dconic.y (full off-diagonal)
+                t[4] = -0.5f * tot[4];             // dL/dconic.z
                 // conic gradient -> covariance gradient (rasterize_backward.cu:211-221)
-                const float vx = s_a[tid].z, vy = s_c[tid].y, vz = s_b[tid].x;
                 const float gx = t[2], gy = 0.5f * t[3], gz = t[4];
-                const float dA = -(vx * vx * gx + 2.0f * vx * vy * gy + vy * vy * gz);
-                const float dB = -2.0f * (vx * vy * gx + (vx * vz + vy * vy) * gy + vy * vz * gz);
-                const float dC = -(vy * vy * gx + 2.0f * vy * vz * gy + vz * vz * gz);
+                const float dA = -(cx * cx * gx + 2.0f * cx * cy * gy + cy * cy * gz);
+                const float dB = -2.0f * (cx * cy * gx + (cx * cz + cy * cy) * gy + cy * cz * gz);
+                const float dC = -(cy * cy * gx + 2.0f * cy * cz * gy + cz * cz * gz);
                 unsafeAtomicAdd(&dmean[2 * (size_t)g], t[0]);
                 unsafeAtomicAdd(&dmean[2 * (size_t)g + 1], t[1]);
                 unsafeAtomicAdd(&dcov[3 * (size_t)g], dA);
                 unsafeAtomicAdd(&dcov[3 * (size_t)g + 1], dB);
                 unsafeAtomicAdd(&dcov[3 * (size_t)g + 2], dC);
-                unsafeAtomicAdd(&dcol[3 * (size_t)g], t[5]);
-                unsafeAtomicAdd(&dcol[3 * (size_t)g + 1], t[6]);
-                unsafeAtomicAdd(&dcol[3 * (size_t)g + 2], t[7]);
-                unsafeAtomicAdd(&dalpha[g], t[8]);
+                unsafeAtomicAdd(&dcol[3 * (size_t)g], tot[5]);
+                unsafeAtomicAdd(&dcol[3 * (size_t)g + 1], tot[6]);
+                unsafeAtomicAdd(&dcol[3 * (size_t)g + 2], tot[7]);
+                unsafeAtomicAdd(&dalpha[g], tot[8]);
             }
         }
     }
@@ -402,6 +465,71 @@ __global__ __launch_bounds__(kTilePixels) void tile_work_bwd_kernel(
         clamp_range(ranges[tile], m, start, end);
         const uint32_t mx = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
         work[tile] = min(mx, (uint32_t)(end - start));
+    }
+}
+
+// Forward work of a tile: the list entries it takes until five sample pixels
+// (the corners and the centre) are done (T < 1e-4), or the whole list when one
+// never is (the forward walks a tile's list until every pixel is done).  An
+// ordering heuristic only: it uses the hardware exp and log and no culling.
+constexpr int kEstPoints = 5;
+
+// One wave per tile, 64 entries per step, the next step's ids prefetched.  A
+// sample pixel still live after kEstCap entries counts as never done.
+constexpr int kEstTilesPerBlock = 4;
+constexpr int kEstCap = 1024;
+
+__global__ __launch_bounds__(kEstTilesPerBlock * kWave) void tile_work_fwd_kernel(
+    int T, int tiles_x, int n, uint64_t m, const int2* __restrict__ ranges,
+    const int32_t* __restrict__ ids, const BlendRec* __restrict__ recs,
+    uint32_t* __restrict__ work) {
+    constexpr float kLnTmin = -9.21034037f;  // ln(1e-4)
+    const int lane = threadIdx.x & 63;
+    const int tile = blockIdx.x * kEstTilesPerBlock + (int)(threadIdx.x >> 6);
+    if (tile >= T) return;  // whole waves
+    int start, end;
+    clamp_range(ranges[tile], m, start, end);
+    const int len = end - start;
+    const float x0 = (float)((tile % tiles_x) * kTileSize);
+    const float y0 = (float)((tile / tiles_x) * kTileSize);
+    const float sx[kEstPoints] = {x0, x0 + 15.0f, x0, x0 + 15.0f, x0 + 7.0f};
+    const float sy[kEstPoints] = {y0, y0, y0 + 15.0f, y0 + 15.0f, y0 + 7.0f};
+    float carry[kEstPoints] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    int sat[kEstPoints] = {-1, -1, -1, -1, -1};
+    int next = (lane < len) ? ids[start + lane] : -1;
+    for (int c = 0; c < min(len, kEstCap); c += kWave) {
+        const int g = next;
+        const bool ok = g >= 0 && g < n;  // false past the list end as well
+        BlendRec r;
+        if (ok) r = recs[g];
+        next = (c + kWave + lane < len) ? ids[start + c + kWave + lane] : -1;
+        bool all = true;
+#pragma unroll
+        for (int q = 0; q < kEstPoints; ++q) {
+            float l = 0.0f;
+            if (ok) {
+                const float dx = sx[q] - r.a.x, dy = sy[q] - r.a.y;
+                const float power = -0.5f * (r.a.z * dx * dx + r.a.w * dx * dy + r.b.x * dy * dy);
+                const float alpha = fminf(kAlphaMax, r.b.y * __expf(power));
+                l = (power <= 0.0f && alpha >= kAlphaMin) ? __logf(1.0f - alpha) : 0.0f;
+            }
+            const float incl = wave_inclusive_scan_f(l);
+            const uint64_t below = ballot(c + lane < len && carry[q] + incl < kLnTmin);
+            if (sat[q] < 0 && below != 0) sat[q] = c + (int)__builtin_ctzll(below);
+            carry[q] += __shfl(incl, 63, kWave);
+            all &= sat[q] >= 0;
+        }
+        if (all) break;
+    }
+    if (lane == 0) {
+        int w = 0;
+        bool open = false;
+#pragma unroll
+        for (int q = 0; q < kEstPoints; ++q) {
+            if (sat[q] < 0) open = true;
+            else w = max(w, sat[q] + 1);
+        }
+        work[tile] = (uint32_t)(open ? len : w);
     }
 }
 
@@ -485,17 +613,22 @@ int bwd_pix() {
 
 hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
                             uint64_t m, const void* recs, float* img, float* finalT,
-                            int32_t* ncontrib, uint32_t* order, hipStream_t st) {
+                            int32_t* ncontrib, uint32_t* work, uint32_t* order,
+                            hipStream_t st) {
     const int tiles_x = (W + kTileSize - 1) / kTileSize;
     const int tiles_y = (H + kTileSize - 1) / kTileSize;
     const unsigned tiles = (unsigned)(tiles_x * tiles_y);
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
     const auto* rc = static_cast<const BlendRec*>(recs);
-    if (!tile_order_enabled()) order = nullptr;
+    if (!tile_order_enabled() || !work) order = nullptr;
     if (order) {
+        hipLaunchKernelGGL(tile_work_fwd_kernel,
+                           dim3((tiles + kEstTilesPerBlock - 1) / kEstTilesPerBlock),
+                           dim3(kEstTilesPerBlock * kWave), 0, st, (int)tiles, tiles_x, n, m, r,
+                           ids, rc, work);
         hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles, m,
-                           r, nullptr, order);
+                           r, work, order);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

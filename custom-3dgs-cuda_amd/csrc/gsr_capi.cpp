@@ -101,7 +101,7 @@ BinLayout bin_layout(int n) {
 }
 
 struct SortLayout {
-    size_t ctl, part_rank, ctl_end, tk0, tk1, vbuf, order, end;
+    size_t ctl, part_rank, ctl_end, tk0, tk1, vbuf, work, order, end;
 };
 
 SortLayout sort_layout(int64_t m, int passes, int64_t T) {
@@ -119,6 +119,7 @@ SortLayout sort_layout(int64_t m, int passes, int64_t T) {
     L.tk0 = take(4 * um);
     L.tk1 = take(4 * um);
     L.vbuf = take(4 * um);
+    L.work = take(4 * (size_t)(T > 0 ? T : 0));
     L.order = take(4 * (size_t)(T > 0 ? T : 0));
     L.end = off;
     return L;
@@ -370,9 +371,10 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                     "rasterize: keys");
     }
     StageTimer timer("blend_fwd", st);
+    uint32_t* work = m > 0 ? at<uint32_t>(sort_ws, SL.work) : nullptr;
     uint32_t* order = m > 0 ? at<uint32_t>(sort_ws, SL.order) : nullptr;
     GSR_HIP(gsr::launch_blend_fwd(n, height, width, tile_ranges, sorted_ids, m, recs, img, final_T,
-                                  n_contrib, order, st),
+                                  n_contrib, work, order, st),
             "rasterize: blend");
     return GSR_OK;
 }

@@ -27,12 +27,10 @@ constexpr float kTransmittanceMin = 1e-4f;  // rasterize.cu:265
 // Faithfully rounded (max 0.955 ulp over [-87.34, 88.72]); results below
 // FLT_MIN are flushed to +0.  Host and device evaluate the same IEEE
 // operations, so their results agree bit for bit.
-// Branch-free: the polynomial runs on x clamped to the finite range (bit-identical
-// for in-range x) and the out-of-range results are selected afterwards, so a
-// wave never diverges inside exp.
-__device__ __forceinline__ float exp_gs(float x) {
-    constexpr float kHi = 88.72283935546875f, kLo = -87.33654022216796875f;
-    const float xc = fminf(fmaxf(x, kLo), kHi);
+constexpr float kExpHi = 88.72283935546875f, kExpLo = -87.33654022216796875f;
+
+// The reduction and polynomial for x in [kExpLo, kExpHi] (NaN stays NaN).
+__device__ __forceinline__ float exp_core(float xc) {
     const float k = __builtin_rintf(xc * 1.44269502162933349609375f);
     float r = __builtin_fmaf(-k, 0.693145751953125f, xc);
     r = __builtin_fmaf(-k, 1.428606765330187045e-06f, r);
@@ -43,9 +41,25 @@ __device__ __forceinline__ float exp_gs(float x) {
     p = __builtin_fmaf(p, r, 0.49999988079071045f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    const float e = __builtin_ldexpf(p, (int)k);
+    return __builtin_ldexpf(p, (int)k);
+}
+
+// Branch-free: the polynomial runs on x clamped to the finite range (bit-identical
+// for in-range x) and the out-of-range results are selected afterwards, so a
+// wave never diverges inside exp.
+__device__ __forceinline__ float exp_gs(float x) {
+    const float e = exp_core(fminf(fmaxf(x, kExpLo), kExpHi));
     const float below = (x != x) ? x : 0.0f;
-    return (x > kHi) ? __builtin_inff() : ((x >= kLo) ? e : below);
+    return (x > kExpHi) ? __builtin_inff() : ((x >= kExpLo) ? e : below);
+}
+
+// exp_gs for the blends' G = exp(power): identical for x <= kExpHi and NaN.
+// Larger x only occurs with power > 0, which both blends skip before G is
+// used, so the upper clamp is left out (one compare and two selects).
+__device__ __forceinline__ float exp_blend(float x) {
+    const bool below = x < kExpLo;
+    const float e = exp_core(below ? kExpLo : x);
+    return below ? 0.0f : e;
 }
 
 // Saturating float -> int32 with NaN -> 0 (the GPU conversion the reference's
@@ -162,14 +176,35 @@ __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
     return v;
 }
 
-// Inclusive prefix sum over the wave (u32).
+// Inclusive prefix sums over the wave with DPP: row shifts by 1, 2, 4 and 8
+// within each 16-lane row (lanes shifted in from outside the row read 0), then
+// lane 15's row total broadcast to rows 1 and 3 and lane 31's to rows 2 and 3
+// (gfx9 row_bcast).  Twelve VALU, no LDS.
+template <int Ctrl, int RowMask>
+__device__ __forceinline__ uint32_t dpp_or_zero(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, Ctrl, RowMask, 0xf, true);
+}
+constexpr int kDppRowShr1 = 0x111, kDppRowShr2 = 0x112,
+              kDppRowShr8 = 0x118, kDppRowBcast15 = 0x142, kDppRowBcast31 = 0x143;
+
 __device__ __forceinline__ uint32_t wave_inclusive_scan(uint32_t v) {
-    const int l = lane_id();
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        uint32_t o = (uint32_t)__shfl_up((int)v, off, kWave);
-        if (l >= off) v += o;
-    }
+    v += dpp_or_zero<kDppRowShr1, 0xf>(v);
+    v += dpp_or_zero<kDppRowShr2, 0xf>(v);
+    v += dpp_or_zero<kDppRowShr4, 0xf>(v);
+    v += dpp_or_zero<kDppRowShr8, 0xf>(v);
+    v += dpp_or_zero<kDppRowBcast15, 0xa>(v);
+    v += dpp_or_zero<kDppRowBcast31, 0xc>(v);
+    return v;
+}
+
+__device__ __forceinline__ float wave_inclusive_scan_f(float v) {
+    auto step = [](float x, uint32_t y) { return x + __uint_as_float(y); };
+    v = step(v, dpp_or_zero<kDppRowShr1, 0xf>(__float_as_uint(v)));
+    v = step(v, dpp_or_zero<kDppRowShr2, 0xf>(__float_as_uint(v)));
+    v = step(v, dpp_or_zero<kDppRowShr4, 0xf>(__float_as_uint(v)));
+    v = step(v, dpp_or_zero<kDppRowShr8, 0xf>(__float_as_uint(v)));
+    v = step(v, dpp_or_zero<kDppRowBcast15, 0xa>(__float_as_uint(v)));
+    v = step(v, dpp_or_zero<kDppRowBcast31, 0xc>(__float_as_uint(v)));
     return v;
 }
 

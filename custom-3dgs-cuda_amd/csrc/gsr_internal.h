@@ -103,14 +103,15 @@ hipError_t launch_full_keys(uint64_t m, const uint32_t* sorted_tiles, const int3
 
 // ---- blend ----
 // order (T entries, optional) receives the tiles' launch order, longest
-// estimated work first; work (T entries) is the backward's per-tile estimate.
+// estimated work first; work (T entries) holds the per-tile estimates.
 hipError_t launch_blend_records(int n, const float* mean2d, const float* cov2d,
                                 const float* colors, const float* alpha, void* recs,
                                 hipStream_t st);
 
 hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
                             uint64_t m, const void* recs, float* img, float* finalT,
-                            int32_t* ncontrib, uint32_t* order, hipStream_t st);
+                            int32_t* ncontrib, uint32_t* work, uint32_t* order,
+                            hipStream_t st);
 
 hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_t* ranges,
                             const int32_t* ids, uint64_t num_pairs, const void* recs,
