@@ -232,7 +232,9 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization(
     Tensor grad_colors = torch::empty({num_gaussians, 3}, options);
     Tensor grad_alpha = torch::empty({num_gaussians, 1}, options);
     Tensor ws =
-        workspace((int64_t)gsr_backward_workspace_bytes(num_gaussians, height, width), mean_2d);
+        workspace((int64_t)gsr_backward_workspace_bytes(num_gaussians, sorted_ids.numel(),
+                                                         height, width),
+                  mean_2d);
     check_rc(gsr_rasterize_backward(
                  num_gaussians, height, width, cfp(grad_output), cfp(mean_2d), cfp(cov_2d),
                  cfp(colors), cfp(alpha), sorted_ids.data_ptr<int32_t>(), sorted_ids.numel(),

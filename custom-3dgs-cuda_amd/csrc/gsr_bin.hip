@@ -190,32 +190,35 @@ __global__ __launch_bounds__(kThreads) void full_keys_kernel(uint64_t m,
     keys[i] = ((uint64_t)tiles[i] << 32) | (uint64_t)dbits;
 }
 
-// Squared distance d^2 beyond which o * exp(-q/2) < 1/255 for every pixel, with
-// q = d^T C d >= lambda_min(C) |d|^2.  Computed in double from the fp32 conic and
-// opacity; lambda_min is lowered by 2e-5 (mid + |cy|) to cover the fp32
-// rounding of q in the per-pixel evaluation (~4e-7 of the same scale), and the
-// threshold raised by 0.1% + 1e-4 to cover exp and the o*G product, so an entry
-// is skipped only where the reference's per-pixel tests skip it too.
-__device__ __forceinline__ float alpha_cut_radius2(float cx, float cy, float cz, float o) {
-    if (!(o >= kAlphaMin)) return -1.0f;  // alpha <= o < 1/255 for every pixel
-    const double mid = 0.5 * ((double)cx + (double)cz);
-    const double det = (double)cx * cz - (double)cy * cy;
-    if (!(det > 0.0) || !(mid > 0.0)) return __builtin_inff();
-    const double lmax = mid + sqrt(fmax(0.0, mid * mid - det));
-    const double k = 0.5 * (det / lmax - 2e-5 * (mid + fabs((double)cy)));
-    if (!(k > 0.0)) return __builtin_inff();
-    const double r2 = (log(255.0 * (double)o) * 1.001 + 1e-4) / k;
-    return nextafterf((float)r2, __builtin_inff());
+// Threshold on q = d^T conic d above which o * exp(-q/2) < 1/255, so alpha
+// stays below 1/255 (rasterize.cu:256): 2 ln(255 o), computed in double and
+// raised by 1e-5 relative + 1e-4 to cover exp_gs (<= 1 ulp), the o * G
+// product and the rounding of this threshold.  NaN for a NaN opacity, which
+// then disables every cull.
+__device__ __forceinline__ float alpha_q_threshold(float o) {
+    const double t = 2.0 * log(255.0 * (double)o);
+    return (float)(t + 1e-5 * fabs(t) + 1e-4);
 }
 
 // Conic = cov^-1 with 1/det first (rasterize.cu:224-232), packed with mean,
 // opacity and colour so the blend loads one 48 B record per list entry.
+// With counts != null (the backward), also each Gaussian's tile rectangle and
+// count, exactly as bin_count_kernel forms them.
 __global__ __launch_bounds__(kThreads) void blend_records_kernel(
     int n, const float* __restrict__ mean2d, const float* __restrict__ cov2d,
     const float* __restrict__ colors, const float* __restrict__ alpha,
-    BlendRec* __restrict__ recs) {
+    BlendRec* __restrict__ recs, int H, int W, uint32_t* __restrict__ counts,
+    uint2* __restrict__ rects) {
     const int i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= n) return;
+    if (counts) {
+        const TileRect tr = tile_rect(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1],
+                                      cov2d[3 * (size_t)i], cov2d[3 * (size_t)i + 1],
+                                      cov2d[3 * (size_t)i + 2], W, H);
+        counts[i] = tr.ok ? (uint32_t)(max(0, tr.x1 - tr.x0) * max(0, tr.y1 - tr.y0)) : 0u;
+        rects[i] = make_uint2((uint32_t)tr.x0 | ((uint32_t)tr.x1 << 16),
+                              (uint32_t)tr.y0 | ((uint32_t)tr.y1 << 16));
+    }
     const float a = cov2d[3 * (size_t)i], b = cov2d[3 * (size_t)i + 1], c = cov2d[3 * (size_t)i + 2];
     const float det = a * c - b * b;
     const float det_inv = (det > 0.0f) ? (1.0f / det) : 0.0f;
@@ -223,8 +226,7 @@ __global__ __launch_bounds__(kThreads) void blend_records_kernel(
     BlendRec r;
     r.a = make_float4(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1], cx, 2.0f * cy);
     r.b = make_float4(cz, alpha[i], colors[3 * (size_t)i], colors[3 * (size_t)i + 1]);
-    r.c = make_float4(colors[3 * (size_t)i + 2], cy, alpha_cut_radius2(cx, cy, cz, alpha[i]),
-                      0.0f);
+    r.c = make_float4(colors[3 * (size_t)i + 2], cy, alpha_q_threshold(alpha[i]), 0.0f);
     recs[i] = r;
 }
 
@@ -274,10 +276,11 @@ hipError_t launch_full_keys(uint64_t m, const uint32_t* sorted_tiles, const int3
 
 hipError_t launch_blend_records(int n, const float* mean2d, const float* cov2d,
                                 const float* colors, const float* alpha, void* recs,
-                                hipStream_t st) {
+                                hipStream_t st, int H, int W, uint32_t* counts, uint2* rects) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(blend_records_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, n,
-                       mean2d, cov2d, colors, alpha, static_cast<BlendRec*>(recs));
+                       mean2d, cov2d, colors, alpha, static_cast<BlendRec*>(recs), H, W, counts,
+                       rects);
     return hipGetLastError();
 }
 

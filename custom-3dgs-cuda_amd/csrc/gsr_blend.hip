@@ -12,11 +12,13 @@
 // for operation (rasterize.cu:241-270); the backward's decisions are too
 // (rasterize_backward.cu:113-200).
 //
-// Exact strip culling: each record carries cut2, a squared distance beyond
-// which no pixel can reach alpha >= 1/255 (gsr_bin.hip).  When the batch is
-// staged, each entry gets one bit per strip: clear when the strip lies beyond
-// cut2 from the mean.  Every pixel of such a strip would skip the entry in the
-// reference's own tests, so the wave skips it without changing any result.
+// Exact strip culling: each record carries qthr, a bound on the quadratic
+// form above which no pixel can reach alpha >= 1/255 (gsr_bin.hip).  When the
+// batch is staged, each entry gets one bit per strip: clear when the least
+// value of the quadratic form over the strip's rectangle exceeds qthr (with
+// margins for the per-pixel fp32 rounding).  Every pixel of such a strip would
+// skip the entry in the reference's own tests, so the wave skips it without
+// changing any result.
 //
 // Forward early exit: a pixel is done once T < 1e-4; a wave leaves the batch
 // when none of its pixels is live; the tile stops when all are done.
@@ -30,6 +32,7 @@
 // Work-groups take their tile from a launch order, longest estimated work
 // first (tile_order_kernel), so long tiles do not start last.
 #include <cstdlib>
+#include <string>
 
 #include "gsr_internal.h"
 #include "gsr_common.h"
@@ -74,23 +77,49 @@ __device__ __forceinline__ void clamp_range(int2 rg, uint64_t m, int& start, int
     end = (int)e;
 }
 
-// Bit w set: a pixel of strip w may lie within cut2 of the mean.  The fp32
-// distance carries ~3e-7 relative rounding; the 1e-6 slack keeps the test
-// conservative.
+// Minimum over the pixel rectangle [x0, x1] x [y0, y1] of the quadratic form
+// q = A u^2 + 2 B u v + C v^2, (u, v) = (x - mx, y - my), for a positive
+// definite conic (A > 0, AC > B^2): 0 when the mean is inside, else the least
+// of the four edges' minima (each a clamped 1D quadratic).  The computed
+// minimiser is off by a few ulp, which raises q only at second order; the
+// evaluation's own rounding is covered by the caller's margin.
+__device__ __forceinline__ float qmin_rect(float mx, float my, float A, float B, float C,
+                                          float rA, float rC, float x0, float x1, float y0,
+                                          float y1) {
+    if (mx >= x0 && mx <= x1 && my >= y0 && my <= y1) return 0.0f;
+    const float ux0 = x0 - mx, ux1 = x1 - mx, vy0 = y0 - my, vy1 = y1 - my;
+    auto q = [&](float u, float v) { return A * u * u + 2.0f * B * u * v + C * v * v; };
+    float best = q(fminf(fmaxf(-B * vy0 * rA, ux0), ux1), vy0);
+    best = fminf(best, q(fminf(fmaxf(-B * vy1 * rA, ux0), ux1), vy1));
+    best = fminf(best, q(ux0, fminf(fmaxf(-B * ux0 * rC, vy0), vy1)));
+    best = fminf(best, q(ux1, fminf(fmaxf(-B * ux1 * rC, vy0), vy1)));
+    return best;
+}
+
+// Bit w set: some pixel of strip w may reach alpha >= 1/255.  A strip is
+// culled when the least q over its rectangle, lowered by 1e-5 of the largest
+// sum of |terms| there (the fp32 rounding of the per-pixel q and of this
+// bound are each within ~1e-6 of that sum), still exceeds qthr.  Conics that
+// are not positive definite, and NaN anywhere, cull nothing.
 template <int kPix>
 __device__ __forceinline__ uint32_t strip_bits(const BlendRec& r, int tile, int tiles_x) {
-    const float cut2 = r.c.z;
+    constexpr uint32_t kAll = (1u << Layout<kPix>::kWaves) - 1u;
+    const float A = r.a.z, B = r.c.y, C = r.b.x, thr = r.c.z;
+    if (!(A > 0.0f) || !(C > 0.0f) || !((double)A * C - (double)B * B > 0.0)) return kAll;
+    const float mx = r.a.x, my = r.a.y;
+    const float rA = 1.0f / A, rC = 1.0f / C;
     const int tx = tile % tiles_x, ty = tile / tiles_x;
     const float x0 = (float)(tx * kTileSize), x1 = x0 + (float)(kTileSize - 1);
-    const float ddx = fmaxf(fmaxf(x0 - r.a.x, r.a.x - x1), 0.0f);
+    const float dxm = fmaxf(fabsf(x0 - mx), fabsf(x1 - mx));
     uint32_t bits = 0;
-#pragma unroll
+#pragma unroll 1
     for (int w = 0; w < Layout<kPix>::kWaves; ++w) {
         const float y0 = (float)(ty * kTileSize + w * Layout<kPix>::kRows);
         const float y1 = y0 + (float)(Layout<kPix>::kRows - 1);
-        const float ddy = fmaxf(fmaxf(y0 - r.a.y, r.a.y - y1), 0.0f);
-        const float d2 = ddx * ddx + ddy * ddy;
-        const bool skip = d2 * (1.0f - 1e-6f) > cut2;
+        const float dym = fmaxf(fabsf(y0 - my), fabsf(y1 - my));
+        const float absq = A * dxm * dxm + 2.0f * fabsf(B) * dxm * dym + C * dym * dym;
+        const float q = qmin_rect(mx, my, A, B, C, rA, rC, x0, x1, y0, y1) - 1e-5f * absq;
+        const bool skip = q > thr;  // false for NaN
         bits |= skip ? 0u : (1u << w);
     }
     return bits;
@@ -297,15 +326,26 @@ __device__ __forceinline__ BwdPixel load_bwd_pixel(bool in, int px, int py, int 
 // = (-P1 dx / 2, -P2 dx, -P5 / 2); then dL/dcolour (3) and dL/dopacity.
 constexpr int kTerms = 9;
 
-template <int kPix>
+// dL/dcov2d (a, b, c) from dL/dconic (x, y full off-diagonal, z) for conic =
+// (cx, cy, cz) = cov^-1 (rasterize_backward.cu:211-221).
+__device__ __forceinline__ void conic_to_cov_grad(float cx, float cy, float cz, float dx, float dy,
+                                                  float dz, float out[3]) {
+    const float gx = dx, gy = 0.5f * dy, gz = dz;
+    out[0] = -(cx * cx * gx + 2.0f * cx * cy * gy + cy * cy * gz);
+    out[1] = -2.0f * (cx * cy * gx + (cx * cz + cy * cy) * gy + cy * cz * gz);
+    out[2] = -(cy * cy * gx + 2.0f * cy * cz * gy + cz * cz * gz);
+}
+
+template <int kPix, int kBatch>
 __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     int n, int H, int W, int tiles_x, uint64_t m, const float* __restrict__ grad,
     const int2* __restrict__ ranges, const int32_t* __restrict__ ids,
     const BlendRec* __restrict__ recs, const float* __restrict__ finalT,
     const int32_t* __restrict__ ncontrib, float* __restrict__ dmean, float* __restrict__ dcov,
-    float* __restrict__ dcol, float* __restrict__ dalpha, const uint32_t* __restrict__ order) {
+    float* __restrict__ dcol, float* __restrict__ dalpha, GradSlots gs,
+    const uint32_t* __restrict__ order) {
     constexpr int kWaves = Layout<kPix>::kWaves;
-    constexpr int kBatch = Layout<kPix>::kBatch;
+    static_assert(kBatch <= Layout<kPix>::kThreads, "one staged entry per thread");
     __shared__ float4 s_a[kBatch];
     __shared__ float4 s_b[kBatch];
     __shared__ float4 s_c[kBatch];
@@ -319,6 +359,7 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: uniform branches
     const uint32_t my_bit = 1u << wave;
     const Pixels<kPix> pp = pixels_of<kPix>(tile, tiles_x, W, H);
+    const int tx = tile % tiles_x, ty = tile / tiles_x;
     const float fx = (float)pp.px;
     float fy[kPix];
     BwdPixel p[kPix];
@@ -416,29 +457,86 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                 any |= acc != 0.0f;
             }
             if (g >= 0 && any) {
-                const float cx = s_a[tid].z, cy = s_c[tid].y, cz = s_b[tid].x;
-                float t[5];
-                t[0] = tot[0];                     // dL/dmean.x
-                t[1] = tot[1];                     // dL/dmean.y
-                t[2] = -0.5f * tot[2];             // dL/dconic.x
-                t[3] = -tot[3];                    // dL/dconic.y (full off-diagonal)
-                t[4] = -0.5f * tot[4];             // dL/dconic.z
-                // conic gradient -> covariance gradient (rasterize_backward.cu:211-221)
-                const float gx = t[2], gy = 0.5f * t[3], gz = t[4];
-                const float dA = -(cx * cx * gx + 2.0f * cx * cy * gy + cy * cy * gz);
-                const float dB = -2.0f * (cx * cy * gx + (cx * cz + cy * cy) * gy + cy * cz * gz);
-                const float dC = -(cy * cy * gx + 2.0f * cy * cz * gy + cz * cz * gz);
-                unsafeAtomicAdd(&dmean[2 * (size_t)g], t[0]);
-                unsafeAtomicAdd(&dmean[2 * (size_t)g + 1], t[1]);
-                unsafeAtomicAdd(&dcov[3 * (size_t)g], dA);
-                unsafeAtomicAdd(&dcov[3 * (size_t)g + 1], dB);
-                unsafeAtomicAdd(&dcov[3 * (size_t)g + 2], dC);
-                unsafeAtomicAdd(&dcol[3 * (size_t)g], tot[5]);
-                unsafeAtomicAdd(&dcol[3 * (size_t)g + 1], tot[6]);
-                unsafeAtomicAdd(&dcol[3 * (size_t)g + 2], tot[7]);
-                unsafeAtomicAdd(&dalpha[g], tot[8]);
+                float t[kTerms];
+                t[0] = tot[0];         // dL/dmean.x
+                t[1] = tot[1];         // dL/dmean.y
+                t[2] = -0.5f * tot[2];  // dL/dconic.x
+                t[3] = -tot[3];        // dL/dconic.y (full off-diagonal)
+                t[4] = -0.5f * tot[4];  // dL/dconic.z
+                t[5] = tot[5];         // dL/dcolour
+                t[6] = tot[6];
+                t[7] = tot[7];
+                t[8] = tot[8];         // dL/dopacity
+                // the pair's slot: goff[g] + this tile's index in g's rectangle
+                const uint2 rc = gs.rects[g];
+                const int rx0 = (int)(rc.x & 0xffffu), rx1 = (int)(rc.x >> 16);
+                const int ry0 = (int)(rc.y & 0xffffu), ry1 = (int)(rc.y >> 16);
+                const uint64_t slot = (uint64_t)gs.goff[g] +
+                                      (uint64_t)((ty - ry0) * (rx1 - rx0) + (tx - rx0));
+                if (tx >= rx0 && tx < rx1 && ty >= ry0 && ty < ry1 && slot < gs.slots) {
+                    float* d = gs.sums + 9 * slot;
+#pragma unroll
+                    for (int k = 0; k < kTerms; ++k) d[k] = t[k];
+                    gs.flags[slot] = 1;
+                } else {
+                    // not a pair of the rectangles: straight to the outputs
+                    const float cx = s_a[tid].z, cy = s_c[tid].y, cz = s_b[tid].x;
+                    float dc[3];
+                    conic_to_cov_grad(cx, cy, cz, t[2], t[3], t[4], dc);
+                    unsafeAtomicAdd(&dmean[2 * (size_t)g], t[0]);
+                    unsafeAtomicAdd(&dmean[2 * (size_t)g + 1], t[1]);
+                    unsafeAtomicAdd(&dcov[3 * (size_t)g], dc[0]);
+                    unsafeAtomicAdd(&dcov[3 * (size_t)g + 1], dc[1]);
+                    unsafeAtomicAdd(&dcov[3 * (size_t)g + 2], dc[2]);
+                    unsafeAtomicAdd(&dcol[3 * (size_t)g], t[5]);
+                    unsafeAtomicAdd(&dcol[3 * (size_t)g + 1], t[6]);
+                    unsafeAtomicAdd(&dcol[3 * (size_t)g + 2], t[7]);
+                    unsafeAtomicAdd(&dalpha[g], t[8]);
+                }
             }
         }
+    }
+}
+
+// One wave per Gaussian: the nine sums of its flagged slots, the conic part
+// converted to the covariance gradient, added to the outputs (which hold
+// zeros and any fallback atomics from the blend).
+constexpr int kReduceGaussiansPerBlock = 4;
+
+__global__ __launch_bounds__(kReduceGaussiansPerBlock * kWave) void pair_grad_reduce_kernel(
+    int n, const BlendRec* __restrict__ recs, GradSlots gs, float* __restrict__ dmean,
+    float* __restrict__ dcov, float* __restrict__ dcol, float* __restrict__ dalpha) {
+    const int lane = threadIdx.x & 63;
+    const int g = blockIdx.x * kReduceGaussiansPerBlock + (int)(threadIdx.x >> 6);
+    if (g >= n) return;  // whole waves
+    const uint64_t base = gs.goff[g];
+    const uint32_t cnt = gs.counts[g];
+    float v[kTerms] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (uint32_t i = (uint32_t)lane; i < cnt; i += kWave) {
+        const uint64_t slot = base + i;
+        if (slot < gs.slots && gs.flags[slot]) {
+            const float* d = gs.sums + 9 * slot;
+#pragma unroll
+            for (int k = 0; k < kTerms; ++k) v[k] += d[k];
+        }
+    }
+    const float w = wave_reduce9(v);
+    float t[kTerms];
+#pragma unroll
+    for (int k = 0; k < kTerms; ++k) t[k] = __shfl(w, kReduce9Lane[k], kWave);
+    if (lane == 0) {
+        const BlendRec r = recs[g];
+        float dc[3];
+        conic_to_cov_grad(r.a.z, r.c.y, r.b.x, t[2], t[3], t[4], dc);
+        dmean[2 * (size_t)g] += t[0];
+        dmean[2 * (size_t)g + 1] += t[1];
+        dcov[3 * (size_t)g] += dc[0];
+        dcov[3 * (size_t)g + 1] += dc[1];
+        dcov[3 * (size_t)g + 2] += dc[2];
+        dcol[3 * (size_t)g] += t[5];
+        dcol[3 * (size_t)g + 1] += t[6];
+        dcol[3 * (size_t)g + 2] += t[7];
+        dalpha[g] += t[8];
     }
 }
 
@@ -604,6 +702,13 @@ int fwd_pix() {
     static const int p = pix_setting("GSR_BLEND_FWD_PIX", 1);
     return p;
 }
+int bwd_batch() {
+    static const int b = [] {
+        const char* v = std::getenv("GSR_BLEND_BWD_BATCH");
+        return (v && std::string(v) == "64") ? 64 : 128;
+    }();
+    return b;
+}
 int bwd_pix() {
     static const int p = pix_setting("GSR_BLEND_BWD_PIX", 2);
     return p;
@@ -644,8 +749,8 @@ hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const in
 hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_t* ranges,
                             const int32_t* ids, uint64_t num_pairs, const void* recs,
                             const float* finalT, const int32_t* ncontrib, float* dmean,
-                            float* dcov, float* dcol, float* dalpha, uint32_t* work,
-                            uint32_t* order, hipStream_t st) {
+                            float* dcov, float* dcol, float* dalpha, const GradSlots& gs,
+                            uint32_t* work, uint32_t* order, hipStream_t st) {
     const int tiles_x = (W + kTileSize - 1) / kTileSize;
     const int tiles_y = (H + kTileSize - 1) / kTileSize;
     const unsigned tiles = (unsigned)(tiles_x * tiles_y);
@@ -661,14 +766,29 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
-    if (bwd_pix() == 2)
-        hipLaunchKernelGGL(blend_bwd_kernel<2>, dim3(tiles), dim3(Layout<2>::kThreads), 0, st, n,
-                           H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib, dmean,
-                           dcov, dcol, dalpha, order);
+    const bool small_batch = bwd_batch() == 64;
+    if (bwd_pix() == 2 && small_batch)
+        hipLaunchKernelGGL((blend_bwd_kernel<2, 64>), dim3(tiles), dim3(Layout<2>::kThreads), 0,
+                           st, n, H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib,
+                           dmean, dcov, dcol, dalpha, gs, order);
+    else if (bwd_pix() == 2)
+        hipLaunchKernelGGL((blend_bwd_kernel<2, 128>), dim3(tiles), dim3(Layout<2>::kThreads), 0,
+                           st, n, H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib,
+                           dmean, dcov, dcol, dalpha, gs, order);
     else
-        hipLaunchKernelGGL(blend_bwd_kernel<1>, dim3(tiles), dim3(Layout<1>::kThreads), 0, st, n,
-                           H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib, dmean,
-                           dcov, dcol, dalpha, order);
+        hipLaunchKernelGGL((blend_bwd_kernel<1, 256>), dim3(tiles), dim3(Layout<1>::kThreads), 0,
+                           st, n, H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib,
+                           dmean, dcov, dcol, dalpha, gs, order);
+    return hipGetLastError();
+}
+
+hipError_t launch_pair_grad_reduce(int n, const void* recs, const GradSlots& gs, float* dmean,
+                                   float* dcov, float* dcol, float* dalpha, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(pair_grad_reduce_kernel,
+                       dim3((unsigned)((n + kReduceGaussiansPerBlock - 1) / kReduceGaussiansPerBlock)),
+                       dim3(kReduceGaussiansPerBlock * kWave), 0, st, n,
+                       static_cast<const BlendRec*>(recs), gs, dmean, dcov, dcol, dalpha);
     return hipGetLastError();
 }
 

@@ -125,6 +125,42 @@ SortLayout sort_layout(int64_t m, int passes, int64_t T) {
     return L;
 }
 
+// Backward workspace: blend records, the tile schedule, the per-Gaussian tile
+// rectangles, counts and gradient-slot offsets, then (cleared each call) the
+// status block, the scan state and one flag byte per slot, then nine floats
+// per slot.
+struct BwdLayout {
+    size_t recs, work, order, counts, rects, goff, ctl, misc, scanctl, flags, ctl_end, sums, end;
+};
+
+BwdLayout backward_layout(int n, int64_t m, int height, int width) {
+    BwdLayout L;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = align_up(off + bytes, 256);
+        return o;
+    };
+    const size_t un = (size_t)(n > 0 ? n : 0), um = (size_t)(m > 0 ? m : 0);
+    const size_t T = (height > 0 && width > 0)
+                         ? (size_t)tiles_x_of(width) * (size_t)tiles_y_of(height)
+                         : 0;
+    L.recs = take(kRecBytes * un);
+    L.work = take(4 * T);
+    L.order = take(4 * T);
+    L.counts = take(4 * un);
+    L.rects = take(8 * un);
+    L.goff = take(4 * un);
+    L.ctl = off;
+    L.misc = take(sizeof(Misc));
+    L.scanctl = take(gsr::scan_control_bytes(n));
+    L.flags = take(um);
+    L.ctl_end = off;
+    L.sums = take(36 * um);
+    L.end = off;
+    return L;
+}
+
 template <typename T>
 T* at(void* base, size_t off) {
     return reinterpret_cast<T*>(static_cast<char*>(base) + off);
@@ -391,11 +427,8 @@ int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream) {
     return GSR_OK;
 }
 
-size_t gsr_backward_workspace_bytes(int n, int height, int width) {
-    const size_t T = (height > 0 && width > 0)
-                         ? (size_t)tiles_x_of(width) * (size_t)tiles_y_of(height)
-                         : 0;
-    return align_up(kRecBytes * (size_t)(n > 0 ? n : 0), 256) + 2 * align_up(4 * T, 256);
+size_t gsr_backward_workspace_bytes(int n, int64_t num_pairs, int height, int width) {
+    return backward_layout(n, num_pairs, height, width).end;
 }
 
 int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
@@ -406,13 +439,13 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
                            float* d_cov2d, float* d_colors, float* d_alpha, void* stream) {
     GSR_REQUIRE(n >= 0, "n must be non-negative");
     if (int rc = check_screen(height, width)) return rc;
-    GSR_REQUIRE(num_pairs >= 0, "num_pairs must be non-negative");
+    GSR_REQUIRE(num_pairs >= 0 && num_pairs <= kMaxPairs, "num_pairs out of range");
     hipStream_t st = as_stream(stream);
     if (n == 0) return GSR_OK;
     GSR_REQUIRE(mean2d && cov2d && colors && alpha && d_mean2d && d_cov2d && d_colors && d_alpha,
                 "null pointer");
-    if (ws_bytes < gsr_backward_workspace_bytes(n, height, width) || !ws)
-        return fail(GSR_ERR_WORKSPACE, "backward workspace too small");
+    const BwdLayout L = backward_layout(n, num_pairs, height, width);
+    if (ws_bytes < L.end || !ws) return fail(GSR_ERR_WORKSPACE, "backward workspace too small");
     GSR_HIP(gsr::zero_fill(d_mean2d, 8 * (size_t)n, st), "backward: clear");
     GSR_HIP(gsr::zero_fill(d_cov2d, 12 * (size_t)n, st), "backward: clear");
     GSR_HIP(gsr::zero_fill(d_colors, 12 * (size_t)n, st), "backward: clear");
@@ -420,16 +453,33 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
     const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
     if (T == 0 || num_pairs == 0) return GSR_OK;
     GSR_REQUIRE(grad_img && sorted_ids && tile_ranges && final_T && n_contrib, "null pointer");
-    GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, ws, st),
+    GSR_HIP(gsr::zero_fill(at<void>(ws, L.ctl), L.ctl_end - L.ctl, st), "backward: clear state");
+    Misc* misc = at<Misc>(ws, L.misc);
+    uint32_t* counts = at<uint32_t>(ws, L.counts);
+    uint2* rects = at<uint2>(ws, L.rects);
+    uint32_t* goff = at<uint32_t>(ws, L.goff);
+    GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, at<void>(ws, L.recs), st,
+                                      height, width, counts, rects),
             "backward: records");
-    const size_t rec_end = align_up(kRecBytes * (size_t)n, 256);
-    uint32_t* work = at<uint32_t>(ws, rec_end);
-    uint32_t* order = at<uint32_t>(ws, rec_end + align_up(4 * (size_t)T, 256));
+    GSR_HIP(gsr::launch_scan_counts(n, nullptr, counts, goff, &misc->total,
+                                    at<void>(ws, L.scanctl), &misc->err, st),
+            "backward: slot layout");
+    gsr::GradSlots gs;
+    gs.goff = goff;
+    gs.counts = counts;
+    gs.rects = rects;
+    gs.sums = at<float>(ws, L.sums);
+    gs.flags = at<uint8_t>(ws, L.flags);
+    gs.slots = (uint64_t)num_pairs;
     StageTimer timer("blend_bwd", st);
     GSR_HIP(gsr::launch_blend_bwd(n, height, width, grad_img, tile_ranges, sorted_ids,
-                                  (uint64_t)num_pairs, ws, final_T, n_contrib, d_mean2d, d_cov2d,
-                                  d_colors, d_alpha, work, order, st),
+                                  (uint64_t)num_pairs, at<void>(ws, L.recs), final_T, n_contrib,
+                                  d_mean2d, d_cov2d, d_colors, d_alpha, gs,
+                                  at<uint32_t>(ws, L.work), at<uint32_t>(ws, L.order), st),
             "backward: blend");
+    GSR_HIP(gsr::launch_pair_grad_reduce(n, at<void>(ws, L.recs), gs, d_mean2d, d_cov2d, d_colors,
+                                         d_alpha, st),
+            "backward: gradient sums");
     return GSR_OK;
 }
 

@@ -227,12 +227,12 @@ constexpr uint32_t kSpinLimit = 1u << 22;
 
 // Per-Gaussian blend record (48 B), built once per frame from the
 // rasterize inputs: (mean.x, mean.y, conic.x, 2*conic.y), (conic.z,
-// opacity, r, g), (b, conic.y, cut2, -).  2*conic.y is an exact scaling of
+// opacity, r, g), (b, conic.y, qthr, -).  2*conic.y is an exact scaling of
 // the reference's conic.y, so ((2*cy)*dx)*dy is the same product it forms.
-// cut2 is a squared pixel distance from the mean beyond which no pixel can
-// reach alpha >= 1/255 (conservative; -1 when the opacity alone rules every
-// pixel out, +inf when no bound applies): the blends use it to skip entries
-// for whole pixel regions without changing any per-pixel result.
+// qthr bounds the quadratic form from above for any pixel that can reach
+// alpha >= 1/255 (conservative; negative when the opacity alone rules every
+// pixel out): the blends use it to skip entries for whole pixel regions
+// without changing any per-pixel result.
 struct __align__(16) BlendRec {
     float4 a;
     float4 b;

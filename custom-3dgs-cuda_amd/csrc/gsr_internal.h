@@ -80,8 +80,8 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             hipStream_t st);
 
-// Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r]; the total
-// (u64) is written to *total.
+// Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r] (perm null:
+// the identity); the total (u64) is written to *total.
 size_t scan_control_bytes(int n);
 hipError_t launch_scan_counts(int n, const uint32_t* perm, const uint32_t* counts,
                               uint32_t* offsets, uint64_t* total, void* control, int* err,
@@ -104,19 +104,42 @@ hipError_t launch_full_keys(uint64_t m, const uint32_t* sorted_tiles, const int3
 // ---- blend ----
 // order (T entries, optional) receives the tiles' launch order, longest
 // estimated work first; work (T entries) holds the per-tile estimates.
+// With counts/rects (the backward) also the tile rectangle and count per
+// Gaussian, as the binning forms them.
 hipError_t launch_blend_records(int n, const float* mean2d, const float* cov2d,
                                 const float* colors, const float* alpha, void* recs,
-                                hipStream_t st);
+                                hipStream_t st, int H = 0, int W = 0, uint32_t* counts = nullptr,
+                                uint2* rects = nullptr);
 
 hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
                             uint64_t m, const void* recs, float* img, float* finalT,
                             int32_t* ncontrib, uint32_t* work, uint32_t* order,
                             hipStream_t st);
 
+// Gradient slots: the (Gaussian, tile) pairs in Gaussian-major order, pair
+// (g, t) at goff[g] + its index in g's tile rectangle (row-major); the backward
+// writes each processed pair's nine sums to sums[9 slot ..] and sets
+// flags[slot], and pair_grad_reduce adds each Gaussian's flagged slots to the
+// gradient outputs.  Pairs outside the layout (inputs that disagree with the
+// rectangles) fall back to atomics on the outputs.
+struct GradSlots {
+    const uint32_t* goff = nullptr;
+    const uint32_t* counts = nullptr;
+    const uint2* rects = nullptr;
+    float* sums = nullptr;
+    uint8_t* flags = nullptr;
+    uint64_t slots = 0;
+};
+
 hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_t* ranges,
                             const int32_t* ids, uint64_t num_pairs, const void* recs,
                             const float* finalT, const int32_t* ncontrib, float* dmean,
-                            float* dcov, float* dcol, float* dalpha, uint32_t* work,
-                            uint32_t* order, hipStream_t st);
+                            float* dcov, float* dcol, float* dalpha, const GradSlots& gs,
+                            uint32_t* work, uint32_t* order, hipStream_t st);
+
+// outputs += the per-Gaussian sums of the flagged slots (conic gradient
+// converted to the covariance gradient after the sum).
+hipError_t launch_pair_grad_reduce(int n, const void* recs, const GradSlots& gs, float* dmean,
+                                   float* dcov, float* dcol, float* dalpha, hipStream_t st);
 
 }  // namespace gsr

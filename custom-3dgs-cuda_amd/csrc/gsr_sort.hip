@@ -330,7 +330,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_counts_kernel(
 #pragma unroll
     for (int i = 0; i < kScanItems; ++i) {
         const int64_t r = first + i;
-        const uint32_t g = (r < n) ? perm[r] : 0xffffffffu;
+        const uint32_t g = (r < n) ? (perm ? perm[r] : (uint32_t)r) : 0xffffffffu;
         c[i] = (g < (uint32_t)n) ? counts[g] : 0u;
         sum += c[i];
     }

@@ -84,8 +84,11 @@ int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream);
  * the length of sorted_ids (tile ranges are clamped to it); ids outside
  * [0, n) are skipped as in the reference.  Outputs: d_mean2d [N,2],
  * d_cov2d [N,3] (dL/d(a,b,c)), d_colors [N,3], d_alpha [N].  The workspace
- * holds the blend records and the per-tile schedule. */
-size_t gsr_backward_workspace_bytes(int n, int height, int width);
+ * (about 37 B per pair plus 68 B per Gaussian) holds the blend records, the
+ * per-tile schedule and one gradient slot per (Gaussian, tile) pair: the
+ * per-tile sums are written to their slots and summed per Gaussian, with no
+ * float atomics, so the result does not depend on scheduling. */
+size_t gsr_backward_workspace_bytes(int n, int64_t num_pairs, int height, int width);
 int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
                            const float* mean2d, const float* cov2d, const float* colors,
                            const float* alpha, const int32_t* sorted_ids, int64_t num_pairs,

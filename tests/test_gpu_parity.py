@@ -193,6 +193,43 @@ def test_rasterize_backward_skips_corrupt_ids(crc, device):
     _backward_case(crc, device, a, corrupt=True)
 
 
+def test_rasterize_backward_inputs_off_the_rectangles(crc, device):
+    """Backward inputs whose (Gaussian, tile) pairs do not all lie in the tile
+    rectangles of mean2d/cov2d (the reference takes sorted ids and ranges as
+    given): such pairs take the direct path and must still match."""
+    a = scene_arrays(synthetic.config_scene("c1", requires_grad=False, n=3000, width=96, height=64))
+    fw = gpu_forward(crc, a, device)
+    want = oracle_forward(a)
+    H, W = a["H"], a["W"]
+    G = synthetic.grad_image(H, W, seed=5).numpy()
+    t = fw["tensors"]
+    cov = (want["cov2d"] * np.float32(0.25)).astype(np.float32)  # smaller rectangles
+    n = a["mu"].shape[0]
+    got = crc.backwards_rasterization(_dev(G, device), t["mean2d"], _dev(cov, device), t["colors"],
+                                      t["alpha"], t["ids"], t["ranges"], t["final_T"],
+                                      t["n_contrib"], n, H, W)
+    torch.cuda.synchronize()
+    ref = orc.blend_bwd(G, want["mean2d"], cov, want["colors"], a["alpha"], want["ids"],
+                        want["ranges"], want["final_T"], want["n_contrib"], H, W, with_abs=True)
+    for got_t, r, ab, nm in zip(got, ref[:4], ref[4:], ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")):
+        assert_grad_close(_np(got_t), r, ab, nm)
+
+
+def test_rasterize_backward_is_deterministic(crc, device):
+    """Each Gaussian's gradient is a fixed-order sum of its per-tile slots."""
+    a = scene_arrays(synthetic.config_scene("c3", requires_grad=False, n=30_000, width=480, height=270))
+    fw = gpu_forward(crc, a, device)
+    t = fw["tensors"]
+    G = _dev(synthetic.grad_image(a["H"], a["W"], seed=2).numpy(), device)
+    n = a["mu"].shape[0]
+    args = (G, t["mean2d"], t["cov2d"], t["colors"], t["alpha"], t["ids"], t["ranges"],
+            t["final_T"], t["n_contrib"], n, a["H"], a["W"])
+    r1 = [_np(x) for x in crc.backwards_rasterization(*args)]
+    r2 = [_np(x) for x in crc.backwards_rasterization(*args)]
+    for x, y, nm in zip(r1, r2, ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")):
+        assert_bitwise(x, y, nm)
+
+
 def test_sh_and_projection_backward_parity(crc, device):
     rng = np.random.default_rng(9)
     n = 50_000
