@@ -62,6 +62,13 @@ int tile_passes(int64_t T) {
 }
 constexpr int kMaxTilePasses = 4;
 
+// Significant bits of tile ids in [0, T).
+int tile_key_bits(int64_t T) {
+    int bits = 0;
+    for (uint64_t v = (uint64_t)(T > 1 ? T - 1 : 0); v; v >>= 1) ++bits;
+    return bits;
+}
+
 // Misc block at the head of the bin workspace.
 struct Misc {
     uint64_t total;  // pair count written by the scan
@@ -391,7 +398,8 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
             GSR_HIP(gsr::launch_partition_starts(n, es.perm, es.counts, es.offsets, m, part_rank,
                                                  st),
                     "rasterize: partition starts");
-            GSR_HIP(gsr::launch_tile_sort(es, m, passes, at<uint32_t>(bin_ws, BL.tilehist),
+            GSR_HIP(gsr::launch_tile_sort(es, m, passes, tile_key_bits(T),
+                                          at<uint32_t>(bin_ws, BL.tilehist),
                                           at<void>(sort_ws, SL.ctl), tk0, tk1,
                                           at<uint32_t>(sort_ws, SL.vbuf), ids, ktiles,
                                           &misc->err, st),

@@ -64,13 +64,15 @@ struct EmitSource {
 // Status words and partition counters of `passes` onesweep passes over n
 // elements (zero before use).
 size_t onesweep_state_bytes(uint64_t n, int passes);
-// Stable LSD sort of the m pairs described by es on tile-id digits 0..passes-1.
+// Stable LSD sort of the m pairs described by es on tile-id digits 0..passes-1
+// (tile ids below 2^key_bits).
 // hist holds the passes' global digit histograms ([passes][256], from the
 // tile rectangles).  Values (Gaussian ids) end in out_vals; keys (tile ids)
 // in out_keys when it is not null.  k0/k1/vbuf are m-element scratch.
-hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, const uint32_t* hist,
-                            void* state, uint32_t* k0, uint32_t* k1, uint32_t* vbuf,
-                            uint32_t* out_vals, uint32_t* out_keys, int* err, hipStream_t st);
+hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, int key_bits,
+                            const uint32_t* hist, void* state, uint32_t* k0, uint32_t* k1,
+                            uint32_t* vbuf, uint32_t* out_vals, uint32_t* out_keys, int* err,
+                            hipStream_t st);
 
 // ---- binning ----
 // counts[g], packed tile rect, depth key (float bits or 0xffffffff when the

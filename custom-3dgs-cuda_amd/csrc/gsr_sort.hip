@@ -27,6 +27,7 @@ namespace gsr {
 namespace {
 
 constexpr int kHistMaxPasses = 4;
+constexpr int kLookback = 4;
 static_assert(kSortThreads == kRadixBins, "one thread per digit in the onesweep kernel");
 static_assert(kSortThreads == 256, "four waves per onesweep work-group");
 
@@ -51,11 +52,13 @@ SortCtl carve(void* control, uint64_t n, int passes) {
     return c;
 }
 
-// Lanes of `active` whose 8-bit digit equals this lane's.
-__device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active) {
+// Lanes of `active` whose digit equals this lane's, comparing the low `bits`
+// bits (the digit's higher bits are known to be zero in every key).
+__device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active, int bits = 8) {
     uint64_t m = active;
 #pragma unroll
     for (int b = 0; b < 8; ++b) {
+        if (b >= bits) break;
         const bool bit = (d >> b) & 1u;
         const uint64_t t = ballot(bit);
         m &= bit ? t : ~t;
@@ -101,17 +104,32 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restr
     }
 }
 
+// The emission's staging index: one padding word per 16 slots, so a wave's
+// blocked writes (16 slots per lane) and striped reads spread over the banks.
+__device__ __forceinline__ int pad16(int slot) { return slot + (slot >> 4); }
+
 // Expands the (tile, Gaussian) pairs of sort slots [base, base + nvalid) into
-// s_keys / s_vals, slot order.  Pair slots are laid out by depth rank r at
+// s_keys / s_vals at pad16(slot).  Pair slots are laid out by depth rank r at
 // offsets[r] (ty outer, tx inner over the rank's tile rectangle), the order in
 // which the reference emits keys per Gaussian (rasterize.cu:124-135).  Ranks
-// r_lo..r_lo+nr-1 overlap the partition; the first kSortPartition of their
-// offsets are staged in s_off (more only occur when ranks without pairs sit
-// between ranks with pairs, and are then read from global memory).  Each
-// thread expands 16 consecutive slots: one binary search, then a linear walk.
+// r_lo..r_lo+nr-1 overlap the partition; the first kStageRanks of them have
+// their offset, Gaussian id and tile rectangle staged in LDS by one parallel
+// load (more only occur for partitions of very small Gaussians, or when ranks
+// without pairs sit between ranks with pairs, and are read from global
+// memory).  Each thread expands 16 consecutive slots: one binary search, one
+// division, then a walk that steps the column and row.
+constexpr int kStageRanks = kSortPartition / 4;
+
+struct RankStage {
+    uint32_t off[kStageRanks];
+    uint32_t g[kStageRanks];
+    uint2 rect[kStageRanks];
+};
+static_assert(sizeof(RankStage) == kSortPartition * 4, "fits the aux region");
+
 __device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base, int nvalid,
                                              uint32_t* s_keys, uint32_t* s_vals,
-                                             uint32_t* s_off) {
+                                             RankStage* st) {
     const int tid = threadIdx.x;
     const uint32_t part = (uint32_t)(base / kSortPartition);
     const uint32_t r_lo = es.part_rank[part];
@@ -121,11 +139,16 @@ __device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base
     const uint32_t r_last =
         (part + 1 < es.nparts && (uint64_t)es.offsets[r_next] < next_base) ? r_next : r_next - 1;
     const uint32_t nr = (r_last >= r_lo) ? r_last - r_lo + 1 : 1u;
-    const uint32_t nstage = min(nr, (uint32_t)kSortPartition);
-    for (uint32_t j = tid; j < nstage; j += kSortThreads) s_off[j] = es.offsets[r_lo + j];
+    const uint32_t nstage = min(nr, (uint32_t)kStageRanks);
+    for (uint32_t j = tid; j < nstage; j += kSortThreads) {
+        const uint32_t g = es.perm[r_lo + j];
+        st->off[j] = es.offsets[r_lo + j];
+        st->g[j] = g;
+        st->rect[j] = es.rects[g];
+    }
     __syncthreads();
     auto off_of = [&](uint32_t j) -> uint64_t {
-        return (j < (uint32_t)kSortPartition) ? s_off[j] : es.offsets[r_lo + j];
+        return (j < (uint32_t)kStageRanks) ? st->off[j] : es.offsets[r_lo + j];
     };
     const int first = tid * kSortItems;
     if (first < nvalid) {
@@ -135,31 +158,44 @@ __device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base
             const uint32_t mid = (lo + hi + 1) >> 1;
             if (off_of(mid) <= s0) lo = mid; else hi = mid - 1;
         }
-        uint32_t j = lo;
-        uint32_t g = es.perm[r_lo + j];
-        uint2 rc = es.rects[g];
-        uint32_t x0 = rc.x & 0xffffu, w = (rc.x >> 16) - x0, y0 = rc.y & 0xffffu;
+        uint32_t j = lo, g, x0, w, y0;
+        auto load_rank = [&](uint32_t jj) {
+            uint2 rc;
+            if (jj < (uint32_t)kStageRanks) {
+                g = st->g[jj];
+                rc = st->rect[jj];
+            } else {
+                g = es.perm[r_lo + jj];
+                rc = es.rects[g];
+            }
+            x0 = rc.x & 0xffffu;
+            w = (rc.x >> 16) - x0;
+            y0 = rc.y & 0xffffu;
+        };
+        load_rank(j);
         uint64_t kbase = off_of(j);
         uint64_t next = (j + 1 < nr) ? off_of(j + 1) : ~0ull;
+        const uint32_t k0 = (uint32_t)(s0 - kbase);
+        uint32_t row = w ? k0 / w : 0u;
+        uint32_t col = k0 - row * w;
         for (int i = 0; i < kSortItems; ++i) {
             const int slot = first + i;
             if (slot >= nvalid) break;
             const uint64_t sg = base + (uint64_t)slot;
-            while (sg >= next) {
+            while (sg >= next) {  // the next rank with pairs starts at this slot
                 ++j;
-                g = es.perm[r_lo + j];
-                rc = es.rects[g];
-                x0 = rc.x & 0xffffu;
-                w = (rc.x >> 16) - x0;
-                y0 = rc.y & 0xffffu;
+                load_rank(j);
                 kbase = next;
                 next = (j + 1 < nr) ? off_of(j + 1) : ~0ull;
+                row = 0;
+                col = 0;
             }
-            const uint32_t k = (uint32_t)(sg - kbase);
-            const uint32_t row = w ? k / w : 0u;
-            const uint32_t col = k - row * w;
-            s_keys[slot] = (y0 + row) * (uint32_t)es.tiles_x + x0 + col;
-            s_vals[slot] = g;
+            s_keys[pad16(slot)] = (y0 + row) * (uint32_t)es.tiles_x + x0 + col;
+            s_vals[pad16(slot)] = g;
+            if (++col == w) {
+                col = 0;
+                ++row;
+            }
         }
     }
     __syncthreads();
@@ -173,13 +209,13 @@ template <bool kEmit, bool kWriteKeys>
 __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n, int shift,
-    const uint32_t* __restrict__ hist, uint64_t* __restrict__ status,
+    int digit_bits, const uint32_t* __restrict__ hist, uint64_t* __restrict__ status,
     uint32_t* __restrict__ counter, int* __restrict__ err, EmitSource es) {
     // s_aux holds the emission's staged offsets first, then the digit counters,
     // digit starts and global bases (7 KB).
     constexpr int kAuxWords = kEmit ? kSortPartition : 7 * kRadixBins;
-    __shared__ uint32_t s_keys[kSortPartition];
-    __shared__ uint32_t s_vals[kSortPartition];
+    __shared__ uint32_t s_keys[kSortPartition + kSortPartition / 16];
+    __shared__ uint32_t s_vals[kSortPartition + kSortPartition / 16];
     __shared__ __align__(16) uint32_t s_aux[kAuxWords];
     __shared__ uint32_t s_scan[4];
     __shared__ uint32_t s_hscan[4];
@@ -197,13 +233,14 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
 
     uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
     if constexpr (kEmit) {
-        expand_pairs(es, base, nvalid, s_keys, s_vals, s_aux);  // ends with a barrier
+        expand_pairs(es, base, nvalid, s_keys, s_vals,
+                     reinterpret_cast<RankStage*>(s_aux));  // ends with a barrier
 #pragma unroll
         for (int i = 0; i < kSortItems; ++i) {
             const int e = wave * (kSortItems * 64) + i * 64 + lane;
             const bool v = e < nvalid;
-            key[i] = v ? s_keys[e] : 0u;
-            val[i] = v ? s_vals[e] : 0u;
+            key[i] = v ? s_keys[pad16(e)] : 0u;
+            val[i] = v ? s_vals[pad16(e)] : 0u;
         }
     } else {
 #pragma unroll
@@ -222,7 +259,7 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
         const int e = wave * (kSortItems * 64) + i * 64 + lane;
         const bool v = e < nvalid;
         const uint32_t d = (key[i] >> shift) & 0xffu;
-        const uint64_t peers = match_digit(d, ballot(v));
+        const uint64_t peers = match_digit(d, ballot(v), digit_bits);
         rank[i] = 0;
         if (v) {
             const uint32_t before = s_wcnt[wave][d];
@@ -273,25 +310,38 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
         }
     }
 
-    // Decoupled look-back for digit d over earlier partitions.
+    // Decoupled look-back for digit d over earlier partitions, kLookback
+    // status words per round trip (before partition 0 reads as inclusive 0).
     uint64_t excl = 0;
     if (part > 0) {
-        uint64_t p = part - 1;
+        int64_t p = (int64_t)part - 1;
         uint32_t spins = 0;
         while (true) {
-            const uint64_t s = load_agent(status + p * kRadixBins + d);
-            const uint64_t flag = s & ~kValueMask;
-            if (flag == 0) {
+            uint64_t sw[kLookback];
+#pragma unroll
+            for (int k = 0; k < kLookback; ++k)
+                sw[k] = (p - k >= 0) ? load_agent(status + (uint64_t)(p - k) * kRadixBins + d)
+                                     : kFlagInclusive;
+            int k = 0;
+            bool done = false;
+            for (; k < kLookback; ++k) {
+                const uint64_t flag = sw[k] & ~kValueMask;
+                if (flag == 0) break;  // not published yet: reload from here
+                excl += sw[k] & kValueMask;
+                if (flag == kFlagInclusive) {
+                    done = true;
+                    break;
+                }
+            }
+            if (done) break;
+            p -= k;
+            if (k < kLookback) {
                 if (++spins > kSpinLimit) {
                     atomicOr(err, 1);
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
-                continue;
             }
-            excl += s & kValueMask;
-            if (flag == kFlagInclusive || p == 0) break;
-            --p;
         }
         store_agent(my_status, kFlagInclusive | (excl + total));
     }
@@ -412,7 +462,7 @@ hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t*
     uint32_t *ki = k0, *vi = v0, *ko = k1, *vo = v1;
     for (int p = 0; p < passes; ++p) {
         hipLaunchKernelGGL((onesweep_kernel<false, true>), dim3((unsigned)parts),
-                           dim3(kSortThreads), 0, st, ki, vi, ko, vo, n, begin_bit + 8 * p,
+                           dim3(kSortThreads), 0, st, ki, vi, ko, vo, n, begin_bit + 8 * p, 8,
                            c.hist + p * kRadixBins, c.status + (size_t)p * parts * kRadixBins,
                            c.counters + p * 16, err, EmitSource{});
         e = hipGetLastError();
@@ -427,9 +477,10 @@ size_t onesweep_state_bytes(uint64_t n, int passes) {
     return align_up((size_t)passes * 64, 256) + (size_t)passes * parts_for(n) * kRadixBins * 8;
 }
 
-hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, const uint32_t* hist,
-                            void* state, uint32_t* k0, uint32_t* k1, uint32_t* vbuf,
-                            uint32_t* out_vals, uint32_t* out_keys, int* err, hipStream_t st) {
+hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, int key_bits,
+                            const uint32_t* hist, void* state, uint32_t* k0, uint32_t* k1,
+                            uint32_t* vbuf, uint32_t* out_vals, uint32_t* out_keys, int* err,
+                            hipStream_t st) {
     if (m == 0) return hipSuccess;
     if (passes < 1 || passes > 4) return hipErrorInvalidValue;
     const uint64_t parts = parts_for(m);
@@ -450,20 +501,21 @@ hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, const 
         uint64_t* stat = status + (size_t)p * parts * kRadixBins;
         const uint32_t* h = hist + p * kRadixBins;
         uint32_t* ctr = counters + p * 16;
+        const int bits = std::max(1, std::min(8, key_bits - 8 * p));  // significant digit bits
         if (p == 0) {
             if (ko)
                 hipLaunchKernelGGL((onesweep_kernel<true, true>), grid, block, 0, st, ki, vi, ko,
-                                   vdst[p], m, 8 * p, h, stat, ctr, err, es);
+                                   vdst[p], m, 8 * p, bits, h, stat, ctr, err, es);
             else
                 hipLaunchKernelGGL((onesweep_kernel<true, false>), grid, block, 0, st, ki, vi, ko,
-                                   vdst[p], m, 8 * p, h, stat, ctr, err, es);
+                                   vdst[p], m, 8 * p, bits, h, stat, ctr, err, es);
         } else {
             if (ko)
                 hipLaunchKernelGGL((onesweep_kernel<false, true>), grid, block, 0, st, ki, vi, ko,
-                                   vdst[p], m, 8 * p, h, stat, ctr, err, es);
+                                   vdst[p], m, 8 * p, bits, h, stat, ctr, err, es);
             else
                 hipLaunchKernelGGL((onesweep_kernel<false, false>), grid, block, 0, st, ki, vi,
-                                   ko, vdst[p], m, 8 * p, h, stat, ctr, err, es);
+                                   ko, vdst[p], m, 8 * p, bits, h, stat, ctr, err, es);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
