@@ -81,22 +81,24 @@ __device__ __forceinline__ void hist_row(uint32_t a, uint32_t w, int passes, int
 }
 
 // Per Gaussian: tile rectangle and count (rasterize.cu:19-59, :98-105), the
-// depth sort's key and value, and the Gaussian's share of the tile sort's
-// global digit histograms (tile_hist[p][d] counts the pairs whose tile id has
-// digit d in pass p), accumulated per work-group and flushed with one global
-// atomic per non-zero bin.
+// depth sort's key and value, and the Gaussian's share of both sorts' global
+// digit histograms (depth_hist[p][d]: keys with digit d in pass p;
+// tile_hist[p][d]: pairs whose tile id has digit d in pass p), accumulated per
+// work-group and flushed with one global atomic per non-zero bin.
 __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     int n, const float* __restrict__ mean2d, const float* __restrict__ cov2d,
     const float* __restrict__ depth, int H, int W, uint32_t* __restrict__ counts,
     uint2* __restrict__ rects, uint32_t* __restrict__ dkeys, uint32_t* __restrict__ dvals,
-    int passes, uint32_t* __restrict__ tile_hist) {
+    int passes, uint32_t* __restrict__ tile_hist, uint32_t* __restrict__ depth_hist) {
     __shared__ int s_d0[kRadixBins + 1];
     __shared__ uint32_t s_h[3][kRadixBins];
+    __shared__ uint32_t s_dh[4][kRadixBins];
     __shared__ uint32_t s_full[kThreads / kWave];
     __shared__ uint32_t s_scan[kThreads / kWave];
     const int tid = threadIdx.x;
     for (int j = tid; j <= kRadixBins; j += kThreads) s_d0[j] = 0;
     for (int j = tid; j < 3 * kRadixBins; j += kThreads) (&s_h[0][0])[j] = 0;
+    for (int j = tid; j < 4 * kRadixBins; j += kThreads) (&s_dh[0][0])[j] = 0;
     __syncthreads();
     const int tiles_x = (W + 15) / 16;
     uint32_t full = 0;
@@ -110,8 +112,11 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
                               (uint32_t)r.y0 | ((uint32_t)r.y1 << 16));
         // Gaussians without tiles sort last; they emit nothing, so their place
         // in the depth order never shows.
-        dkeys[i] = cnt ? __float_as_uint(depth[i]) : 0xffffffffu;
+        const uint32_t dk = cnt ? __float_as_uint(depth[i]) : 0xffffffffu;
+        dkeys[i] = dk;
         dvals[i] = (uint32_t)i;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) atomicAdd(&s_dh[p][(dk >> (8 * p)) & 0xffu], 1u);
         if (cnt) {
             const uint32_t w = (uint32_t)(r.x1 - r.x0);
             for (int y = r.y0; y < r.y1; ++y)
@@ -134,6 +139,11 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     for (int p = 1; p < passes; ++p) {
         const uint32_t v = s_h[p - 1][tid];
         if (v) atomicAdd(&tile_hist[p * kRadixBins + tid], v);
+    }
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+        const uint32_t v = s_dh[p][tid];
+        if (v) atomicAdd(&depth_hist[p * kRadixBins + tid], v);
     }
 }
 
@@ -237,14 +247,15 @@ inline unsigned blocks_for(uint64_t n) { return (unsigned)((n + kThreads - 1) / 
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
-                            hipStream_t st) {
+                            uint32_t* depth_hist, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     if (tile_passes < 1 || tile_passes > 4) return hipErrorInvalidValue;
     // at most one work-group per CU: the histogram flush costs one global
     // atomic per bin and work-group
     const unsigned blocks = std::min(blocks_for(n), 256u);
     hipLaunchKernelGGL(bin_count_kernel, dim3(blocks), dim3(kThreads), 0, st, n, mean2d, cov2d,
-                       depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist);
+                       depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist,
+                       depth_hist);
     return hipGetLastError();
 }
 

@@ -311,14 +311,16 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
         const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
         GSR_HIP(gsr::launch_bin_count(n, mean2d, cov2d, depth, height, width, counts,
                                       at<uint2>(bin_ws, L.rects), dk0, dv0, tile_passes(T),
-                                      at<uint32_t>(bin_ws, L.tilehist), st),
+                                      at<uint32_t>(bin_ws, L.tilehist),
+                                      at<uint32_t>(bin_ws, L.sortctl), st),
                 "rasterize: count");
     }
     {
         StageTimer timer("depth_sort", st);
         GSR_HIP(gsr::launch_radix_sort(dk0, dv0, at<uint32_t>(bin_ws, L.dk1),
                                        at<uint32_t>(bin_ws, L.dv1), (uint64_t)n, 0, kDepthPasses,
-                                       at<void>(bin_ws, L.sortctl), err, st),
+                                       at<void>(bin_ws, L.sortctl), err, st,
+                                       /*hist_ready=*/true),
                 "rasterize: depth sort");
     }
     {
@@ -366,7 +368,10 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
     const int passes = tile_passes(T);
     const SortLayout SL = sort_layout(num_pairs, passes, T);
     hipStream_t st = as_stream(stream);
-    GSR_HIP(gsr::zero_fill(tile_ranges, (size_t)T * 8, st), "rasterize: clear ranges");
+    gsr::FillList clear;
+    clear.add(tile_ranges, (size_t)T * 8);
+    if (num_pairs > 0 && sort_ws && sort_ws_bytes >= SL.end) clear.add(sort_ws, SL.ctl_end);
+    GSR_HIP(gsr::zero_fill(clear, st), "rasterize: clear");
     const uint64_t m = (uint64_t)num_pairs;
     void* recs = at<void>(bin_ws, BL.recs);
     if (m > 0) {
@@ -374,7 +379,6 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
         if (sort_ws_bytes < SL.end) return fail(GSR_ERR_WORKSPACE, "sort workspace too small");
         GSR_REQUIRE(mean2d && cov2d && colors && alpha && depth, "null pointer");
         Misc* misc = at<Misc>(bin_ws, BL.misc);
-        GSR_HIP(gsr::zero_fill(sort_ws, SL.ctl_end, st), "rasterize: clear sort state");
         {
             StageTimer timer("records", st);
             GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, recs, st),
@@ -454,14 +458,18 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
                 "null pointer");
     const BwdLayout L = backward_layout(n, num_pairs, height, width);
     if (ws_bytes < L.end || !ws) return fail(GSR_ERR_WORKSPACE, "backward workspace too small");
-    GSR_HIP(gsr::zero_fill(d_mean2d, 8 * (size_t)n, st), "backward: clear");
-    GSR_HIP(gsr::zero_fill(d_cov2d, 12 * (size_t)n, st), "backward: clear");
-    GSR_HIP(gsr::zero_fill(d_colors, 12 * (size_t)n, st), "backward: clear");
-    GSR_HIP(gsr::zero_fill(d_alpha, 4 * (size_t)n, st), "backward: clear");
     const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
-    if (T == 0 || num_pairs == 0) return GSR_OK;
-    GSR_REQUIRE(grad_img && sorted_ids && tile_ranges && final_T && n_contrib, "null pointer");
-    GSR_HIP(gsr::zero_fill(at<void>(ws, L.ctl), L.ctl_end - L.ctl, st), "backward: clear state");
+    const bool work = T > 0 && num_pairs > 0;
+    if (work)
+        GSR_REQUIRE(grad_img && sorted_ids && tile_ranges && final_T && n_contrib, "null pointer");
+    gsr::FillList clear;
+    clear.add(d_mean2d, 8 * (size_t)n);
+    clear.add(d_cov2d, 12 * (size_t)n);
+    clear.add(d_colors, 12 * (size_t)n);
+    clear.add(d_alpha, 4 * (size_t)n);
+    if (work) clear.add(at<void>(ws, L.ctl), L.ctl_end - L.ctl);
+    GSR_HIP(gsr::zero_fill(clear, st), "backward: clear");
+    if (!work) return GSR_OK;
     Misc* misc = at<Misc>(ws, L.misc);
     uint32_t* counts = at<uint32_t>(ws, L.counts);
     uint2* rects = at<uint2>(ws, L.rects);

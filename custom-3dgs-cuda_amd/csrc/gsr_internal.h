@@ -41,11 +41,28 @@ size_t sort_control_bytes(uint64_t n, int passes);
 // Ping-pongs between (k0,v0) and (k1,v1); the result lands in (k0,v0) for an
 // even pass count and in (k1,v1) for an odd one.  `control` must be zeroed
 // on the stream first (zero_fill).  err (device int) is set when a look-back
-// exceeds kSpinLimit.
+// exceeds kSpinLimit.  hist_ready: the passes' digit histograms ([passes][256]
+// u32 at the start of `control`) were accumulated already.
 hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
-                             int begin_bit, int passes, void* control, int* err, hipStream_t st);
+                             int begin_bit, int passes, void* control, int* err, hipStream_t st,
+                             bool hist_ready = false);
 
 hipError_t zero_fill(void* p, size_t bytes, hipStream_t st);
+// Several regions in one launch.
+struct FillList {
+    static constexpr int kMaxFills = 6;
+    void* ptr[kMaxFills] = {};
+    size_t bytes[kMaxFills] = {};
+    int count = 0;
+    void add(void* p, size_t b) {
+        if (b > 0 && count < kMaxFills) {
+            ptr[count] = p;
+            bytes[count] = b;
+            ++count;
+        }
+    }
+};
+hipError_t zero_fill(const FillList& f, hipStream_t st);
 
 // Where the first tile-sort pass generates its (tile, Gaussian) pairs: depth
 // order perm, per-Gaussian counts and packed tile rectangles, per-rank pair
@@ -76,11 +93,12 @@ hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, int ke
 
 // ---- binning ----
 // counts[g], packed tile rect, depth key (float bits or 0xffffffff when the
-// Gaussian touches no tile) and identity values.
+// Gaussian touches no tile) and identity values, plus the digit histograms of
+// the tile sort (tile_hist) and of the 4-pass depth sort (depth_hist).
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
-                            hipStream_t st);
+                            uint32_t* depth_hist, hipStream_t st);
 
 // Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r] (perm null:
 // the identity); the total (u64) is written to *total.

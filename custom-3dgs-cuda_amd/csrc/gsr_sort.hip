@@ -66,13 +66,22 @@ __device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active, int
     return m;
 }
 
-__global__ __launch_bounds__(256) void fill_zero_kernel(uint4* __restrict__ p, size_t n16,
-                                                        uint8_t* __restrict__ tail,
-                                                        int tail_bytes) {
+// Zeroes up to kMaxFills regions in one launch: bytes up to the first 16-byte
+// boundary, 16-byte stores, then the tail bytes.
+__global__ __launch_bounds__(256) void fill_zero_kernel(FillList f) {
     const size_t stride = (size_t)gridDim.x * 256;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
-        p[i] = make_uint4(0u, 0u, 0u, 0u);
-    if (blockIdx.x == 0 && (int)threadIdx.x < tail_bytes) tail[threadIdx.x] = 0;
+    const size_t t = (size_t)blockIdx.x * 256 + threadIdx.x;
+    for (int r = 0; r < f.count; ++r) {
+        uint8_t* b = static_cast<uint8_t*>(f.ptr[r]);
+        const size_t len = f.bytes[r];
+        const size_t head = std::min<size_t>(len, (16 - ((uintptr_t)b & 15)) & 15);
+        if (t < head) b[t] = 0;
+        uint4* p = reinterpret_cast<uint4*>(b + head);
+        const size_t n16 = (len - head) / 16;
+        for (size_t i = t; i < n16; i += stride) p[i] = make_uint4(0u, 0u, 0u, 0u);
+        const size_t tail = len - head - n16 * 16;
+        if (t < tail) reinterpret_cast<uint8_t*>(p + n16)[t] = 0;
+    }
 }
 
 // Global digit histograms of every pass in one read of the keys.  Digit
@@ -432,15 +441,19 @@ __global__ __launch_bounds__(kScanThreads) void scan_counts_kernel(
 
 }  // namespace
 
-hipError_t zero_fill(void* p, size_t bytes, hipStream_t st) {
-    if (bytes == 0) return hipSuccess;
-    const size_t n16 = bytes / 16;
-    const int tail = (int)(bytes - n16 * 16);
-    uint8_t* tailp = static_cast<uint8_t*>(p) + n16 * 16;
-    const size_t blocks = std::min<size_t>(std::max<size_t>((n16 + 255) / 256, 1), 2048);
-    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
-                       static_cast<uint4*>(p), n16, tailp, tail);
+hipError_t zero_fill(const FillList& f, hipStream_t st) {
+    size_t most = 0;
+    for (int r = 0; r < f.count; ++r) most = std::max(most, f.bytes[r] / 16);
+    if (f.count == 0) return hipSuccess;
+    const size_t blocks = std::min<size_t>(std::max<size_t>((most + 255) / 256, 1), 2048);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st, f);
     return hipGetLastError();
+}
+
+hipError_t zero_fill(void* p, size_t bytes, hipStream_t st) {
+    FillList f;
+    f.add(p, bytes);
+    return zero_fill(f, st);
 }
 
 size_t sort_control_bytes(uint64_t n, int passes) {
@@ -449,16 +462,20 @@ size_t sort_control_bytes(uint64_t n, int passes) {
 }
 
 hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
-                             int begin_bit, int passes, void* control, int* err, hipStream_t st) {
+                             int begin_bit, int passes, void* control, int* err, hipStream_t st,
+                             bool hist_ready) {
     if (n == 0 || passes <= 0) return hipSuccess;
     if (passes > kHistMaxPasses) return hipErrorInvalidValue;
     const uint64_t parts = parts_for(n);
     SortCtl c = carve(control, n, passes);
-    const unsigned hblocks = (unsigned)std::min<uint64_t>(parts, 512);
-    hipLaunchKernelGGL(radix_hist_kernel, dim3(hblocks), dim3(256), 0, st, k0, n, begin_bit,
-                       passes, c.hist);
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
+    hipError_t e = hipSuccess;
+    if (!hist_ready) {
+        const unsigned hblocks = (unsigned)std::min<uint64_t>(parts, 512);
+        hipLaunchKernelGGL(radix_hist_kernel, dim3(hblocks), dim3(256), 0, st, k0, n, begin_bit,
+                           passes, c.hist);
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
     uint32_t *ki = k0, *vi = v0, *ko = k1, *vo = v1;
     for (int p = 0; p < passes; ++p) {
         hipLaunchKernelGGL((onesweep_kernel<false, true>), dim3((unsigned)parts),
