@@ -38,26 +38,47 @@ def _tiles(W, H):
 
 def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
     """Algorithmic bytes per call: the rasterizer baseline's per-stage formulas
-    (N Gaussians, M pairs, P pixels, T tiles); the two sorts use this build's own
-    algorithm (8 B read + 8 B written per element and pass, plus one 4 B histogram read)."""
+    (N Gaussians, M pairs, P pixels, T tiles) for the blends and the per-Gaussian
+    stages; the sorts and the schedules use this build's own algorithm."""
     P, T = W * H, _tiles(W, H)
     tile_passes = max(1, math.ceil((T - 1).bit_length() / 8)) if T > 1 else 1
     return {
         "project": 64 * N,
         "sh": 216 * N,
         "bin_count": 20 * N + 28 * N,          # mean2d + cov2d + depth in; count, rect, key, val out
-        "depth_sort": 4 * 16 * N + 4 * N,
+        "depth_sort": 4 * 16 * N,
         "scan": 12 * N,
         "records": 36 * N + 48 * N,
         # the first pass generates its pairs from per-Gaussian data (perm,
         # offset, rect: 16 B) and writes 8 B per pair; later passes move 16 B
         "tile_sort": (16 * tile_passes - 8) * M + 16 * N,
         "ranges": 4 * M + 8 * T,
+        "fwd_schedule": 16 * T,                 # ranges in, estimates + order out (walk not counted)
         "blend_fwd": 40 * M + 20 * P + 8 * T,
+        "bwd_records": 96 * N,
+        "bwd_slots": 8 * N,
+        "bwd_schedule": 4 * P + 16 * T,
         "blend_bwd": 76 * M + 20 * P + 8 * T,
+        "grad_reduce": M + 8 * N,               # slot flags + offsets (sums of processed pairs not counted)
         "sh_bwd": 420 * N,
         "project_bwd": 100 * N,
     }[stage]
+
+
+# Highest wave64 VALU issue rate measured on MI355X (v_add_f32 / v_mul_f32 chains,
+# 8 independent per lane, 16 waves per SIMD; SQ_INSTS_VALU-calibrated): 945 G/s.
+# v_fma_f32 issues at ~600 G/s (one per CU per 2.4 GHz cycle).
+VALU_PEAK_GINST = 945.0
+
+
+def _profile_json(kind: str, kernel: str, workload: str):
+    p = ROOT / "profiles" / f"{kind}_{kernel}_{workload}.json"
+    if p.exists():
+        try:
+            return json.loads(p.read_text())
+        except (OSError, ValueError):
+            return None
+    return None
 
 
 def _clear(g):
@@ -155,16 +176,6 @@ def cpu_baseline(sc, budget_s: float = 30.0) -> dict:
                       f"fp32 CPU oracle with {threads} OpenMP threads"}
 
 
-def _traffic(kernel: str, workload: str):
-    p = ROOT / "profiles" / f"traffic_{kernel}_{workload}.json"
-    if p.exists():
-        try:
-            return json.loads(p.read_text()).get("bytes_per_launch")
-        except (OSError, ValueError):
-            return None
-    return None
-
-
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -221,12 +232,21 @@ def main() -> int:
     roofline = None
     if dominant:
         avg_s = per_stage[dominant]["ms"] * 1e-3
-        ach = stage_bytes(dominant, N, M, W, H) / avg_s / 1e9
+        alg = stage_bytes(dominant, N, M, W, H)
+        ach = alg / avg_s / 1e9
+        tr = _profile_json("traffic", dominant, workload)
         roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(ach, 1),
                     "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                    "traffic": _traffic(dominant, workload),
-                    "algorithmic_bytes": stage_bytes(dominant, N, M, W, H),
-                    "avg_launch_ms": per_stage[dominant]["ms"]}
+                    "traffic": tr.get("bytes_per_launch") if tr else None,
+                    "algorithmic_bytes": alg, "avg_launch_ms": per_stage[dominant]["ms"]}
+        va = _profile_json("valu", dominant, workload)
+        if va and va.get("valu_insts_per_launch"):
+            g = va["valu_insts_per_launch"] / avg_s / 1e9
+            # the blends issue VALU, not HBM, at their limit: issue rate against
+            # the chip's wave64 instruction rate
+            roofline["valu"] = {"insts_per_launch": va["valu_insts_per_launch"],
+                                "achieved_ginst_s": round(g, 1), "peak_ginst_s": VALU_PEAK_GINST,
+                                "frac": round(g / VALU_PEAK_GINST, 4)}
 
     value = 1000.0 / total
     out = {

@@ -325,9 +325,9 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     m.def("profile_collect", []() {
         check_rc(gsr_profile_collect(), "profile_collect");
         py::dict out;
-        for (const char* st : {"project", "sh", "bin_count", "depth_sort", "scan", "records",
-                               "emit", "tile_sort", "ranges", "blend_fwd", "blend_bwd", "sh_bwd",
-                               "project_bwd"}) {
+        for (int i = 0;; ++i) {
+            const char* st = gsr_profile_stage(i);
+            if (!st) break;
             int64_t c = 0;
             double ms = 0.0;
             gsr_profile_get(st, &c, &ms);

@@ -32,7 +32,6 @@
 // Work-groups take their tile from a launch order, longest estimated work
 // first (tile_order_kernel), so long tiles do not start last.
 #include <cstdlib>
-#include <string>
 
 #include "gsr_internal.h"
 #include "gsr_common.h"
@@ -498,45 +497,70 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     }
 }
 
-// One wave per Gaussian: the nine sums of its flagged slots, the conic part
-// converted to the covariance gradient, added to the outputs (which hold
-// zeros and any fallback atomics from the blend).
-constexpr int kReduceGaussiansPerBlock = 4;
+// One 16-lane row per Gaussian (four per wave): the nine sums of its flagged
+// slots, the conic part converted to the covariance gradient, added to the
+// outputs (which hold zeros and any fallback atomics from the blend).
+constexpr int kReduceRowLanes = 16;
+constexpr int kReduceGaussiansPerBlock = 256 / kReduceRowLanes;
 
-__global__ __launch_bounds__(kReduceGaussiansPerBlock * kWave) void pair_grad_reduce_kernel(
+// Sum over the 16 lanes of each row, result in every lane of the row.
+__device__ __forceinline__ float row_sum16(float x) {
+    x += dpp_move<kDppRowRor8>(x);
+    x += lane_xor4(x);
+    x += dpp_move<kDppQuadXor2>(x);
+    x += dpp_move<kDppQuadXor1>(x);
+    return x;
+}
+
+__global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
     int n, const BlendRec* __restrict__ recs, GradSlots gs, float* __restrict__ dmean,
     float* __restrict__ dcov, float* __restrict__ dcol, float* __restrict__ dalpha) {
-    const int lane = threadIdx.x & 63;
-    const int g = blockIdx.x * kReduceGaussiansPerBlock + (int)(threadIdx.x >> 6);
-    if (g >= n) return;  // whole waves
-    const uint64_t base = gs.goff[g];
-    const uint32_t cnt = gs.counts[g];
+    const int sub = threadIdx.x & (kReduceRowLanes - 1);
+    const int g = blockIdx.x * kReduceGaussiansPerBlock + (int)(threadIdx.x / kReduceRowLanes);
     float v[kTerms] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (uint32_t i = (uint32_t)lane; i < cnt; i += kWave) {
-        const uint64_t slot = base + i;
-        if (slot < gs.slots && gs.flags[slot]) {
-            const float* d = gs.sums + 9 * slot;
+    if (g < n) {
+        const uint64_t base = gs.goff[g];
+        const uint64_t end = min(base + (uint64_t)gs.counts[g], gs.slots);
+        // flags eight at a time from 8-byte aligned groups (the flag array is
+        // 256-byte aligned and padded to a multiple of 8 bytes)
+        for (uint64_t grp = (base & ~7ull) + 8ull * sub; grp < end;
+             grp += 8ull * kReduceRowLanes) {
+            uint64_t bits = *reinterpret_cast<const uint64_t*>(gs.flags + grp);
+            while (bits) {
+                const int b = __builtin_ctzll(bits) >> 3;  // flag bytes hold 0 or 1
+                bits &= bits - 1;
+                const uint64_t slot = grp + (uint64_t)b;
+                if (slot >= base && slot < end) {
+                    const float* d = gs.sums + 9 * slot;
 #pragma unroll
-            for (int k = 0; k < kTerms; ++k) v[k] += d[k];
+                    for (int k = 0; k < kTerms; ++k) v[k] += d[k];
+                }
+            }
         }
     }
-    const float w = wave_reduce9(v);
+    // every lane takes part in the row sums (rows past n add zeros)
     float t[kTerms];
 #pragma unroll
-    for (int k = 0; k < kTerms; ++k) t[k] = __shfl(w, kReduce9Lane[k], kWave);
-    if (lane == 0) {
+    for (int k = 0; k < kTerms; ++k) t[k] = row_sum16(v[k]);
+    if (g < n && sub == 0) {
         const BlendRec r = recs[g];
         float dc[3];
         conic_to_cov_grad(r.a.z, r.c.y, r.b.x, t[2], t[3], t[4], dc);
-        dmean[2 * (size_t)g] += t[0];
-        dmean[2 * (size_t)g + 1] += t[1];
-        dcov[3 * (size_t)g] += dc[0];
-        dcov[3 * (size_t)g + 1] += dc[1];
-        dcov[3 * (size_t)g + 2] += dc[2];
-        dcol[3 * (size_t)g] += t[5];
-        dcol[3 * (size_t)g + 1] += t[6];
-        dcol[3 * (size_t)g + 2] += t[7];
-        dalpha[g] += t[8];
+        const float m0 = dmean[2 * (size_t)g], m1 = dmean[2 * (size_t)g + 1];
+        const float c0 = dcov[3 * (size_t)g], c1 = dcov[3 * (size_t)g + 1],
+                    c2 = dcov[3 * (size_t)g + 2];
+        const float k0 = dcol[3 * (size_t)g], k1 = dcol[3 * (size_t)g + 1],
+                    k2 = dcol[3 * (size_t)g + 2];
+        const float a0 = dalpha[g];
+        dmean[2 * (size_t)g] = m0 + t[0];
+        dmean[2 * (size_t)g + 1] = m1 + t[1];
+        dcov[3 * (size_t)g] = c0 + dc[0];
+        dcov[3 * (size_t)g + 1] = c1 + dc[1];
+        dcov[3 * (size_t)g + 2] = c2 + dc[2];
+        dcol[3 * (size_t)g] = k0 + t[5];
+        dcol[3 * (size_t)g + 1] = k1 + t[6];
+        dcol[3 * (size_t)g + 2] = k2 + t[7];
+        dalpha[g] = a0 + t[8];
     }
 }
 
@@ -702,13 +726,6 @@ int fwd_pix() {
     static const int p = pix_setting("GSR_BLEND_FWD_PIX", 1);
     return p;
 }
-int bwd_batch() {
-    static const int b = [] {
-        const char* v = std::getenv("GSR_BLEND_BWD_BATCH");
-        return (v && std::string(v) == "64") ? 64 : 128;
-    }();
-    return b;
-}
 int bwd_pix() {
     static const int p = pix_setting("GSR_BLEND_BWD_PIX", 2);
     return p;
@@ -716,27 +733,33 @@ int bwd_pix() {
 
 }  // namespace
 
+bool launch_order_enabled() { return tile_order_enabled(); }
+
+hipError_t launch_fwd_schedule(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
+                               uint64_t m, const void* recs, uint32_t* work, uint32_t* order,
+                               hipStream_t st) {
+    const int tiles_x = (W + kTileSize - 1) / kTileSize;
+    const unsigned tiles = (unsigned)(tiles_x * ((H + kTileSize - 1) / kTileSize));
+    if (tiles == 0) return hipSuccess;
+    const auto* r = reinterpret_cast<const int2*>(ranges);
+    hipLaunchKernelGGL(tile_work_fwd_kernel,
+                       dim3((tiles + kEstTilesPerBlock - 1) / kEstTilesPerBlock),
+                       dim3(kEstTilesPerBlock * kWave), 0, st, (int)tiles, tiles_x, n, m, r, ids,
+                       static_cast<const BlendRec*>(recs), work);
+    hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles, m, r,
+                       work, order);
+    return hipGetLastError();
+}
+
 hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
                             uint64_t m, const void* recs, float* img, float* finalT,
-                            int32_t* ncontrib, uint32_t* work, uint32_t* order,
-                            hipStream_t st) {
+                            int32_t* ncontrib, const uint32_t* order, hipStream_t st) {
     const int tiles_x = (W + kTileSize - 1) / kTileSize;
     const int tiles_y = (H + kTileSize - 1) / kTileSize;
     const unsigned tiles = (unsigned)(tiles_x * tiles_y);
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
     const auto* rc = static_cast<const BlendRec*>(recs);
-    if (!tile_order_enabled() || !work) order = nullptr;
-    if (order) {
-        hipLaunchKernelGGL(tile_work_fwd_kernel,
-                           dim3((tiles + kEstTilesPerBlock - 1) / kEstTilesPerBlock),
-                           dim3(kEstTilesPerBlock * kWave), 0, st, (int)tiles, tiles_x, n, m, r,
-                           ids, rc, work);
-        hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles, m,
-                           r, work, order);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    }
     if (fwd_pix() == 2)
         hipLaunchKernelGGL(blend_fwd_kernel<2>, dim3(tiles), dim3(Layout<2>::kThreads), 0, st, n,
                            H, W, tiles_x, m, r, ids, rc, img, finalT, ncontrib, order);
@@ -746,32 +769,32 @@ hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const in
     return hipGetLastError();
 }
 
+hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num_pairs,
+                               const int32_t* ncontrib, uint32_t* work, uint32_t* order,
+                               hipStream_t st) {
+    const int tiles_x = (W + kTileSize - 1) / kTileSize;
+    const unsigned tiles = (unsigned)(tiles_x * ((H + kTileSize - 1) / kTileSize));
+    if (tiles == 0) return hipSuccess;
+    const auto* r = reinterpret_cast<const int2*>(ranges);
+    hipLaunchKernelGGL(tile_work_bwd_kernel, dim3(tiles), dim3(kTilePixels), 0, st, H, W, tiles_x,
+                       num_pairs, r, ncontrib, work);
+    hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles,
+                       num_pairs, r, work, order);
+    return hipGetLastError();
+}
+
 hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_t* ranges,
                             const int32_t* ids, uint64_t num_pairs, const void* recs,
                             const float* finalT, const int32_t* ncontrib, float* dmean,
                             float* dcov, float* dcol, float* dalpha, const GradSlots& gs,
-                            uint32_t* work, uint32_t* order, hipStream_t st) {
+                            const uint32_t* order, hipStream_t st) {
     const int tiles_x = (W + kTileSize - 1) / kTileSize;
     const int tiles_y = (H + kTileSize - 1) / kTileSize;
     const unsigned tiles = (unsigned)(tiles_x * tiles_y);
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
     const auto* rc = static_cast<const BlendRec*>(recs);
-    if (!tile_order_enabled() || !work) order = nullptr;
-    if (order) {
-        hipLaunchKernelGGL(tile_work_bwd_kernel, dim3(tiles), dim3(kTilePixels), 0, st, H, W,
-                           tiles_x, num_pairs, r, ncontrib, work);
-        hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles,
-                           num_pairs, r, work, order);
-        const hipError_t e = hipGetLastError();
-        if (e != hipSuccess) return e;
-    }
-    const bool small_batch = bwd_batch() == 64;
-    if (bwd_pix() == 2 && small_batch)
-        hipLaunchKernelGGL((blend_bwd_kernel<2, 64>), dim3(tiles), dim3(Layout<2>::kThreads), 0,
-                           st, n, H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib,
-                           dmean, dcov, dcol, dalpha, gs, order);
-    else if (bwd_pix() == 2)
+    if (bwd_pix() == 2)
         hipLaunchKernelGGL((blend_bwd_kernel<2, 128>), dim3(tiles), dim3(Layout<2>::kThreads), 0,
                            st, n, H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib,
                            dmean, dcov, dcol, dalpha, gs, order);
@@ -787,8 +810,8 @@ hipError_t launch_pair_grad_reduce(int n, const void* recs, const GradSlots& gs,
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(pair_grad_reduce_kernel,
                        dim3((unsigned)((n + kReduceGaussiansPerBlock - 1) / kReduceGaussiansPerBlock)),
-                       dim3(kReduceGaussiansPerBlock * kWave), 0, st, n,
-                       static_cast<const BlendRec*>(recs), gs, dmean, dcov, dcol, dalpha);
+                       dim3(256), 0, st, n, static_cast<const BlendRec*>(recs), gs, dmean, dcov,
+                       dcol, dalpha);
     return hipGetLastError();
 }
 

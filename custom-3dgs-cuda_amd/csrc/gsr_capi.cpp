@@ -161,7 +161,7 @@ BwdLayout backward_layout(int n, int64_t m, int height, int width) {
     L.ctl = off;
     L.misc = take(sizeof(Misc));
     L.scanctl = take(gsr::scan_control_bytes(n));
-    L.flags = take(um);
+    L.flags = take(align_up(um, 8));  // read as 8-byte groups
     L.ctl_end = off;
     L.sums = take(36 * um);
     L.end = off;
@@ -418,11 +418,17 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
             GSR_HIP(gsr::launch_full_keys(m, ktiles, sorted_ids, depth, n, sorted_keys, st),
                     "rasterize: keys");
     }
+    uint32_t* order = (m > 0 && gsr::launch_order_enabled()) ? at<uint32_t>(sort_ws, SL.order)
+                                                               : nullptr;
+    if (order) {
+        StageTimer timer("fwd_schedule", st);
+        GSR_HIP(gsr::launch_fwd_schedule(n, height, width, tile_ranges, sorted_ids, m, recs,
+                                         at<uint32_t>(sort_ws, SL.work), order, st),
+                "rasterize: schedule");
+    }
     StageTimer timer("blend_fwd", st);
-    uint32_t* work = m > 0 ? at<uint32_t>(sort_ws, SL.work) : nullptr;
-    uint32_t* order = m > 0 ? at<uint32_t>(sort_ws, SL.order) : nullptr;
     GSR_HIP(gsr::launch_blend_fwd(n, height, width, tile_ranges, sorted_ids, m, recs, img, final_T,
-                                  n_contrib, work, order, st),
+                                  n_contrib, order, st),
             "rasterize: blend");
     return GSR_OK;
 }
@@ -474,12 +480,18 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
     uint32_t* counts = at<uint32_t>(ws, L.counts);
     uint2* rects = at<uint2>(ws, L.rects);
     uint32_t* goff = at<uint32_t>(ws, L.goff);
-    GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, at<void>(ws, L.recs), st,
-                                      height, width, counts, rects),
-            "backward: records");
-    GSR_HIP(gsr::launch_scan_counts(n, nullptr, counts, goff, &misc->total,
-                                    at<void>(ws, L.scanctl), &misc->err, st),
-            "backward: slot layout");
+    {
+        StageTimer timer("bwd_records", st);
+        GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, at<void>(ws, L.recs),
+                                          st, height, width, counts, rects),
+                "backward: records");
+    }
+    {
+        StageTimer timer("bwd_slots", st);
+        GSR_HIP(gsr::launch_scan_counts(n, nullptr, counts, goff, &misc->total,
+                                        at<void>(ws, L.scanctl), &misc->err, st),
+                "backward: slot layout");
+    }
     gsr::GradSlots gs;
     gs.goff = goff;
     gs.counts = counts;
@@ -487,12 +499,22 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
     gs.sums = at<float>(ws, L.sums);
     gs.flags = at<uint8_t>(ws, L.flags);
     gs.slots = (uint64_t)num_pairs;
-    StageTimer timer("blend_bwd", st);
-    GSR_HIP(gsr::launch_blend_bwd(n, height, width, grad_img, tile_ranges, sorted_ids,
-                                  (uint64_t)num_pairs, at<void>(ws, L.recs), final_T, n_contrib,
-                                  d_mean2d, d_cov2d, d_colors, d_alpha, gs,
-                                  at<uint32_t>(ws, L.work), at<uint32_t>(ws, L.order), st),
-            "backward: blend");
+    uint32_t* order = gsr::launch_order_enabled() ? at<uint32_t>(ws, L.order) : nullptr;
+    if (order) {
+        StageTimer timer("bwd_schedule", st);
+        GSR_HIP(gsr::launch_bwd_schedule(height, width, tile_ranges, (uint64_t)num_pairs, n_contrib,
+                                         at<uint32_t>(ws, L.work), order, st),
+                "backward: schedule");
+    }
+    {
+        StageTimer timer("blend_bwd", st);
+        GSR_HIP(gsr::launch_blend_bwd(n, height, width, grad_img, tile_ranges, sorted_ids,
+                                      (uint64_t)num_pairs, at<void>(ws, L.recs), final_T,
+                                      n_contrib, d_mean2d, d_cov2d, d_colors, d_alpha, gs, order,
+                                      st),
+                "backward: blend");
+    }
+    StageTimer timer("grad_reduce", st);
     GSR_HIP(gsr::launch_pair_grad_reduce(n, at<void>(ws, L.recs), gs, d_mean2d, d_cov2d, d_colors,
                                          d_alpha, st),
             "backward: gradient sums");
@@ -563,6 +585,15 @@ int gsr_profile_get(const char* stage, int64_t* count, double* total_ms) {
     *count = it == P.acc.end() ? 0 : it->second.first;
     *total_ms = it == P.acc.end() ? 0.0 : it->second.second;
     return GSR_OK;
+}
+
+const char* gsr_profile_stage(int index) {
+    ProfState& P = prof();
+    std::lock_guard<std::mutex> lk(P.mu);
+    if (index < 0 || index >= (int)P.acc.size()) return nullptr;
+    auto it = P.acc.begin();
+    std::advance(it, index);
+    return it->first.c_str();
 }
 
 void gsr_profile_reset(void) {

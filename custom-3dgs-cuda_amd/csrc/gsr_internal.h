@@ -122,8 +122,6 @@ hipError_t launch_full_keys(uint64_t m, const uint32_t* sorted_tiles, const int3
                             const float* depth, int n, uint64_t* keys, hipStream_t st);
 
 // ---- blend ----
-// order (T entries, optional) receives the tiles' launch order, longest
-// estimated work first; work (T entries) holds the per-tile estimates.
 // With counts/rects (the backward) also the tile rectangle and count per
 // Gaussian, as the binning forms them.
 hipError_t launch_blend_records(int n, const float* mean2d, const float* cov2d,
@@ -131,10 +129,22 @@ hipError_t launch_blend_records(int n, const float* mean2d, const float* cov2d,
                                 hipStream_t st, int H = 0, int W = 0, uint32_t* counts = nullptr,
                                 uint2* rects = nullptr);
 
+// Whether the blends take their tiles in a longest-first order (on unless
+// GSR_TILE_ORDER=0).
+bool launch_order_enabled();
+// Forward schedule: per-tile work estimates (work, T entries) and the launch
+// order (order, T entries).
+hipError_t launch_fwd_schedule(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
+                               uint64_t m, const void* recs, uint32_t* work, uint32_t* order,
+                               hipStream_t st);
 hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
                             uint64_t m, const void* recs, float* img, float* finalT,
-                            int32_t* ncontrib, uint32_t* work, uint32_t* order,
-                            hipStream_t st);
+                            int32_t* ncontrib, const uint32_t* order, hipStream_t st);
+
+// Backward schedule: entries up to each tile's largest n_contrib, then the order.
+hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num_pairs,
+                               const int32_t* ncontrib, uint32_t* work, uint32_t* order,
+                               hipStream_t st);
 
 // Gradient slots: the (Gaussian, tile) pairs in Gaussian-major order, pair
 // (g, t) at goff[g] + its index in g's tile rectangle (row-major); the backward
@@ -155,7 +165,7 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_
                             const int32_t* ids, uint64_t num_pairs, const void* recs,
                             const float* finalT, const int32_t* ncontrib, float* dmean,
                             float* dcov, float* dcol, float* dalpha, const GradSlots& gs,
-                            uint32_t* work, uint32_t* order, hipStream_t st);
+                            const uint32_t* order, hipStream_t st);
 
 // outputs += the per-Gaussian sums of the flagged slots (conic gradient
 // converted to the covariance gradient after the sum).

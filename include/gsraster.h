@@ -118,12 +118,15 @@ int gsr_project_backward(int n, const float* d_mean2d, const float* d_cov2d, con
 /* Stage timing (no counterpart in the reference; for benchmarks).  While
  * enabled, each entry point records a pair of HIP events on its stream around
  * its stage's kernels: "project", "sh", "bin_count", "depth_sort", "scan",
- * "records", "emit", "tile_sort", "ranges", "blend_fwd", "blend_bwd",
+ * "records", "tile_sort", "ranges", "fwd_schedule", "blend_fwd",
+ * "bwd_records", "bwd_slots", "bwd_schedule", "blend_bwd", "grad_reduce",
  * "sh_bwd", "project_bwd".  gsr_profile_collect waits for the recorded events
- * and adds their durations to per-stage totals read by gsr_profile_get. */
+ * and adds their durations to per-stage totals read by gsr_profile_get;
+ * gsr_profile_stage(i) names the i-th stage with a total (NULL past the end). */
 void gsr_profile_enable(int on);
 int gsr_profile_collect(void);
 int gsr_profile_get(const char* stage, int64_t* count, double* total_ms);
+const char* gsr_profile_stage(int index);
 void gsr_profile_reset(void);
 
 #ifdef __cplusplus
