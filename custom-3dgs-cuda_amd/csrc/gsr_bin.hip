@@ -171,15 +171,16 @@ __global__ __launch_bounds__(kThreads) void partition_starts_kernel(
 // sorted tile keys; tiles without pairs keep the zeros written before.
 __global__ __launch_bounds__(kThreads) void tile_ranges_kernel(uint64_t m, uint32_t T,
                                                                const uint32_t* __restrict__ tiles,
+                                                               int shift,
                                                                int32_t* __restrict__ ranges) {
     const uint64_t i = (uint64_t)blockIdx.x * kThreads + threadIdx.x;
     if (i >= m) return;
-    const uint32_t cur = tiles[i];
-    if (cur >= T || (i > 0 && tiles[i - 1] >= T)) return;  // keys come from [0, T)
+    const uint32_t cur = tiles[i] >> shift;
+    if (cur >= T || (i > 0 && (tiles[i - 1] >> shift) >= T)) return;  // keys come from [0, T)
     if (i == 0) {
         ranges[2 * (size_t)cur] = 0;
     } else {
-        const uint32_t prev = tiles[i - 1];
+        const uint32_t prev = tiles[i - 1] >> shift;
         if (cur != prev) {
             ranges[2 * (size_t)prev + 1] = (int32_t)i;
             ranges[2 * (size_t)cur] = (int32_t)i;
@@ -190,6 +191,7 @@ __global__ __launch_bounds__(kThreads) void tile_ranges_kernel(uint64_t m, uint3
 
 __global__ __launch_bounds__(kThreads) void full_keys_kernel(uint64_t m,
                                                              const uint32_t* __restrict__ tiles,
+                                                             int shift,
                                                              const int32_t* __restrict__ ids,
                                                              const float* __restrict__ depth,
                                                              int n, uint64_t* __restrict__ keys) {
@@ -197,7 +199,7 @@ __global__ __launch_bounds__(kThreads) void full_keys_kernel(uint64_t m,
     if (i >= m) return;
     const int g = ids[i];
     const uint32_t dbits = (g >= 0 && g < n) ? __float_as_uint(depth[g]) : 0xffffffffu;
-    keys[i] = ((uint64_t)tiles[i] << 32) | (uint64_t)dbits;
+    keys[i] = ((uint64_t)(tiles[i] >> shift) << 32) | (uint64_t)dbits;
 }
 
 // Threshold on q = d^T conic d above which o * exp(-q/2) < 1/255, so alpha
@@ -269,19 +271,20 @@ hipError_t launch_partition_starts(int n, const uint32_t* perm, const uint32_t* 
     return hipGetLastError();
 }
 
-hipError_t launch_tile_ranges(uint64_t m, uint32_t T, const uint32_t* sorted_tiles,
+hipError_t launch_tile_ranges(uint64_t m, uint32_t T, const uint32_t* sorted_tiles, int shift,
                               int32_t* ranges, hipStream_t st) {
     if (m == 0) return hipSuccess;
     hipLaunchKernelGGL(tile_ranges_kernel, dim3(blocks_for(m)), dim3(kThreads), 0, st, m, T,
-                       sorted_tiles, ranges);
+                       sorted_tiles, shift, ranges);
     return hipGetLastError();
 }
 
-hipError_t launch_full_keys(uint64_t m, const uint32_t* sorted_tiles, const int32_t* ids,
-                            const float* depth, int n, uint64_t* keys, hipStream_t st) {
+hipError_t launch_full_keys(uint64_t m, const uint32_t* sorted_tiles, int shift,
+                            const int32_t* ids, const float* depth, int n, uint64_t* keys,
+                            hipStream_t st) {
     if (m == 0) return hipSuccess;
     hipLaunchKernelGGL(full_keys_kernel, dim3(blocks_for(m)), dim3(kThreads), 0, st, m,
-                       sorted_tiles, ids, depth, n, keys);
+                       sorted_tiles, shift, ids, depth, n, keys);
     return hipGetLastError();
 }
 

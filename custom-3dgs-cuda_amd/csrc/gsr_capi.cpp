@@ -62,6 +62,10 @@ int tile_passes(int64_t T) {
 }
 constexpr int kMaxTilePasses = 4;
 
+// Bits of a Gaussian id in the packed tile-sort word, or 0 for the two-word
+// form (tile and id do not fit in 32 bits together, or GSR_PACKED_SORT=0).
+int packed_id_bits(int n, int64_t T);
+
 // Significant bits of tile ids in [0, T).
 int tile_key_bits(int64_t T) {
     int bits = 0;
@@ -242,6 +246,17 @@ class StageTimer {
     bool active_ = false;
 };
 
+int packed_id_bits(int n, int64_t T) {
+    static const bool off = [] {
+        const char* v = std::getenv("GSR_PACKED_SORT");
+        return v && v[0] == '0';
+    }();
+    if (off) return 0;
+    int gb = 0;
+    for (uint32_t v = (uint32_t)(n > 1 ? n - 1 : 1); v; v >>= 1) ++gb;
+    return gb + tile_key_bits(T) <= 32 ? gb : 0;
+}
+
 int check_screen(int height, int width) {
     GSR_REQUIRE(height >= 0 && width >= 0, "height and width must be non-negative");
     GSR_REQUIRE(tiles_x_of(width) < 65536 && tiles_y_of(height) < 65536,
@@ -388,6 +403,8 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
         uint32_t* tk1 = at<uint32_t>(sort_ws, SL.tk1);
         uint32_t* ids = reinterpret_cast<uint32_t*>(sorted_ids);
         uint32_t* ktiles = ((passes - 1) % 2 == 0) ? tk0 : tk1;  // the last pass's keys
+        // one packed word per pair when tile and Gaussian id fit in 32 bits
+        const int gbits = packed_id_bits(n, T);
         {
             StageTimer timer("tile_sort", st);
             uint32_t* part_rank = at<uint32_t>(sort_ws, SL.part_rank);
@@ -402,7 +419,7 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
             GSR_HIP(gsr::launch_partition_starts(n, es.perm, es.counts, es.offsets, m, part_rank,
                                                  st),
                     "rasterize: partition starts");
-            GSR_HIP(gsr::launch_tile_sort(es, m, passes, tile_key_bits(T),
+            GSR_HIP(gsr::launch_tile_sort(es, m, passes, tile_key_bits(T), gbits,
                                           at<uint32_t>(bin_ws, BL.tilehist),
                                           at<void>(sort_ws, SL.ctl), tk0, tk1,
                                           at<uint32_t>(sort_ws, SL.vbuf), ids, ktiles,
@@ -411,11 +428,11 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
         }
         {
             StageTimer timer("ranges", st);
-            GSR_HIP(gsr::launch_tile_ranges(m, (uint32_t)T, ktiles, tile_ranges, st),
+            GSR_HIP(gsr::launch_tile_ranges(m, (uint32_t)T, ktiles, gbits, tile_ranges, st),
                     "rasterize: ranges");
         }
         if (sorted_keys)
-            GSR_HIP(gsr::launch_full_keys(m, ktiles, sorted_ids, depth, n, sorted_keys, st),
+            GSR_HIP(gsr::launch_full_keys(m, ktiles, gbits, sorted_ids, depth, n, sorted_keys, st),
                     "rasterize: keys");
     }
     uint32_t* order = (m > 0 && gsr::launch_order_enabled()) ? at<uint32_t>(sort_ws, SL.order)

@@ -86,10 +86,12 @@ size_t onesweep_state_bytes(uint64_t n, int passes);
 // hist holds the passes' global digit histograms ([passes][256], from the
 // tile rectangles).  Values (Gaussian ids) end in out_vals; keys (tile ids)
 // in out_keys when it is not null.  k0/k1/vbuf are m-element scratch.
+// gbits > 0: the packed form, one word (tile << gbits) | Gaussian id per pair
+// (gbits + key_bits <= 32); out_keys then receives the sorted words.
 hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, int key_bits,
-                            const uint32_t* hist, void* state, uint32_t* k0, uint32_t* k1,
-                            uint32_t* vbuf, uint32_t* out_vals, uint32_t* out_keys, int* err,
-                            hipStream_t st);
+                            int gbits, const uint32_t* hist, void* state, uint32_t* k0,
+                            uint32_t* k1, uint32_t* vbuf, uint32_t* out_vals, uint32_t* out_keys,
+                            int* err, hipStream_t st);
 
 // ---- binning ----
 // counts[g], packed tile rect, depth key (float bits or 0xffffffff when the
@@ -113,13 +115,15 @@ hipError_t launch_partition_starts(int n, const uint32_t* perm, const uint32_t* 
                                    const uint32_t* offsets, uint64_t m, uint32_t* part_rank,
                                    hipStream_t st);
 
-// [start, end) per tile from sorted tile keys; ranges must be zeroed.
-hipError_t launch_tile_ranges(uint64_t m, uint32_t T, const uint32_t* sorted_tiles,
+// [start, end) per tile from sorted tile keys (tile = key >> shift); ranges
+// must be zeroed.
+hipError_t launch_tile_ranges(uint64_t m, uint32_t T, const uint32_t* sorted_tiles, int shift,
                               int32_t* ranges, hipStream_t st);
 
 // Optional debug output: (tile << 32) | float_bits(depth[id]).
-hipError_t launch_full_keys(uint64_t m, const uint32_t* sorted_tiles, const int32_t* ids,
-                            const float* depth, int n, uint64_t* keys, hipStream_t st);
+hipError_t launch_full_keys(uint64_t m, const uint32_t* sorted_tiles, int shift,
+                            const int32_t* ids, const float* depth, int n, uint64_t* keys,
+                            hipStream_t st);
 
 // ---- blend ----
 // With counts/rects (the backward) also the tile rectangle and count per

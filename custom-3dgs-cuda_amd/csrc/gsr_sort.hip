@@ -118,7 +118,8 @@ __global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restr
 __device__ __forceinline__ int pad16(int slot) { return slot + (slot >> 4); }
 
 // Expands the (tile, Gaussian) pairs of sort slots [base, base + nvalid) into
-// s_keys / s_vals at pad16(slot).  Pair slots are laid out by depth rank r at
+// s_keys / s_vals at pad16(slot) (kPacked: the one word (tile << gbits) | g in
+// s_keys).  Pair slots are laid out by depth rank r at
 // offsets[r] (ty outer, tx inner over the rank's tile rectangle), the order in
 // which the reference emits keys per Gaussian (rasterize.cu:124-135).  Ranks
 // r_lo..r_lo+nr-1 overlap the partition; the first kStageRanks of them have
@@ -136,9 +137,10 @@ struct RankStage {
 };
 static_assert(sizeof(RankStage) == kSortPartition * 4, "fits the aux region");
 
+template <bool kPacked>
 __device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base, int nvalid,
                                              uint32_t* s_keys, uint32_t* s_vals,
-                                             RankStage* st) {
+                                             RankStage* st, int gbits) {
     const int tid = threadIdx.x;
     const uint32_t part = (uint32_t)(base / kSortPartition);
     const uint32_t r_lo = es.part_rank[part];
@@ -199,8 +201,13 @@ __device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base
                 row = 0;
                 col = 0;
             }
-            s_keys[pad16(slot)] = (y0 + row) * (uint32_t)es.tiles_x + x0 + col;
-            s_vals[pad16(slot)] = g;
+            const uint32_t tile = (y0 + row) * (uint32_t)es.tiles_x + x0 + col;
+            if constexpr (kPacked) {
+                s_keys[pad16(slot)] = (tile << gbits) | g;
+            } else {
+                s_keys[pad16(slot)] = tile;
+                s_vals[pad16(slot)] = g;
+            }
             if (++col == w) {
                 col = 0;
                 ++row;
@@ -212,19 +219,21 @@ __device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base
 
 // One LSD pass over 8-bit digit (key >> shift) & 0xff.  kEmit: the partition's
 // (tile, Gaussian) pairs are generated from the depth order instead of being
-// read (the first tile pass).  kWriteKeys: store keys as well as values (the
-// final pass only needs the values unless a caller asked for the keys).
-template <bool kEmit, bool kWriteKeys>
+// read (the first tile pass).  kPacked: each element is the one word
+// (tile << gbits) | Gaussian id, sorted on its tile bits; kout receives the
+// words and, when vout is not null (the last pass), vout the Gaussian ids.
+// Otherwise keys and values are separate words, both written.
+template <bool kEmit, bool kPacked>
 __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n, int shift,
     int digit_bits, const uint32_t* __restrict__ hist, uint64_t* __restrict__ status,
-    uint32_t* __restrict__ counter, int* __restrict__ err, EmitSource es) {
+    uint32_t* __restrict__ counter, int* __restrict__ err, EmitSource es, int gbits) {
     // s_aux holds the emission's staged offsets first, then the digit counters,
     // digit starts and global bases (7 KB).
     constexpr int kAuxWords = kEmit ? kSortPartition : 7 * kRadixBins;
     __shared__ uint32_t s_keys[kSortPartition + kSortPartition / 16];
-    __shared__ uint32_t s_vals[kSortPartition + kSortPartition / 16];
+    __shared__ uint32_t s_vals[kPacked ? 1 : kSortPartition + kSortPartition / 16];
     __shared__ __align__(16) uint32_t s_aux[kAuxWords];
     __shared__ uint32_t s_scan[4];
     __shared__ uint32_t s_hscan[4];
@@ -241,15 +250,16 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     const int nvalid = (int)min((uint64_t)kSortPartition, n - base);
 
     uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
+    (void)val;
     if constexpr (kEmit) {
-        expand_pairs(es, base, nvalid, s_keys, s_vals,
-                     reinterpret_cast<RankStage*>(s_aux));  // ends with a barrier
+        expand_pairs<kPacked>(es, base, nvalid, s_keys, s_vals,
+                              reinterpret_cast<RankStage*>(s_aux), gbits);  // ends with a barrier
 #pragma unroll
         for (int i = 0; i < kSortItems; ++i) {
             const int e = wave * (kSortItems * 64) + i * 64 + lane;
             const bool v = e < nvalid;
             key[i] = v ? s_keys[pad16(e)] : 0u;
-            val[i] = v ? s_vals[pad16(e)] : 0u;
+            if constexpr (!kPacked) val[i] = v ? s_vals[pad16(e)] : 0u;
         }
     } else {
 #pragma unroll
@@ -257,7 +267,7 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
             const int e = wave * (kSortItems * 64) + i * 64 + lane;
             const bool v = e < nvalid;
             key[i] = v ? kin[base + e] : 0u;
-            val[i] = v ? vin[base + e] : 0u;
+            if constexpr (!kPacked) val[i] = v ? vin[base + e] : 0u;
         }
     }
     for (int j = tid; j < 4 * kRadixBins; j += kSortThreads) (&s_wcnt[0][0])[j] = 0;
@@ -315,7 +325,7 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
             const uint32_t dd = (key[i] >> shift) & 0xffu;
             const uint32_t pos = s_dstart[dd] + s_wcnt[wave][dd] + rank[i];
             s_keys[pos] = key[i];
-            s_vals[pos] = val[i];
+            if constexpr (!kPacked) s_vals[pos] = val[i];
         }
     }
 
@@ -361,8 +371,13 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
         const uint32_t k = s_keys[j];
         const uint64_t o = s_gbase[(k >> shift) & 0xffu] + (uint64_t)j;
         if (o < n) {  // always true for consistent histograms; guards the stores
-            if constexpr (kWriteKeys) kout[o] = k;
-            vout[o] = s_vals[j];
+            if constexpr (kPacked) {
+                kout[o] = k;
+                if (vout) vout[o] = k & ((1u << gbits) - 1u);
+            } else {
+                kout[o] = k;
+                vout[o] = s_vals[j];
+            }
         }
     }
 }
@@ -478,10 +493,10 @@ hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t*
     }
     uint32_t *ki = k0, *vi = v0, *ko = k1, *vo = v1;
     for (int p = 0; p < passes; ++p) {
-        hipLaunchKernelGGL((onesweep_kernel<false, true>), dim3((unsigned)parts),
+        hipLaunchKernelGGL((onesweep_kernel<false, false>), dim3((unsigned)parts),
                            dim3(kSortThreads), 0, st, ki, vi, ko, vo, n, begin_bit + 8 * p, 8,
                            c.hist + p * kRadixBins, c.status + (size_t)p * parts * kRadixBins,
-                           c.counters + p * 16, err, EmitSource{});
+                           c.counters + p * 16, err, EmitSource{}, 0);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         std::swap(ki, ko);
@@ -495,45 +510,48 @@ size_t onesweep_state_bytes(uint64_t n, int passes) {
 }
 
 hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, int key_bits,
-                            const uint32_t* hist, void* state, uint32_t* k0, uint32_t* k1,
-                            uint32_t* vbuf, uint32_t* out_vals, uint32_t* out_keys, int* err,
-                            hipStream_t st) {
+                            int gbits, const uint32_t* hist, void* state, uint32_t* k0,
+                            uint32_t* k1, uint32_t* vbuf, uint32_t* out_vals, uint32_t* out_keys,
+                            int* err, hipStream_t st) {
     if (m == 0) return hipSuccess;
-    if (passes < 1 || passes > 4) return hipErrorInvalidValue;
+    if (passes < 1 || passes > 4 || !out_keys) return hipErrorInvalidValue;
+    const bool packed = gbits > 0;
+    if (packed && gbits + key_bits > 32) return hipErrorInvalidValue;
     const uint64_t parts = parts_for(m);
     uint32_t* counters = static_cast<uint32_t*>(state);
     uint64_t* status = reinterpret_cast<uint64_t*>(static_cast<char*>(state) +
                                                    align_up((size_t)passes * 64, 256));
-    // values: the last pass writes out_vals; earlier passes alternate back from it
-    // keys: pass p writes keys[p & 1] and the next pass reads them
+    // keys (or packed words): pass p writes kbuf[p & 1], the last pass out_keys
+    // values (two-word form): the last pass writes out_vals, earlier passes
+    // alternate back from it
     uint32_t* kbuf[2] = {k0, k1};
-    uint32_t* vdst[4];
-    for (int p = passes - 1, flip = 0; p >= 0; --p, flip ^= 1) vdst[p] = flip ? vbuf : out_vals;
+    uint32_t* vdst[4] = {nullptr, nullptr, nullptr, nullptr};
+    if (!packed)
+        for (int p = passes - 1, flip = 0; p >= 0; --p, flip ^= 1) vdst[p] = flip ? vbuf : out_vals;
     for (int p = 0; p < passes; ++p) {
         const bool last = p == passes - 1;
         uint32_t* ko = last ? out_keys : kbuf[p & 1];
         const uint32_t* ki = p == 0 ? nullptr : kbuf[(p - 1) & 1];
-        const uint32_t* vi = p == 0 ? nullptr : vdst[p - 1];
+        const uint32_t* vi = (p == 0 || packed) ? nullptr : vdst[p - 1];
+        uint32_t* vo = packed ? (last ? out_vals : nullptr) : vdst[p];
         const dim3 grid((unsigned)parts), block(kSortThreads);
         uint64_t* stat = status + (size_t)p * parts * kRadixBins;
         const uint32_t* h = hist + p * kRadixBins;
         uint32_t* ctr = counters + p * 16;
+        const int shift = (packed ? gbits : 0) + 8 * p;
         const int bits = std::max(1, std::min(8, key_bits - 8 * p));  // significant digit bits
-        if (p == 0) {
-            if (ko)
-                hipLaunchKernelGGL((onesweep_kernel<true, true>), grid, block, 0, st, ki, vi, ko,
-                                   vdst[p], m, 8 * p, bits, h, stat, ctr, err, es);
-            else
-                hipLaunchKernelGGL((onesweep_kernel<true, false>), grid, block, 0, st, ki, vi, ko,
-                                   vdst[p], m, 8 * p, bits, h, stat, ctr, err, es);
-        } else {
-            if (ko)
-                hipLaunchKernelGGL((onesweep_kernel<false, true>), grid, block, 0, st, ki, vi, ko,
-                                   vdst[p], m, 8 * p, bits, h, stat, ctr, err, es);
-            else
-                hipLaunchKernelGGL((onesweep_kernel<false, false>), grid, block, 0, st, ki, vi,
-                                   ko, vdst[p], m, 8 * p, bits, h, stat, ctr, err, es);
-        }
+        if (p == 0 && packed)
+            hipLaunchKernelGGL((onesweep_kernel<true, true>), grid, block, 0, st, ki, vi, ko, vo,
+                               m, shift, bits, h, stat, ctr, err, es, gbits);
+        else if (p == 0)
+            hipLaunchKernelGGL((onesweep_kernel<true, false>), grid, block, 0, st, ki, vi, ko, vo,
+                               m, shift, bits, h, stat, ctr, err, es, 0);
+        else if (packed)
+            hipLaunchKernelGGL((onesweep_kernel<false, true>), grid, block, 0, st, ki, vi, ko, vo,
+                               m, shift, bits, h, stat, ctr, err, es, gbits);
+        else
+            hipLaunchKernelGGL((onesweep_kernel<false, false>), grid, block, 0, st, ki, vi, ko,
+                               vo, m, shift, bits, h, stat, ctr, err, es, 0);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }

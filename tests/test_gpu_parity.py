@@ -85,6 +85,16 @@ def test_forward_parity_bench_scene(crc, device):
     _check_forward(gpu_forward(crc, a, device), oracle_forward(a))
 
 
+def test_forward_parity_two_word_sort(crc, device):
+    """600k Gaussians at 1080p: 20 id bits + 13 tile bits exceed one 32-bit word,
+    so the tile sort carries keys and ids as separate words (the packed form is
+    what every smaller test above uses)."""
+    print("[gpu] forward parity, two-word tile sort (600k Gaussians, 1920x1080)", flush=True)
+    sc = synthetic.config_scene("c3", requires_grad=False, n=600_000, width=1920, height=1080)
+    a = scene_arrays(sc)
+    _check_forward(gpu_forward(crc, a, device), oracle_forward(a))
+
+
 @pytest.mark.parametrize("H,W", [(16, 16), (17, 33), (1, 1), (100, 7), (240, 321)])
 def test_forward_parity_odd_screens(crc, device, H, W):
     sc = synthetic.config_scene("c1", requires_grad=False, n=3000, width=W, height=H)
