@@ -57,6 +57,12 @@ void check_numel(const Tensor& t, int64_t want, const char* msg) {
     TORCH_CHECK(t.numel() >= want, msg);
 }
 
+// The kernels read quaternions and SH coefficients in 16-byte units; a
+// contiguous view that starts mid-allocation is copied to fresh storage.
+Tensor aligned16(const Tensor& t) {
+    return (reinterpret_cast<uintptr_t>(t.data_ptr()) & 15) ? t.clone() : t;
+}
+
 // ---- project (bindings.cpp:12-29 / projection.cu:109-153) ----
 std::tuple<Tensor, Tensor, Tensor> project(int total_gaussians, const Tensor mu3d,
                                            const Tensor q3d, const Tensor s3d,
@@ -80,7 +86,8 @@ std::tuple<Tensor, Tensor, Tensor> project(int total_gaussians, const Tensor mu3
     Tensor mean_2d = torch::empty({n, 2}, options);
     Tensor cov_2d = torch::empty({n, 3}, options);
     Tensor depths = torch::empty({n}, options);
-    check_rc(gsr_project(total_gaussians, cfp(mu3d), cfp(q3d), cfp(s3d), cfp(camera_rotation),
+    const Tensor q_al = aligned16(q3d);
+    check_rc(gsr_project(total_gaussians, cfp(mu3d), cfp(q_al), cfp(s3d), cfp(camera_rotation),
                          cfp(camera_translation), fx, fy, cx, cy, fp(mean_2d), fp(cov_2d),
                          fp(depths), current_stream()),
              "project");
@@ -104,8 +111,9 @@ Tensor spherical_harmonics(int total_gaussians, const Tensor camera_position,
     c10::hip::HIPGuardMasqueradingAsCUDA guard(mu_world.device());
     auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mu_world.device());
     Tensor colors = torch::empty({n, 3}, options);
+    const Tensor k_al = aligned16(illumination_coeff);
     check_rc(gsr_sh(total_gaussians, cfp(camera_position), cfp(mu_world), cfp(albedo_coeff),
-                    cfp(illumination_coeff), fp(colors), current_stream()),
+                    cfp(k_al), fp(colors), current_stream()),
              "SH");
     return colors;
 }
@@ -264,7 +272,8 @@ std::tuple<Tensor, Tensor, Tensor> backwards_SH(const Tensor colors_grad, const 
     Tensor albedo_grad = torch::empty({n, 3}, options);
     Tensor k_j_grad = torch::empty({n, 15, 3}, options);
     Tensor mu_grad = torch::empty({n, 3}, options);
-    check_rc(gsr_sh_backward((int)n, cfp(colors_grad), cfp(mu), cfp(albedo), cfp(k_j),
+    const Tensor k_al = aligned16(k_j);
+    check_rc(gsr_sh_backward((int)n, cfp(colors_grad), cfp(mu), cfp(albedo), cfp(k_al),
                              cfp(camera_position), fp(albedo_grad), fp(k_j_grad), fp(mu_grad),
                              current_stream()),
              "backwards_SH");
@@ -295,7 +304,8 @@ std::tuple<Tensor, Tensor, Tensor> backwards_projection(
     Tensor mu_grad = torch::empty({n, 3}, options);
     Tensor q_grad = torch::empty({n, 4}, options);
     Tensor s_grad = torch::empty({n, 3}, options);
-    check_rc(gsr_project_backward((int)n, cfp(mean_2d_grad), cfp(cov_2d_grad), cfp(mu), cfp(q),
+    const Tensor q_al = aligned16(q);
+    check_rc(gsr_project_backward((int)n, cfp(mean_2d_grad), cfp(cov_2d_grad), cfp(mu), cfp(q_al),
                                   cfp(s), cfp(camera_rotation), cfp(camera_translation), fx, fy,
                                   cx, cy, fp(mu_grad), fp(q_grad), fp(s_grad), current_stream()),
              "backwards_projection");

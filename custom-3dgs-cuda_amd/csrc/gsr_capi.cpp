@@ -291,6 +291,7 @@ int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, co
     GSR_REQUIRE(n >= 0, "n must be non-negative");
     if (n == 0) return GSR_OK;
     GSR_REQUIRE(cam_pos && mu && albedo && k_j && colors, "null pointer");
+    GSR_REQUIRE(((uintptr_t)k_j & 15) == 0, "k_j must be 16-byte aligned");
     StageTimer timer("sh", as_stream(stream));
     GSR_HIP(gsr::launch_sh_fwd(n, cam_pos, mu, albedo, k_j, colors, as_stream(stream)), "SH");
     return GSR_OK;
@@ -545,6 +546,8 @@ int gsr_sh_backward(int n, const float* colors_grad, const float* mu, const floa
     if (n == 0) return GSR_OK;
     GSR_REQUIRE(colors_grad && mu && albedo && k_j && cam_pos && d_albedo && d_k_j && d_mu,
                 "null pointer");
+    GSR_REQUIRE(((uintptr_t)k_j & 15) == 0 && ((uintptr_t)d_k_j & 15) == 0,
+                "k_j and d_k_j must be 16-byte aligned");
     StageTimer timer("sh_bwd", as_stream(stream));
     GSR_HIP(gsr::launch_sh_bwd(n, colors_grad, mu, albedo, k_j, cam_pos, d_albedo, d_k_j, d_mu,
                                as_stream(stream)),

@@ -1,8 +1,9 @@
-// gsr_sh.hip — degree-3 SH colour forward (a2) and backward (a11), one thread
-// per Gaussian.  The 45 coefficients of a Gaussian are 180 contiguous bytes;
-// a work-group stages its 256 x 45 floats through LDS with coalesced
-// dword loads (and stages dk_j the same way on the way out), so every HBM
-// access of the dominant stream is a full, contiguous wave transaction.
+// gsr_sh.hip — degree-3 SH colour forward and backward, one thread per
+// Gaussian, one wave per work-group.  The 45 coefficients of a Gaussian are
+// 180 contiguous bytes; a work-group's 64 x 45 floats (11.25 KB, 16-byte
+// aligned) are staged through LDS with coalesced 16-byte loads (and dk_j
+// leaves the same way), so every HBM access of the dominant stream is a full,
+// contiguous transaction and many work-groups per CU keep loads in flight.
 // HBM bytes per Gaussian: 216 forward, 420 backward.
 #include "gsr_internal.h"
 #include "gsr_math.h"
@@ -11,16 +12,33 @@ namespace gsr {
 
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 64;
 constexpr int kCoef = 45;  // 15 x 3 band-1..3 coefficients per Gaussian
 
-// Copy floats [base*45, base*45 + cnt*45) of src into LDS, coalesced.
+// Copy floats [base*45, base*45 + cnt*45) of src into LDS: 16-byte chunks
+// (base is a multiple of 64, so the block's span starts 16-byte aligned),
+// then the remainder singly.
 __device__ __forceinline__ void stage_coeffs(float* __restrict__ lds,
                                              const float* __restrict__ src, size_t base,
                                              int cnt) {
-    const int total = cnt * kCoef;
-    const float* g = src + base * kCoef;
-    for (int j = threadIdx.x; j < total; j += kThreads) lds[j] = g[j];
+    const int total = cnt * kCoef, total4 = total / 4;
+    const float4* g4 = reinterpret_cast<const float4*>(src + base * kCoef);
+    float4* l4 = reinterpret_cast<float4*>(lds);
+#pragma unroll 4
+    for (int j = threadIdx.x; j < total4; j += kThreads) l4[j] = g4[j];
+    for (int j = total4 * 4 + threadIdx.x; j < total; j += kThreads) lds[j] = src[base * kCoef + j];
+}
+
+// The reverse: LDS floats [0, cnt*45) to dst[base*45 ..].
+__device__ __forceinline__ void unstage_coeffs(float* __restrict__ dst,
+                                               const float* __restrict__ lds, size_t base,
+                                               int cnt) {
+    const int total = cnt * kCoef, total4 = total / 4;
+    float4* g4 = reinterpret_cast<float4*>(dst + base * kCoef);
+    const float4* l4 = reinterpret_cast<const float4*>(lds);
+#pragma unroll 4
+    for (int j = threadIdx.x; j < total4; j += kThreads) g4[j] = l4[j];
+    for (int j = total4 * 4 + threadIdx.x; j < total; j += kThreads) dst[base * kCoef + j] = lds[j];
 }
 
 // SH.cu:57-93.  dir = glm::normalize(mu - cam) = v * (1 / sqrt(dot(v, v))).
@@ -29,7 +47,7 @@ __global__ __launch_bounds__(kThreads) void sh_fwd_kernel(int n, const float* __
                                                           const float* __restrict__ albedo,
                                                           const float* __restrict__ kj,
                                                           float* __restrict__ colors) {
-    __shared__ float s_k[kThreads * kCoef];
+    __shared__ __align__(16) float s_k[kThreads * kCoef];
     const size_t base = (size_t)blockIdx.x * kThreads;
     const int cnt = (int)min((size_t)kThreads, (size_t)n - base);
     stage_coeffs(s_k, kj, base, cnt);
@@ -61,7 +79,7 @@ __global__ __launch_bounds__(kThreads) void sh_bwd_kernel(
     int n, const float* __restrict__ cgrad, const float* __restrict__ mu,
     const float* __restrict__ albedo, const float* __restrict__ kj, const float* __restrict__ cam,
     float* __restrict__ dA, float* __restrict__ dkj, float* __restrict__ dmu) {
-    __shared__ float s_k[kThreads * kCoef];
+    __shared__ __align__(16) float s_k[kThreads * kCoef];
     const size_t base = (size_t)blockIdx.x * kThreads;
     const int cnt = (int)min((size_t)kThreads, (size_t)n - base);
     stage_coeffs(s_k, kj, base, cnt);
@@ -139,9 +157,7 @@ __global__ __launch_bounds__(kThreads) void sh_bwd_kernel(
         dmu[3 * i + 2] = inv * (gz - z * ddot);
     }
     __syncthreads();
-    const int total = cnt * kCoef;
-    float* out = dkj + base * kCoef;
-    for (int j = threadIdx.x; j < total; j += kThreads) out[j] = s_k[j];
+    unstage_coeffs(dkj, s_k, base, cnt);
 }
 
 inline int blocks_for(int n) { return (n + kThreads - 1) / kThreads; }

@@ -48,7 +48,7 @@ int gsr_project(int n, const float* mu, const float* q, const float* s, const fl
 /* Replaces launch_spherical_harmonics_kernel (csrc/forward/SH.h:4,
  * csrc/forward/SH.cu:95-131; bound as `SH` at csrc/bindings.cpp:32-46,143).
  * cam_pos is a device pointer to 3 floats (the reference copies it to the
- * host first). */
+ * host first).  k_j [N,15,3] must be 16-byte aligned. */
 int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, const float* k_j,
            float* colors, void* stream);
 
@@ -98,7 +98,8 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
 
 /* Replaces launch_backward_SH (csrc/backward/delight_backward.h:5,
  * csrc/backward/delight_backward.cu:176-218; bound as `backwards_SH` at
- * csrc/bindings.cpp:102-116,148).  cam_pos is a device pointer. */
+ * csrc/bindings.cpp:102-116,148).  cam_pos is a device pointer; k_j and d_k_j
+ * must be 16-byte aligned. */
 int gsr_sh_backward(int n, const float* colors_grad, const float* mu, const float* albedo,
                     const float* k_j, const float* cam_pos, float* d_albedo, float* d_k_j,
                     float* d_mu, void* stream);

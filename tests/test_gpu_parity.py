@@ -135,6 +135,31 @@ def test_sh_bitwise(crc, device):
     assert_bitwise(_np(got), want, "colors")
 
 
+def test_unaligned_views_are_accepted(crc, device):
+    """Contiguous views that start 4 bytes into their storage (the reference
+    accepts them): quaternions and SH coefficients are realigned internally."""
+    rng = np.random.default_rng(11)
+    n = 1000
+    mu = rng.normal(size=(n, 3)).astype(np.float32)
+    mu[:, 2] += 5.0
+    q = rng.normal(size=(n, 4)).astype(np.float32)
+    s = rng.uniform(-4, -2, (n, 3)).astype(np.float32)
+    R, t = np.eye(3, dtype=np.float32), np.zeros(3, np.float32)
+    qbig = _dev(np.r_[np.zeros(1, np.float32), q.ravel()], device)[1:].view(n, 4)
+    assert qbig.data_ptr() % 16 == 4
+    got = crc.project(n, _dev(mu, device), qbig, _dev(s, device), _dev(R, device), _dev(t, device),
+                      300.0, 300.0, 64.0, 48.0)
+    want = orc.project(mu, q, s, R, t, 300.0, 300.0, 64.0, 48.0)
+    for g, w_, nm in zip(got, want, ("mean2d", "cov2d", "depth")):
+        assert_bitwise(_np(g), w_, nm)
+    A = rng.uniform(0, 1, (n, 3)).astype(np.float32)
+    kj = rng.normal(0, 0.2, (n, 15, 3)).astype(np.float32)
+    cam = np.array([0.1, 0.2, -1.0], np.float32)
+    kbig = _dev(np.r_[np.zeros(1, np.float32), kj.ravel()], device)[1:].view(n, 15, 3)
+    got = crc.SH(n, _dev(cam, device), _dev(mu, device), _dev(A, device), kbig)
+    assert_bitwise(_np(got), orc.sh(cam, mu, A, kj), "colors")
+
+
 def test_empty_frames(crc, device):
     f = lambda *s: torch.zeros(*s, device=device)
     img, ids, ranges, fT, nc = crc.rasterize(0, f(0), f(0, 2), f(0, 3), f(0, 3), f(0), 40, 50)
