@@ -94,6 +94,31 @@ std::tuple<Tensor, Tensor, Tensor> project(int total_gaussians, const Tensor mu3
     return {mean_2d, cov_2d, depths};
 }
 
+// ---- glue helpers (no counterpart in the reference's module; used by the
+// autograd glue in place of its torch ops, rasterize.py:43-53) ----
+Tensor screen_radii(const Tensor cov_2d) {
+    CHECK_INPUT_FP32(cov_2d);
+    TORCH_CHECK(cov_2d.dim() == 2 && cov_2d.size(1) == 3, "cov_2d must have shape (N, 3)");
+    const int64_t n = cov_2d.size(0);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(cov_2d.device());
+    Tensor radii = torch::empty({n}, cov_2d.options());
+    check_rc(gsr_screen_radii((int)n, cfp(cov_2d), fp(radii), current_stream()), "screen_radii");
+    return radii;
+}
+
+Tensor camera_position(const Tensor camera_rotation, const Tensor camera_translation) {
+    CHECK_INPUT_FP32(camera_rotation);
+    CHECK_INPUT_FP32(camera_translation);
+    check_numel(camera_rotation, 9, "camera_rotation must hold 3 x 3 values");
+    check_numel(camera_translation, 3, "camera_translation must hold 3 values");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(camera_rotation.device());
+    Tensor cam = torch::empty({3}, camera_rotation.options());
+    check_rc(gsr_camera_position(cfp(camera_rotation), cfp(camera_translation), fp(cam),
+                                 current_stream()),
+             "camera_position");
+    return cam;
+}
+
 // ---- SH (bindings.cpp:32-46 / SH.cu:95-131) ----
 Tensor spherical_harmonics(int total_gaussians, const Tensor camera_position,
                            const Tensor mu_world, const Tensor albedo_coeff,
@@ -328,6 +353,8 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     m.def("rasterize_with_keys", &rasterize_with_keys,
           "rasterize, also returning the sorted 64-bit keys (tile << 32 | depth bits)");
     m.def("library_version", []() { return std::string(gsr_version()); });
+    m.def("screen_radii", &screen_radii, "glue: approximate screen radii (one kernel)");
+    m.def("camera_position", &camera_position, "glue: camera position -R^T t (one kernel)");
     // Stage timing of libgsraster (HIP events on the launch stream); not part of
     // the reference surface.
     m.def("profile_enable", [](bool on) { gsr_profile_enable(on ? 1 : 0); });

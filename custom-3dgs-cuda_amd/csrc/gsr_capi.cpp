@@ -286,6 +286,21 @@ int gsr_project(int n, const float* mu, const float* q, const float* s, const fl
     return GSR_OK;
 }
 
+int gsr_screen_radii(int n, const float* cov2d, float* radii, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(cov2d && radii, "null pointer");
+    GSR_HIP(gsr::launch_screen_radii(n, cov2d, radii, as_stream(stream)), "screen radii");
+    return GSR_OK;
+}
+
+int gsr_camera_position(const float* rot, const float* trans, float* cam_pos, void* stream) {
+    GSR_REQUIRE(rot && trans && cam_pos, "null pointer");
+    GSR_HIP(gsr::launch_camera_position(rot, trans, cam_pos, as_stream(stream)),
+            "camera position");
+    return GSR_OK;
+}
+
 int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, const float* k_j,
            float* colors, void* stream) {
     GSR_REQUIRE(n >= 0, "n must be non-negative");

@@ -14,6 +14,9 @@ hipError_t launch_project_fwd(int n, const float* mu, const float* q, const floa
                               float cy, float* mean2d, float* cov2d, float* depth,
                               hipStream_t st);
 
+hipError_t launch_screen_radii(int n, const float* cov2d, float* radii, hipStream_t st);
+hipError_t launch_camera_position(const float* rot, const float* trans, float* cam,
+                                  hipStream_t st);
 hipError_t launch_project_bwd(int n, const float* dmean, const float* dcov, const float* mu,
                               const float* q, const float* s, const float* rot, const float* tr,
                               float fx, float fy, float* dmu, float* dq, float* ds, int ref_quat,

@@ -158,7 +158,48 @@ __global__ __launch_bounds__(kThreads) void project_bwd_kernel(
 
 inline int blocks_for(int n) { return (n + kThreads - 1) / kThreads; }
 
+// The autograd glue's screen radius for densification
+// (gaussian_splatting/rasterizer/rasterize.py:49-53), one op per rounding in
+// torch's order: mid = 0.5 (a + c); radius = mid + sqrt(clamp((0.5 (a - c))^2
+// + b b, min 0.1)); radii = 3 sqrt(clamp(radius, min 0)).  A clamp keeps NaN,
+// as torch's does.
+__global__ __launch_bounds__(256) void screen_radii_kernel(int n, const float* __restrict__ cov,
+                                                           float* __restrict__ radii) {
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    const float a = cov[3 * (size_t)i], b = cov[3 * (size_t)i + 1], c = cov[3 * (size_t)i + 2];
+    const float mid = 0.5f * (a + c);
+    const float h = 0.5f * (a - c);
+    const float q = h * h + b * b;
+    const float qc = (q < 0.1f) ? 0.1f : q;
+    const float radius = mid + __builtin_sqrtf(qc);
+    const float rc = (radius < 0.0f) ? 0.0f : radius;
+    radii[i] = 3.0f * __builtin_sqrtf(rc);
+}
+
+// cam = -R^T t (the glue's -matmul(R.T, t)), one thread.
+__global__ void camera_position_kernel(const float* __restrict__ R, const float* __restrict__ t,
+                                       float* __restrict__ cam) {
+    if (threadIdx.x != 0) return;
+#pragma unroll
+    for (int i = 0; i < 3; ++i)
+        cam[i] = -(R[i] * t[0] + R[3 + i] * t[1] + R[6 + i] * t[2]);
+}
+
 }  // namespace
+
+hipError_t launch_screen_radii(int n, const float* cov2d, float* radii, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(screen_radii_kernel, dim3((n + 255) / 256), dim3(256), 0, st, n, cov2d,
+                       radii);
+    return hipGetLastError();
+}
+
+hipError_t launch_camera_position(const float* rot, const float* trans, float* cam,
+                                  hipStream_t st) {
+    hipLaunchKernelGGL(camera_position_kernel, dim3(1), dim3(64), 0, st, rot, trans, cam);
+    return hipGetLastError();
+}
 
 hipError_t launch_project_fwd(int n, const float* mu, const float* q, const float* s,
                               const float* rot, const float* tr, float fx, float fy, float cx,

@@ -128,14 +128,15 @@ __device__ __forceinline__ int pad16(int slot) { return slot + (slot >> 4); }
 // without pairs sit between ranks with pairs, and are read from global
 // memory).  Each thread expands 16 consecutive slots: one binary search, one
 // division, then a walk that steps the column and row.
-constexpr int kStageRanks = kSortPartition / 4;
+constexpr int kStageRanks = 512;
 
 struct RankStage {
     uint32_t off[kStageRanks];
     uint32_t g[kStageRanks];
     uint2 rect[kStageRanks];
 };
-static_assert(sizeof(RankStage) == kSortPartition * 4, "fits the aux region");
+constexpr int kRankStageWords = (int)(sizeof(RankStage) / 4);
+static_assert(kRankStageWords >= 7 * kRadixBins, "the aux region also holds the digit counters");
 
 template <bool kPacked>
 __device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base, int nvalid,
@@ -231,7 +232,7 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     uint32_t* __restrict__ counter, int* __restrict__ err, EmitSource es, int gbits) {
     // s_aux holds the emission's staged offsets first, then the digit counters,
     // digit starts and global bases (7 KB).
-    constexpr int kAuxWords = kEmit ? kSortPartition : 7 * kRadixBins;
+    constexpr int kAuxWords = kEmit ? kRankStageWords : 7 * kRadixBins;
     __shared__ uint32_t s_keys[kSortPartition + kSortPartition / 16];
     __shared__ uint32_t s_vals[kPacked ? 1 : kSortPartition + kSortPartition / 16];
     __shared__ __align__(16) uint32_t s_aux[kAuxWords];

@@ -64,17 +64,15 @@ class RasterizeFunction(t.autograd.Function):
         cx_f, cy_f = float(cx), float(cy)
         img_h, img_w = int(height), int(width)
 
-        cam_position = -t.matmul(cam_rotation.T, cam_translation)
-        cam_position = cam_position.reshape(3).contiguous()
+        # -R^T t (rasterize.py:43-44) in one kernel
+        cam_position = crc.camera_position(cam_rotation, cam_translation)
 
         mean_2d, cov_2d, depths = crc.project(
             num_gaussians, mu, q, s, cam_rotation, cam_translation, fx_f, fy_f, cx_f, cy_f
         )
-        # Screen radius ~ 3 * sqrt(max eigenvalue of [[a, b], [b, c]]) (rasterize.py:49-53).
-        a, b, c = cov_2d[:, 0], cov_2d[:, 1], cov_2d[:, 2]
-        mid = 0.5 * (a + c)
-        radius = mid + t.sqrt(t.clamp((0.5 * (a - c)) ** 2 + b * b, min=0.1))
-        RasterizeFunction.last_radii2d = (3.0 * t.sqrt(t.clamp(radius, min=0.0))).detach()
+        # Screen radius ~ 3 * sqrt(max eigenvalue of [[a, b], [b, c]]) (rasterize.py:49-53):
+        # the same fp32 operations in one kernel
+        RasterizeFunction.last_radii2d = crc.screen_radii(cov_2d)
 
         colors = crc.SH(num_gaussians, cam_position, mu, albedo, k_j)
         rendered_img, sorted_ids, tile_ranges, final_T, n_contrib = crc.rasterize(

@@ -45,6 +45,15 @@ int gsr_project(int n, const float* mu, const float* q, const float* s, const fl
                 const float* trans, float fx, float fy, float cx, float cy, float* mean2d,
                 float* cov2d, float* depth, void* stream);
 
+/* The autograd glue's approximate screen radii for densification
+ * (gaussian_splatting/rasterizer/rasterize.py:49-53, torch ops there): one
+ * kernel with the same fp32 operations in the same order. */
+int gsr_screen_radii(int n, const float* cov2d, float* radii, void* stream);
+
+/* The glue's camera position -R^T t (rasterize.py:43-44, a torch matmul there),
+ * from device pointers to R [3,3] row-major and t [3]. */
+int gsr_camera_position(const float* rot, const float* trans, float* cam_pos, void* stream);
+
 /* Replaces launch_spherical_harmonics_kernel (csrc/forward/SH.h:4,
  * csrc/forward/SH.cu:95-131; bound as `SH` at csrc/bindings.cpp:32-46,143).
  * cam_pos is a device pointer to 3 floats (the reference copies it to the

@@ -160,6 +160,32 @@ def test_unaligned_views_are_accepted(crc, device):
     assert_bitwise(_np(got), orc.sh(cam, mu, A, kj), "colors")
 
 
+def test_glue_radii_and_camera_position(crc, device):
+    """The glue's one-kernel screen radii equal the torch formula of the
+    reference's rasterize.py:49-53 bit for bit (NaN kept, clamps hit), and its
+    camera position is -R^T t to fp32 rounding."""
+    rng = np.random.default_rng(12)
+    n = 50_000
+    cov = np.c_[rng.uniform(-0.5, 40, n), rng.normal(0, 5, n), rng.uniform(-0.5, 40, n)].astype(np.float32)
+    cov[:5] = [[0.0, 0.0, 0.0], [np.nan, 1.0, 2.0], [-3.0, 0.0, -3.0], [1e-3, 0.0, 1e-3], [np.inf, 0.0, 1.0]]
+    c = _dev(cov, device)
+    a, b, cc = c[:, 0], c[:, 1], c[:, 2]
+    mid = 0.5 * (a + cc)
+    radius = mid + torch.sqrt(torch.clamp((0.5 * (a - cc)) ** 2 + b * b, min=0.1))
+    want = 3.0 * torch.sqrt(torch.clamp(radius, min=0.0))
+    got = crc.screen_radii(c)
+    assert_bitwise(_np(got), _np(want), "radii")
+    ang = rng.normal(size=4)
+    w, x, y, z = ang / np.linalg.norm(ang)
+    R = np.array([[1 - 2 * (y * y + z * z), 2 * (x * y - w * z), 2 * (x * z + w * y)],
+                  [2 * (x * y + w * z), 1 - 2 * (x * x + z * z), 2 * (y * z - w * x)],
+                  [2 * (x * z - w * y), 2 * (y * z + w * x), 1 - 2 * (x * x + y * y)]], np.float32)
+    tt = np.array([0.3, -1.2, 2.5], np.float32)
+    cam = _np(crc.camera_position(_dev(R, device), _dev(tt, device)))
+    ref = -(R.astype(np.float64).T @ tt.astype(np.float64))
+    assert np.abs(cam - ref).max() <= 4e-7 * np.abs(ref).max()
+
+
 def test_empty_frames(crc, device):
     f = lambda *s: torch.zeros(*s, device=device)
     img, ids, ranges, fT, nc = crc.rasterize(0, f(0), f(0, 2), f(0, 3), f(0, 3), f(0), 40, 50)
