@@ -95,6 +95,10 @@ __device__ __forceinline__ float qmin_rect(float mx, float my, float A, float B,
     return best;
 }
 
+// Staged strip bits: bit w for wave w of the tile, and this flag for the
+// backward (opacity in [0, 0.99)).
+constexpr uint32_t kFastExpBit = 1u << 31;
+
 // Bit w set: some pixel of strip w may reach alpha >= 1/255.  A strip is
 // culled when the least q over its rectangle, lowered by 1e-5 of the largest
 // sum of |terms| there (the fp32 rounding of the per-pixel q and of this
@@ -138,7 +142,9 @@ __device__ __forceinline__ void stage_entry(const BlendRec* __restrict__ recs, i
     s_a[slot] = r.a;
     s_b[slot] = r.b;
     s_c[slot] = r.c;
-    s_bits[slot] = ok ? strip_bits<kPix>(r, tile, tiles_x) : 0u;
+    // bit 31: opacity in [0, 0.99), so alpha = opacity * G is never clamped
+    const uint32_t fast = (__float_as_uint(r.b.y) < __float_as_uint(kAlphaMax)) ? kFastExpBit : 0u;
+    s_bits[slot] = ok ? (strip_bits<kPix>(r, tile, tiles_x) | fast) : 0u;
     if (s_id) s_id[slot] = ok ? g : -1;
 }
 
@@ -256,49 +262,65 @@ struct BwdTerms {
     float aT;   // alpha * T_before: dL/dcolour = aT * dL/dpixel
     float dpw;  // dL/dpower
     float dop;  // dL/dopacity
-    float dy;   // pixel y - mean.y
-    bool act;
 };
 
-// One pixel's backward step for one list entry (rasterize_backward.cu:117-198).
-// The decision part (power, exp, alpha) is evaluated exactly as in the forward
-// so the skips (beyond n_contrib, power > 0, alpha < 1/255) match it.  A
-// skipped entry enters the update with alpha 0, which leaves T (x / 1) and
-// accg unchanged and gives zero terms.  The gradient arithmetic after the
-// decision only has to meet the fp32 gradient tolerance and may use fused
-// multiply-adds.  dxdx = (conic.x * dx) * dx and wdx = (2 conic.y) * dx are
-// shared by the lane's pixels, which have the same column.
-__device__ __forceinline__ BwdTerms bwd_step(BwdPixel& p, float dxdx, float wdx, float fy,
-                                             const float4& A, const float4& B, float cb,
-                                             int contributor) {
-    const float dy = fy - A.y;
-    const float power = -0.5f * (dxdx + wdx * dy + B.x * dy * dy);
-    const float G = exp_blend(power);
-    const float araw = B.y * G;
-    const float alpha = fminf(kAlphaMax, araw);
-    const bool act = (contributor <= p.last) & !(power > 0.0f) & !(alpha < kAlphaMin);
-    // alpha = min(0.99, o G): a clamped alpha passes no gradient to o or G
-    const bool unc = act & (araw < kAlphaMax);
-    BwdTerms t;
-    t.act = act;
-    t.dy = dy;
-    {
+// One pixel's decision for one list entry (rasterize_backward.cu:117-140):
+// G = exp(power), alpha = min(0.99, opacity G), and whether the entry blends
+// (within n_contrib, power <= 0, alpha >= 1/255) and passes gradient through
+// the clamp.
+struct BwdDecision {
+    float dy, power, G, alpha;
+    bool act, unc;
+};
+
+// The forward's own evaluation: exp_blend and the same fp32 operations, so
+// every skip agrees with the forward bit for bit.
+__device__ __forceinline__ void decide_exact(BwdDecision& d, float o, int contributor, int last) {
+    d.G = exp_blend(d.power);
+    const float araw = o * d.G;
+    d.alpha = fminf(kAlphaMax, araw);
+    d.act = (contributor <= last) & !(d.power > 0.0f) & !(d.alpha < kAlphaMin);
+    d.unc = d.act & (araw < kAlphaMax);
+}
+
+// For an entry with opacity in [0, 0.99): G from the hardware exp2, which is
+// within 1e-6 relative of exp_blend wherever alpha can reach 1/255 (power in
+// [-5.6, 0]), so the alpha >= 1/255 test agrees with the exact one unless
+// alpha lies within kNearAlpha of 1/255; alpha <= opacity < 0.99 is never
+// clamped.  Returns true when the lane needs the exact evaluation (near the
+// threshold, or a NaN alpha).
+constexpr float kNearAlpha = kAlphaMin * 2e-5f;
+__device__ __forceinline__ bool decide_fast(BwdDecision& d, float o, int contributor, int last) {
+    d.G = __builtin_amdgcn_exp2f(d.power * 1.44269504088896341f);
+    d.alpha = o * d.G;
+    d.act = (contributor <= last) & !(d.power > 0.0f) & !(d.alpha < kAlphaMin);
+    d.unc = d.act;
+    return !(fabsf(d.alpha - kAlphaMin) > kNearAlpha);
+}
+
+// One pixel's gradient step for a decided entry (rasterize_backward.cu:
+// 141-198).  A skipped entry enters with alpha 0, which leaves T (x / 1) and
+// accg unchanged and gives zero terms.  This arithmetic only has to meet the
+// fp32 gradient tolerance and may use fused multiply-adds.
+__device__ __forceinline__ BwdTerms bwd_update(BwdPixel& p, const BwdDecision& d,
+                                               const float4& B, float cb) {
 #pragma clang fp contract(fast)
-        const float ae = act ? alpha : 0.0f;
-        // T / max(1 - alpha, 1e-4): reciprocal refined by one Newton step (~1 ulp)
-        const float d = fmaxf(1.0f - ae, 1e-4f);
-        float r = __builtin_amdgcn_rcpf(d);
-        r = __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
-        const float Tb = p.T * r;
-        const float cg = B.z * p.g0 + B.w * p.g1 + cb * p.g2;
-        const float diff = cg - p.accg;
-        const float dal = diff * Tb;
-        t.aT = ae * Tb;
-        t.dpw = (unc ? alpha : 0.0f) * dal;
-        t.dop = (unc ? G : 0.0f) * dal;
-        p.accg = __builtin_fmaf(ae, diff, p.accg);
-        p.T = Tb;
-    }
+    BwdTerms t;
+    const float ae = d.act ? d.alpha : 0.0f;
+    // T / (1 - alpha) with 1 - alpha in [0.01, 1]: the reference's 1e-4 floor
+    // never applies.  Reciprocal refined by one Newton step (~1 ulp).
+    const float den = 1.0f - ae;
+    float r = __builtin_amdgcn_rcpf(den);
+    r = __builtin_fmaf(__builtin_fmaf(-den, r, 1.0f), r, r);
+    const float Tb = p.T * r;
+    const float cg = B.z * p.g0 + B.w * p.g1 + cb * p.g2;
+    const float diff = cg - p.accg;
+    const float dal = diff * Tb;
+    t.aT = ae * Tb;
+    t.dpw = (d.unc ? d.alpha : 0.0f) * dal;
+    t.dop = (d.unc ? d.G : 0.0f) * dal;
+    p.accg = __builtin_fmaf(ae, diff, p.accg);
+    p.T = Tb;
     return t;
 }
 
@@ -392,43 +414,63 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
             const int contributor = lo + j + 1;
             float w9 = 0.0f;
             // wave-uniform skips: beyond every pixel's n_contrib, or culled
-            if (contributor <= wave_last && (uniform_bits(s_bits, j) & my_bit) != 0) {
+            const uint32_t bits = uniform_bits(s_bits, j);
+            if (contributor <= wave_last && (bits & my_bit) != 0) {
                 const float4 A = s_a[j];
                 const float4 B = s_b[j];
                 const float2 Cc = *reinterpret_cast<const float2*>(&s_c[j]);  // (b, conic.y)
                 const float dx = fx - A.x;
                 const float dxdx = A.z * dx * dx;
                 const float wdx = A.w * dx;
+                BwdDecision d[kPix];
+#pragma unroll
+                for (int k = 0; k < kPix; ++k) {
+                    // the forward's power, bit for bit (rasterize.cu:249-251)
+                    d[k].dy = fy[k] - A.y;
+                    d[k].power = -0.5f * (dxdx + wdx * d[k].dy + B.x * d[k].dy * d[k].dy);
+                }
+                bool exact = (bits & kFastExpBit) == 0;
+                if (!exact) {
+                    bool near = false;
+#pragma unroll
+                    for (int k = 0; k < kPix; ++k)
+                        near |= decide_fast(d[k], B.y, contributor, p[k].last);
+                    exact = ballot(near) != 0;
+                }
+                if (exact) {
+#pragma unroll
+                    for (int k = 0; k < kPix; ++k) decide_exact(d[k], B.y, contributor, p[k].last);
+                }
                 // per-lane sums over its pixels, started from the first pixel's terms
                 float S0, P2, P5, c0, c1, c2, dop;
                 bool act;
                 {
-                    const BwdTerms t = bwd_step(p[0], dxdx, wdx, fy[0], A, B, Cc.x, contributor);
-                    const float e = t.dpw * t.dy;
+                    const BwdTerms t = bwd_update(p[0], d[0], B, Cc.x);
+                    const float e = t.dpw * d[0].dy;
                     S0 = t.dpw;
                     P2 = e;
-                    P5 = e * t.dy;
+                    P5 = e * d[0].dy;
                     c0 = t.aT * p[0].g0;
                     c1 = t.aT * p[0].g1;
                     c2 = t.aT * p[0].g2;
                     dop = t.dop;
-                    act = t.act;
+                    act = d[0].act;
                 }
 #pragma unroll
                 for (int k = 1; k < kPix; ++k) {
-                    const BwdTerms t = bwd_step(p[k], dxdx, wdx, fy[k], A, B, Cc.x, contributor);
+                    const BwdTerms t = bwd_update(p[k], d[k], B, Cc.x);
                     {
 #pragma clang fp contract(fast)
-                        const float e = t.dpw * t.dy;
+                        const float e = t.dpw * d[k].dy;
                         S0 += t.dpw;
                         P2 += e;
-                        P5 += e * t.dy;
+                        P5 += e * d[k].dy;
                         c0 += t.aT * p[k].g0;
                         c1 += t.aT * p[k].g1;
                         c2 += t.aT * p[k].g2;
                         dop += t.dop;
                     }
-                    act |= t.act;
+                    act |= d[k].act;
                 }
                 if (ballot(act) != 0) {
                     const float P1 = dx * S0;

@@ -276,6 +276,79 @@ def test_rasterize_backward_inputs_off_the_rectangles(crc, device):
         assert_grad_close(_np(got_t), r, ab, nm)
 
 
+def _threshold_scene(seed=17, H=48, W=64, crafted=600, others=500):
+    """2D inputs whose skips sit on the edges: `crafted` Gaussians each put one
+    pixel's alpha within a few ulp of 1/255 (variance 0.25-0.35 px^2, mean
+    0.2-0.45 px from the pixel, so every other pixel's alpha is below 0.9/255),
+    and `others` of 1-6 px with opacities in (0, 1), at and above the 0.99
+    clamp, zero and negative."""
+    rng = np.random.default_rng(seed)
+    f32 = np.float32
+    px = rng.integers(2, W - 2, crafted).astype(f32)
+    py = rng.integers(2, H - 2, crafted).astype(f32)
+    mx = (px - rng.uniform(0.2, 0.45, crafted)).astype(f32)
+    my = (py - rng.uniform(0.2, 0.45, crafted)).astype(f32)
+    var = rng.uniform(0.25, 0.35, crafted).astype(f32)
+    # the blend's power at (px, py) in fp32 (rasterize.cu:249-251); conic.y = -0
+    inv = (f32(1.0) / (var * var)).astype(f32)
+    cn = (var * inv).astype(f32)
+    dx, dy = (px - mx).astype(f32), (py - my).astype(f32)
+    power = (f32(-0.5) * ((cn * dx) * dx + (cn * dy) * dy)).astype(f32)
+    G = orc.expf_array(power).astype(f32)
+    o = (f32(1.0 / 255.0) / G).astype(f32)
+    for i, k in enumerate(rng.integers(-4, 5, crafted)):
+        for _ in range(abs(int(k))):
+            o[i] = np.nextafter(o[i], f32(np.inf) if k > 0 else f32(0.0))
+    mean = [np.stack([mx, my], 1)]
+    cov = [np.stack([var, np.zeros_like(var), var], 1)]
+    opac = [o]
+    sig = rng.uniform(1.0, 6.0, (others, 2))
+    rho = rng.uniform(-0.8, 0.8, others)
+    mean.append(np.stack([rng.uniform(-4, W + 4, others), rng.uniform(-4, H + 4, others)], 1))
+    cov.append(np.stack([sig[:, 0] ** 2, rho * sig[:, 0] * sig[:, 1], sig[:, 1] ** 2], 1))
+    oth = rng.uniform(0.0, 1.0, others)
+    pick = rng.integers(0, 8, others)
+    oth = np.where(pick == 0, rng.choice([0.99, 0.995, 1.0, 3.0], others), oth)
+    oth = np.where(pick == 1, rng.choice([0.0, -0.3, 0.98999994], others), oth)
+    opac.append(oth)
+    mean2d = np.concatenate(mean).astype(f32)
+    cov2d = np.concatenate(cov).astype(f32)
+    alpha = np.concatenate(opac).astype(f32).reshape(-1, 1)
+    n = alpha.shape[0]
+    depth = rng.uniform(0.5, 20.0, n).astype(f32)
+    colors = rng.uniform(0.0, 1.0, (n, 3)).astype(f32)
+    return dict(H=H, W=W, mean2d=mean2d, cov2d=cov2d, alpha=alpha, depth=depth, colors=colors)
+
+
+def test_rasterize_backward_alpha_at_the_thresholds(crc, device):
+    """The backward's skips (power > 0, alpha < 1/255, the 0.99 clamp) must be
+    the forward's bit for bit, also where alpha is within a few ulp of 1/255:
+    forward n_contrib exact, gradients within the fp32 bar."""
+    s = _threshold_scene()
+    H, W, n = s["H"], s["W"], s["alpha"].shape[0]
+    t = {k: _dev(s[k], device) for k in ("depth", "mean2d", "cov2d", "colors", "alpha")}
+    img, ids, ranges, fT, nc, _ = crc.rasterize_with_keys(n, t["depth"], t["mean2d"], t["cov2d"],
+                                                          t["colors"], t["alpha"], H, W)
+    want = orc.rasterize(s["depth"], s["mean2d"], s["cov2d"], s["colors"], s["alpha"], H, W)
+    w_img, w_ids, w_rng, w_fT, w_nc, _ = want
+    assert_bitwise(_np(ids), w_ids, "sorted_ids")
+    assert_bitwise(_np(nc), w_nc, "n_contrib")
+    assert np.abs(_np(img) - w_img).max() <= 1e-5
+    G = synthetic.grad_image(H, W, seed=4).numpy()
+    got = crc.backwards_rasterization(_dev(G, device), t["mean2d"], t["cov2d"], t["colors"],
+                                      t["alpha"], ids, ranges, fT, nc, n, H, W)
+    torch.cuda.synchronize()
+    ref = orc.blend_bwd(G, s["mean2d"], s["cov2d"], s["colors"], s["alpha"], w_ids, w_rng, w_fT,
+                        w_nc, H, W, with_abs=True)
+    for got_t, r, ab, nm in zip(got, ref[:4], ref[4:], ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")):
+        assert_grad_close(_np(got_t), r, ab, nm)
+    # the crafted Gaussians' single-pixel contributions decide d_alpha on their own
+    crafted = 600
+    live = np.abs(ref[3][:crafted]).ravel() > 0
+    assert live.any() and (~live).any()
+    assert np.array_equal(np.abs(_np(got[3])[:crafted]).ravel() > 0, live)
+
+
 def test_rasterize_backward_is_deterministic(crc, device):
     """Each Gaussian's gradient is a fixed-order sum of its per-tile slots."""
     a = scene_arrays(synthetic.config_scene("c3", requires_grad=False, n=30_000, width=480, height=270))
