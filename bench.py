@@ -53,6 +53,9 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
         # offset, rect: 16 B) and writes 8 B per pair; later passes move 16 B
         "tile_sort": (16 * tile_passes - 8) * M + 16 * N,
         "ranges": 4 * M + 8 * T,
+        # depth order + rects read twice per level-1 pass, block lists written
+        # once and read twice (counted at one entry per Gaussian), ids written
+        "tile_binning": 4 * M + 2 * 12 * N + 3 * 4 * N + 8 * T,
         "fwd_schedule": 16 * T,                 # ranges in, estimates + order out (walk not counted)
         "blend_fwd": 40 * M + 20 * P + 8 * T,
         "bwd_records": 96 * N,

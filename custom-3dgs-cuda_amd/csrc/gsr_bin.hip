@@ -89,19 +89,25 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     int n, const float* __restrict__ mean2d, const float* __restrict__ cov2d,
     const float* __restrict__ depth, int H, int W, uint32_t* __restrict__ counts,
     uint2* __restrict__ rects, uint32_t* __restrict__ dkeys, uint32_t* __restrict__ dvals,
-    int passes, uint32_t* __restrict__ tile_hist, uint32_t* __restrict__ depth_hist) {
+    int passes, uint32_t* __restrict__ tile_hist, uint32_t* __restrict__ depth_hist,
+    BlockGrid bg, uint32_t* __restrict__ block_hist, uint64_t* __restrict__ pair_total) {
     __shared__ int s_d0[kRadixBins + 1];
     __shared__ uint32_t s_h[3][kRadixBins];
     __shared__ uint32_t s_dh[4][kRadixBins];
+    __shared__ uint32_t s_bh[kMaxBlocks];
     __shared__ uint32_t s_full[kThreads / kWave];
     __shared__ uint32_t s_scan[kThreads / kWave];
     const int tid = threadIdx.x;
+    const bool blocks = block_hist != nullptr;
     for (int j = tid; j <= kRadixBins; j += kThreads) s_d0[j] = 0;
     for (int j = tid; j < 3 * kRadixBins; j += kThreads) (&s_h[0][0])[j] = 0;
     for (int j = tid; j < 4 * kRadixBins; j += kThreads) (&s_dh[0][0])[j] = 0;
+    if (blocks)
+        for (int j = tid; j < bg.nb; j += kThreads) s_bh[j] = 0;
     __syncthreads();
     const int tiles_x = (W + 15) / 16;
     uint32_t full = 0;
+    uint64_t pairs = 0;
     for (int i = blockIdx.x * kThreads + tid; i < n; i += gridDim.x * kThreads) {
         const TileRect r = tile_rect(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1],
                                      cov2d[3 * (size_t)i], cov2d[3 * (size_t)i + 1],
@@ -117,11 +123,18 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
         dvals[i] = (uint32_t)i;
 #pragma unroll
         for (int p = 0; p < 4; ++p) atomicAdd(&s_dh[p][(dk >> (8 * p)) & 0xffu], 1u);
-        if (cnt) {
+        pairs += cnt;
+        if (cnt && passes > 0) {
             const uint32_t w = (uint32_t)(r.x1 - r.x0);
             for (int y = r.y0; y < r.y1; ++y)
                 hist_row((uint32_t)y * (uint32_t)tiles_x + (uint32_t)r.x0, w, passes, s_d0, s_h,
                          &full);
+        }
+        if (cnt && blocks) {
+            // the 8x8-tile blocks the rectangle meets
+            for (int by = r.y0 >> 3; by < (r.y1 + 7) >> 3; ++by)
+                for (int bx = r.x0 >> 3; bx < (r.x1 + 7) >> 3; ++bx)
+                    atomicAdd(&s_bh[by * bg.bw + bx], 1u);
         }
     }
     const uint32_t wfull = (uint32_t)wave_sum_u32(full);
@@ -135,10 +148,19 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     uint32_t pre = 0;
     for (int w = 0; w < (tid >> 6); ++w) pre += s_scan[w];
     const uint32_t d0 = all + pre + inc;
-    if (d0) atomicAdd(&tile_hist[tid], d0);
+    if (passes > 0 && d0) atomicAdd(&tile_hist[tid], d0);
     for (int p = 1; p < passes; ++p) {
         const uint32_t v = s_h[p - 1][tid];
         if (v) atomicAdd(&tile_hist[p * kRadixBins + tid], v);
+    }
+    if (blocks) {
+        for (int j = tid; j < bg.nb; j += kThreads) {
+            const uint32_t v = s_bh[j];
+            if (v) atomicAdd(&block_hist[j], v);
+        }
+        const uint64_t wp = wave_sum_u64(pairs);
+        if ((tid & 63) == 0 && wp) atomicAdd(reinterpret_cast<unsigned long long*>(pair_total),
+                                             (unsigned long long)wp);
     }
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
@@ -249,15 +271,18 @@ inline unsigned blocks_for(uint64_t n) { return (unsigned)((n + kThreads - 1) / 
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
-                            uint32_t* depth_hist, hipStream_t st) {
+                            uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
+                            hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    if (tile_passes < 1 || tile_passes > 4) return hipErrorInvalidValue;
+    if (tile_passes < 0 || tile_passes > 4) return hipErrorInvalidValue;
+    const BlockGrid bg = block_grid((W + 15) / 16, (H + 15) / 16);
+    if (block_hist && (bg.nb > kMaxBlocks || !pair_total)) return hipErrorInvalidValue;
     // at most one work-group per CU: the histogram flush costs one global
     // atomic per bin and work-group
     const unsigned blocks = std::min(blocks_for(n), 256u);
     hipLaunchKernelGGL(bin_count_kernel, dim3(blocks), dim3(kThreads), 0, st, n, mean2d, cov2d,
                        depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist,
-                       depth_hist);
+                       depth_hist, bg, block_hist, pair_total);
     return hipGetLastError();
 }
 

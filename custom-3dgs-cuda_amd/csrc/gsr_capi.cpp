@@ -4,6 +4,7 @@
 // buffer comes from the caller.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -80,12 +81,22 @@ struct Misc {
     int pad;
 };
 
+// Which tile binning a frame uses: the two-level block binning, unless the
+// grid has more 8x8-tile blocks than its histogram holds or GSR_TILE_BINNING
+// is "sort" (the LSD tile sort).  Read on every call: it must not change
+// between the bin and render calls of one frame.
+bool block_binning(int H, int W) {
+    const char* v = std::getenv("GSR_TILE_BINNING");
+    if (v && std::strcmp(v, "sort") == 0) return false;
+    return gsr::block_grid(tiles_x_of(W), tiles_y_of(H)).nb <= gsr::kMaxBlocks;
+}
+
 struct BinLayout {
-    size_t misc, sortctl, scanctl, tilehist, ctl_end;
-    size_t counts, rects, dk0, dv0, dk1, dv1, offsets, recs, end;
+    size_t misc, sortctl, scanctl, tilehist, blockhist, ctl_end;
+    size_t counts, rects, dk0, dv0, dk1, dv1, offsets, block_start, seg_start, recs, end;
 };
 
-BinLayout bin_layout(int n) {
+BinLayout bin_layout(int n, int H, int W) {
     BinLayout L;
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -98,6 +109,9 @@ BinLayout bin_layout(int n) {
     L.sortctl = take(gsr::sort_control_bytes(un, kDepthPasses));
     L.scanctl = take(gsr::scan_control_bytes(n));
     L.tilehist = take((size_t)kMaxTilePasses * 256 * 4);
+    const gsr::BlockGrid bg = gsr::block_grid(tiles_x_of(W), tiles_y_of(H));
+    const size_t nb = (size_t)bg.nb;
+    L.blockhist = take(4 * nb);
     L.ctl_end = off;
     L.counts = take(4 * un);
     L.rects = take(8 * un);
@@ -106,16 +120,24 @@ BinLayout bin_layout(int n) {
     L.dk1 = take(4 * un);
     L.dv1 = take(4 * un);
     L.offsets = take(4 * un);
+    L.block_start = take(4 * (nb + 1));
+    L.seg_start = take(4 * (nb + 1));
     L.recs = take(kRecBytes * un);
     L.end = off;
     return L;
 }
 
+// Render workspace.  LSD tile sort: look-back state (cleared), then key,
+// value and scratch words per pair.  Block binning: the per-block chunk
+// counts, the block lists, segment owners and counts, and tile totals.  One
+// size serves both; the schedule's work and order arrays follow.
 struct SortLayout {
-    size_t ctl, part_rank, ctl_end, tk0, tk1, vbuf, work, order, end;
+    size_t ctl, part_rank, ctl_end, tk0, tk1, vbuf;
+    size_t bcount, lists, seg_owner, tcount, ttotal;
+    size_t work, order, end;
 };
 
-SortLayout sort_layout(int64_t m, int passes, int64_t T) {
+SortLayout sort_layout(int64_t m, int passes, int64_t T, int n, int H, int W) {
     SortLayout L;
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -127,9 +149,20 @@ SortLayout sort_layout(int64_t m, int passes, int64_t T) {
     L.ctl = take(gsr::onesweep_state_bytes(um, passes));
     L.part_rank = take(4 * ((um + gsr::kSortPartition - 1) / gsr::kSortPartition + 1));
     L.ctl_end = off;
+    const size_t pairs_end = off + 3 * align_up(4 * um, 256);
     L.tk0 = take(4 * um);
     L.tk1 = take(4 * um);
     L.vbuf = take(4 * um);
+    // the block binning's arrays overlay the sort's
+    off = L.ctl_end;
+    const gsr::BlockGrid bg = gsr::block_grid(tiles_x_of(W), tiles_y_of(H));
+    const uint64_t segs = gsr::segment_bound(um, bg);
+    L.bcount = take(4 * (size_t)bg.nb * gsr::block_count_stride(n));
+    L.lists = take(4 * um);
+    L.seg_owner = take(4 * (size_t)segs);
+    L.tcount = take(4 * 64 * (size_t)segs);
+    L.ttotal = take(4 * (size_t)(T > 0 ? T : 0));
+    off = std::max(off, pairs_end);
     L.work = take(4 * (size_t)(T > 0 ? T : 0));
     L.order = take(4 * (size_t)(T > 0 ? T : 0));
     L.end = off;
@@ -313,9 +346,8 @@ int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, co
 }
 
 size_t gsr_bin_workspace_bytes(int n, int height, int width) {
-    (void)height;
-    (void)width;
-    return bin_layout(n).end;
+    if (height < 0 || width < 0) return 0;
+    return bin_layout(n, height, width).end;
 }
 
 int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const float* cov2d,
@@ -325,7 +357,7 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
     GSR_REQUIRE(num_pairs, "num_pairs must not be null");
     if (int rc = check_screen(height, width)) return rc;
     *num_pairs = 0;
-    const BinLayout L = bin_layout(n);
+    const BinLayout L = bin_layout(n, height, width);
     GSR_REQUIRE(bin_ws, "bin workspace must not be null");
     if (bin_ws_bytes < L.end) return fail(GSR_ERR_WORKSPACE, "bin workspace too small");
     hipStream_t st = as_stream(stream);
@@ -337,14 +369,24 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
     uint32_t* counts = at<uint32_t>(bin_ws, L.counts);
     uint32_t* dk0 = at<uint32_t>(bin_ws, L.dk0);
     uint32_t* dv0 = at<uint32_t>(bin_ws, L.dv0);
+    const bool blocks = block_binning(height, width);
     {
         StageTimer timer("bin_count", st);
         const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
         GSR_HIP(gsr::launch_bin_count(n, mean2d, cov2d, depth, height, width, counts,
-                                      at<uint2>(bin_ws, L.rects), dk0, dv0, tile_passes(T),
+                                      at<uint2>(bin_ws, L.rects), dk0, dv0,
+                                      blocks ? 0 : tile_passes(T),
                                       at<uint32_t>(bin_ws, L.tilehist),
-                                      at<uint32_t>(bin_ws, L.sortctl), st),
+                                      at<uint32_t>(bin_ws, L.sortctl),
+                                      blocks ? at<uint32_t>(bin_ws, L.blockhist) : nullptr,
+                                      blocks ? &misc->total : nullptr, st),
                 "rasterize: count");
+        if (blocks)
+            GSR_HIP(gsr::launch_block_starts(
+                        gsr::block_grid(tiles_x_of(width), tiles_y_of(height)),
+                        at<uint32_t>(bin_ws, L.blockhist), at<uint32_t>(bin_ws, L.block_start),
+                        at<uint32_t>(bin_ws, L.seg_start), st),
+                    "rasterize: block starts");
     }
     {
         StageTimer timer("depth_sort", st);
@@ -354,7 +396,7 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
                                        /*hist_ready=*/true),
                 "rasterize: depth sort");
     }
-    {
+    if (!blocks) {
         StageTimer timer("scan", st);
         GSR_HIP(gsr::launch_scan_counts(n, dv0, counts, at<uint32_t>(bin_ws, L.offsets),
                                         &misc->total, at<void>(bin_ws, L.scanctl), err, st),
@@ -375,9 +417,9 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
 }
 
 size_t gsr_sort_workspace_bytes(int64_t num_pairs, int n, int height, int width) {
-    (void)n;
+    if (height < 0 || width < 0 || n < 0) return 0;
     const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
-    return sort_layout(num_pairs, tile_passes(T), T).end;
+    return sort_layout(num_pairs, tile_passes(T), T, n, height, width).end;
 }
 
 int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const float* cov2d,
@@ -393,16 +435,20 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
     const int64_t T = (int64_t)tiles_x * tiles_y_of(height);
     if (T == 0) return GSR_OK;
     GSR_REQUIRE(tile_ranges && img && final_T && n_contrib, "null output pointer");
-    const BinLayout BL = bin_layout(n);
+    const BinLayout BL = bin_layout(n, height, width);
     GSR_REQUIRE(bin_ws, "bin workspace must not be null");
     if (bin_ws_bytes < BL.end) return fail(GSR_ERR_WORKSPACE, "bin workspace too small");
     const int passes = tile_passes(T);
-    const SortLayout SL = sort_layout(num_pairs, passes, T);
+    const SortLayout SL = sort_layout(num_pairs, passes, T, n, height, width);
     hipStream_t st = as_stream(stream);
-    gsr::FillList clear;
-    clear.add(tile_ranges, (size_t)T * 8);
-    if (num_pairs > 0 && sort_ws && sort_ws_bytes >= SL.end) clear.add(sort_ws, SL.ctl_end);
-    GSR_HIP(gsr::zero_fill(clear, st), "rasterize: clear");
+    const bool blocks = block_binning(height, width);
+    // the block binning writes every tile range itself
+    if (num_pairs == 0 || !blocks) {
+        gsr::FillList clear;
+        clear.add(tile_ranges, (size_t)T * 8);
+        if (num_pairs > 0 && sort_ws && sort_ws_bytes >= SL.end) clear.add(sort_ws, SL.ctl_end);
+        GSR_HIP(gsr::zero_fill(clear, st), "rasterize: clear");
+    }
     const uint64_t m = (uint64_t)num_pairs;
     void* recs = at<void>(bin_ws, BL.recs);
     if (m > 0) {
@@ -415,41 +461,70 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
             GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, recs, st),
                     "rasterize: records");
         }
-        uint32_t* tk0 = at<uint32_t>(sort_ws, SL.tk0);
-        uint32_t* tk1 = at<uint32_t>(sort_ws, SL.tk1);
         uint32_t* ids = reinterpret_cast<uint32_t*>(sorted_ids);
-        uint32_t* ktiles = ((passes - 1) % 2 == 0) ? tk0 : tk1;  // the last pass's keys
-        // one packed word per pair when tile and Gaussian id fit in 32 bits
-        const int gbits = packed_id_bits(n, T);
-        {
-            StageTimer timer("tile_sort", st);
-            uint32_t* part_rank = at<uint32_t>(sort_ws, SL.part_rank);
-            gsr::EmitSource es;
-            es.perm = at<uint32_t>(bin_ws, BL.dv0);
-            es.counts = at<uint32_t>(bin_ws, BL.counts);
-            es.rects = at<uint2>(bin_ws, BL.rects);
-            es.offsets = at<uint32_t>(bin_ws, BL.offsets);
-            es.part_rank = part_rank;
-            es.nparts = (uint32_t)((m + gsr::kSortPartition - 1) / gsr::kSortPartition);
-            es.tiles_x = tiles_x;
-            GSR_HIP(gsr::launch_partition_starts(n, es.perm, es.counts, es.offsets, m, part_rank,
-                                                 st),
-                    "rasterize: partition starts");
-            GSR_HIP(gsr::launch_tile_sort(es, m, passes, tile_key_bits(T), gbits,
-                                          at<uint32_t>(bin_ws, BL.tilehist),
-                                          at<void>(sort_ws, SL.ctl), tk0, tk1,
-                                          at<uint32_t>(sort_ws, SL.vbuf), ids, ktiles,
-                                          &misc->err, st),
-                    "rasterize: tile sort");
+        if (blocks) {
+            {
+                StageTimer timer("tile_binning", st);
+                gsr::TileBinning tb;
+                tb.n = n;
+                tb.m = m;
+                tb.grid = gsr::block_grid(tiles_x, tiles_y_of(height));
+                tb.perm = at<uint32_t>(bin_ws, BL.dv0);
+                tb.rects = at<uint2>(bin_ws, BL.rects);
+                tb.block_hist = at<uint32_t>(bin_ws, BL.blockhist);
+                tb.block_start = at<uint32_t>(bin_ws, BL.block_start);
+                tb.seg_start = at<uint32_t>(bin_ws, BL.seg_start);
+                tb.bcount = at<uint32_t>(sort_ws, SL.bcount);
+                tb.lists = at<uint32_t>(sort_ws, SL.lists);
+                tb.seg_owner = at<uint32_t>(sort_ws, SL.seg_owner);
+                tb.tcount = at<uint32_t>(sort_ws, SL.tcount);
+                tb.ttotal = at<uint32_t>(sort_ws, SL.ttotal);
+                tb.ranges = tile_ranges;
+                tb.ids = ids;
+                tb.err = &misc->err;
+                GSR_HIP(gsr::launch_tile_binning(tb, st), "rasterize: tile binning");
+            }
+            if (sorted_keys)
+                GSR_HIP(gsr::launch_range_keys((int)T, tile_ranges, sorted_ids, depth, n, m,
+                                               sorted_keys, st),
+                        "rasterize: keys");
+        } else {
+            uint32_t* tk0 = at<uint32_t>(sort_ws, SL.tk0);
+            uint32_t* tk1 = at<uint32_t>(sort_ws, SL.tk1);
+            uint32_t* ktiles = ((passes - 1) % 2 == 0) ? tk0 : tk1;  // the last pass's keys
+            // one packed word per pair when tile and Gaussian id fit in 32 bits
+            const int gbits = packed_id_bits(n, T);
+            {
+                StageTimer timer("tile_sort", st);
+                uint32_t* part_rank = at<uint32_t>(sort_ws, SL.part_rank);
+                gsr::EmitSource es;
+                es.perm = at<uint32_t>(bin_ws, BL.dv0);
+                es.counts = at<uint32_t>(bin_ws, BL.counts);
+                es.rects = at<uint2>(bin_ws, BL.rects);
+                es.offsets = at<uint32_t>(bin_ws, BL.offsets);
+                es.part_rank = part_rank;
+                es.nparts = (uint32_t)((m + gsr::kSortPartition - 1) / gsr::kSortPartition);
+                es.tiles_x = tiles_x;
+                GSR_HIP(gsr::launch_partition_starts(n, es.perm, es.counts, es.offsets, m,
+                                                     part_rank, st),
+                        "rasterize: partition starts");
+                GSR_HIP(gsr::launch_tile_sort(es, m, passes, tile_key_bits(T), gbits,
+                                              at<uint32_t>(bin_ws, BL.tilehist),
+                                              at<void>(sort_ws, SL.ctl), tk0, tk1,
+                                              at<uint32_t>(sort_ws, SL.vbuf), ids, ktiles,
+                                              &misc->err, st),
+                        "rasterize: tile sort");
+            }
+            {
+                StageTimer timer("ranges", st);
+                GSR_HIP(gsr::launch_tile_ranges(m, (uint32_t)T, ktiles, gbits, tile_ranges, st),
+                        "rasterize: ranges");
+            }
+            if (sorted_keys)
+                GSR_HIP(gsr::launch_full_keys(m, ktiles, gbits, sorted_ids, depth, n,
+                                              sorted_keys, st),
+                        "rasterize: keys");
         }
-        {
-            StageTimer timer("ranges", st);
-            GSR_HIP(gsr::launch_tile_ranges(m, (uint32_t)T, ktiles, gbits, tile_ranges, st),
-                    "rasterize: ranges");
-        }
-        if (sorted_keys)
-            GSR_HIP(gsr::launch_full_keys(m, ktiles, gbits, sorted_ids, depth, n, sorted_keys, st),
-                    "rasterize: keys");
     }
     uint32_t* order = (m > 0 && gsr::launch_order_enabled()) ? at<uint32_t>(sort_ws, SL.order)
                                                                : nullptr;

@@ -96,14 +96,61 @@ hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, int ke
                             uint32_t* k1, uint32_t* vbuf, uint32_t* out_vals, uint32_t* out_keys,
                             int* err, hipStream_t st);
 
+// ---- two-level tile binning (8x8-tile blocks, then tiles) ----
+// The tile grid in blocks of 8x8 tiles, row-major.
+struct BlockGrid {
+    int tiles_x = 0, tiles_y = 0;
+    int bw = 0, bh = 0, nb = 0;
+};
+BlockGrid block_grid(int tiles_x, int tiles_y);
+// Blocks the binning's per-work-group block histogram holds.
+constexpr int kMaxBlocks = 8192;
+
+// block_start / seg_start (nb + 1 entries each) from the block histogram:
+// where each block's list begins, and its first 64-entry segment.
+hipError_t launch_block_starts(const BlockGrid& bg, const uint32_t* hist, uint32_t* block_start,
+                               uint32_t* seg_start, hipStream_t st);
+// Row stride (u32) of the per-block chunk counts: n Gaussians in chunks of 64,
+// rounded up to a multiple of 4.
+size_t block_count_stride(int n);
+// Upper bound on level-2 segments for m pairs.
+uint64_t segment_bound(uint64_t m, const BlockGrid& bg);
+
+struct TileBinning {
+    int n = 0;
+    uint64_t m = 0;
+    BlockGrid grid;
+    const uint32_t* perm = nullptr;         // depth order (n)
+    const uint2* rects = nullptr;           // packed tile rectangles (n)
+    const uint32_t* block_hist = nullptr;   // Gaussians per block (nb)
+    const uint32_t* block_start = nullptr;  // nb + 1
+    const uint32_t* seg_start = nullptr;    // nb + 1
+    uint32_t* bcount = nullptr;             // nb * block_count_stride(n)
+    uint32_t* lists = nullptr;              // block lists (m)
+    uint32_t* seg_owner = nullptr;          // segment_bound(m)
+    uint32_t* tcount = nullptr;             // 64 * segment_bound(m)
+    uint32_t* ttotal = nullptr;             // tiles
+    int32_t* ranges = nullptr;              // out: [tiles][2]
+    uint32_t* ids = nullptr;                // out: sorted ids (m)
+    int* err = nullptr;                     // bit 2: inconsistent counts
+};
+// sorted ids and tile ranges from the depth order and tile rectangles.
+hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st);
+// Optional debug output from the ranges: (tile << 32) | float_bits(depth[id]).
+hipError_t launch_range_keys(int T, const int32_t* ranges, const int32_t* ids, const float* depth,
+                             int n, uint64_t m, uint64_t* keys, hipStream_t st);
+
 // ---- binning ----
 // counts[g], packed tile rect, depth key (float bits or 0xffffffff when the
-// Gaussian touches no tile) and identity values, plus the digit histograms of
-// the tile sort (tile_hist) and of the 4-pass depth sort (depth_hist).
+// Gaussian touches no tile) and identity values, the digit histograms of the
+// 4-pass depth sort (depth_hist), and either the digit histograms of the tile
+// sort (tile_passes > 0: tile_hist) or the block histogram (block_hist, with
+// the pair count added to *pair_total).
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
-                            uint32_t* depth_hist, hipStream_t st);
+                            uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
+                            hipStream_t st);
 
 // Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r] (perm null:
 // the identity); the total (u64) is written to *total.

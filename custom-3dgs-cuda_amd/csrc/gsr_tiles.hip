@@ -1,0 +1,566 @@
+// gsr_tiles.hip — two-level tile binning: the (tile, Gaussian) pairs in
+// (tile, depth rank) order without a sort over the pairs.
+//
+// The pairs are the tiles of each Gaussian's tile rectangle (rasterize.cu:
+// 98-135); the reference sorts them on (tile << 32 | depth bits), which with
+// the depth-ordered Gaussians (stable on the Gaussian index) is a stable
+// partition of the depth order into one list per tile.  Here that partition
+// is done in two levels of 64-way buckets:
+//   level 1: each Gaussian, in depth order, goes to the 8x8-tile blocks its
+//            rectangle meets;
+//   level 2: each block's list goes to the block's 64 tiles.
+// Every level is three kernels without inter-work-group waits:
+//   count   — one wave per 64 consecutive list entries; a ballot of "this
+//             lane's rectangle covers bucket b" gives the bucket's count for
+//             the wave and, through the lanes below, each lane's rank in it;
+//   scan    — per bucket, the exclusive prefix of the counts over the waves
+//             in list order (plus the bucket's start);
+//   scatter — each lane writes its entry at start + prefix + rank.
+// Ranks follow lane order and prefixes follow wave order, so each bucket's
+// list keeps the input order: the result is the reference's sorted ids, and
+// the tile ranges come from the per-tile totals.
+//
+// HBM traffic: level 1 reads the depth order and rectangles twice and writes
+// M_1 block entries (M_1 = sum over Gaussians of blocks met, ~5 per Gaussian
+// at 1080p); level 2 reads the block lists twice and writes the M pair ids
+// once, in runs of consecutive addresses (one run per wave and tile).
+#include <algorithm>
+
+#include "gsr_internal.h"
+#include "gsr_common.h"
+
+namespace gsr {
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWavesPer = kThreads / kWave;
+constexpr int kScanThreads = 1024;
+
+struct Rect {
+    int x0, x1, y0, y1;  // tiles [x0, x1) x [y0, y1)
+};
+
+__device__ __forceinline__ Rect unpack_rect(uint2 rc) {
+    return Rect{(int)(rc.x & 0xffffu), (int)(rc.x >> 16), (int)(rc.y & 0xffffu),
+                (int)(rc.y >> 16)};
+}
+
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) {
+        const uint32_t o = (uint32_t)__shfl_xor((int)v, off, kWave);
+        v = v < o ? v : o;
+    }
+    return v;
+}
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
+}
+
+// Lanes of m below this one.
+__device__ __forceinline__ uint32_t rank_in(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                     __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Work-group exclusive scan of one value per thread (kScanThreads threads);
+// *total receives the sum.  Ends with the LDS free for reuse.
+template <int kT>
+__device__ __forceinline__ uint32_t group_exclusive_scan(uint32_t v, uint32_t* s_w,
+                                                         uint32_t* total) {
+    constexpr int kW = kT / kWave;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t inc = wave_inclusive_scan(v);
+    if (lane == 63) s_w[wave] = inc;
+    __syncthreads();
+    uint32_t pre = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+        const uint32_t x = s_w[w];
+        pre += (w < wave) ? x : 0u;
+        all += x;
+    }
+    __syncthreads();
+    *total = all;
+    return pre + inc - v;
+}
+
+// ---- level 1: depth order -> block lists -----------------------------------
+
+// One lane's depth rank: its Gaussian and the block rectangle of its tile
+// rectangle (empty when the Gaussian has no tiles).
+struct RankLane {
+    uint32_t g;
+    int bx0, bx1, by0, by1;
+    bool has;
+};
+
+__device__ __forceinline__ RankLane rank_lane(int n, const uint32_t* __restrict__ perm,
+                                              const uint2* __restrict__ rects, int64_t r) {
+    RankLane L{0u, 0, 0, 0, 0, false};
+    if (r < n) {
+        const uint32_t g = perm[r];
+        if (g < (uint32_t)n) {
+            const Rect t = unpack_rect(rects[g]);
+            if (t.x1 > t.x0 && t.y1 > t.y0) {
+                L.g = g;
+                L.bx0 = t.x0 >> 3;
+                L.bx1 = (t.x1 + 7) >> 3;
+                L.by0 = t.y0 >> 3;
+                L.by1 = (t.y1 + 7) >> 3;
+                L.has = true;
+            }
+        }
+    }
+    return L;
+}
+
+// The row-major block indices [lo, hi) spanned by the wave's bounding box of
+// block rectangles (lo == hi when no lane has one).
+__device__ __forceinline__ void wave_block_span(const RankLane& L, int bw, int* lo, int* hi) {
+    const int x0 = (int)uniform(wave_min_u32(L.has ? (uint32_t)L.bx0 : 0xffffffffu));
+    const int x1 = (int)uniform(wave_max_u32(L.has ? (uint32_t)L.bx1 : 0u));
+    const int y0 = (int)uniform(wave_min_u32(L.has ? (uint32_t)L.by0 : 0xffffffffu));
+    const int y1 = (int)uniform(wave_max_u32(L.has ? (uint32_t)L.by1 : 0u));
+    if (x1 <= x0 || y1 <= y0) {
+        *lo = *hi = 0;
+    } else {
+        *lo = y0 * bw + x0;
+        *hi = (y1 - 1) * bw + x1;
+    }
+}
+
+// counts[b * cstride + c] = how many of chunk c's 64 ranks meet block b, for
+// every block (zeros included), one wave per chunk.
+__global__ __launch_bounds__(kThreads) void block_count_kernel(
+    int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects, BlockGrid bg,
+    int chunks, int cstride, uint32_t* __restrict__ counts) {
+    const int lane = threadIdx.x & 63;
+    const int chunk = (int)uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6));
+    if (chunk >= chunks) return;
+    const RankLane L = rank_lane(n, perm, rects, (int64_t)chunk * kWave + lane);
+    int lo, hi;
+    wave_block_span(L, bg.bw, &lo, &hi);
+    for (int sb = 0; sb < bg.nb; sb += kWave) {
+        uint32_t c = 0;
+        int s = max(sb, lo);
+        const int e = min(sb + kWave, hi);
+        if (s < e) {
+            int sy = s / bg.bw, sx = s - sy * bg.bw;
+            for (; s < e; ++s) {
+                const bool cov = L.has & (sx >= L.bx0) & (sx < L.bx1) & (sy >= L.by0) &
+                                 (sy < L.by1);
+                const uint64_t m = ballot(cov);
+                c = (lane == s - sb) ? (uint32_t)popc64(m) : c;
+                if (++sx == bg.bw) {
+                    sx = 0;
+                    ++sy;
+                }
+            }
+        }
+        if (sb + lane < bg.nb) counts[(size_t)(sb + lane) * cstride + chunk] = c;
+    }
+}
+
+// Per block b: the chunk counts replaced by block_start[b] + their exclusive
+// prefix (the list position of each chunk's first entry in b), and
+// seg_owner[k] = b for b's level-2 segments.  A column total that differs
+// from the binning's block histogram sets err bit 2.
+__global__ __launch_bounds__(kThreads) void block_scan_kernel(
+    int chunks, int cstride, uint32_t* __restrict__ counts, const uint32_t* __restrict__ hist,
+    const uint32_t* __restrict__ block_start, const uint32_t* __restrict__ seg_start,
+    uint32_t* __restrict__ seg_owner, uint32_t seg_cap, int* __restrict__ err) {
+    __shared__ uint32_t s_w[kWavesPer];
+    const int b = blockIdx.x, tid = threadIdx.x;
+    uint4* col = reinterpret_cast<uint4*>(counts + (size_t)b * cstride);
+    const uint32_t start = block_start[b];
+    uint32_t carry = start;
+    for (int base = 0; base < chunks; base += 4 * kThreads) {
+        const int i = base + 4 * tid;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (i < chunks) v = col[i / 4];
+        if (i + 1 >= chunks) v.y = 0u;
+        if (i + 2 >= chunks) v.z = 0u;
+        if (i + 3 >= chunks) v.w = 0u;
+        uint32_t tot;
+        const uint32_t ex = group_exclusive_scan<kThreads>(v.x + v.y + v.z + v.w, s_w, &tot);
+        if (i < chunks) {
+            const uint32_t p0 = carry + ex;
+            col[i / 4] = make_uint4(p0, p0 + v.x, p0 + v.x + v.y, p0 + v.x + v.y + v.z);
+        }
+        carry += tot;
+    }
+    if (tid == 0 && carry - start != hist[b]) atomicOr(err, 2);
+    const uint32_t k1 = min(seg_start[b + 1], seg_cap);
+    for (uint32_t k = seg_start[b] + tid; k < k1; k += kThreads) seg_owner[k] = b;
+}
+
+// Each rank's Gaussian id into the lists of the blocks it meets, at the
+// chunk's position in the block plus the lane's rank among the chunk's lanes
+// meeting the block.  Positions at or beyond cap are dropped.
+__global__ __launch_bounds__(kThreads) void block_scatter_kernel(
+    int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects, BlockGrid bg,
+    int chunks, int cstride, const uint32_t* __restrict__ pos, uint32_t* __restrict__ lists,
+    uint64_t cap) {
+    const int lane = threadIdx.x & 63;
+    const int chunk = (int)uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6));
+    if (chunk >= chunks) return;
+    const RankLane L = rank_lane(n, perm, rects, (int64_t)chunk * kWave + lane);
+    int lo, hi;
+    wave_block_span(L, bg.bw, &lo, &hi);
+    for (int sb = 0; sb < bg.nb; sb += kWave) {
+        int s = max(sb, lo);
+        const int e = min(sb + kWave, hi);
+        if (s >= e) continue;
+        const uint32_t base =
+            (sb + lane < bg.nb) ? pos[(size_t)(sb + lane) * cstride + chunk] : 0u;
+        int sy = s / bg.bw, sx = s - sy * bg.bw;
+        for (; s < e; ++s) {
+            const bool cov =
+                L.has & (sx >= L.bx0) & (sx < L.bx1) & (sy >= L.by0) & (sy < L.by1);
+            const uint64_t m = ballot(cov);
+            if (m != 0) {
+                const uint32_t p0 = (uint32_t)__builtin_amdgcn_readlane((int)base, s - sb);
+                const uint64_t p = (uint64_t)p0 + rank_in(m);
+                if (cov && p < cap) lists[p] = L.g;
+            }
+            if (++sx == bg.bw) {
+                sx = 0;
+                ++sy;
+            }
+        }
+    }
+}
+
+// ---- level 2: block lists -> tile lists ------------------------------------
+
+// One lane of a level-2 segment (64 consecutive entries of one block's list):
+// its Gaussian and the 8x8 bitmap (bit ly * 8 + lx) of the block's tiles its
+// rectangle covers, as two 32-bit halves (rows 0-3, rows 4-7).
+struct SegLane {
+    uint32_t g, lo, hi;
+};
+
+// Bytes [a, b) of a 32-bit word set (0 <= a, b <= 4).
+__device__ __forceinline__ uint32_t byte_span(int a, int b) {
+    if (b <= a) return 0u;
+    const uint32_t upto = (b >= 4) ? 0xffffffffu : ((1u << (8 * b)) - 1u);
+    const uint32_t below = (1u << (8 * a)) - 1u;  // a <= 3 here
+    return upto & ~below;
+}
+
+__device__ __forceinline__ SegLane seg_lane(const uint32_t* __restrict__ lists,
+                                            const uint2* __restrict__ rects, uint32_t first,
+                                            uint32_t end, int ox, int oy, uint64_t cap, int n) {
+    SegLane S{0u, 0u, 0u};
+    const uint32_t e = first + (uint32_t)lane_id();
+    if (e < end && e < cap) {
+        const uint32_t g = lists[e];
+        if (g >= (uint32_t)n) return S;
+        const Rect t = unpack_rect(rects[g]);
+        const int lx0 = min(max(t.x0 - ox, 0), 8), lx1 = min(max(t.x1 - ox, 0), 8);
+        const int ly0 = min(max(t.y0 - oy, 0), 8), ly1 = min(max(t.y1 - oy, 0), 8);
+        S.g = g;
+        if (lx1 > lx0 && ly1 > ly0) {
+            const uint32_t row = ((1u << lx1) - 1u) & ~((1u << lx0) - 1u);
+            const uint32_t rep = row * 0x01010101u;
+            S.lo = rep & byte_span(min(ly0, 4), min(ly1, 4));
+            S.hi = rep & byte_span(max(ly0 - 4, 0), max(ly1 - 4, 0));
+        }
+    }
+    return S;
+}
+
+struct SegInfo {
+    uint32_t first, end;  // the segment's entries in the block lists
+    int ox, oy;           // the block's first tile
+};
+
+__device__ __forceinline__ SegInfo seg_info(uint32_t k, const uint32_t* __restrict__ seg_owner,
+                                            const uint32_t* __restrict__ seg_start,
+                                            const uint32_t* __restrict__ block_start,
+                                            int bw, int nb) {
+    const uint32_t b = min(uniform(seg_owner[k]), (uint32_t)(nb - 1));
+    SegInfo I;
+    I.first = uniform(block_start[b]) + (k - uniform(seg_start[b])) * (uint32_t)kWave;
+    I.end = uniform(block_start[b + 1]);
+    const int by = (int)b / bw;
+    I.ox = ((int)b - by * bw) * 8;
+    I.oy = by * 8;
+    return I;
+}
+
+// Bit t of the lane's bitmap (t wave-uniform after unrolling).
+__device__ __forceinline__ bool bit_of(const SegLane& S, int t) {
+    return ((t < 32 ? (S.lo >> t) : (S.hi >> (t - 32))) & 1u) != 0u;
+}
+
+// tcount[k * 64 + t] = entries of segment k covering the block's tile t.
+// Segments k < seg_start[nb] (at most seg_cap), grid-strided.
+__global__ __launch_bounds__(kThreads) void tile_count_kernel(
+    int n, BlockGrid bg, const uint32_t* __restrict__ seg_owner,
+    const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ block_start,
+    const uint32_t* __restrict__ lists, uint64_t cap, const uint2* __restrict__ rects,
+    uint32_t seg_cap, uint32_t* __restrict__ tcount) {
+    const uint32_t nseg = min(uniform(seg_start[bg.nb]), seg_cap);
+    const uint32_t stride = gridDim.x * kWavesPer;
+    const int lane = lane_id();
+    for (uint32_t k = uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6)); k < nseg;
+         k += stride) {
+        const SegInfo I = seg_info(k, seg_owner, seg_start, block_start, bg.bw, bg.nb);
+        const SegLane S = seg_lane(lists, rects, I.first, I.end, I.ox, I.oy, cap, n);
+        uint32_t c = 0;
+#pragma unroll
+        for (int t = 0; t < 64; ++t) {
+            const uint64_t m = ballot(bit_of(S, t));
+            c = (lane == t) ? (uint32_t)popc64(m) : c;
+        }
+        tcount[(size_t)k * kWave + lane] = c;
+    }
+}
+
+// Per block: each tile's segment counts replaced by their exclusive prefix
+// over the block's segments, and the tile's total to ttotal (tiles on the
+// screen only).  Four waves split the segments into consecutive runs.
+__global__ __launch_bounds__(kThreads) void tile_scan_kernel(
+    BlockGrid bg, const uint32_t* __restrict__ seg_start, uint32_t seg_cap,
+    uint32_t* __restrict__ tcount, uint32_t* __restrict__ ttotal) {
+    __shared__ uint32_t s_sum[kWavesPer][kWave];
+    const int b = blockIdx.x;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t k0 = min(seg_start[b], seg_cap);
+    const uint32_t R = min(seg_start[b + 1], seg_cap) - k0;
+    const uint32_t per = (R + kWavesPer - 1) / kWavesPer;
+    const uint32_t r0 = k0 + min(R, (uint32_t)wave * per);
+    const uint32_t r1 = k0 + min(R, (uint32_t)(wave + 1) * per);
+    uint32_t sum = 0;
+#pragma unroll 8
+    for (uint32_t k = r0; k < r1; ++k) sum += tcount[(size_t)k * kWave + lane];
+    s_sum[wave][lane] = sum;
+    __syncthreads();
+    uint32_t run = 0, total = 0;
+#pragma unroll
+    for (int w = 0; w < kWavesPer; ++w) {
+        run += (w < wave) ? s_sum[w][lane] : 0u;
+        total += s_sum[w][lane];
+    }
+#pragma unroll 8
+    for (uint32_t k = r0; k < r1; ++k) {
+        const uint32_t v = tcount[(size_t)k * kWave + lane];
+        tcount[(size_t)k * kWave + lane] = run;
+        run += v;
+    }
+    if (wave == 0) {
+        const int by = b / bg.bw;
+        const int tx = (b - by * bg.bw) * 8 + (lane & 7), ty = by * 8 + (lane >> 3);
+        if (tx < bg.tiles_x && ty < bg.tiles_y) ttotal[(size_t)ty * bg.tiles_x + tx] = total;
+    }
+}
+
+// ranges[t] = [start, start + count) from the tile totals in tile order,
+// (0, 0) for tiles without pairs (rasterize.cu:140-166); a grand total other
+// than m sets err bit 2.  One work-group.
+__global__ __launch_bounds__(kScanThreads) void tile_starts_kernel(
+    int T, const uint32_t* __restrict__ ttotal, uint64_t m, int2* __restrict__ ranges,
+    int* __restrict__ err) {
+    __shared__ uint32_t s_w[kScanThreads / kWave];
+    const int tid = threadIdx.x;
+    uint32_t carry = 0;
+    for (int base = 0; base < T; base += 4 * kScanThreads) {
+        const int i = base + 4 * tid;
+        uint32_t v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (i + j < T) ? ttotal[i + j] : 0u;
+        uint32_t tot;
+        uint32_t p = carry + group_exclusive_scan<kScanThreads>(v[0] + v[1] + v[2] + v[3],
+                                                                s_w, &tot);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (i + j < T)
+                ranges[i + j] = v[j] ? make_int2((int)p, (int)(p + v[j])) : make_int2(0, 0);
+            p += v[j];
+        }
+        carry += tot;
+    }
+    if (tid == 0 && (uint64_t)carry != m) atomicOr(err, 2);
+}
+
+// Each segment entry's Gaussian id into the lists of the tiles it covers, at
+// the tile's start + the segment's prefix + the lane's rank.  Positions at or
+// beyond m are dropped.
+__global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
+    int n, BlockGrid bg, const uint32_t* __restrict__ seg_owner,
+    const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ block_start,
+    const uint32_t* __restrict__ lists, uint64_t cap, const uint2* __restrict__ rects,
+    uint32_t seg_cap, const uint32_t* __restrict__ tcount, const int2* __restrict__ ranges,
+    uint64_t m, uint32_t* __restrict__ ids) {
+    const uint32_t nseg = min(uniform(seg_start[bg.nb]), seg_cap);
+    const uint32_t stride = gridDim.x * kWavesPer;
+    const int lane = lane_id();
+    for (uint32_t k = uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6)); k < nseg;
+         k += stride) {
+        const SegInfo I = seg_info(k, seg_owner, seg_start, block_start, bg.bw, bg.nb);
+        const SegLane S = seg_lane(lists, rects, I.first, I.end, I.ox, I.oy, cap, n);
+        // lane t: where segment k's entries of tile t begin
+        const int tx = I.ox + (lane & 7), ty = I.oy + (lane >> 3);
+        uint32_t base = 0;
+        if (tx < bg.tiles_x && ty < bg.tiles_y)
+            base = (uint32_t)ranges[(size_t)ty * bg.tiles_x + tx].x +
+                   tcount[(size_t)k * kWave + lane];
+#pragma unroll
+        for (int t = 0; t < 64; ++t) {
+            const bool cov = bit_of(S, t);
+            const uint64_t mk = ballot(cov);
+            if (mk != 0) {
+                const uint64_t p =
+                    (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)base, t) + rank_in(mk);
+                if (cov && p < m) ids[p] = S.g;
+            }
+        }
+    }
+}
+
+// keys[i] = (tile << 32) | depth bits of ids[i], one wave per tile.
+__global__ __launch_bounds__(kThreads) void range_keys_kernel(int T,
+                                                              const int2* __restrict__ ranges,
+                                                              const int32_t* __restrict__ ids,
+                                                              const float* __restrict__ depth,
+                                                              int n, uint64_t m,
+                                                              uint64_t* __restrict__ keys) {
+    const int t = (int)uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6));
+    if (t >= T) return;
+    const int2 r = ranges[t];
+    for (int64_t i = (int64_t)r.x + lane_id(); i < (int64_t)r.y && i < (int64_t)m; i += kWave) {
+        const int g = ids[i];
+        const uint32_t dbits = (g >= 0 && g < n) ? __float_as_uint(depth[g]) : 0xffffffffu;
+        keys[i] = ((uint64_t)(uint32_t)t << 32) | (uint64_t)dbits;
+    }
+}
+
+// block_start[b] / seg_start[b]: exclusive prefixes of the block histogram and
+// of its 64-entry segment counts, nb + 1 entries each.  One work-group.
+__global__ __launch_bounds__(kScanThreads) void block_starts_kernel(
+    int nb, const uint32_t* __restrict__ hist, uint32_t* __restrict__ block_start,
+    uint32_t* __restrict__ seg_start) {
+    __shared__ uint32_t s_w[kScanThreads / kWave];
+    __shared__ uint32_t s_v[kScanThreads / kWave];
+    const int tid = threadIdx.x;
+    uint32_t carry = 0, scarry = 0;
+    for (int base = 0; base < nb; base += 4 * kScanThreads) {
+        const int i = base + 4 * tid;
+        uint32_t v[4], s[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = (i + j < nb) ? hist[i + j] : 0u;
+            s[j] = (v[j] + kWave - 1) / kWave;
+        }
+        uint32_t tot, stot;
+        uint32_t p = carry + group_exclusive_scan<kScanThreads>(v[0] + v[1] + v[2] + v[3], s_w,
+                                                                &tot);
+        uint32_t q = scarry + group_exclusive_scan<kScanThreads>(s[0] + s[1] + s[2] + s[3],
+                                                                 s_v, &stot);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (i + j < nb) {
+                block_start[i + j] = p;
+                seg_start[i + j] = q;
+            }
+            p += v[j];
+            q += s[j];
+        }
+        carry += tot;
+        scarry += stot;
+    }
+    if (tid == 0) {
+        block_start[nb] = carry;
+        seg_start[nb] = scarry;
+    }
+}
+
+inline unsigned groups_for(uint64_t waves) {
+    return (unsigned)((waves + kWavesPer - 1) / kWavesPer);
+}
+
+// Work-groups of the grid-strided segment kernels: enough for the bound on
+// segments, at most 8 per CU of a 256-CU device.
+inline unsigned seg_groups(uint64_t seg_bound) {
+    return (unsigned)std::max<uint64_t>(1, std::min<uint64_t>(groups_for(seg_bound), 2048));
+}
+
+}  // namespace
+
+BlockGrid block_grid(int tiles_x, int tiles_y) {
+    BlockGrid g;
+    g.tiles_x = tiles_x;
+    g.tiles_y = tiles_y;
+    g.bw = (tiles_x + 7) / 8;
+    g.bh = (tiles_y + 7) / 8;
+    g.nb = g.bw * g.bh;
+    return g;
+}
+
+hipError_t launch_block_starts(const BlockGrid& bg, const uint32_t* hist, uint32_t* block_start,
+                               uint32_t* seg_start, hipStream_t st) {
+    if (bg.nb <= 0) return hipSuccess;
+    hipLaunchKernelGGL(block_starts_kernel, dim3(1), dim3(kScanThreads), 0, st, bg.nb, hist,
+                       block_start, seg_start);
+    return hipGetLastError();
+}
+
+size_t block_count_stride(int n) {
+    const size_t chunks = ((size_t)std::max(n, 0) + kWave - 1) / kWave;
+    return (chunks + 3) / 4 * 4;
+}
+
+uint64_t segment_bound(uint64_t m, const BlockGrid& bg) {
+    return m / kWave + (uint64_t)bg.nb + 1;
+}
+
+hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
+    const BlockGrid& bg = tb.grid;
+    if (tb.m == 0 || tb.n <= 0 || bg.nb <= 0) return hipSuccess;
+    const int chunks = (int)(((size_t)tb.n + kWave - 1) / kWave);
+    const int cstride = (int)block_count_stride(tb.n);
+    const uint64_t segs = segment_bound(tb.m, bg);
+    if (segs > 0xffffffffull) return hipErrorInvalidValue;
+    const uint32_t seg_cap = (uint32_t)segs;
+    hipError_t e;
+    hipLaunchKernelGGL(block_count_kernel, dim3(groups_for(chunks)), dim3(kThreads), 0, st, tb.n,
+                       tb.perm, tb.rects, bg, chunks, cstride, tb.bcount);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(block_scan_kernel, dim3(bg.nb), dim3(kThreads), 0, st, chunks, cstride,
+                       tb.bcount, tb.block_hist, tb.block_start, tb.seg_start, tb.seg_owner,
+                       seg_cap, tb.err);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(block_scatter_kernel, dim3(groups_for(chunks)), dim3(kThreads), 0, st,
+                       tb.n, tb.perm, tb.rects, bg, chunks, cstride, tb.bcount, tb.lists, tb.m);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(tile_count_kernel, dim3(seg_groups(segs)), dim3(kThreads), 0, st, tb.n, bg,
+                       tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.rects,
+                       seg_cap, tb.tcount);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(tile_scan_kernel, dim3(bg.nb), dim3(kThreads), 0, st, bg, tb.seg_start,
+                       seg_cap, tb.tcount, tb.ttotal);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    const int T = bg.tiles_x * bg.tiles_y;
+    hipLaunchKernelGGL(tile_starts_kernel, dim3(1), dim3(kScanThreads), 0, st, T, tb.ttotal, tb.m,
+                       reinterpret_cast<int2*>(tb.ranges), tb.err);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(tile_scatter_kernel, dim3(seg_groups(segs)), dim3(kThreads), 0, st, tb.n,
+                       bg, tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.rects,
+                       seg_cap, tb.tcount, reinterpret_cast<const int2*>(tb.ranges), tb.m,
+                       tb.ids);
+    return hipGetLastError();
+}
+
+hipError_t launch_range_keys(int T, const int32_t* ranges, const int32_t* ids, const float* depth,
+                             int n, uint64_t m, uint64_t* keys, hipStream_t st) {
+    if (m == 0 || T <= 0) return hipSuccess;
+    hipLaunchKernelGGL(range_keys_kernel, dim3(groups_for((uint64_t)T)), dim3(kThreads), 0, st, T,
+                       reinterpret_cast<const int2*>(ranges), ids, depth, n, m, keys);
+    return hipGetLastError();
+}
+
+}  // namespace gsr

@@ -85,13 +85,28 @@ def test_forward_parity_bench_scene(crc, device):
     _check_forward(gpu_forward(crc, a, device), oracle_forward(a))
 
 
-def test_forward_parity_two_word_sort(crc, device):
-    """600k Gaussians at 1080p: 20 id bits + 13 tile bits exceed one 32-bit word,
-    so the tile sort carries keys and ids as separate words (the packed form is
-    what every smaller test above uses)."""
-    print("[gpu] forward parity, two-word tile sort (600k Gaussians, 1920x1080)", flush=True)
+@pytest.mark.parametrize("binning", ["blocks", "sort"])
+def test_forward_parity_600k_1080p(crc, device, monkeypatch, binning):
+    """600k Gaussians at 1080p through both tile binnings: the two-level block
+    binning, and the LSD tile sort (screens beyond its block histogram, or
+    GSR_TILE_BINNING=sort), whose 20 id bits + 13 tile bits exceed one 32-bit
+    word so keys and ids travel as separate words."""
+    print(f"[gpu] forward parity, {binning} binning (600k Gaussians, 1920x1080)", flush=True)
+    if binning == "sort":
+        monkeypatch.setenv("GSR_TILE_BINNING", "sort")
     sc = synthetic.config_scene("c3", requires_grad=False, n=600_000, width=1920, height=1080)
     a = scene_arrays(sc)
+    _check_forward(gpu_forward(crc, a, device), oracle_forward(a))
+
+
+@pytest.mark.parametrize("name,kw", [("c3", dict(n=20_000, width=480, height=270)),
+                                     ("c5", dict(n=30_000, width=400, height=224))],
+                         ids=["c3", "c5"])
+def test_forward_parity_tile_sort(crc, device, monkeypatch, name, kw):
+    """The LSD tile sort (packed words) that serves screens with more 8x8-tile
+    blocks than the block binning's histogram holds."""
+    monkeypatch.setenv("GSR_TILE_BINNING", "sort")
+    a = scene_arrays(synthetic.config_scene(name, requires_grad=False, **kw))
     _check_forward(gpu_forward(crc, a, device), oracle_forward(a))
 
 
