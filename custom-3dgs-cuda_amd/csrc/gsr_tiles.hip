@@ -46,15 +46,6 @@ __device__ __forceinline__ Rect unpack_rect(uint2 rc) {
                 (int)(rc.y >> 16)};
 }
 
-__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) {
-        const uint32_t o = (uint32_t)__shfl_xor((int)v, off, kWave);
-        v = v < o ? v : o;
-    }
-    return v;
-}
-
 __device__ __forceinline__ uint32_t uniform(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
 }
@@ -90,16 +81,17 @@ __device__ __forceinline__ uint32_t group_exclusive_scan(uint32_t v, uint32_t* s
 // ---- level 1: depth order -> block lists -----------------------------------
 
 // One lane's depth rank: its Gaussian and the block rectangle of its tile
-// rectangle (empty when the Gaussian has no tiles).
+// rectangle as origin and extent (has: the Gaussian has tiles).
 struct RankLane {
     uint32_t g;
-    int bx0, bx1, by0, by1;
+    int bx0, by0;
+    uint32_t bw, bh;
     bool has;
 };
 
 __device__ __forceinline__ RankLane rank_lane(int n, const uint32_t* __restrict__ perm,
                                               const uint2* __restrict__ rects, int64_t r) {
-    RankLane L{0u, 0, 0, 0, 0, false};
+    RankLane L{0u, 0, 0, 0u, 0u, false};
     if (r < n) {
         const uint32_t g = perm[r];
         if (g < (uint32_t)n) {
@@ -107,9 +99,9 @@ __device__ __forceinline__ RankLane rank_lane(int n, const uint32_t* __restrict_
             if (t.x1 > t.x0 && t.y1 > t.y0) {
                 L.g = g;
                 L.bx0 = t.x0 >> 3;
-                L.bx1 = (t.x1 + 7) >> 3;
                 L.by0 = t.y0 >> 3;
-                L.by1 = (t.y1 + 7) >> 3;
+                L.bw = (uint32_t)(((t.x1 + 7) >> 3) - L.bx0);
+                L.bh = (uint32_t)(((t.y1 + 7) >> 3) - L.by0);
                 L.has = true;
             }
         }
@@ -117,51 +109,58 @@ __device__ __forceinline__ RankLane rank_lane(int n, const uint32_t* __restrict_
     return L;
 }
 
-// The row-major block indices [lo, hi) spanned by the wave's bounding box of
-// block rectangles (lo == hi when no lane has one).
-__device__ __forceinline__ void wave_block_span(const RankLane& L, int bw, int* lo, int* hi) {
-    const int x0 = (int)uniform(wave_min_u32(L.has ? (uint32_t)L.bx0 : 0xffffffffu));
-    const int x1 = (int)uniform(wave_max_u32(L.has ? (uint32_t)L.bx1 : 0u));
-    const int y0 = (int)uniform(wave_min_u32(L.has ? (uint32_t)L.by0 : 0xffffffffu));
-    const int y1 = (int)uniform(wave_max_u32(L.has ? (uint32_t)L.by1 : 0u));
-    if (x1 <= x0 || y1 <= y0) {
-        *lo = *hi = 0;
-    } else {
-        *lo = y0 * bw + x0;
-        *hi = (y1 - 1) * bw + x1;
+// Level-1 work item of one wave: chunk c of 64 depth ranks against window w
+// of 64 consecutive block indices.  Adjacent waves share the chunk.
+struct ChunkWindow {
+    int chunk, window;
+};
+
+__device__ __forceinline__ ChunkWindow chunk_window(int windows) {
+    const int id = (int)uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6));
+    return ChunkWindow{id / windows, id - (id / windows) * windows};
+}
+
+// Walks window w's blocks in row-major order and calls f(idx, m) for each
+// block idx (0..63 within the window) that some lane's rectangle meets, with
+// m the ballot of those lanes.  Rows that no lane meets are skipped whole.
+template <typename F>
+__device__ __forceinline__ void walk_window(const RankLane& L, const BlockGrid& bg, int w,
+                                            F&& f) {
+    const int s0 = w * kWave, s1 = min(s0 + kWave, bg.nb);
+    const uint64_t lanes = ballot(L.has);
+    if (lanes == 0 || s0 >= s1) return;
+    int sy = s0 / bg.bw, sx = s0 - sy * bg.bw;
+    int s = s0;
+    while (s < s1) {
+        const uint64_t rowm = lanes & ballot((uint32_t)(sy - L.by0) < L.bh);
+        const int row_end = min(s1, s + (bg.bw - sx));
+        if (rowm != 0) {
+            for (; s < row_end; ++s, ++sx) {
+                const uint64_t m = rowm & ballot((uint32_t)(sx - L.bx0) < L.bw);
+                if (m != 0) f(s - s0, m);
+            }
+        }
+        s = row_end;
+        sx = 0;
+        ++sy;
     }
 }
 
 // counts[b * cstride + c] = how many of chunk c's 64 ranks meet block b, for
-// every block (zeros included), one wave per chunk.
+// every block (zeros included).
 __global__ __launch_bounds__(kThreads) void block_count_kernel(
     int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects, BlockGrid bg,
-    int chunks, int cstride, uint32_t* __restrict__ counts) {
-    const int lane = threadIdx.x & 63;
-    const int chunk = (int)uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6));
-    if (chunk >= chunks) return;
-    const RankLane L = rank_lane(n, perm, rects, (int64_t)chunk * kWave + lane);
-    int lo, hi;
-    wave_block_span(L, bg.bw, &lo, &hi);
-    for (int sb = 0; sb < bg.nb; sb += kWave) {
-        uint32_t c = 0;
-        int s = max(sb, lo);
-        const int e = min(sb + kWave, hi);
-        if (s < e) {
-            int sy = s / bg.bw, sx = s - sy * bg.bw;
-            for (; s < e; ++s) {
-                const bool cov = L.has & (sx >= L.bx0) & (sx < L.bx1) & (sy >= L.by0) &
-                                 (sy < L.by1);
-                const uint64_t m = ballot(cov);
-                c = (lane == s - sb) ? (uint32_t)popc64(m) : c;
-                if (++sx == bg.bw) {
-                    sx = 0;
-                    ++sy;
-                }
-            }
-        }
-        if (sb + lane < bg.nb) counts[(size_t)(sb + lane) * cstride + chunk] = c;
-    }
+    int chunks, int windows, int cstride, uint32_t* __restrict__ counts) {
+    const int lane = lane_id();
+    const ChunkWindow cw = chunk_window(windows);
+    if (cw.chunk >= chunks) return;
+    const RankLane L = rank_lane(n, perm, rects, (int64_t)cw.chunk * kWave + lane);
+    uint32_t c = 0;
+    walk_window(L, bg, cw.window, [&](int idx, uint64_t m) {
+        c = (lane == idx) ? (uint32_t)popc64(m) : c;
+    });
+    const int b = cw.window * kWave + lane;
+    if (b < bg.nb) counts[(size_t)b * cstride + cw.chunk] = c;
 }
 
 // Per block b: the chunk counts replaced by block_start[b] + their exclusive
@@ -202,36 +201,19 @@ __global__ __launch_bounds__(kThreads) void block_scan_kernel(
 // meeting the block.  Positions at or beyond cap are dropped.
 __global__ __launch_bounds__(kThreads) void block_scatter_kernel(
     int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects, BlockGrid bg,
-    int chunks, int cstride, const uint32_t* __restrict__ pos, uint32_t* __restrict__ lists,
-    uint64_t cap) {
-    const int lane = threadIdx.x & 63;
-    const int chunk = (int)uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6));
-    if (chunk >= chunks) return;
-    const RankLane L = rank_lane(n, perm, rects, (int64_t)chunk * kWave + lane);
-    int lo, hi;
-    wave_block_span(L, bg.bw, &lo, &hi);
-    for (int sb = 0; sb < bg.nb; sb += kWave) {
-        int s = max(sb, lo);
-        const int e = min(sb + kWave, hi);
-        if (s >= e) continue;
-        const uint32_t base =
-            (sb + lane < bg.nb) ? pos[(size_t)(sb + lane) * cstride + chunk] : 0u;
-        int sy = s / bg.bw, sx = s - sy * bg.bw;
-        for (; s < e; ++s) {
-            const bool cov =
-                L.has & (sx >= L.bx0) & (sx < L.bx1) & (sy >= L.by0) & (sy < L.by1);
-            const uint64_t m = ballot(cov);
-            if (m != 0) {
-                const uint32_t p0 = (uint32_t)__builtin_amdgcn_readlane((int)base, s - sb);
-                const uint64_t p = (uint64_t)p0 + rank_in(m);
-                if (cov && p < cap) lists[p] = L.g;
-            }
-            if (++sx == bg.bw) {
-                sx = 0;
-                ++sy;
-            }
-        }
-    }
+    int chunks, int windows, int cstride, const uint32_t* __restrict__ pos,
+    uint32_t* __restrict__ lists, uint64_t cap) {
+    const int lane = lane_id();
+    const ChunkWindow cw = chunk_window(windows);
+    if (cw.chunk >= chunks) return;
+    const RankLane L = rank_lane(n, perm, rects, (int64_t)cw.chunk * kWave + lane);
+    const int b = cw.window * kWave + lane;
+    const uint32_t base = (b < bg.nb) ? pos[(size_t)b * cstride + cw.chunk] : 0u;
+    walk_window(L, bg, cw.window, [&](int idx, uint64_t m) {
+        const uint64_t p =
+            (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)base, idx) + rank_in(m);
+        if (((m >> lane) & 1ull) && p < cap) lists[p] = L.g;
+    });
 }
 
 // ---- level 2: block lists -> tile lists ------------------------------------
@@ -522,20 +504,23 @@ hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
     const BlockGrid& bg = tb.grid;
     if (tb.m == 0 || tb.n <= 0 || bg.nb <= 0) return hipSuccess;
     const int chunks = (int)(((size_t)tb.n + kWave - 1) / kWave);
+    const int windows = (bg.nb + kWave - 1) / kWave;
     const int cstride = (int)block_count_stride(tb.n);
     const uint64_t segs = segment_bound(tb.m, bg);
     if (segs > 0xffffffffull) return hipErrorInvalidValue;
     const uint32_t seg_cap = (uint32_t)segs;
     hipError_t e;
-    hipLaunchKernelGGL(block_count_kernel, dim3(groups_for(chunks)), dim3(kThreads), 0, st, tb.n,
-                       tb.perm, tb.rects, bg, chunks, cstride, tb.bcount);
+    const uint64_t l1_waves = (uint64_t)chunks * (uint64_t)windows;
+    hipLaunchKernelGGL(block_count_kernel, dim3(groups_for(l1_waves)), dim3(kThreads), 0, st,
+                       tb.n, tb.perm, tb.rects, bg, chunks, windows, cstride, tb.bcount);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(block_scan_kernel, dim3(bg.nb), dim3(kThreads), 0, st, chunks, cstride,
                        tb.bcount, tb.block_hist, tb.block_start, tb.seg_start, tb.seg_owner,
                        seg_cap, tb.err);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(block_scatter_kernel, dim3(groups_for(chunks)), dim3(kThreads), 0, st,
-                       tb.n, tb.perm, tb.rects, bg, chunks, cstride, tb.bcount, tb.lists, tb.m);
+    hipLaunchKernelGGL(block_scatter_kernel, dim3(groups_for(l1_waves)), dim3(kThreads), 0, st,
+                       tb.n, tb.perm, tb.rects, bg, chunks, windows, cstride, tb.bcount, tb.lists,
+                       tb.m);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(tile_count_kernel, dim3(seg_groups(segs)), dim3(kThreads), 0, st, tb.n, bg,
                        tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.rects,
