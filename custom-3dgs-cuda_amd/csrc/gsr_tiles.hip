@@ -120,34 +120,60 @@ __device__ __forceinline__ ChunkWindow chunk_window(int windows) {
     return ChunkWindow{id / windows, id - (id / windows) * windows};
 }
 
-// Walks window w's blocks in row-major order and calls f(idx, m) for each
-// block idx (0..63 within the window) that some lane's rectangle meets, with
-// m the ballot of those lanes.  Rows that no lane meets are skipped whole.
-template <typename F>
-__device__ __forceinline__ void walk_window(const RankLane& L, const BlockGrid& bg, int w,
-                                            F&& f) {
-    const int s0 = w * kWave, s1 = min(s0 + kWave, bg.nb);
+// 64-bit value of lane src (all lanes active).
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int src) {
+    const uint32_t lo = (uint32_t)__shfl((int)(uint32_t)v, src, kWave);
+    const uint32_t hi = (uint32_t)__shfl((int)(uint32_t)(v >> 32), src, kWave);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// The lanes whose rectangle meets block (row sy, column sx) are
+// rows[sy] & cols[sx]: one ballot per block row and per block column of the
+// window gives every block's count and every lane's rank.  Lane j holds the
+// mask of the window's j-th row (rowv) and j-th column (colv); the window's
+// blocks [s0, s1) span rows sy_a.. and, in order, the columns col_base + j
+// (mod bw): all bw columns when bw <= 64, else 64 distinct ones.
+struct WindowMasks {
+    int s0, s1, sy_a, sx_a, col_base, nrows, ncols;
+    uint64_t rowv, colv;
+};
+
+__device__ __forceinline__ WindowMasks window_masks(const RankLane& L, const BlockGrid& bg,
+                                                    int w) {
+    const int lane = lane_id();
+    WindowMasks W;
+    W.s0 = w * kWave;
+    W.s1 = min(W.s0 + kWave, bg.nb);
+    W.sy_a = W.s0 / bg.bw;
+    W.sx_a = W.s0 - W.sy_a * bg.bw;
+    W.nrows = (W.s1 - 1) / bg.bw - W.sy_a + 1;
+    W.ncols = min(bg.bw, kWave);
+    W.col_base = (bg.bw <= kWave) ? 0 : W.sx_a;
+    W.rowv = 0;
+    W.colv = 0;
     const uint64_t lanes = ballot(L.has);
-    if (lanes == 0 || s0 >= s1) return;
-    int sy = s0 / bg.bw, sx = s0 - sy * bg.bw;
-    int s = s0;
-    while (s < s1) {
-        const uint64_t rowm = lanes & ballot((uint32_t)(sy - L.by0) < L.bh);
-        const int row_end = min(s1, s + (bg.bw - sx));
-        if (rowm != 0) {
-            for (; s < row_end; ++s, ++sx) {
-                const uint64_t m = rowm & ballot((uint32_t)(sx - L.bx0) < L.bw);
-                if (m != 0) f(s - s0, m);
-            }
-        }
-        s = row_end;
-        sx = 0;
-        ++sy;
+    if (lanes == 0) return W;
+    for (int j = 0; j < W.nrows; ++j) {
+        const uint64_t m = lanes & ballot((uint32_t)(W.sy_a + j - L.by0) < L.bh);
+        W.rowv = (lane == j) ? m : W.rowv;
     }
+    for (int j = 0; j < W.ncols; ++j) {
+        int c = W.col_base + j;
+        c -= (c >= bg.bw) ? bg.bw : 0;
+        const uint64_t m = ballot((uint32_t)(c - L.bx0) < L.bw);
+        W.colv = (lane == j) ? m : W.colv;
+    }
+    return W;
+}
+
+// Index of block column sx among the window's columns.
+__device__ __forceinline__ int window_col(const WindowMasks& W, const BlockGrid& bg, int sx) {
+    const int d = sx - W.col_base;
+    return d < 0 ? d + bg.bw : d;
 }
 
 // counts[b * cstride + c] = how many of chunk c's 64 ranks meet block b, for
-// every block (zeros included).
+// every block (zeros included); lane l counts block 64 w + l.
 __global__ __launch_bounds__(kThreads) void block_count_kernel(
     int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects, BlockGrid bg,
     int chunks, int windows, int cstride, uint32_t* __restrict__ counts) {
@@ -155,12 +181,13 @@ __global__ __launch_bounds__(kThreads) void block_count_kernel(
     const ChunkWindow cw = chunk_window(windows);
     if (cw.chunk >= chunks) return;
     const RankLane L = rank_lane(n, perm, rects, (int64_t)cw.chunk * kWave + lane);
-    uint32_t c = 0;
-    walk_window(L, bg, cw.window, [&](int idx, uint64_t m) {
-        c = (lane == idx) ? (uint32_t)popc64(m) : c;
-    });
-    const int b = cw.window * kWave + lane;
-    if (b < bg.nb) counts[(size_t)b * cstride + cw.chunk] = c;
+    const WindowMasks W = window_masks(L, bg, cw.window);
+    const int s = W.s0 + lane;
+    const int sy = (W.sx_a + lane) / bg.bw;  // rows below sy_a
+    const int sx = W.sx_a + lane - sy * bg.bw;
+    const uint64_t m = lane_u64(W.rowv, min(sy, kWave - 1)) &
+                       lane_u64(W.colv, min(window_col(W, bg, sx), kWave - 1));
+    if (s < W.s1) counts[(size_t)s * cstride + cw.chunk] = (uint32_t)popc64(m);
 }
 
 // Per block b: the chunk counts replaced by block_start[b] + their exclusive
@@ -198,45 +225,55 @@ __global__ __launch_bounds__(kThreads) void block_scan_kernel(
 
 // Each rank's Gaussian id into the lists of the blocks it meets, at the
 // chunk's position in the block plus the lane's rank among the chunk's lanes
-// meeting the block.  Positions at or beyond cap are dropped.
+// meeting the block.  Each lane walks its own blocks in the window.  Positions
+// at or beyond cap are dropped.
 __global__ __launch_bounds__(kThreads) void block_scatter_kernel(
     int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects, BlockGrid bg,
     int chunks, int windows, int cstride, const uint32_t* __restrict__ pos,
     uint32_t* __restrict__ lists, uint64_t cap) {
-    const int lane = lane_id();
+    __shared__ uint64_t s_row[kWavesPer][kWave];
+    __shared__ uint64_t s_col[kWavesPer][kWave];
+    __shared__ uint32_t s_base[kWavesPer][kWave];
+    const int lane = lane_id(), wave = threadIdx.x >> 6;
     const ChunkWindow cw = chunk_window(windows);
     if (cw.chunk >= chunks) return;
     const RankLane L = rank_lane(n, perm, rects, (int64_t)cw.chunk * kWave + lane);
-    const int b = cw.window * kWave + lane;
-    const uint32_t base = (b < bg.nb) ? pos[(size_t)b * cstride + cw.chunk] : 0u;
-    walk_window(L, bg, cw.window, [&](int idx, uint64_t m) {
-        const uint64_t p =
-            (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)base, idx) + rank_in(m);
-        if (((m >> lane) & 1ull) && p < cap) lists[p] = L.g;
-    });
+    const WindowMasks W = window_masks(L, bg, cw.window);
+    const int b = W.s0 + lane;
+    s_row[wave][lane] = W.rowv;
+    s_col[wave][lane] = W.colv;
+    s_base[wave][lane] = (b < W.s1) ? pos[(size_t)b * cstride + cw.chunk] : 0u;
+    __builtin_amdgcn_wave_barrier();
+    if (!L.has) return;
+    const uint64_t below = lanemask_lt();
+    const int y1 = min(L.by0 + (int)L.bh, W.sy_a + W.nrows);
+    for (int sy = max(L.by0, W.sy_a); sy < y1; ++sy) {
+        const uint64_t rm = s_row[wave][sy - W.sy_a];
+        for (int sx = L.bx0; sx < L.bx0 + (int)L.bw; ++sx) {
+            const int s = sy * bg.bw + sx;
+            if (s < W.s0 || s >= W.s1) continue;
+            const uint64_t m = rm & s_col[wave][window_col(W, bg, sx)];
+            const uint64_t p = (uint64_t)s_base[wave][s - W.s0] + (uint64_t)popc64(m & below);
+            if (p < cap) lists[p] = L.g;
+        }
+    }
 }
 
 // ---- level 2: block lists -> tile lists ------------------------------------
 
 // One lane of a level-2 segment (64 consecutive entries of one block's list):
-// its Gaussian and the 8x8 bitmap (bit ly * 8 + lx) of the block's tiles its
-// rectangle covers, as two 32-bit halves (rows 0-3, rows 4-7).
+// its Gaussian and its rectangle within the block's 8x8 tiles (origin and
+// extent; extent 0 when the lane holds no entry).
 struct SegLane {
-    uint32_t g, lo, hi;
+    uint32_t g;
+    int lx0, ly0;
+    uint32_t lw, lh;
 };
-
-// Bytes [a, b) of a 32-bit word set (0 <= a, b <= 4).
-__device__ __forceinline__ uint32_t byte_span(int a, int b) {
-    if (b <= a) return 0u;
-    const uint32_t upto = (b >= 4) ? 0xffffffffu : ((1u << (8 * b)) - 1u);
-    const uint32_t below = (1u << (8 * a)) - 1u;  // a <= 3 here
-    return upto & ~below;
-}
 
 __device__ __forceinline__ SegLane seg_lane(const uint32_t* __restrict__ lists,
                                             const uint2* __restrict__ rects, uint32_t first,
                                             uint32_t end, int ox, int oy, uint64_t cap, int n) {
-    SegLane S{0u, 0u, 0u};
+    SegLane S{0u, 0, 0, 0u, 0u};
     const uint32_t e = first + (uint32_t)lane_id();
     if (e < end && e < cap) {
         const uint32_t g = lists[e];
@@ -246,13 +283,21 @@ __device__ __forceinline__ SegLane seg_lane(const uint32_t* __restrict__ lists,
         const int ly0 = min(max(t.y0 - oy, 0), 8), ly1 = min(max(t.y1 - oy, 0), 8);
         S.g = g;
         if (lx1 > lx0 && ly1 > ly0) {
-            const uint32_t row = ((1u << lx1) - 1u) & ~((1u << lx0) - 1u);
-            const uint32_t rep = row * 0x01010101u;
-            S.lo = rep & byte_span(min(ly0, 4), min(ly1, 4));
-            S.hi = rep & byte_span(max(ly0 - 4, 0), max(ly1 - 4, 0));
+            S.lx0 = lx0;
+            S.ly0 = ly0;
+            S.lw = (uint32_t)(lx1 - lx0);
+            S.lh = (uint32_t)(ly1 - ly0);
         }
     }
     return S;
+}
+
+// Lanes covering tile row r / tile column c of the block.
+__device__ __forceinline__ uint64_t seg_row(const SegLane& S, int r) {
+    return ballot((uint32_t)(r - S.ly0) < S.lh);
+}
+__device__ __forceinline__ uint64_t seg_col(const SegLane& S, int c) {
+    return ballot((uint32_t)(c - S.lx0) < S.lw);
 }
 
 struct SegInfo {
@@ -274,13 +319,9 @@ __device__ __forceinline__ SegInfo seg_info(uint32_t k, const uint32_t* __restri
     return I;
 }
 
-// Bit t of the lane's bitmap (t wave-uniform after unrolling).
-__device__ __forceinline__ bool bit_of(const SegLane& S, int t) {
-    return ((t < 32 ? (S.lo >> t) : (S.hi >> (t - 32))) & 1u) != 0u;
-}
-
-// tcount[k * 64 + t] = entries of segment k covering the block's tile t.
-// Segments k < seg_start[nb] (at most seg_cap), grid-strided.
+// tcount[k * 64 + t] = entries of segment k covering the block's tile t
+// (rows[t / 8] & cols[t % 8]).  Segments k < seg_start[nb] (at most
+// seg_cap), grid-strided.
 __global__ __launch_bounds__(kThreads) void tile_count_kernel(
     int n, BlockGrid bg, const uint32_t* __restrict__ seg_owner,
     const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ block_start,
@@ -293,13 +334,15 @@ __global__ __launch_bounds__(kThreads) void tile_count_kernel(
          k += stride) {
         const SegInfo I = seg_info(k, seg_owner, seg_start, block_start, bg.bw, bg.nb);
         const SegLane S = seg_lane(lists, rects, I.first, I.end, I.ox, I.oy, cap, n);
-        uint32_t c = 0;
+        uint64_t rowv = 0, colv = 0;
 #pragma unroll
-        for (int t = 0; t < 64; ++t) {
-            const uint64_t m = ballot(bit_of(S, t));
-            c = (lane == t) ? (uint32_t)popc64(m) : c;
+        for (int j = 0; j < 8; ++j) {
+            const uint64_t r = seg_row(S, j), c = seg_col(S, j);
+            rowv = (lane == j) ? r : rowv;
+            colv = (lane == j) ? c : colv;
         }
-        tcount[(size_t)k * kWave + lane] = c;
+        const uint64_t m = lane_u64(rowv, lane >> 3) & lane_u64(colv, lane & 7);
+        tcount[(size_t)k * kWave + lane] = (uint32_t)popc64(m);
     }
 }
 
@@ -370,8 +413,9 @@ __global__ __launch_bounds__(kScanThreads) void tile_starts_kernel(
 }
 
 // Each segment entry's Gaussian id into the lists of the tiles it covers, at
-// the tile's start + the segment's prefix + the lane's rank.  Positions at or
-// beyond m are dropped.
+// the tile's start + the segment's prefix + the lane's rank.  The tile masks
+// rows[t / 8] & cols[t % 8] are wave-uniform.  Positions at or beyond m are
+// dropped.
 __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
     int n, BlockGrid bg, const uint32_t* __restrict__ seg_owner,
     const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ block_start,
@@ -381,6 +425,7 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
     const uint32_t nseg = min(uniform(seg_start[bg.nb]), seg_cap);
     const uint32_t stride = gridDim.x * kWavesPer;
     const int lane = lane_id();
+    const uint64_t below = lanemask_lt();
     for (uint32_t k = uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6)); k < nseg;
          k += stride) {
         const SegInfo I = seg_info(k, seg_owner, seg_start, block_start, bg.bw, bg.nb);
@@ -391,14 +436,19 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
         if (tx < bg.tiles_x && ty < bg.tiles_y)
             base = (uint32_t)ranges[(size_t)ty * bg.tiles_x + tx].x +
                    tcount[(size_t)k * kWave + lane];
+        uint64_t rows[8], cols[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            rows[j] = seg_row(S, j);
+            cols[j] = seg_col(S, j);
+        }
 #pragma unroll
         for (int t = 0; t < 64; ++t) {
-            const bool cov = bit_of(S, t);
-            const uint64_t mk = ballot(cov);
+            const uint64_t mk = rows[t >> 3] & cols[t & 7];
             if (mk != 0) {
-                const uint64_t p =
-                    (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)base, t) + rank_in(mk);
-                if (cov && p < m) ids[p] = S.g;
+                const uint64_t p = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)base, t) +
+                                   (uint64_t)popc64(mk & below);
+                if (((mk >> lane) & 1ull) && p < m) ids[p] = S.g;
             }
         }
     }
