@@ -221,6 +221,13 @@ Misc* pinned_misc() {
     return p;
 }
 
+// Marks the pair count's arrival in pinned memory (one per host thread).
+hipEvent_t count_event() {
+    thread_local hipEvent_t e = nullptr;
+    if (!e && hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) e = nullptr;
+    return e;
+}
+
 int ref_quat_mode() {
     static const int mode = [] {
         const char* v = std::getenv("GSR_REFERENCE_QUAT_GRAD");
@@ -388,25 +395,39 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
                         at<uint32_t>(bin_ws, L.seg_start), st),
                     "rasterize: block starts");
     }
-    {
+    Misc* host = pinned_misc();
+    if (!host) return fail(GSR_ERR_HIP, "rasterize: pinned host buffer allocation failed");
+    auto depth_sort = [&]() -> int {
         StageTimer timer("depth_sort", st);
         GSR_HIP(gsr::launch_radix_sort(dk0, dv0, at<uint32_t>(bin_ws, L.dk1),
                                        at<uint32_t>(bin_ws, L.dv1), (uint64_t)n, 0, kDepthPasses,
                                        at<void>(bin_ws, L.sortctl), err, st,
                                        /*hist_ready=*/true),
                 "rasterize: depth sort");
-    }
-    if (!blocks) {
+        return GSR_OK;
+    };
+    if (blocks) {
+        // The pair count is final after bin_count: read it back, queue the
+        // depth sort behind the copy and wait only for the copy, so the sort
+        // runs while the host returns and queues the render.  A spin-bound
+        // error of the sort stays in the status word (gsr_rasterize_status).
+        hipEvent_t ev = count_event();
+        if (!ev) return fail(GSR_ERR_HIP, "rasterize: event creation failed");
+        GSR_HIP(hipMemcpyAsync(host, misc, sizeof(Misc), hipMemcpyDeviceToHost, st),
+                "rasterize: read pair count");
+        GSR_HIP(hipEventRecord(ev, st), "rasterize: record");
+        if (int rc = depth_sort()) return rc;
+        GSR_HIP(hipEventSynchronize(ev), "rasterize: synchronize");
+    } else {
+        if (int rc = depth_sort()) return rc;
         StageTimer timer("scan", st);
         GSR_HIP(gsr::launch_scan_counts(n, dv0, counts, at<uint32_t>(bin_ws, L.offsets),
                                         &misc->total, at<void>(bin_ws, L.scanctl), err, st),
                 "rasterize: scan");
+        GSR_HIP(hipMemcpyAsync(host, misc, sizeof(Misc), hipMemcpyDeviceToHost, st),
+                "rasterize: read pair count");
+        GSR_HIP(hipStreamSynchronize(st), "rasterize: synchronize");
     }
-    Misc* host = pinned_misc();
-    if (!host) return fail(GSR_ERR_HIP, "rasterize: pinned host buffer allocation failed");
-    GSR_HIP(hipMemcpyAsync(host, misc, sizeof(Misc), hipMemcpyDeviceToHost, st),
-            "rasterize: read pair count");
-    GSR_HIP(hipStreamSynchronize(st), "rasterize: synchronize");
     if (host->err) return fail(GSR_ERR_DEVICE, "rasterize: look-back spin bound reached");
     if (host->total > (uint64_t)kMaxPairs)
         return fail(GSR_ERR_TOO_MANY_PAIRS,

@@ -11,7 +11,8 @@
  *   img [H,W,3], final_T [H,W], n_contrib [H,W] int32,
  *   sorted_ids [M] int32, tile_ranges [T,2] int32, T = ceil(W/16)*ceil(H/16).
  * `stream` is a hipStream_t (NULL = the null stream); all work is enqueued
- * on it.  Only gsr_rasterize_bin and gsr_rasterize_status synchronize it.
+ * on it.  Only gsr_rasterize_bin (for the pair count) and gsr_rasterize_status
+ * wait on it.
  *
  * Every entry point returns GSR_OK or an error code; gsr_last_error() gives
  * the calling thread's message for the last failure.  Outputs are fully
@@ -65,9 +66,10 @@ int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, co
  * csrc/forward/rasterize.cu:284-487; bound as `rasterize` at
  * csrc/bindings.cpp:50-70,144), split where the reference itself reads the
  * pair count back to the host (rasterize.cu:382-390):
- *   1. gsr_rasterize_bin: per-Gaussian tile counts, depth order, pair
- *      offsets; writes M to *num_pairs (synchronizes `stream`).
- *   2. gsr_rasterize_render: pair emission, tile sort, tile ranges, blend.
+ *   1. gsr_rasterize_bin: per-Gaussian tile rectangles and counts, the depth
+ *      order; writes M to *num_pairs (waits for the pair count on `stream`;
+ *      the depth sort may still be running on the stream when it returns).
+ *   2. gsr_rasterize_render: tile binning (sorted ids, tile ranges), blend.
  * bin_ws (gsr_bin_workspace_bytes) must stay untouched between the calls;
  * sort_ws is sized by gsr_sort_workspace_bytes(M, ...).  sorted_keys
  * (optional, may be NULL) receives the reference's 64-bit sort keys
@@ -83,8 +85,9 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                          size_t sort_ws_bytes, int32_t* sorted_ids, int32_t* tile_ranges,
                          float* img, float* final_T, int32_t* n_contrib, uint64_t* sorted_keys,
                          void* stream);
-/* Synchronizes `stream` and reports GSR_ERR_DEVICE if a sort or scan kernel of
- * the last bin/render calls on this bin_ws hit its look-back spin bound. */
+/* Synchronizes `stream` and reports GSR_ERR_DEVICE if a kernel of the last
+ * bin/render calls on this bin_ws hit its look-back spin bound or found
+ * inconsistent counts. */
 int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream);
 
 /* Replaces launch_backward_rasterization (csrc/backward/rasterize_backward.h:5,

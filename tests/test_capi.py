@@ -106,3 +106,63 @@ def test_c_abi_project_matches_extension(lib, crc, device):
     torch.cuda.synchronize()
     for a, b in zip(out, want):
         assert torch.equal(a, b)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("binning", ["blocks", "sort"])
+def test_c_abi_rasterize_matches_extension_and_reports_no_error(lib, crc, device, monkeypatch,
+                                                                 binning):
+    """gsr_rasterize_bin + gsr_rasterize_render through ctypes give the extension's
+    sorted ids, tile ranges and image, and gsr_rasterize_status then finds no
+    device-side error (look-back spin bound, inconsistent counts)."""
+    import torch
+
+    from gaussian_splatting import synthetic
+
+    if binning == "sort":
+        monkeypatch.setenv("GSR_TILE_BINNING", "sort")
+    sc = synthetic.config_scene("c3", requires_grad=False, n=20_000, width=480, height=270,
+                                device=device)
+    g, v = sc.gaussians, sc.view
+    n, H, W = g.mu.shape[0], int(v["height"]), int(v["width"])
+    mean2d, cov2d, depth = crc.project(n, g.mu.contiguous(), g.q.contiguous(), g.s.contiguous(),
+                                       v["R"].contiguous(), v["T"].contiguous(), float(v["fx"]),
+                                       float(v["fy"]), float(v["cx"]), float(v["cy"]))
+    cam = crc.camera_position(v["R"].contiguous(), v["T"].contiguous())
+    colors = crc.SH(n, cam, g.mu.contiguous(), g.A.contiguous(), g.k_j.contiguous())
+    alpha = torch.sigmoid(g.alpha).contiguous().reshape(-1)
+    img_w, ids_w, rng_w, _, _, _ = crc.rasterize_with_keys(n, depth, mean2d, cov2d, colors,
+                                                           alpha, H, W)
+    vp = lambda t: ctypes.c_void_p(t.data_ptr())
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sz, i64 = ctypes.c_size_t, ctypes.c_int64
+    T = ((W + 15) // 16) * ((H + 15) // 16)
+    bb = lib.gsr_bin_workspace_bytes(n, H, W)
+    bws = torch.empty(bb, dtype=torch.uint8, device=device)
+    m = i64()
+    lib.gsr_rasterize_bin.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 3 + [
+        ctypes.c_int, ctypes.c_int, ctypes.c_void_p, sz, ctypes.POINTER(i64), ctypes.c_void_p]
+    rc = lib.gsr_rasterize_bin(n, vp(depth), vp(mean2d), vp(cov2d), H, W, vp(bws), bb,
+                               ctypes.byref(m), stream)
+    assert rc == 0, lib.gsr_last_error()
+    assert m.value == ids_w.numel()
+    sb = lib.gsr_sort_workspace_bytes(m.value, n, H, W)
+    sws = torch.empty(sb, dtype=torch.uint8, device=device)
+    ids = torch.empty(m.value, dtype=torch.int32, device=device)
+    ranges = torch.full((T, 2), -7, dtype=torch.int32, device=device)
+    img = torch.empty(H, W, 3, device=device)
+    fT = torch.empty(H, W, device=device)
+    nc = torch.empty(H, W, dtype=torch.int32, device=device)
+    lib.gsr_rasterize_render.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 5 + [
+        ctypes.c_int, ctypes.c_int, ctypes.c_void_p, sz, i64, ctypes.c_void_p, sz] + \
+        [ctypes.c_void_p] * 7
+    rc = lib.gsr_rasterize_render(n, vp(depth), vp(mean2d), vp(cov2d), vp(colors), vp(alpha),
+                                  H, W, vp(bws), bb, m.value, vp(sws), sb, vp(ids), vp(ranges),
+                                  vp(img), vp(fT), vp(nc), None, stream)
+    assert rc == 0, lib.gsr_last_error()
+    lib.gsr_rasterize_status.argtypes = [ctypes.c_void_p, sz, ctypes.c_void_p]
+    assert lib.gsr_rasterize_status(vp(bws), bb, stream) == 0, lib.gsr_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(ids, ids_w)
+    assert torch.equal(ranges, rng_w.reshape(T, 2))
+    assert torch.equal(img, img_w.reshape(H, W, 3))
