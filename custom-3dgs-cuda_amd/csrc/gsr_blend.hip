@@ -131,7 +131,8 @@ __device__ __forceinline__ uint32_t strip_bits(const BlendRec& r, int tile, int 
 template <int kPix>
 __device__ __forceinline__ void stage_entry(const BlendRec* __restrict__ recs, int g, int n,
                                             int tile, int tiles_x, float4* s_a, float4* s_b,
-                                            float4* s_c, uint32_t* s_bits, int* s_id, int slot) {
+                                            float4* s_c, uint32_t* s_bits, int* s_id,
+                                            int slot) {
     BlendRec r;
     const bool ok = g >= 0 && g < n;
     if (ok) {
@@ -141,10 +142,14 @@ __device__ __forceinline__ void stage_entry(const BlendRec* __restrict__ recs, i
     }
     s_a[slot] = r.a;
     s_b[slot] = r.b;
-    s_c[slot] = r.c;
+    if (s_bits) s_c[slot] = r.c;
     // bit 31: opacity in [0, 0.99), so alpha = opacity * G is never clamped
     const uint32_t fast = (__float_as_uint(r.b.y) < __float_as_uint(kAlphaMax)) ? kFastExpBit : 0u;
-    s_bits[slot] = ok ? (strip_bits<kPix>(r, tile, tiles_x) | fast) : 0u;
+    const uint32_t bits = ok ? (strip_bits<kPix>(r, tile, tiles_x) | fast) : 0u;
+    if (s_bits)
+        s_bits[slot] = bits;
+    else  // in the record's unused fourth word
+        s_c[slot] = make_float4(r.c.x, r.c.y, r.c.z, __uint_as_float(bits));
     if (s_id) s_id[slot] = ok ? g : -1;
 }
 
@@ -184,9 +189,13 @@ __device__ __forceinline__ bool any_live(const FwdPixel (&p)[kPix]) {
     return l;
 }
 
-// Entry j's strip bits as a wave-uniform (scalar) value.
+// A staged entry's strip bits as a wave-uniform (scalar) value: from the
+// separate array, or from the record's unused fourth word.
 __device__ __forceinline__ uint32_t uniform_bits(const uint32_t* s_bits, int j) {
     return __builtin_amdgcn_readfirstlane(s_bits[j]);
+}
+__device__ __forceinline__ uint32_t uniform_bits(const float4& c) {
+    return __builtin_amdgcn_readfirstlane(__float_as_uint(c.w));
 }
 
 template <int kPix>
@@ -370,12 +379,12 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     __shared__ float4 s_a[kBatch];
     __shared__ float4 s_b[kBatch];
     __shared__ float4 s_c[kBatch];
-    __shared__ uint32_t s_bits[kBatch];
     __shared__ int s_id[kBatch];
     __shared__ float s_part[kWaves][kTerms][kBatch + 1];  // +1: the 9 writers hit 9 banks
     __shared__ uint32_t s_max[kWaves];
 
-    const int tile = order ? (int)order[blockIdx.x] : (int)blockIdx.x;
+    const int tile = __builtin_amdgcn_readfirstlane(order ? (int)order[blockIdx.x]
+                                                          : (int)blockIdx.x);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: uniform branches
     const uint32_t my_bit = 1u << wave;
@@ -399,7 +408,8 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     uint32_t tile_last = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) tile_last = max(tile_last, s_max[w]);
-    const int maxc = min((int)tile_last, end - start);
+    const int maxc = __builtin_amdgcn_readfirstlane(min((int)tile_last, end - start));
+    start = __builtin_amdgcn_readfirstlane(start);
     const int my_value = reduce9_value_of_lane(lane);
 
     for (int hi = maxc; hi > 0; hi -= kBatch) {
@@ -408,17 +418,17 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
         __syncthreads();
         if (tid < cnt)
             stage_entry<kPix>(recs, ids[start + lo + tid], n, tile, tiles_x, s_a, s_b, s_c,
-                              s_bits, s_id, tid);
+                              nullptr, s_id, tid);
         __syncthreads();
         for (int j = cnt - 1; j >= 0; --j) {
             const int contributor = lo + j + 1;
             float w9 = 0.0f;
             // wave-uniform skips: beyond every pixel's n_contrib, or culled
-            const uint32_t bits = uniform_bits(s_bits, j);
+            const float4 Cc = s_c[j];  // (b, conic.y, qthr, strip bits)
+            const uint32_t bits = uniform_bits(Cc);
             if (contributor <= wave_last && (bits & my_bit) != 0) {
                 const float4 A = s_a[j];
                 const float4 B = s_b[j];
-                const float2 Cc = *reinterpret_cast<const float2*>(&s_c[j]);  // (b, conic.y)
                 const float dx = fx - A.x;
                 const float dxdx = A.z * dx * dx;
                 const float wdx = A.w * dx;
