@@ -258,9 +258,9 @@ __global__ __launch_bounds__(kThreads) void blend_records_kernel(
     const float det_inv = (det > 0.0f) ? (1.0f / det) : 0.0f;
     const float cx = c * det_inv, cy = -b * det_inv, cz = a * det_inv;
     BlendRec r;
-    r.a = make_float4(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1], cx, 2.0f * cy);
-    r.b = make_float4(cz, alpha[i], colors[3 * (size_t)i], colors[3 * (size_t)i + 1]);
-    r.c = make_float4(colors[3 * (size_t)i + 2], cy, alpha_q_threshold(alpha[i]), 0.0f);
+    r.a = make_float4(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1], -0.5f * cx, -cy);
+    r.b = make_float4(-0.5f * cz, alpha[i], colors[3 * (size_t)i], colors[3 * (size_t)i + 1]);
+    r.c = make_float4(colors[3 * (size_t)i + 2], -0.5f * cy, alpha_q_threshold(alpha[i]), 0.0f);
     recs[i] = r;
 }
 

@@ -107,7 +107,8 @@ constexpr uint32_t kFastExpBit = 1u << 31;
 template <int kPix>
 __device__ __forceinline__ uint32_t strip_bits(const BlendRec& r, int tile, int tiles_x) {
     constexpr uint32_t kAll = (1u << Layout<kPix>::kWaves) - 1u;
-    const float A = r.a.z, B = r.c.y, C = r.b.x, thr = r.c.z;
+    // the conic from the record's scaled coefficients (exact)
+    const float A = -2.0f * r.a.z, B = -2.0f * r.c.y, C = -2.0f * r.b.x, thr = r.c.z;
     if (!(A > 0.0f) || !(C > 0.0f) || !((double)A * C - (double)B * B > 0.0)) return kAll;
     const float mx = r.a.x, my = r.a.y;
     const float rA = 1.0f / A, rC = 1.0f / C;
@@ -163,20 +164,29 @@ struct FwdPixel {
 
 __device__ __forceinline__ bool live(const FwdPixel& p) { return p.T >= kTransmittanceMin; }
 
+// power = -0.5 (cx dx^2 + 2 cy dx dy + cz dy^2) (rasterize.cu:249-251) with
+// its two additions fused, from the record's coefficients a = -cx/2 (A.z),
+// b = -cy (A.w), c = -cz/2 (B.x): fma(c dy, dy, fma(b dx, dy, (a dx) dx)).
+__device__ __forceinline__ float blend_power(float dx, float dy, const float4& A,
+                                             const float4& B) {
+    return __builtin_fmaf(B.x * dy, dy, __builtin_fmaf(A.w * dx, dy, (A.z * dx) * dx));
+}
+
 // One pixel's forward step for one list entry (rasterize.cu:243-268), with the
-// reference's skips as selects: the same fp32 operations in the same order.
+// reference's skips as selects: the same fp32 operations in the same order,
+// the colour sums fused (pix_color += colour * weight).
 __device__ __forceinline__ void fwd_step(FwdPixel& p, float fx, float fy, const float4& A,
                                          const float4& B, float cb, int contributor) {
     const float dx = fx - A.x;
     const float dy = fy - A.y;
-    const float power = -0.5f * (A.z * dx * dx + A.w * dx * dy + B.x * dy * dy);
+    const float power = blend_power(dx, dy, A, B);
     const float alpha = fminf(kAlphaMax, B.y * exp_blend(power));
     const bool blend = live(p) & !(power > 0.0f) & !(alpha < kAlphaMin);
     const float w = alpha * p.T;
     const float Tn = p.T * (1.0f - alpha);
-    p.C0 = blend ? p.C0 + B.z * w : p.C0;
-    p.C1 = blend ? p.C1 + B.w * w : p.C1;
-    p.C2 = blend ? p.C2 + cb * w : p.C2;
+    p.C0 = blend ? __builtin_fmaf(B.z, w, p.C0) : p.C0;
+    p.C1 = blend ? __builtin_fmaf(B.w, w, p.C1) : p.C1;
+    p.C2 = blend ? __builtin_fmaf(cb, w, p.C2) : p.C2;
     p.T = blend ? Tn : p.T;
     p.last = blend ? contributor : p.last;
 }
@@ -430,14 +440,16 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                 const float4 A = s_a[j];
                 const float4 B = s_b[j];
                 const float dx = fx - A.x;
-                const float dxdx = A.z * dx * dx;
-                const float wdx = A.w * dx;
+                // blend_power's shared column terms: (a dx) dx and b dx
+                const float adxdx = (A.z * dx) * dx;
+                const float bdx = A.w * dx;
                 BwdDecision d[kPix];
 #pragma unroll
                 for (int k = 0; k < kPix; ++k) {
-                    // the forward's power, bit for bit (rasterize.cu:249-251)
+                    // the forward's power, bit for bit (blend_power)
                     d[k].dy = fy[k] - A.y;
-                    d[k].power = -0.5f * (dxdx + wdx * d[k].dy + B.x * d[k].dy * d[k].dy);
+                    d[k].power = __builtin_fmaf(B.x * d[k].dy, d[k].dy,
+                                                __builtin_fmaf(bdx, d[k].dy, adxdx));
                 }
                 bool exact = (bits & kFastExpBit) == 0;
                 if (!exact) {
@@ -486,8 +498,10 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                     const float P1 = dx * S0;
                     // mean terms formed in the lane, before the wide sum, as the
                     // per-pixel dpw (conic.x dx + conic.y dy) is
-                    const float cy = Cc.y;
-                    const float vals[kTerms] = {A.z * P1 + cy * P2, cy * P1 + B.x * P2, dx * P1,
+                    // with the record's -cx/2, -cy/2 (Cc.y), -cz/2: -1/2 of
+                    // (cx P1 + cy P2, cy P1 + cz P2), rescaled at the flush
+                    const float hy = Cc.y;
+                    const float vals[kTerms] = {A.z * P1 + hy * P2, hy * P1 + B.x * P2, dx * P1,
                                                 dx * P2, P5, c0, c1, c2, dop};
                     w9 = wave_reduce9(vals);
                 }
@@ -509,8 +523,8 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
             }
             if (g >= 0 && any) {
                 float t[kTerms];
-                t[0] = tot[0];         // dL/dmean.x
-                t[1] = tot[1];         // dL/dmean.y
+                t[0] = -2.0f * tot[0];  // dL/dmean.x
+                t[1] = -2.0f * tot[1];  // dL/dmean.y
                 t[2] = -0.5f * tot[2];  // dL/dconic.x
                 t[3] = -tot[3];        // dL/dconic.y (full off-diagonal)
                 t[4] = -0.5f * tot[4];  // dL/dconic.z
@@ -531,7 +545,8 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                     gs.flags[slot] = 1;
                 } else {
                     // not a pair of the rectangles: straight to the outputs
-                    const float cx = s_a[tid].z, cy = s_c[tid].y, cz = s_b[tid].x;
+                    const float cx = -2.0f * s_a[tid].z, cy = -2.0f * s_c[tid].y,
+                                cz = -2.0f * s_b[tid].x;
                     float dc[3];
                     conic_to_cov_grad(cx, cy, cz, t[2], t[3], t[4], dc);
                     unsafeAtomicAdd(&dmean[2 * (size_t)g], t[0]);
@@ -597,7 +612,7 @@ __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
     if (g < n && sub == 0) {
         const BlendRec r = recs[g];
         float dc[3];
-        conic_to_cov_grad(r.a.z, r.c.y, r.b.x, t[2], t[3], t[4], dc);
+        conic_to_cov_grad(-2.0f * r.a.z, -2.0f * r.c.y, -2.0f * r.b.x, t[2], t[3], t[4], dc);
         const float m0 = dmean[2 * (size_t)g], m1 = dmean[2 * (size_t)g + 1];
         const float c0 = dcov[3 * (size_t)g], c1 = dcov[3 * (size_t)g + 1],
                     c2 = dcov[3 * (size_t)g + 2];
@@ -683,7 +698,7 @@ __global__ __launch_bounds__(kEstTilesPerBlock * kWave) void tile_work_fwd_kerne
             float l = 0.0f;
             if (ok) {
                 const float dx = sx[q] - r.a.x, dy = sy[q] - r.a.y;
-                const float power = -0.5f * (r.a.z * dx * dx + r.a.w * dx * dy + r.b.x * dy * dy);
+                const float power = blend_power(dx, dy, r.a, r.b);
                 const float alpha = fminf(kAlphaMax, r.b.y * __expf(power));
                 l = (power <= 0.0f && alpha >= kAlphaMin) ? __logf(1.0f - alpha) : 0.0f;
             }

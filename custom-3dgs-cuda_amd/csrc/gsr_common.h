@@ -4,7 +4,9 @@
 // forward math keeps the reference's operation order (one rounding per
 // multiply and add), so projected means, covariances, colours and the blend's
 // transmittance sequence are bit-identical to the CPU restatement.  The only
-// fused multiply-adds are the explicit fmaf calls below.
+// fused multiply-adds in that math are explicit fmaf calls (the exp below,
+// and the blend's power and colour sums, which the CPU restatement fuses in
+// the same places).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -236,9 +238,11 @@ constexpr uint64_t kValueMask = (1ull << 62) - 1;
 constexpr uint32_t kSpinLimit = 1u << 22;
 
 // Per-Gaussian blend record (48 B), built once per frame from the
-// rasterize inputs: (mean.x, mean.y, conic.x, 2*conic.y), (conic.z,
-// opacity, r, g), (b, conic.y, qthr, -).  2*conic.y is an exact scaling of
-// the reference's conic.y, so ((2*cy)*dx)*dy is the same product it forms.
+// rasterize inputs: (mean.x, mean.y, -conic.x/2, -conic.y), (-conic.z/2,
+// opacity, r, g), (b, -conic.y/2, qthr, -).  The conic terms carry the
+// power's -1/2 (exact scalings by powers of two), so the blend evaluates
+// power = fma(c dy, dy, fma(b dx, dy, (a dx) dx)) without the final multiply;
+// the conic itself is -2 times them, exactly.
 // qthr bounds the quadratic form from above for any pixel that can reach
 // alpha >= 1/255 (conservative; negative when the opacity alone rules every
 // pixel out): the blends use it to skip entries for whole pixel regions

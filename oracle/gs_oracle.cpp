@@ -10,8 +10,12 @@
 //   * float  — the reference's fp32 semantics, operation by operation, in the
 //              order the reference source writes them.  Built with
 //              -ffp-contract=off so no multiply-add is fused except the
-//              explicit fmaf calls inside orc_expf.  The HIP kernels follow
-//              the same order, so fp32 forward outputs agree bit for bit.
+//              explicit fma calls: inside orc_expf, and in the blend's
+//              power and colour sums, where they stand for the
+//              multiply-adds nvcc forms from the reference's a * b + c
+//              expressions by default (--fmad=true).  The HIP kernels
+//              evaluate the same operations, so fp32 forward outputs agree
+//              bit for bit.
 //   * double — the same mathematics in float64 (std::exp), used for tight
 //              finite-difference pins of the backward formulas.
 //
@@ -324,10 +328,15 @@ void conic_of_t(const T* cov, T* cn) {
     cn[2] = cov[0] * det_inv;
 }
 
-// power = -0.5 (cx dx^2 + 2 cy dx dy + cz dy^2) (rasterize.cu:249-251).
+// power = -0.5 (cx dx^2 + 2 cy dx dy + cz dy^2) (rasterize.cu:249-251), the
+// two additions fused: -0.5 fma(cz dy, dy, fma(2 cy dx, dy, (cx dx) dx)).
+// The -0.5 is applied to the coefficients first (exact scalings by powers of
+// two), which gives the same value: fma(c dy, dy, fma(b dx, dy, (a dx) dx))
+// with a = -cx/2, b = -cy, c = -cz/2.
 template <typename T>
 inline T power_of(const T* cn, T dx, T dy) {
-    return T(-0.5f) * (cn[0] * dx * dx + T(2) * cn[1] * dx * dy + cn[2] * dy * dy);
+    const T a = T(-0.5f) * cn[0], b = -cn[1], c = T(-0.5f) * cn[2];
+    return std::fma(c * dy, dy, std::fma(b * dx, dy, (a * dx) * dx));
 }
 
 // ----- a8: per-pixel front-to-back blend (rasterize.cu:184-280) ------------
@@ -359,7 +368,9 @@ void blend_fwd_all(int n, int H, int W, const int32_t* ranges, const int32_t* id
                     T a = std::fmin(T(0.99f), alpha[g] * M<T>::exp(power));
                     if (a < T(1.0f / 255.0f)) continue;
                     T wgt = a * Tr;
-                    for (int ch = 0; ch < 3; ++ch) C[ch] = C[ch] + colors[3 * (size_t)g + ch] * wgt;
+                    // pix_color += colour * weight, fused (rasterize.cu:259-261)
+                    for (int ch = 0; ch < 3; ++ch)
+                        C[ch] = std::fma(colors[3 * (size_t)g + ch], wgt, C[ch]);
                     Tr = Tr * (T(1) - a);
                     last = contributor;
                     if (Tr < T(1e-4f)) break;
