@@ -33,6 +33,9 @@
 // first (tile_order_kernel), so long tiles do not start last.
 #include <cstdlib>
 
+#include <map>
+#include <mutex>
+
 #include "gsr_internal.h"
 #include "gsr_common.h"
 
@@ -798,6 +801,26 @@ int bwd_pix() {
     return p;
 }
 
+// Work-groups of `kernel` (with `threads` threads, no dynamic LDS) that fit on
+// the current device at once: per-CU occupancy times the CU count, cached.
+unsigned resident_groups(const void* kernel, int threads) {
+    static std::mutex mu;
+    static std::map<std::pair<int, const void*>, unsigned> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1;
+    std::lock_guard<std::mutex> lock(mu);
+    const auto key = std::make_pair(dev, kernel);
+    auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 1;
+    const unsigned g = (unsigned)std::max(1, per_cu * cus);
+    cache.emplace(key, g);
+    return g;
+}
+
 }  // namespace
 
 bool launch_order_enabled() { return tile_order_enabled(); }
@@ -861,7 +884,17 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
     const auto* rc = static_cast<const BlendRec*>(recs);
-    if (bwd_pix() == 2)
+    // The 64-entry batch halves the work-group's LDS (8 KB), so registers, not
+    // LDS, bound the resident waves; it pays when the grid does not fit on the
+    // device at once.  When it would, the 128-entry batch leaves part of the
+    // grid to be placed as CUs free up, which balances the long tiles better.
+    if (bwd_pix() == 2 && tiles > resident_groups(reinterpret_cast<const void*>(
+                                      &blend_bwd_kernel<2, 64>),
+                                  Layout<2>::kThreads))
+        hipLaunchKernelGGL((blend_bwd_kernel<2, 64>), dim3(tiles), dim3(Layout<2>::kThreads), 0,
+                           st, n, H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib,
+                           dmean, dcov, dcol, dalpha, gs, order);
+    else if (bwd_pix() == 2)
         hipLaunchKernelGGL((blend_bwd_kernel<2, 128>), dim3(tiles), dim3(Layout<2>::kThreads), 0,
                            st, n, H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib,
                            dmean, dcov, dcol, dalpha, gs, order);

@@ -256,11 +256,14 @@ def _backward_case(crc, device, a, seed=3, corrupt=False):
 
 
 @pytest.mark.parametrize("name,kw", [("c1", dict()), ("c3", dict(n=20_000, width=480, height=270)),
-                                     ("c5", dict(n=20_000, width=320, height=192))],
-                         ids=["c1", "c3", "c5"])
+                                     ("c5", dict(n=20_000, width=320, height=192)),
+                                     ("c3_1080p", dict(n=60_000, width=1920, height=1080))],
+                         ids=["c1", "c3", "c5", "c3_1080p"])
 def test_rasterize_backward_parity(crc, device, name, kw):
+    """c3_1080p: 8160 tiles, more than fit on the device at once, so the
+    backward runs its 64-entry-batch kernel."""
     print(f"[gpu] backward parity {name} {kw}", flush=True)
-    a = scene_arrays(synthetic.config_scene(name, requires_grad=False, **kw))
+    a = scene_arrays(synthetic.config_scene(name.split("_")[0], requires_grad=False, **kw))
     _backward_case(crc, device, a)
 
 
