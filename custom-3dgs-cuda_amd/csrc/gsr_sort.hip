@@ -249,6 +249,45 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     const uint64_t part = s_part;
     const uint64_t base = part * kSortPartition;
     const int nvalid = (int)min((uint64_t)kSortPartition, n - base);
+    if constexpr (!kEmit) {
+        // Every key has the same digit: the stable pass is the identity, so the
+        // partition is copied through (no ranking, no look-back).
+        if (__syncthreads_or(hist[tid] == (uint32_t)n)) {
+            // 16-byte copies when every array is 16-byte aligned (partitions start
+            // 16 KB apart), the rest word by word
+            const uint32_t mask = kPacked ? ((1u << gbits) - 1u) : 0u;
+            const uintptr_t al = reinterpret_cast<uintptr_t>(kin) |
+                                 reinterpret_cast<uintptr_t>(kout) |
+                                 reinterpret_cast<uintptr_t>(vin) |
+                                 reinterpret_cast<uintptr_t>(vout);
+            const int n4 = (al & 15) ? 0 : nvalid / 4;
+            const uint4* k4 = reinterpret_cast<const uint4*>(kin + base);
+            uint4* ko4 = reinterpret_cast<uint4*>(kout + base);
+#pragma unroll 4
+            for (int e = tid; e < n4; e += kSortThreads) {
+                const uint4 k = k4[e];
+                ko4[e] = k;
+                if constexpr (kPacked) {
+                    if (vout)
+                        reinterpret_cast<uint4*>(vout + base)[e] =
+                            make_uint4(k.x & mask, k.y & mask, k.z & mask, k.w & mask);
+                } else {
+                    reinterpret_cast<uint4*>(vout + base)[e] =
+                        reinterpret_cast<const uint4*>(vin + base)[e];
+                }
+            }
+            for (int e = 4 * n4 + tid; e < nvalid; e += kSortThreads) {
+                const uint32_t k = kin[base + e];
+                kout[base + e] = k;
+                if constexpr (kPacked) {
+                    if (vout) vout[base + e] = k & mask;
+                } else {
+                    vout[base + e] = vin[base + e];
+                }
+            }
+            return;
+        }
+    }
 
     uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
     (void)val;
