@@ -17,6 +17,7 @@
 
 #include "gsr_internal.h"
 #include "gsr_common.h"
+#include "gsr_group.h"
 
 namespace gsr {
 
@@ -90,13 +91,17 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     const float* __restrict__ depth, int H, int W, uint32_t* __restrict__ counts,
     uint2* __restrict__ rects, uint32_t* __restrict__ dkeys, uint32_t* __restrict__ dvals,
     int passes, uint32_t* __restrict__ tile_hist, uint32_t* __restrict__ depth_hist,
-    BlockGrid bg, uint32_t* __restrict__ block_hist, uint64_t* __restrict__ pair_total) {
+    BlockGrid bg, uint32_t* __restrict__ block_hist, uint64_t* __restrict__ pair_total,
+    uint32_t* __restrict__ block_start, uint32_t* __restrict__ seg_start,
+    uint32_t* __restrict__ done) {
     __shared__ int s_d0[kRadixBins + 1];
     __shared__ uint32_t s_h[3][kRadixBins];
     __shared__ uint32_t s_dh[4][kRadixBins];
     __shared__ uint32_t s_bh[kMaxBlocks];
     __shared__ uint32_t s_full[kThreads / kWave];
     __shared__ uint32_t s_scan[kThreads / kWave];
+    __shared__ uint32_t s_v[kThreads / kWave];
+    __shared__ uint32_t s_flag;
     const int tid = threadIdx.x;
     const bool blocks = block_hist != nullptr;
     for (int j = tid; j <= kRadixBins; j += kThreads) s_d0[j] = 0;
@@ -161,6 +166,9 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
         const uint64_t wp = wave_sum_u64(pairs);
         if ((tid & 63) == 0 && wp) atomicAdd(reinterpret_cast<unsigned long long*>(pair_total),
                                              (unsigned long long)wp);
+        // the last work-group to finish turns the histogram into the starts
+        if (last_group(done, &s_flag))
+            block_starts_body<kThreads>(bg.nb, block_hist, block_start, seg_start, s_scan, s_v);
     }
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
@@ -272,17 +280,19 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
+                            uint32_t* block_start, uint32_t* seg_start, uint32_t* done,
                             hipStream_t st) {
     if (n <= 0) return hipSuccess;
     if (tile_passes < 0 || tile_passes > 4) return hipErrorInvalidValue;
     const BlockGrid bg = block_grid((W + 15) / 16, (H + 15) / 16);
-    if (block_hist && (bg.nb > kMaxBlocks || !pair_total)) return hipErrorInvalidValue;
-    // at most one work-group per CU: the histogram flush costs one global
-    // atomic per bin and work-group
-    const unsigned blocks = std::min(blocks_for(n), 256u);
+    if (block_hist && (bg.nb > kMaxBlocks || !pair_total || !block_start || !seg_start || !done))
+        return hipErrorInvalidValue;
+    // at most one work-group per two CUs: the histogram flush costs one
+    // global atomic per bin and work-group
+    const unsigned blocks = std::min(blocks_for(n), 128u);
     hipLaunchKernelGGL(bin_count_kernel, dim3(blocks), dim3(kThreads), 0, st, n, mean2d, cov2d,
                        depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist,
-                       depth_hist, bg, block_hist, pair_total);
+                       depth_hist, bg, block_hist, pair_total, block_start, seg_start, done);
     return hipGetLastError();
 }
 

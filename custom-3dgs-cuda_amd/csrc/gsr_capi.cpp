@@ -76,9 +76,9 @@ int tile_key_bits(int64_t T) {
 
 // Misc block at the head of the bin workspace.
 struct Misc {
-    uint64_t total;  // pair count written by the scan
-    int err;         // set by a kernel that hit its look-back spin bound
-    int pad;
+    uint64_t total;       // pair count
+    int err;              // set by a kernel that hit its spin bound or found bad counts
+    uint32_t bin_done;    // bin_count's finished work-groups (left at zero)
 };
 
 // Which tile binning a frame uses: the two-level block binning, unless the
@@ -386,14 +386,10 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
                                       at<uint32_t>(bin_ws, L.tilehist),
                                       at<uint32_t>(bin_ws, L.sortctl),
                                       blocks ? at<uint32_t>(bin_ws, L.blockhist) : nullptr,
-                                      blocks ? &misc->total : nullptr, st),
+                                      blocks ? &misc->total : nullptr,
+                                      at<uint32_t>(bin_ws, L.block_start),
+                                      at<uint32_t>(bin_ws, L.seg_start), &misc->bin_done, st),
                 "rasterize: count");
-        if (blocks)
-            GSR_HIP(gsr::launch_block_starts(
-                        gsr::block_grid(tiles_x_of(width), tiles_y_of(height)),
-                        at<uint32_t>(bin_ws, L.blockhist), at<uint32_t>(bin_ws, L.block_start),
-                        at<uint32_t>(bin_ws, L.seg_start), st),
-                    "rasterize: block starts");
     }
     Misc* host = pinned_misc();
     if (!host) return fail(GSR_ERR_HIP, "rasterize: pinned host buffer allocation failed");

@@ -1,0 +1,125 @@
+// gsr_group.h — work-group scans and the "last work-group" hand-off shared by
+// the binning kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "gsr_common.h"
+
+namespace gsr {
+
+// Work-group exclusive scan of one value per thread (kT threads); *total
+// receives the sum.  s_w holds kT / 64 words.  Ends with the LDS free for reuse.
+template <int kT>
+__device__ __forceinline__ uint32_t group_exclusive_scan(uint32_t v, uint32_t* s_w,
+                                                         uint32_t* total) {
+    constexpr int kW = kT / kWave;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t inc = wave_inclusive_scan(v);
+    if (lane == 63) s_w[wave] = inc;
+    __syncthreads();
+    uint32_t pre = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+        const uint32_t x = s_w[w];
+        pre += (w < wave) ? x : 0u;
+        all += x;
+    }
+    __syncthreads();
+    *total = all;
+    return pre + inc - v;
+}
+
+// Device-coherent 32-bit accesses for values one work-group hands to another
+// within a kernel (every XCD sees the latest value).
+__device__ __forceinline__ uint32_t load_agent_u32(const uint32_t* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_agent_u32(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// True in every thread of the last work-group of the grid to get here; that
+// work-group then sees every other work-group's writes made before its call
+// (release fence, counter, acquire fence).  The last one resets the counter,
+// so it starts at zero for the next launch.
+__device__ __forceinline__ bool last_group(uint32_t* done, uint32_t* s_flag) {
+    __threadfence();
+    if (threadIdx.x == 0) {
+        const uint32_t groups = gridDim.x * gridDim.y * gridDim.z;
+        *s_flag = (atomicAdd(done, 1u) == groups - 1u) ? 1u : 0u;
+    }
+    __syncthreads();
+    const bool last = *s_flag != 0;
+    if (last) {
+        __threadfence();
+        if (threadIdx.x == 0) store_agent_u32(done, 0u);
+    }
+    return last;
+}
+
+// block_start[b] / seg_start[b] (nb + 1 entries each): exclusive prefixes of
+// the block histogram and of its 64-entry segment counts.  One work-group of
+// kT threads; s_w and s_v hold kT / 64 words each.
+template <int kT>
+__device__ void block_starts_body(int nb, const uint32_t* hist, uint32_t* block_start,
+                                  uint32_t* seg_start, uint32_t* s_w, uint32_t* s_v) {
+    const int tid = threadIdx.x;
+    uint32_t carry = 0, scarry = 0;
+    for (int base = 0; base < nb; base += 4 * kT) {
+        const int i = base + 4 * tid;
+        uint32_t v[4], s[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            v[j] = (i + j < nb) ? load_agent_u32(hist + i + j) : 0u;
+            s[j] = (v[j] + kWave - 1) / kWave;
+        }
+        uint32_t tot, stot;
+        uint32_t p = carry + group_exclusive_scan<kT>(v[0] + v[1] + v[2] + v[3], s_w, &tot);
+        uint32_t q = scarry + group_exclusive_scan<kT>(s[0] + s[1] + s[2] + s[3], s_v, &stot);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (i + j < nb) {
+                block_start[i + j] = p;
+                seg_start[i + j] = q;
+            }
+            p += v[j];
+            q += s[j];
+        }
+        carry += tot;
+        scarry += stot;
+    }
+    if (tid == 0) {
+        block_start[nb] = carry;
+        seg_start[nb] = scarry;
+    }
+}
+
+// ranges[t] = [start, start + count) from the tile totals in tile order,
+// (0, 0) for tiles without pairs (rasterize.cu:140-166); a grand total other
+// than m sets err bit 2.  One work-group of kT threads; s_w holds kT / 64 words.
+template <int kT>
+__device__ void tile_starts_body(int T, const uint32_t* __restrict__ ttotal, uint64_t m,
+                                 int2* __restrict__ ranges, int* err, uint32_t* s_w) {
+    const int tid = threadIdx.x;
+    uint32_t carry = 0;
+    for (int base = 0; base < T; base += 4 * kT) {
+        const int i = base + 4 * tid;
+        uint32_t v[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = (i + j < T) ? ttotal[i + j] : 0u;
+        uint32_t tot;
+        uint32_t p = carry + group_exclusive_scan<kT>(v[0] + v[1] + v[2] + v[3], s_w, &tot);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            if (i + j < T)
+                ranges[i + j] = v[j] ? make_int2((int)p, (int)(p + v[j])) : make_int2(0, 0);
+            p += v[j];
+        }
+        carry += tot;
+    }
+    if (tid == 0 && (uint64_t)carry != m) atomicOr(err, 2);
+}
+
+}  // namespace gsr

@@ -106,10 +106,6 @@ BlockGrid block_grid(int tiles_x, int tiles_y);
 // Blocks the binning's per-work-group block histogram holds.
 constexpr int kMaxBlocks = 8192;
 
-// block_start / seg_start (nb + 1 entries each) from the block histogram:
-// where each block's list begins, and its first 64-entry segment.
-hipError_t launch_block_starts(const BlockGrid& bg, const uint32_t* hist, uint32_t* block_start,
-                               uint32_t* seg_start, hipStream_t st);
 // Row stride (u32) of the per-block chunk counts: n Gaussians in chunks of 64,
 // rounded up to a multiple of 4.
 size_t block_count_stride(int n);
@@ -144,12 +140,15 @@ hipError_t launch_range_keys(int T, const int32_t* ranges, const int32_t* ids, c
 // counts[g], packed tile rect, depth key (float bits or 0xffffffff when the
 // Gaussian touches no tile) and identity values, the digit histograms of the
 // 4-pass depth sort (depth_hist), and either the digit histograms of the tile
-// sort (tile_passes > 0: tile_hist) or the block histogram (block_hist, with
-// the pair count added to *pair_total).
+// sort (tile_passes > 0: tile_hist) or the block histogram (block_hist), with
+// the pair count added to *pair_total and, by the last work-group, the block
+// and segment starts (block_start / seg_start, nb + 1 entries each; `done` a
+// zero counter, left at zero).
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
+                            uint32_t* block_start, uint32_t* seg_start, uint32_t* done,
                             hipStream_t st);
 
 // Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r] (perm null:

@@ -28,6 +28,7 @@
 
 #include "gsr_internal.h"
 #include "gsr_common.h"
+#include "gsr_group.h"
 
 namespace gsr {
 
@@ -35,7 +36,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWavesPer = kThreads / kWave;
-constexpr int kScanThreads = 1024;
 
 struct Rect {
     int x0, x1, y0, y1;  // tiles [x0, x1) x [y0, y1)
@@ -54,28 +54,6 @@ __device__ __forceinline__ uint32_t uniform(uint32_t v) {
 __device__ __forceinline__ uint32_t rank_in(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
                                      __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
-}
-
-// Work-group exclusive scan of one value per thread (kScanThreads threads);
-// *total receives the sum.  Ends with the LDS free for reuse.
-template <int kT>
-__device__ __forceinline__ uint32_t group_exclusive_scan(uint32_t v, uint32_t* s_w,
-                                                         uint32_t* total) {
-    constexpr int kW = kT / kWave;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t inc = wave_inclusive_scan(v);
-    if (lane == 63) s_w[wave] = inc;
-    __syncthreads();
-    uint32_t pre = 0, all = 0;
-#pragma unroll
-    for (int w = 0; w < kW; ++w) {
-        const uint32_t x = s_w[w];
-        pre += (w < wave) ? x : 0u;
-        all += x;
-    }
-    __syncthreads();
-    *total = all;
-    return pre + inc - v;
 }
 
 // ---- level 1: depth order -> block lists -----------------------------------
@@ -384,32 +362,13 @@ __global__ __launch_bounds__(kThreads) void tile_scan_kernel(
     }
 }
 
-// ranges[t] = [start, start + count) from the tile totals in tile order,
-// (0, 0) for tiles without pairs (rasterize.cu:140-166); a grand total other
-// than m sets err bit 2.  One work-group.
-__global__ __launch_bounds__(kScanThreads) void tile_starts_kernel(
+// The tile ranges from the tile totals: one work-group of 1024 threads.
+constexpr int kStartsThreads = 1024;
+__global__ __launch_bounds__(kStartsThreads) void tile_starts_kernel(
     int T, const uint32_t* __restrict__ ttotal, uint64_t m, int2* __restrict__ ranges,
     int* __restrict__ err) {
-    __shared__ uint32_t s_w[kScanThreads / kWave];
-    const int tid = threadIdx.x;
-    uint32_t carry = 0;
-    for (int base = 0; base < T; base += 4 * kScanThreads) {
-        const int i = base + 4 * tid;
-        uint32_t v[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) v[j] = (i + j < T) ? ttotal[i + j] : 0u;
-        uint32_t tot;
-        uint32_t p = carry + group_exclusive_scan<kScanThreads>(v[0] + v[1] + v[2] + v[3],
-                                                                s_w, &tot);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (i + j < T)
-                ranges[i + j] = v[j] ? make_int2((int)p, (int)(p + v[j])) : make_int2(0, 0);
-            p += v[j];
-        }
-        carry += tot;
-    }
-    if (tid == 0 && (uint64_t)carry != m) atomicOr(err, 2);
+    __shared__ uint32_t s_w[kStartsThreads / kWave];
+    tile_starts_body<kStartsThreads>(T, ttotal, m, ranges, err, s_w);
 }
 
 // Each segment entry's Gaussian id into the lists of the tiles it covers, at
@@ -471,46 +430,6 @@ __global__ __launch_bounds__(kThreads) void range_keys_kernel(int T,
     }
 }
 
-// block_start[b] / seg_start[b]: exclusive prefixes of the block histogram and
-// of its 64-entry segment counts, nb + 1 entries each.  One work-group.
-__global__ __launch_bounds__(kScanThreads) void block_starts_kernel(
-    int nb, const uint32_t* __restrict__ hist, uint32_t* __restrict__ block_start,
-    uint32_t* __restrict__ seg_start) {
-    __shared__ uint32_t s_w[kScanThreads / kWave];
-    __shared__ uint32_t s_v[kScanThreads / kWave];
-    const int tid = threadIdx.x;
-    uint32_t carry = 0, scarry = 0;
-    for (int base = 0; base < nb; base += 4 * kScanThreads) {
-        const int i = base + 4 * tid;
-        uint32_t v[4], s[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            v[j] = (i + j < nb) ? hist[i + j] : 0u;
-            s[j] = (v[j] + kWave - 1) / kWave;
-        }
-        uint32_t tot, stot;
-        uint32_t p = carry + group_exclusive_scan<kScanThreads>(v[0] + v[1] + v[2] + v[3], s_w,
-                                                                &tot);
-        uint32_t q = scarry + group_exclusive_scan<kScanThreads>(s[0] + s[1] + s[2] + s[3],
-                                                                 s_v, &stot);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            if (i + j < nb) {
-                block_start[i + j] = p;
-                seg_start[i + j] = q;
-            }
-            p += v[j];
-            q += s[j];
-        }
-        carry += tot;
-        scarry += stot;
-    }
-    if (tid == 0) {
-        block_start[nb] = carry;
-        seg_start[nb] = scarry;
-    }
-}
-
 inline unsigned groups_for(uint64_t waves) {
     return (unsigned)((waves + kWavesPer - 1) / kWavesPer);
 }
@@ -531,14 +450,6 @@ BlockGrid block_grid(int tiles_x, int tiles_y) {
     g.bh = (tiles_y + 7) / 8;
     g.nb = g.bw * g.bh;
     return g;
-}
-
-hipError_t launch_block_starts(const BlockGrid& bg, const uint32_t* hist, uint32_t* block_start,
-                               uint32_t* seg_start, hipStream_t st) {
-    if (bg.nb <= 0) return hipSuccess;
-    hipLaunchKernelGGL(block_starts_kernel, dim3(1), dim3(kScanThreads), 0, st, bg.nb, hist,
-                       block_start, seg_start);
-    return hipGetLastError();
 }
 
 size_t block_count_stride(int n) {
@@ -579,8 +490,8 @@ hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
     hipLaunchKernelGGL(tile_scan_kernel, dim3(bg.nb), dim3(kThreads), 0, st, bg, tb.seg_start,
                        seg_cap, tb.tcount, tb.ttotal);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    const int T = bg.tiles_x * bg.tiles_y;
-    hipLaunchKernelGGL(tile_starts_kernel, dim3(1), dim3(kScanThreads), 0, st, T, tb.ttotal, tb.m,
+    hipLaunchKernelGGL(tile_starts_kernel, dim3(1), dim3(kStartsThreads), 0, st,
+                       bg.tiles_x * bg.tiles_y, tb.ttotal, tb.m,
                        reinterpret_cast<int2*>(tb.ranges), tb.err);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(tile_scatter_kernel, dim3(seg_groups(segs)), dim3(kThreads), 0, st, tb.n,
