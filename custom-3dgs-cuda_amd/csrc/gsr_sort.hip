@@ -41,6 +41,16 @@ struct SortCtl {
 
 inline uint64_t parts_for(uint64_t n) { return (n + kSortPartition - 1) / kSortPartition; }
 
+// Items per thread of the key sort (launch_radix_sort): small inputs take
+// 1024-element partitions, so a pass runs on more work-groups, each with less
+// to rank; larger ones 4096, which keeps the look-back chain short.
+constexpr uint64_t kSmallSortMax = 1u << 18;
+inline int sort_items(uint64_t n) { return n <= kSmallSortMax ? 4 : kSortItems; }
+inline uint64_t sort_parts(uint64_t n) {
+    const uint64_t part = (uint64_t)kSortThreads * (uint64_t)sort_items(n);
+    return (n + part - 1) / part;
+}
+
 SortCtl carve(void* control, uint64_t n, int passes) {
     char* p = static_cast<char*>(control);
     SortCtl c;
@@ -224,7 +234,7 @@ __device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base
 // (tile << gbits) | Gaussian id, sorted on its tile bits; kout receives the
 // words and, when vout is not null (the last pass), vout the Gaussian ids.
 // Otherwise keys and values are separate words, both written.
-template <bool kEmit, bool kPacked>
+template <bool kEmit, bool kPacked, int kItems = kSortItems>
 __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n, int shift,
@@ -233,8 +243,10 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     // s_aux holds the emission's staged offsets first, then the digit counters,
     // digit starts and global bases (7 KB).
     constexpr int kAuxWords = kEmit ? kRankStageWords : 7 * kRadixBins;
-    __shared__ uint32_t s_keys[kSortPartition + kSortPartition / 16];
-    __shared__ uint32_t s_vals[kPacked ? 1 : kSortPartition + kSortPartition / 16];
+    constexpr int kPart = kSortThreads * kItems;  // elements per partition
+    static_assert(!kEmit || kItems == kSortItems, "the emission expands kSortPartition slots");
+    __shared__ uint32_t s_keys[kPart + kPart / 16];
+    __shared__ uint32_t s_vals[kPacked ? 1 : kPart + kPart / 16];
     __shared__ __align__(16) uint32_t s_aux[kAuxWords];
     __shared__ uint32_t s_scan[4];
     __shared__ uint32_t s_hscan[4];
@@ -247,14 +259,14 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     if (tid == 0) s_part = atomicAdd(counter, 1u);
     __syncthreads();
     const uint64_t part = s_part;
-    const uint64_t base = part * kSortPartition;
-    const int nvalid = (int)min((uint64_t)kSortPartition, n - base);
+    const uint64_t base = part * kPart;
+    const int nvalid = (int)min((uint64_t)kPart, n - base);
     if constexpr (!kEmit) {
         // Every key has the same digit: the stable pass is the identity, so the
         // partition is copied through (no ranking, no look-back).
         if (__syncthreads_or(hist[tid] == (uint32_t)n)) {
             // 16-byte copies when every array is 16-byte aligned (partitions start
-            // 16 KB apart), the rest word by word
+            // a multiple of 4 KB apart), the rest word by word
             const uint32_t mask = kPacked ? ((1u << gbits) - 1u) : 0u;
             const uintptr_t al = reinterpret_cast<uintptr_t>(kin) |
                                  reinterpret_cast<uintptr_t>(kout) |
@@ -289,22 +301,22 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
         }
     }
 
-    uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
+    uint32_t key[kItems], val[kItems], rank[kItems];
     (void)val;
     if constexpr (kEmit) {
         expand_pairs<kPacked>(es, base, nvalid, s_keys, s_vals,
                               reinterpret_cast<RankStage*>(s_aux), gbits);  // ends with a barrier
 #pragma unroll
-        for (int i = 0; i < kSortItems; ++i) {
-            const int e = wave * (kSortItems * 64) + i * 64 + lane;
+        for (int i = 0; i < kItems; ++i) {
+            const int e = wave * (kItems * 64) + i * 64 + lane;
             const bool v = e < nvalid;
             key[i] = v ? s_keys[pad16(e)] : 0u;
             if constexpr (!kPacked) val[i] = v ? s_vals[pad16(e)] : 0u;
         }
     } else {
 #pragma unroll
-        for (int i = 0; i < kSortItems; ++i) {
-            const int e = wave * (kSortItems * 64) + i * 64 + lane;
+        for (int i = 0; i < kItems; ++i) {
+            const int e = wave * (kItems * 64) + i * 64 + lane;
             const bool v = e < nvalid;
             key[i] = v ? kin[base + e] : 0u;
             if constexpr (!kPacked) val[i] = v ? vin[base + e] : 0u;
@@ -314,8 +326,8 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     __syncthreads();
     // Stable ranks within the wave's slice, in element order.
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-        const int e = wave * (kSortItems * 64) + i * 64 + lane;
+    for (int i = 0; i < kItems; ++i) {
+        const int e = wave * (kItems * 64) + i * 64 + lane;
         const bool v = e < nvalid;
         const uint32_t d = (key[i] >> shift) & 0xffu;
         const uint64_t peers = match_digit(d, ballot(v), digit_bits);
@@ -359,8 +371,8 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
 
     // Reorder the partition in LDS by digit (stable).
 #pragma unroll
-    for (int i = 0; i < kSortItems; ++i) {
-        const int e = wave * (kSortItems * 64) + i * 64 + lane;
+    for (int i = 0; i < kItems; ++i) {
+        const int e = wave * (kItems * 64) + i * 64 + lane;
         if (e < nvalid) {
             const uint32_t dd = (key[i] >> shift) & 0xffu;
             const uint32_t pos = s_dstart[dd] + s_wcnt[wave][dd] + rank[i];
@@ -513,7 +525,7 @@ hipError_t zero_fill(void* p, size_t bytes, hipStream_t st) {
 
 size_t sort_control_bytes(uint64_t n, int passes) {
     return align_up((size_t)passes * kRadixBins * 4, 256) + align_up((size_t)passes * 64, 256) +
-           (size_t)passes * parts_for(n) * kRadixBins * 8;
+           (size_t)passes * sort_parts(n) * kRadixBins * 8;
 }
 
 hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
@@ -521,7 +533,8 @@ hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t*
                              bool hist_ready) {
     if (n == 0 || passes <= 0) return hipSuccess;
     if (passes > kHistMaxPasses) return hipErrorInvalidValue;
-    const uint64_t parts = parts_for(n);
+    const uint64_t parts = sort_parts(n);
+    const bool small = sort_items(n) == 4;
     SortCtl c = carve(control, n, passes);
     hipError_t e = hipSuccess;
     if (!hist_ready) {
@@ -533,10 +546,18 @@ hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t*
     }
     uint32_t *ki = k0, *vi = v0, *ko = k1, *vo = v1;
     for (int p = 0; p < passes; ++p) {
-        hipLaunchKernelGGL((onesweep_kernel<false, false>), dim3((unsigned)parts),
-                           dim3(kSortThreads), 0, st, ki, vi, ko, vo, n, begin_bit + 8 * p, 8,
-                           c.hist + p * kRadixBins, c.status + (size_t)p * parts * kRadixBins,
-                           c.counters + p * 16, err, EmitSource{}, 0);
+        if (small)
+            hipLaunchKernelGGL((onesweep_kernel<false, false, 4>), dim3((unsigned)parts),
+                               dim3(kSortThreads), 0, st, ki, vi, ko, vo, n, begin_bit + 8 * p, 8,
+                               c.hist + p * kRadixBins,
+                               c.status + (size_t)p * parts * kRadixBins, c.counters + p * 16,
+                               err, EmitSource{}, 0);
+        else
+            hipLaunchKernelGGL((onesweep_kernel<false, false>), dim3((unsigned)parts),
+                               dim3(kSortThreads), 0, st, ki, vi, ko, vo, n, begin_bit + 8 * p, 8,
+                               c.hist + p * kRadixBins,
+                               c.status + (size_t)p * parts * kRadixBins, c.counters + p * 16,
+                               err, EmitSource{}, 0);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         std::swap(ki, ko);
