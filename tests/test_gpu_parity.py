@@ -338,6 +338,28 @@ def _threshold_scene(seed=17, H=48, W=64, crafted=600, others=500):
     return dict(H=H, W=W, mean2d=mean2d, cov2d=cov2d, alpha=alpha, depth=depth, colors=colors)
 
 
+def test_forward_parity_nonfinite_colours(crc, device):
+    """Entries with an infinite colour channel take the forward's select path
+    (a skipped entry must not add inf * 0); images, final T and n_contrib
+    equal the oracle's bit for bit, infinities included."""
+    s = _threshold_scene(seed=23)
+    n = s["alpha"].shape[0]
+    rng = np.random.default_rng(5)
+    pick = rng.choice(np.arange(600, n), 12, replace=False)
+    s["colors"][pick, rng.integers(0, 3, 12)] = np.float32(np.inf)
+    H, W = s["H"], s["W"]
+    t = {k: _dev(s[k], device) for k in ("depth", "mean2d", "cov2d", "colors", "alpha")}
+    img, ids, ranges, fT, nc, _ = crc.rasterize_with_keys(n, t["depth"], t["mean2d"], t["cov2d"],
+                                                          t["colors"], t["alpha"], H, W)
+    w_img, w_ids, w_rng, w_fT, w_nc, _ = orc.rasterize(s["depth"], s["mean2d"], s["cov2d"],
+                                                       s["colors"], s["alpha"], H, W)
+    assert np.isinf(w_img).any()
+    assert_bitwise(_np(ids), w_ids, "sorted_ids")
+    assert_bitwise(_np(nc), w_nc, "n_contrib")
+    assert_bitwise(_np(img), w_img, "img")
+    assert_bitwise(_np(fT), w_fT, "final_T")
+
+
 def test_rasterize_backward_alpha_at_the_thresholds(crc, device):
     """The backward's skips (power > 0, alpha < 1/255, the 0.99 clamp) must be
     the forward's bit for bit, also where alpha is within a few ulp of 1/255:
