@@ -280,9 +280,12 @@ struct BwdPixel {
     int last;
 };
 
+// dL/dpower = alpha dL/dalpha = opacity * (G dL/dalpha) = opacity * dL/dopacity
+// for an unclamped entry, and both are 0 for a clamped or skipped one
+// (rasterize_backward.cu:155-161), so only dL/dopacity is formed per pixel and
+// the power terms are scaled by the entry's opacity once, at the flush.
 struct BwdTerms {
     float aT;   // alpha * T_before: dL/dcolour = aT * dL/dpixel
-    float dpw;  // dL/dpower
     float dop;  // dL/dopacity
 };
 
@@ -339,7 +342,6 @@ __device__ __forceinline__ BwdTerms bwd_update(BwdPixel& p, const BwdDecision& d
     const float diff = cg - p.accg;
     const float dal = diff * Tb;
     t.aT = ae * Tb;
-    t.dpw = (d.unc ? d.alpha : 0.0f) * dal;
     t.dop = (d.unc ? d.G : 0.0f) * dal;
     p.accg = __builtin_fmaf(ae, diff, p.accg);
     p.T = Tb;
@@ -364,9 +366,10 @@ __device__ __forceinline__ BwdPixel load_bwd_pixel(bool in, int px, int py, int 
 
 // Per (tile, entry) the wave sums nine values.  A lane's pixels share dx, so
 // the reference's per-pixel mean and conic terms (rasterize_backward.cu:
-// 163-176) summed over the lane follow from P1 = sum dpw dx, P2 = sum dpw dy
-// and P5 = sum dpw dy^2: dL/dmean = (cx P1 + cy P2, cy P1 + cz P2), dL/dconic
-// = (-P1 dx / 2, -P2 dx, -P5 / 2); then dL/dcolour (3) and dL/dopacity.
+// 163-176) summed over the lane follow from S0 = sum dop, P1 = dx S0,
+// P2 = sum dop dy and P5 = sum dop dy^2 (dop = dL/dopacity, dL/dpower being
+// opacity * dop): dL/dmean = o (cx P1 + cy P2, cy P1 + cz P2), dL/dconic =
+// o (-P1 dx / 2, -P2 dx, -P5 / 2); then dL/dcolour (3) and dL/dopacity (S0).
 constexpr int kTerms = 9;
 
 // dL/dcov2d (a, b, c) from dL/dconic (x, y full off-diagonal, z) for conic =
@@ -467,18 +470,17 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                     for (int k = 0; k < kPix; ++k) decide_exact(d[k], B.y, contributor, p[k].last);
                 }
                 // per-lane sums over its pixels, started from the first pixel's terms
-                float S0, P2, P5, c0, c1, c2, dop;
+                float S0, P2, P5, c0, c1, c2;
                 bool act;
                 {
                     const BwdTerms t = bwd_update(p[0], d[0], B, Cc.x);
-                    const float e = t.dpw * d[0].dy;
-                    S0 = t.dpw;
+                    const float e = t.dop * d[0].dy;
+                    S0 = t.dop;
                     P2 = e;
                     P5 = e * d[0].dy;
                     c0 = t.aT * p[0].g0;
                     c1 = t.aT * p[0].g1;
                     c2 = t.aT * p[0].g2;
-                    dop = t.dop;
                     act = d[0].act;
                 }
 #pragma unroll
@@ -486,26 +488,25 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                     const BwdTerms t = bwd_update(p[k], d[k], B, Cc.x);
                     {
 #pragma clang fp contract(fast)
-                        const float e = t.dpw * d[k].dy;
-                        S0 += t.dpw;
+                        const float e = t.dop * d[k].dy;
+                        S0 += t.dop;
                         P2 += e;
                         P5 += e * d[k].dy;
                         c0 += t.aT * p[k].g0;
                         c1 += t.aT * p[k].g1;
                         c2 += t.aT * p[k].g2;
-                        dop += t.dop;
                     }
                     act |= d[k].act;
                 }
                 if (ballot(act) != 0) {
                     const float P1 = dx * S0;
                     // mean terms formed in the lane, before the wide sum, as the
-                    // per-pixel dpw (conic.x dx + conic.y dy) is
-                    // with the record's -cx/2, -cy/2 (Cc.y), -cz/2: -1/2 of
+                    // per-pixel dpw (conic.x dx + conic.y dy) is; with the
+                    // record's -cx/2, -cy/2 (Cc.y), -cz/2 they are -1/2 of
                     // (cx P1 + cy P2, cy P1 + cz P2), rescaled at the flush
                     const float hy = Cc.y;
                     const float vals[kTerms] = {A.z * P1 + hy * P2, hy * P1 + B.x * P2, dx * P1,
-                                                dx * P2, P5, c0, c1, c2, dop};
+                                                dx * P2, P5, c0, c1, c2, S0};
                     w9 = wave_reduce9(vals);
                 }
             }
@@ -526,11 +527,12 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
             }
             if (g >= 0 && any) {
                 float t[kTerms];
-                t[0] = -2.0f * tot[0];  // dL/dmean.x
-                t[1] = -2.0f * tot[1];  // dL/dmean.y
-                t[2] = -0.5f * tot[2];  // dL/dconic.x
-                t[3] = -tot[3];        // dL/dconic.y (full off-diagonal)
-                t[4] = -0.5f * tot[4];  // dL/dconic.z
+                const float o = s_b[tid].y;  // the power terms carry dL/dopacity
+                t[0] = (-2.0f * o) * tot[0];  // dL/dmean.x
+                t[1] = (-2.0f * o) * tot[1];  // dL/dmean.y
+                t[2] = (-0.5f * o) * tot[2];  // dL/dconic.x
+                t[3] = -o * tot[3];           // dL/dconic.y (full off-diagonal)
+                t[4] = (-0.5f * o) * tot[4];  // dL/dconic.z
                 t[5] = tot[5];         // dL/dcolour
                 t[6] = tot[6];
                 t[7] = tot[7];
