@@ -132,18 +132,22 @@ __device__ __forceinline__ uint32_t strip_bits(const BlendRec& r, int tile, int 
     return bits;
 }
 
-template <int kPix>
-__device__ __forceinline__ void stage_entry(const BlendRec* __restrict__ recs, int g, int n,
-                                            int tile, int tiles_x, float4* s_a, float4* s_b,
-                                            float4* s_c, uint32_t* s_bits, int* s_id,
-                                            int slot) {
+// The record of list entry g, zeros for an id outside [0, n) (such entries are
+// skipped: rasterize_backward.cu:79-86).
+__device__ __forceinline__ BlendRec load_record(const BlendRec* __restrict__ recs, int g, int n) {
     BlendRec r;
-    const bool ok = g >= 0 && g < n;
-    if (ok) {
+    if (g >= 0 && g < n) {
         r = recs[g];
-    } else {  // corrupt id: skipped (rasterize_backward.cu:79-86)
+    } else {
         r.a = r.b = r.c = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     }
+    return r;
+}
+
+template <int kPix>
+__device__ __forceinline__ void stage_record(const BlendRec& r, bool ok, int g, int tile,
+                                             int tiles_x, float4* s_a, float4* s_b, float4* s_c,
+                                             uint32_t* s_bits, int* s_id, int slot) {
     s_a[slot] = r.a;
     s_b[slot] = r.b;
     if (s_bits) s_c[slot] = r.c;
@@ -155,6 +159,15 @@ __device__ __forceinline__ void stage_entry(const BlendRec* __restrict__ recs, i
     else  // in the record's unused fourth word
         s_c[slot] = make_float4(r.c.x, r.c.y, r.c.z, __uint_as_float(bits));
     if (s_id) s_id[slot] = ok ? g : -1;
+}
+
+template <int kPix>
+__device__ __forceinline__ void stage_entry(const BlendRec* __restrict__ recs, int g, int n,
+                                            int tile, int tiles_x, float4* s_a, float4* s_b,
+                                            float4* s_c, uint32_t* s_bits, int* s_id,
+                                            int slot) {
+    stage_record<kPix>(load_record(recs, g, n), g >= 0 && g < n, g, tile, tiles_x, s_a, s_b, s_c,
+                       s_bits, s_id, slot);
 }
 
 // Forward pixel state.  A pixel is done once a blend takes T below 1e-4
@@ -238,12 +251,15 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
     int start, end;
     clamp_range(ranges[tile], m, start, end);
 
+    // each batch's ids are loaded while the batch before it is blended
+    int next_id = (start + tid < end) ? ids[start + tid] : -1;
     for (int b0 = start; b0 < end; b0 += kBatch) {
         const int cnt = min(kBatch, end - b0);
+        const int g = next_id;
         __syncthreads();
         if (tid < cnt)
-            stage_entry<kPix>(recs, ids[b0 + tid], n, tile, tiles_x, s_a, s_b, s_c, s_bits,
-                              nullptr, tid);
+            stage_entry<kPix>(recs, g, n, tile, tiles_x, s_a, s_b, s_c, s_bits, nullptr, tid);
+        if (b0 + kBatch + tid < end) next_id = ids[b0 + kBatch + tid];
         __syncthreads();
         if (ballot(any_live(p)) != 0) {
             const int cbase = b0 - start + 1;
@@ -428,13 +444,19 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     start = __builtin_amdgcn_readfirstlane(start);
     const int my_value = reduce9_value_of_lane(lane);
 
+    // each batch's ids are loaded while the batch after it is walked
+    int next_id = (tid < min(maxc, kBatch)) ? ids[start + max(0, maxc - kBatch) + tid] : -1;
     for (int hi = maxc; hi > 0; hi -= kBatch) {
         const int lo = max(0, hi - kBatch);
         const int cnt = hi - lo;
+        const int g = next_id;
         __syncthreads();
         if (tid < cnt)
-            stage_entry<kPix>(recs, ids[start + lo + tid], n, tile, tiles_x, s_a, s_b, s_c,
-                              nullptr, s_id, tid);
+            stage_entry<kPix>(recs, g, n, tile, tiles_x, s_a, s_b, s_c, nullptr, s_id, tid);
+        if (lo > 0) {
+            const int nlo = max(0, lo - kBatch);
+            if (tid < lo - nlo) next_id = ids[start + nlo + tid];
+        }
         __syncthreads();
         for (int j = cnt - 1; j >= 0; --j) {
             const int contributor = lo + j + 1;
