@@ -106,6 +106,47 @@ Tensor screen_radii(const Tensor cov_2d) {
     return radii;
 }
 
+// The glue's forward head in one kernel (rasterize.py:42-54): (mean_2d,
+// cov_2d, depths, radii, colors, camera_position), bit for bit those of
+// camera_position, project, screen_radii and SH.
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> project_sh(
+    int total_gaussians, const Tensor mu3d, const Tensor q3d, const Tensor s3d,
+    const Tensor camera_rotation, const Tensor camera_translation, float fx, float fy, float cx,
+    float cy, const Tensor albedo_coeff, const Tensor illumination_coeff) {
+    CHECK_INPUT_FP32(mu3d);
+    CHECK_INPUT_FP32(q3d);
+    CHECK_INPUT_FP32(s3d);
+    CHECK_INPUT_FP32(camera_rotation);
+    CHECK_INPUT_FP32(camera_translation);
+    CHECK_INPUT_FP32(albedo_coeff);
+    CHECK_INPUT_FP32(illumination_coeff);
+    TORCH_CHECK(total_gaussians >= 0, "total_gaussians must be non-negative");
+    const int64_t n = total_gaussians;
+    check_numel(mu3d, 3 * n, "mu3d must hold N x 3 values");
+    check_numel(q3d, 4 * n, "q3d must hold N x 4 values");
+    check_numel(s3d, 3 * n, "s3d must hold N x 3 values");
+    check_numel(camera_rotation, 9, "camera_rotation must hold 3 x 3 values");
+    check_numel(camera_translation, 3, "camera_translation must hold 3 values");
+    check_numel(albedo_coeff, 3 * n, "albedo_coeff must hold N x 3 values");
+    check_numel(illumination_coeff, 45 * n, "illumination_coeff must hold N x 15 x 3 values");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(mu3d.device());
+    auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mu3d.device());
+    Tensor mean_2d = torch::empty({n, 2}, options);
+    Tensor cov_2d = torch::empty({n, 3}, options);
+    Tensor depths = torch::empty({n}, options);
+    Tensor radii = torch::empty({n}, options);
+    Tensor colors = torch::empty({n, 3}, options);
+    Tensor cam = torch::empty({3}, options);
+    const Tensor q_al = aligned16(q3d);
+    const Tensor k_al = aligned16(illumination_coeff);
+    check_rc(gsr_project_sh(total_gaussians, cfp(mu3d), cfp(q_al), cfp(s3d), cfp(camera_rotation),
+                            cfp(camera_translation), fx, fy, cx, cy, cfp(albedo_coeff),
+                            cfp(k_al), fp(mean_2d), fp(cov_2d), fp(depths), fp(radii),
+                            fp(colors), fp(cam), current_stream()),
+             "project_sh");
+    return {mean_2d, cov_2d, depths, radii, colors, cam};
+}
+
 Tensor camera_position(const Tensor camera_rotation, const Tensor camera_translation) {
     CHECK_INPUT_FP32(camera_rotation);
     CHECK_INPUT_FP32(camera_translation);
@@ -337,6 +378,55 @@ std::tuple<Tensor, Tensor, Tensor> backwards_projection(
     return {mu_grad, q_grad, s_grad};
 }
 
+// The glue's backward tail in one kernel (rasterize.py:100-117): (mu_grad,
+// q_grad, s_grad, albedo_grad, k_j_grad) with mu_grad = the projection's +
+// the SH's, bit for bit backwards_SH, backwards_projection and that sum.
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backwards_project_sh(
+    const Tensor mean_2d_grad, const Tensor cov_2d_grad, const Tensor colors_grad,
+    const Tensor mu, const Tensor q, const Tensor s, const Tensor camera_rotation,
+    const Tensor camera_translation, float fx, float fy, const Tensor albedo, const Tensor k_j,
+    const Tensor camera_position) {
+    CHECK_INPUT_FP32(mean_2d_grad);
+    CHECK_INPUT_FP32(cov_2d_grad);
+    CHECK_INPUT_FP32(colors_grad);
+    CHECK_INPUT_FP32(mu);
+    CHECK_INPUT_FP32(q);
+    CHECK_INPUT_FP32(s);
+    CHECK_INPUT_FP32(camera_rotation);
+    CHECK_INPUT_FP32(camera_translation);
+    CHECK_INPUT_FP32(albedo);
+    CHECK_INPUT_FP32(k_j);
+    CHECK_INPUT_FP32(camera_position);
+    const int64_t n = mu.size(0);
+    check_numel(mean_2d_grad, 2 * n, "mean_2d_grad must hold N x 2 values");
+    check_numel(cov_2d_grad, 3 * n, "cov_2d_grad must hold N x 3 values");
+    check_numel(colors_grad, 3 * n, "colors_grad must hold N x 3 values");
+    check_numel(q, 4 * n, "q must hold N x 4 values");
+    check_numel(s, 3 * n, "s must hold N x 3 values");
+    check_numel(camera_rotation, 9, "camera_rotation must hold 3 x 3 values");
+    check_numel(camera_translation, 3, "camera_translation must hold 3 values");
+    check_numel(albedo, 3 * n, "albedo must hold N x 3 values");
+    check_numel(k_j, 45 * n, "k_j must hold N x 15 x 3 values");
+    TORCH_CHECK(camera_position.numel() >= 3, "camera_position must have 3 elements");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(mu.device());
+    auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mu.device());
+    Tensor mu_grad = torch::empty({n, 3}, options);
+    Tensor q_grad = torch::empty({n, 4}, options);
+    Tensor s_grad = torch::empty({n, 3}, options);
+    Tensor albedo_grad = torch::empty({n, 3}, options);
+    Tensor k_j_grad = torch::empty({n, 15, 3}, options);
+    const Tensor q_al = aligned16(q);
+    const Tensor k_al = aligned16(k_j);
+    check_rc(gsr_project_sh_backward((int)n, cfp(mean_2d_grad), cfp(cov_2d_grad),
+                                     cfp(colors_grad), cfp(mu), cfp(q_al), cfp(s),
+                                     cfp(camera_rotation), cfp(camera_translation), fx, fy,
+                                     cfp(albedo), cfp(k_al), cfp(camera_position), fp(mu_grad),
+                                     fp(q_grad), fp(s_grad), fp(albedo_grad), fp(k_j_grad),
+                                     current_stream()),
+             "backwards_project_sh");
+    return {mu_grad, q_grad, s_grad, albedo_grad, k_j_grad};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(custom_rasterizer_cuda, m) {
@@ -355,6 +445,10 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     m.def("library_version", []() { return std::string(gsr_version()); });
     m.def("screen_radii", &screen_radii, "glue: approximate screen radii (one kernel)");
     m.def("camera_position", &camera_position, "glue: camera position -R^T t (one kernel)");
+    m.def("project_sh", &project_sh,
+          "glue: camera position, project, screen radii and SH in one kernel");
+    m.def("backwards_project_sh", &backwards_project_sh,
+          "glue: backwards_SH, backwards_projection and their dL/dmu sum in one kernel");
     // Stage timing of libgsraster (HIP events on the launch stream); not part of
     // the reference surface.
     m.def("profile_enable", [](bool on) { gsr_profile_enable(on ? 1 : 0); });

@@ -93,7 +93,7 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     int passes, uint32_t* __restrict__ tile_hist, uint32_t* __restrict__ depth_hist,
     BlockGrid bg, uint32_t* __restrict__ block_hist, uint64_t* __restrict__ pair_total,
     uint32_t* __restrict__ block_start, uint32_t* __restrict__ seg_start,
-    uint32_t* __restrict__ done) {
+    uint32_t* __restrict__ done, uint64_t* __restrict__ host_total) {
     __shared__ int s_d0[kRadixBins + 1];
     __shared__ uint32_t s_h[3][kRadixBins];
     __shared__ uint32_t s_dh[4][kRadixBins];
@@ -167,8 +167,17 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
         if ((tid & 63) == 0 && wp) atomicAdd(reinterpret_cast<unsigned long long*>(pair_total),
                                              (unsigned long long)wp);
         // the last work-group to finish turns the histogram into the starts
-        if (last_group(done, &s_flag))
+        // and hands the final pair count to the host
+        if (last_group(done, &s_flag)) {
+            if (tid == 0 && host_total) {
+                const uint64_t total = __hip_atomic_load(pair_total, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(host_total, total, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
+                __threadfence_system();
+            }
             block_starts_body<kThreads>(bg.nb, block_hist, block_start, seg_start, s_scan, s_v);
+        }
     }
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
@@ -281,7 +290,7 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
                             uint32_t* block_start, uint32_t* seg_start, uint32_t* done,
-                            hipStream_t st) {
+                            uint64_t* host_total, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     if (tile_passes < 0 || tile_passes > 4) return hipErrorInvalidValue;
     const BlockGrid bg = block_grid((W + 15) / 16, (H + 15) / 16);
@@ -292,7 +301,8 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
     const unsigned blocks = std::min(blocks_for(n), 128u);
     hipLaunchKernelGGL(bin_count_kernel, dim3(blocks), dim3(kThreads), 0, st, n, mean2d, cov2d,
                        depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist,
-                       depth_hist, bg, block_hist, pair_total, block_start, seg_start, done);
+                       depth_hist, bg, block_hist, pair_total, block_start, seg_start, done,
+                       block_hist ? host_total : nullptr);
     return hipGetLastError();
 }
 

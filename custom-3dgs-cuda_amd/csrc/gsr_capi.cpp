@@ -221,6 +221,32 @@ Misc* pinned_misc() {
     return p;
 }
 
+// The pair count as bin_count's last work-group stores it: one host-mapped,
+// coherent word per host thread, with its device address.
+struct HostCount {
+    volatile uint64_t* host = nullptr;
+    uint64_t* dev = nullptr;
+};
+HostCount host_count() {
+    thread_local HostCount c;
+    if (!c.host) {
+        void* h = nullptr;
+        void* d = nullptr;
+        if (hipHostMalloc(&h, 64, hipHostMallocMapped | hipHostMallocCoherent |
+                                      hipHostMallocPortable) != hipSuccess)
+            return HostCount{};
+        if (hipHostGetDevicePointer(&d, h, 0) != hipSuccess) {
+            (void)hipHostFree(h);
+            return HostCount{};
+        }
+        c.host = static_cast<volatile uint64_t*>(h);
+        c.dev = static_cast<uint64_t*>(d);
+    }
+    return c;
+}
+// Stands in the host word until bin_count has stored the count.
+constexpr uint64_t kNoCount = ~0ull;
+
 // Marks the pair count's arrival in pinned memory (one per host thread).
 hipEvent_t count_event() {
     thread_local hipEvent_t e = nullptr;
@@ -352,6 +378,25 @@ int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, co
     return GSR_OK;
 }
 
+int gsr_project_sh(int n, const float* mu, const float* q, const float* s, const float* rot,
+                   const float* trans, float fx, float fy, float cx, float cy,
+                   const float* albedo, const float* k_j, float* mean2d, float* cov2d,
+                   float* depth, float* radii, float* colors, float* cam_pos, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    GSR_REQUIRE(rot && trans && cam_pos, "null pointer");
+    if (n == 0) return gsr_camera_position(rot, trans, cam_pos, stream);
+    GSR_REQUIRE(mu && q && s && albedo && k_j && mean2d && cov2d && depth && radii && colors,
+                "null pointer");
+    GSR_REQUIRE(((uintptr_t)q & 15) == 0, "q must be 16-byte aligned");
+    GSR_REQUIRE(((uintptr_t)k_j & 15) == 0, "k_j must be 16-byte aligned");
+    StageTimer timer("project_sh", as_stream(stream));
+    GSR_HIP(gsr::launch_project_sh_fwd(n, mu, q, s, rot, trans, fx, fy, cx, cy, albedo, k_j,
+                                       mean2d, cov2d, depth, radii, colors, cam_pos,
+                                       as_stream(stream)),
+            "project_sh");
+    return GSR_OK;
+}
+
 size_t gsr_bin_workspace_bytes(int n, int height, int width) {
     if (height < 0 || width < 0) return 0;
     return bin_layout(n, height, width).end;
@@ -377,6 +422,9 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
     uint32_t* dk0 = at<uint32_t>(bin_ws, L.dk0);
     uint32_t* dv0 = at<uint32_t>(bin_ws, L.dv0);
     const bool blocks = block_binning(height, width);
+    const HostCount hc = blocks ? host_count() : HostCount{};
+    if (blocks && !hc.host) return fail(GSR_ERR_HIP, "rasterize: host-mapped count allocation failed");
+    if (blocks) *hc.host = kNoCount;
     {
         StageTimer timer("bin_count", st);
         const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
@@ -388,7 +436,8 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
                                       blocks ? at<uint32_t>(bin_ws, L.blockhist) : nullptr,
                                       blocks ? &misc->total : nullptr,
                                       at<uint32_t>(bin_ws, L.block_start),
-                                      at<uint32_t>(bin_ws, L.seg_start), &misc->bin_done, st),
+                                      at<uint32_t>(bin_ws, L.seg_start), &misc->bin_done,
+                                      hc.dev, st),
                 "rasterize: count");
     }
     Misc* host = pinned_misc();
@@ -403,17 +452,25 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
         return GSR_OK;
     };
     if (blocks) {
-        // The pair count is final after bin_count: read it back, queue the
-        // depth sort behind the copy and wait only for the copy, so the sort
-        // runs while the host returns and queues the render.  A spin-bound
-        // error of the sort stays in the status word (gsr_rasterize_status).
+        // The pair count is final after bin_count, whose last work-group
+        // stores it to host-mapped memory: queue the depth sort behind
+        // bin_count and wait only for bin_count, so the sort runs while the
+        // host returns and queues the render.  A spin-bound error of the sort
+        // stays in the status word (gsr_rasterize_status).
         hipEvent_t ev = count_event();
         if (!ev) return fail(GSR_ERR_HIP, "rasterize: event creation failed");
-        GSR_HIP(hipMemcpyAsync(host, misc, sizeof(Misc), hipMemcpyDeviceToHost, st),
-                "rasterize: read pair count");
         GSR_HIP(hipEventRecord(ev, st), "rasterize: record");
         if (int rc = depth_sort()) return rc;
         GSR_HIP(hipEventSynchronize(ev), "rasterize: synchronize");
+        const uint64_t total = *hc.host;
+        if (total == kNoCount) return fail(GSR_ERR_DEVICE, "rasterize: pair count not stored");
+        if (total > (uint64_t)kMaxPairs)
+            return fail(GSR_ERR_TOO_MANY_PAIRS,
+                        "rasterize: " + std::to_string(total) +
+                            " (Gaussian, tile) pairs exceed the int32 limit; render in screen "
+                            "bands");
+        *num_pairs = (int64_t)total;
+        return GSR_OK;
     } else {
         if (int rc = depth_sort()) return rc;
         StageTimer timer("scan", st);
@@ -659,6 +716,29 @@ int gsr_sh_backward(int n, const float* colors_grad, const float* mu, const floa
     GSR_HIP(gsr::launch_sh_bwd(n, colors_grad, mu, albedo, k_j, cam_pos, d_albedo, d_k_j, d_mu,
                                as_stream(stream)),
             "backwards_SH");
+    return GSR_OK;
+}
+
+int gsr_project_sh_backward(int n, const float* d_mean2d, const float* d_cov2d,
+                            const float* d_colors, const float* mu, const float* q,
+                            const float* s, const float* rot, const float* trans, float fx,
+                            float fy, const float* albedo, const float* k_j,
+                            const float* cam_pos, float* d_mu, float* d_q, float* d_s,
+                            float* d_albedo, float* d_k_j, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(d_mean2d && d_cov2d && d_colors && mu && q && s && rot && trans && albedo && k_j &&
+                    cam_pos && d_mu && d_q && d_s && d_albedo && d_k_j,
+                "null pointer");
+    GSR_REQUIRE(((uintptr_t)q & 15) == 0 && ((uintptr_t)d_q & 15) == 0,
+                "q and d_q must be 16-byte aligned");
+    GSR_REQUIRE(((uintptr_t)k_j & 15) == 0 && ((uintptr_t)d_k_j & 15) == 0,
+                "k_j and d_k_j must be 16-byte aligned");
+    StageTimer timer("project_sh_bwd", as_stream(stream));
+    GSR_HIP(gsr::launch_project_sh_bwd(n, d_mean2d, d_cov2d, d_colors, mu, q, s, rot, trans, fx,
+                                       fy, albedo, k_j, cam_pos, d_mu, d_q, d_s, d_albedo, d_k_j,
+                                       ref_quat_mode(), as_stream(stream)),
+            "project_sh_backward");
     return GSR_OK;
 }
 

@@ -29,6 +29,21 @@ hipError_t launch_sh_bwd(int n, const float* cgrad, const float* mu, const float
                          const float* kj, const float* cam, float* dA, float* dkj, float* dmu,
                          hipStream_t st);
 
+// Fused per-Gaussian passes: camera position + projection + screen radius +
+// SH colour (cam: 3 floats out), and SH backward + projection backward with
+// dL/dmu summed.  Bit for bit the single-pass kernels' results.
+hipError_t launch_project_sh_fwd(int n, const float* mu, const float* q, const float* s,
+                                 const float* rot, const float* tr, float fx, float fy, float cx,
+                                 float cy, const float* albedo, const float* kj, float* mean2d,
+                                 float* cov2d, float* depth, float* radii, float* colors,
+                                 float* cam, hipStream_t st);
+hipError_t launch_project_sh_bwd(int n, const float* dmean, const float* dcov,
+                                 const float* cgrad, const float* mu, const float* q,
+                                 const float* s, const float* rot, const float* tr, float fx,
+                                 float fy, const float* albedo, const float* kj, const float* cam,
+                                 float* dmu, float* dq, float* ds, float* dA, float* dkj,
+                                 int ref_quat, hipStream_t st);
+
 // ---- radix sort (u32 keys, u32 values), LSD onesweep with 8-bit digits ----
 // Partition size of one onesweep work-group.
 constexpr int kSortThreads = 256;
@@ -143,13 +158,14 @@ hipError_t launch_range_keys(int T, const int32_t* ranges, const int32_t* ids, c
 // sort (tile_passes > 0: tile_hist) or the block histogram (block_hist), with
 // the pair count added to *pair_total and, by the last work-group, the block
 // and segment starts (block_start / seg_start, nb + 1 entries each; `done` a
-// zero counter, left at zero).
+// zero counter, left at zero) and, when host_total is not null, the final pair
+// count stored to that host-mapped coherent word (block histogram mode only).
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
                             uint32_t* block_start, uint32_t* seg_start, uint32_t* done,
-                            hipStream_t st);
+                            uint64_t* host_total, hipStream_t st);
 
 // Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r] (perm null:
 // the identity); the total (u64) is written to *total.

@@ -2,10 +2,13 @@
 gaussian_splatting/rasterizer/rasterize.py:10-160, same call order and semantics:
 
 forward:  cam_position = -R^T t; project -> (mean2d, cov2d, depth); approximate screen
-          radii for densification; SH colours; rasterize -> image.
+          radii for densification; SH colours (these four in one kernel,
+          ``project_sh``, bit for bit the separate ops); rasterize -> image.
 backward: backwards_rasterization -> (d mean2d, d cov2d, d colours, d alpha);
           backwards_SH -> (d albedo, d k_j, d mu via view direction);
-          backwards_projection -> (d mu, d q, d log-scale); d mu = sum of both paths.
+          backwards_projection -> (d mu, d q, d log-scale); d mu = sum of both paths
+          (these three in one kernel, ``backwards_project_sh``, bit for bit the
+          separate ops and the sum).
 
 The extension is the MI355X HIP build (libgsraster.so); there is no fallback path.
 """
@@ -64,17 +67,14 @@ class RasterizeFunction(t.autograd.Function):
         cx_f, cy_f = float(cx), float(cy)
         img_h, img_w = int(height), int(width)
 
-        # -R^T t (rasterize.py:43-44) in one kernel
-        cam_position = crc.camera_position(cam_rotation, cam_translation)
-
-        mean_2d, cov_2d, depths = crc.project(
-            num_gaussians, mu, q, s, cam_rotation, cam_translation, fx_f, fy_f, cx_f, cy_f
+        # -R^T t, project, the screen radius ~ 3 * sqrt(max eigenvalue of
+        # [[a, b], [b, c]]) and SH (rasterize.py:42-54), the same fp32 operations
+        # in one kernel
+        mean_2d, cov_2d, depths, radii, colors, cam_position = crc.project_sh(
+            num_gaussians, mu, q, s, cam_rotation, cam_translation, fx_f, fy_f, cx_f, cy_f,
+            albedo, k_j
         )
-        # Screen radius ~ 3 * sqrt(max eigenvalue of [[a, b], [b, c]]) (rasterize.py:49-53):
-        # the same fp32 operations in one kernel
-        RasterizeFunction.last_radii2d = crc.screen_radii(cov_2d)
-
-        colors = crc.SH(num_gaussians, cam_position, mu, albedo, k_j)
+        RasterizeFunction.last_radii2d = radii
         rendered_img, sorted_ids, tile_ranges, final_T, n_contrib = crc.rasterize(
             num_gaussians, depths, mean_2d, cov_2d, colors, alpha, img_h, img_w
         )
@@ -110,14 +110,12 @@ class RasterizeFunction(t.autograd.Function):
         )
         RasterizeFunction.last_mean2d_grad = mean_2d_grad.detach()
 
-        albedo_grad, k_j_grad, mu_sh_grad = crc.backwards_SH(
-            colors_grad, mu, albedo, k_j, cam_position
+        # backwards_SH, backwards_projection and mu_grad + mu_sh_grad
+        # (rasterize.py:100-117) in one kernel
+        mu_grad, q_grad, s_grad, albedo_grad, k_j_grad = crc.backwards_project_sh(
+            mean_2d_grad, cov_2d_grad, colors_grad, mu, q, s, cam_rotation, cam_translation,
+            ctx.fx, ctx.fy, albedo, k_j, cam_position,
         )
-        mu_grad, q_grad, s_grad = crc.backwards_projection(
-            mean_2d_grad, cov_2d_grad, mu, q, s, cam_rotation, cam_translation,
-            ctx.fx, ctx.fy, ctx.cx, ctx.cy,
-        )
-        mu_grad = mu_grad + mu_sh_grad
         # alpha arrives as [N] or [N, 1]; hand back a gradient of the same shape
         alpha_grad = alpha_grad.reshape(alpha.shape)
 

@@ -62,6 +62,18 @@ int gsr_camera_position(const float* rot, const float* trans, float* cam_pos, vo
 int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, const float* k_j,
            float* colors, void* stream);
 
+/* No counterpart in the reference: its autograd glue's forward head
+ * (gaussian_splatting/rasterizer/rasterize.py:42-54: camera position, project,
+ * the screen radii, SH) in one kernel, for callers that run the whole
+ * pipeline.  Every output is bit for bit what gsr_camera_position,
+ * gsr_project, gsr_screen_radii and gsr_sh give: mean2d [N,2], cov2d [N,3],
+ * depth [N], radii [N], colors [N,3] and cam_pos [3] (device pointers).
+ * q and k_j must be 16-byte aligned. */
+int gsr_project_sh(int n, const float* mu, const float* q, const float* s, const float* rot,
+                   const float* trans, float fx, float fy, float cx, float cy,
+                   const float* albedo, const float* k_j, float* mean2d, float* cov2d,
+                   float* depth, float* radii, float* colors, float* cam_pos, void* stream);
+
 /* Replaces launch_rasterization (csrc/forward/rasterize.h:11,
  * csrc/forward/rasterize.cu:284-487; bound as `rasterize` at
  * csrc/bindings.cpp:50-70,144), split where the reference itself reads the
@@ -128,12 +140,27 @@ int gsr_project_backward(int n, const float* d_mean2d, const float* d_cov2d, con
                          float fx, float fy, float cx, float cy, float* d_mu, float* d_q,
                          float* d_s, void* stream);
 
+/* No counterpart in the reference: its glue's backward tail
+ * (rasterize.py:100-117: backwards_SH, backwards_projection and the sum of
+ * their dL/dmu) in one kernel.  d_colors is dL/dcolors (the SH input
+ * gradient); d_mu = the projection's dL/dmu + the SH's, in one fp32 addition
+ * as the glue does; every output is bit for bit what gsr_sh_backward and
+ * gsr_project_backward give (GSR_REFERENCE_QUAT_GRAD applies here too).  q,
+ * d_q, k_j and d_k_j must be 16-byte aligned. */
+int gsr_project_sh_backward(int n, const float* d_mean2d, const float* d_cov2d,
+                            const float* d_colors, const float* mu, const float* q,
+                            const float* s, const float* rot, const float* trans, float fx,
+                            float fy, const float* albedo, const float* k_j,
+                            const float* cam_pos, float* d_mu, float* d_q, float* d_s,
+                            float* d_albedo, float* d_k_j, void* stream);
+
 /* Stage timing (no counterpart in the reference; for benchmarks).  While
  * enabled, each entry point records a pair of HIP events on its stream around
- * its stage's kernels: "project", "sh", "bin_count", "depth_sort", "scan",
- * "records", "tile_sort", "ranges", "fwd_schedule", "blend_fwd",
- * "bwd_records", "bwd_slots", "bwd_schedule", "blend_bwd", "grad_reduce",
- * "sh_bwd", "project_bwd".  gsr_profile_collect waits for the recorded events
+ * its stage's kernels: "project", "sh", "project_sh", "bin_count",
+ * "depth_sort", "scan", "records", "tile_binning", "tile_sort", "ranges",
+ * "fwd_schedule", "blend_fwd", "bwd_records", "bwd_slots", "bwd_schedule",
+ * "blend_bwd", "grad_reduce", "sh_bwd", "project_bwd", "project_sh_bwd".
+ * gsr_profile_collect waits for the recorded events
  * and adds their durations to per-stage totals read by gsr_profile_get;
  * gsr_profile_stage(i) names the i-th stage with a total (NULL past the end). */
 void gsr_profile_enable(int on);

@@ -425,6 +425,67 @@ def test_sh_and_projection_backward_parity(crc, device):
         assert_bitwise(_np(g), w, nm)
 
 
+@pytest.mark.parametrize("n", [50_003, 64, 1])
+def test_project_sh_matches_the_separate_ops(crc, device, n):
+    """The glue's fused forward head: bit for bit camera_position, project,
+    screen_radii and SH (and the oracle's projection and SH), culled points and
+    a partial last work-group included."""
+    a = scene_arrays(synthetic.config_scene("c3", requires_grad=False, n=max(n, 2)))
+    mu, q, s = (_dev(a[k][:n], device) for k in ("mu", "q", "s"))
+    mu[::7, 2] = -1.0  # behind the camera: culled
+    A, kj = _dev(a["A"][:n], device), _dev(a["kj"][:n], device)
+    R, T = _dev(a["R"], device), _dev(a["t"], device)
+    cam0 = crc.camera_position(R, T)
+    sep = crc.project(n, mu, q, s, R, T, a["fx"], a["fy"], a["cx"], a["cy"])
+    sep = (*sep, crc.screen_radii(sep[1]), crc.SH(n, cam0, mu, A, kj), cam0)
+    got = crc.project_sh(n, mu, q, s, R, T, a["fx"], a["fy"], a["cx"], a["cy"], A, kj)
+    for g, w, nm in zip(got, sep, ("mean2d", "cov2d", "depth", "radii", "colors", "cam")):
+        assert_bitwise(_np(g), _np(w), nm)
+    want = orc.project(_np(mu), _np(q), _np(s), a["R"], a["t"], a["fx"], a["fy"], a["cx"], a["cy"])
+    for g, w, nm in zip(got[:3], want, ("mean2d", "cov2d", "depth")):
+        assert_bitwise(_np(g), w, nm)
+    assert_bitwise(_np(got[4]), orc.sh(_np(got[5]), _np(mu), _np(A), _np(kj)), "colors")
+
+
+def test_project_sh_without_gaussians_gives_the_camera(crc, device):
+    a = scene_arrays(synthetic.config_scene("c1", requires_grad=False))
+    R, T = _dev(a["R"], device), _dev(a["t"], device)
+    z3 = torch.zeros(0, 3, device=device)
+    out = crc.project_sh(0, z3, torch.zeros(0, 4, device=device), z3, R, T, a["fx"], a["fy"],
+                         a["cx"], a["cy"], z3, torch.zeros(0, 15, 3, device=device))
+    assert [tuple(x.shape) for x in out[:5]] == [(0, 2), (0, 3), (0,), (0,), (0, 3)]
+    assert_bitwise(_np(out[5]), _np(crc.camera_position(R, T)), "cam")
+
+
+@pytest.mark.parametrize("n", [50_003, 1])
+def test_backwards_project_sh_matches_the_separate_ops(crc, device, n):
+    """The glue's fused backward tail: bit for bit backwards_SH,
+    backwards_projection and mu_grad + mu_sh_grad (and the oracle's)."""
+    rng = np.random.default_rng(21)
+    a = scene_arrays(synthetic.config_scene("c3", requires_grad=False, n=max(n, 2)))
+    mu, q, s = (_dev(a[k][:n], device) for k in ("mu", "q", "s"))
+    mu[::5, 2] = -1.0
+    A, kj = _dev(a["A"][:n], device), _dev(a["kj"][:n], device)
+    R, T, cam = _dev(a["R"], device), _dev(a["t"], device), _dev(a["cam"], device)
+    dm = _dev(rng.normal(size=(n, 2)), device)
+    dc = _dev(rng.normal(size=(n, 3)), device)
+    cg = _dev(rng.normal(size=(n, 3)), device)
+    dA, dkj, dmu_sh = crc.backwards_SH(cg, mu, A, kj, cam)
+    dmu_p, dq, ds = crc.backwards_projection(dm, dc, mu, q, s, R, T, a["fx"], a["fy"], a["cx"],
+                                             a["cy"])
+    got = crc.backwards_project_sh(dm, dc, cg, mu, q, s, R, T, a["fx"], a["fy"], A, kj, cam)
+    for g, w, nm in zip(got, (dmu_p + dmu_sh, dq, ds, dA, dkj),
+                        ("d_mu", "d_q", "d_s", "d_albedo", "d_k_j")):
+        assert_bitwise(_np(g), _np(w), nm)
+    w_sh = orc.sh_bwd(_np(cg), _np(mu), _np(A), _np(kj), a["cam"])
+    w_p = orc.project_bwd(_np(dm), _np(dc), _np(mu), _np(q), _np(s), a["R"], a["t"], a["fx"],
+                          a["fy"], a["cx"], a["cy"])
+    assert_bitwise(_np(got[0]), (w_p[0] + w_sh[2]).astype(np.float32), "d_mu (oracle)")
+    for g, w, nm in zip(got[1:], (w_p[1], w_p[2], w_sh[0], w_sh[1]),
+                        ("d_q", "d_s", "d_albedo", "d_k_j")):
+        assert_bitwise(_np(g), w, nm + " (oracle)")
+
+
 def test_forward_is_deterministic(crc, device):
     a = scene_arrays(synthetic.config_scene("c2", requires_grad=False, n=40_000))
     r1 = gpu_forward(crc, a, device)
