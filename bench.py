@@ -45,6 +45,8 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
     return {
         "project": 64 * N,
         "sh": 216 * N,
+        # one pass: mu, q, s, albedo, k_j in (mu once); mean, cov, depth, radius, colour out
+        "project_sh": 272 * N,
         "bin_count": 20 * N + 28 * N,          # mean2d + cov2d + depth in; count, rect, key, val out
         "depth_sort": 4 * 16 * N,
         "scan": 12 * N,
@@ -65,7 +67,9 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
         "grad_reduce": M + 8 * N,               # slot flags + offsets (sums of processed pairs not counted)
         "sh_bwd": 420 * N,
         "project_bwd": 100 * N,
-    }[stage]
+        # the two backwards in one pass: mu read once, dL/dmu written once
+        "project_sh_bwd": 496 * N,
+    }.get(stage)
 
 
 # Highest wave64 VALU issue rate measured on MI355X (v_add_f32 / v_mul_f32 chains,
@@ -227,10 +231,11 @@ def main() -> int:
     for name, (count, ms) in stages.items():
         avg = ms / max(count, 1)
         b = stage_bytes(name, N, M, W, H)
+        rate = b is not None and avg > 0
         per_stage[name] = {"ms": round(avg, 4), "calls": int(count),
-                           "GBps": round(b / (avg * 1e-3) / 1e9, 1) if avg > 0 else None,
+                           "GBps": round(b / (avg * 1e-3) / 1e9, 1) if rate else None,
                            "pct_hbm_peak": round(100 * b / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
-                           if avg > 0 else None}
+                           if rate else None}
     dominant = max(per_stage, key=lambda k: per_stage[k]["ms"]) if per_stage else None
     roofline = None
     if dominant:

@@ -236,6 +236,8 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
     __shared__ float4 s_c[kBatch];
     __shared__ uint32_t s_bits[kBatch];
     const int tile = order ? (int)order[blockIdx.x] : (int)blockIdx.x;
+    // a launch order is a permutation of the tiles; nothing else is touched
+    if ((unsigned)tile >= (unsigned)(tiles_x * ((H + kTileSize - 1) / kTileSize))) return;
     const int tid = threadIdx.x;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: uniform branches
     const uint32_t my_bit = 1u << wave;
@@ -417,6 +419,8 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
 
     const int tile = __builtin_amdgcn_readfirstlane(order ? (int)order[blockIdx.x]
                                                           : (int)blockIdx.x);
+    // a launch order is a permutation of the tiles; nothing else is touched
+    if ((unsigned)tile >= (unsigned)(tiles_x * ((H + kTileSize - 1) / kTileSize))) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: uniform branches
     const uint32_t my_bit = 1u << wave;

@@ -42,10 +42,12 @@ __device__ __forceinline__ void store_agent_u32(uint32_t* p, uint32_t v) {
 
 // True in every thread of the last work-group of the grid to get here; that
 // work-group then sees every other work-group's writes made before its call
-// (release fence, counter, acquire fence).  The last one resets the counter,
-// so it starts at zero for the next launch.
+// (each thread's release fence, a barrier so that the whole work-group has
+// written before it is counted, the counter, an acquire fence).  The last one
+// resets the counter, so it starts at zero for the next launch.
 __device__ __forceinline__ bool last_group(uint32_t* done, uint32_t* s_flag) {
     __threadfence();
+    __syncthreads();
     if (threadIdx.x == 0) {
         const uint32_t groups = gridDim.x * gridDim.y * gridDim.z;
         *s_flag = (atomicAdd(done, 1u) == groups - 1u) ? 1u : 0u;
