@@ -247,10 +247,14 @@ HostCount host_count() {
 // Stands in the host word until bin_count has stored the count.
 constexpr uint64_t kNoCount = ~0ull;
 
-// Marks the pair count's arrival in pinned memory (one per host thread).
+// Marks bin_count's completion (one per host thread).  No system-scope fence:
+// the count reaches the host through the kernel's own system-scope store to
+// coherent host memory, so the event only has to say that the kernel is done.
 hipEvent_t count_event() {
     thread_local hipEvent_t e = nullptr;
-    if (!e && hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) e = nullptr;
+    if (!e && hipEventCreateWithFlags(&e, hipEventDisableTiming | hipEventDisableSystemFence) !=
+                  hipSuccess)
+        e = nullptr;
     return e;
 }
 
