@@ -272,11 +272,22 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_with_keys(
 }
 
 // ---- backwards_rasterization (bindings.cpp:72-100 / rasterize_backward.cu:239-309) ----
-std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization(
-    const Tensor grad_output, const Tensor mean_2d, const Tensor cov_2d, const Tensor colors,
-    const Tensor alpha, const Tensor sorted_ids, const Tensor tile_ranges, const Tensor final_T,
-    const Tensor n_contrib, int num_gaussians, int height, int width) {
-    CHECK_INPUT_FP32(grad_output);
+// strided: grad_output is any [H, W, 3] fp32 view (the glue's variant, no
+// counterpart in the reference, which requires it contiguous).
+std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization_impl(
+    const Tensor& grad_output, const Tensor& mean_2d, const Tensor& cov_2d, const Tensor& colors,
+    const Tensor& alpha, const Tensor& sorted_ids, const Tensor& tile_ranges,
+    const Tensor& final_T, const Tensor& n_contrib, int num_gaussians, int height, int width,
+    bool strided) {
+    if (strided) {
+        CHECK_CUDA(grad_output);
+        CHECK_FP32(grad_output);
+        TORCH_CHECK(grad_output.dim() == 3 && grad_output.size(0) == height &&
+                        grad_output.size(1) == width && grad_output.size(2) == 3,
+                    "grad_output must have shape (H, W, 3)");
+    } else {
+        CHECK_INPUT_FP32(grad_output);
+    }
     CHECK_INPUT_FP32(mean_2d);
     CHECK_INPUT_FP32(cov_2d);
     CHECK_INPUT_FP32(colors);
@@ -309,14 +320,45 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization(
         workspace((int64_t)gsr_backward_workspace_bytes(num_gaussians, sorted_ids.numel(),
                                                          height, width),
                   mean_2d);
-    check_rc(gsr_rasterize_backward(
-                 num_gaussians, height, width, cfp(grad_output), cfp(mean_2d), cfp(cov_2d),
-                 cfp(colors), cfp(alpha), sorted_ids.data_ptr<int32_t>(), sorted_ids.numel(),
-                 tile_ranges.data_ptr<int32_t>(), cfp(final_T), n_contrib.data_ptr<int32_t>(),
-                 ws.data_ptr(), (size_t)ws.numel(), fp(grad_mean_2d), fp(grad_cov_2d),
-                 fp(grad_colors), fp(grad_alpha), current_stream()),
-             "backwards_rasterization");
+    if (strided) {
+        check_rc(gsr_rasterize_backward_strided(
+                     num_gaussians, height, width, cfp(grad_output), grad_output.stride(0),
+                     grad_output.stride(1), grad_output.stride(2), cfp(mean_2d), cfp(cov_2d),
+                     cfp(colors), cfp(alpha), sorted_ids.data_ptr<int32_t>(), sorted_ids.numel(),
+                     tile_ranges.data_ptr<int32_t>(), cfp(final_T),
+                     n_contrib.data_ptr<int32_t>(), ws.data_ptr(), (size_t)ws.numel(),
+                     fp(grad_mean_2d), fp(grad_cov_2d), fp(grad_colors), fp(grad_alpha),
+                     current_stream()),
+                 "backwards_rasterization_strided");
+    } else {
+        check_rc(gsr_rasterize_backward(
+                     num_gaussians, height, width, cfp(grad_output), cfp(mean_2d), cfp(cov_2d),
+                     cfp(colors), cfp(alpha), sorted_ids.data_ptr<int32_t>(), sorted_ids.numel(),
+                     tile_ranges.data_ptr<int32_t>(), cfp(final_T),
+                     n_contrib.data_ptr<int32_t>(), ws.data_ptr(), (size_t)ws.numel(),
+                     fp(grad_mean_2d), fp(grad_cov_2d), fp(grad_colors), fp(grad_alpha),
+                     current_stream()),
+                 "backwards_rasterization");
+    }
     return {grad_mean_2d, grad_cov_2d, grad_colors, grad_alpha};
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization(
+    const Tensor grad_output, const Tensor mean_2d, const Tensor cov_2d, const Tensor colors,
+    const Tensor alpha, const Tensor sorted_ids, const Tensor tile_ranges, const Tensor final_T,
+    const Tensor n_contrib, int num_gaussians, int height, int width) {
+    return backwards_rasterization_impl(grad_output, mean_2d, cov_2d, colors, alpha, sorted_ids,
+                                        tile_ranges, final_T, n_contrib, num_gaussians, height,
+                                        width, false);
+}
+
+std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization_strided(
+    const Tensor grad_output, const Tensor mean_2d, const Tensor cov_2d, const Tensor colors,
+    const Tensor alpha, const Tensor sorted_ids, const Tensor tile_ranges, const Tensor final_T,
+    const Tensor n_contrib, int num_gaussians, int height, int width) {
+    return backwards_rasterization_impl(grad_output, mean_2d, cov_2d, colors, alpha, sorted_ids,
+                                        tile_ranges, final_T, n_contrib, num_gaussians, height,
+                                        width, true);
 }
 
 // ---- backwards_SH (bindings.cpp:102-116 / delight_backward.cu:176-218) ----
@@ -437,6 +479,8 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     m.def("rasterize", &rasterize, "3DGS tile rasterization (HIP, gfx950)");
     m.def("backwards_rasterization", &backwards_rasterization,
           "3DGS backward rasterization (HIP, gfx950)");
+    m.def("backwards_rasterization_strided", &backwards_rasterization_strided,
+          "glue: backwards_rasterization with grad_output any (H, W, 3) view, no copy");
     m.def("backwards_SH", &backwards_SH, "3DGS backward spherical harmonics (HIP, gfx950)");
     m.def("backwards_projection", &backwards_projection,
           "3DGS backward projection (HIP, gfx950)");

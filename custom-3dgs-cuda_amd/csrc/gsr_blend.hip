@@ -368,14 +368,16 @@ __device__ __forceinline__ BwdTerms bwd_update(BwdPixel& p, const BwdDecision& d
 
 __device__ __forceinline__ BwdPixel load_bwd_pixel(bool in, int px, int py, int W,
                                                    const float* __restrict__ grad,
+                                                   const GradStrides& gst,
                                                    const float* __restrict__ finalT,
                                                    const int32_t* __restrict__ ncontrib) {
     BwdPixel p{0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0};
     if (in) {
+        const float* g = grad + (int64_t)py * gst.h + (int64_t)px * gst.w;
+        p.g0 = g[0];
+        p.g1 = g[gst.c];
+        p.g2 = g[2 * gst.c];
         const size_t q = (size_t)py * W + px;
-        p.g0 = grad[3 * q];
-        p.g1 = grad[3 * q + 1];
-        p.g2 = grad[3 * q + 2];
         p.T = finalT[q];
         p.last = max(ncontrib[q], 0);
     }
@@ -402,7 +404,7 @@ __device__ __forceinline__ void conic_to_cov_grad(float cx, float cy, float cz, 
 
 template <int kPix, int kBatch>
 __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
-    int n, int H, int W, int tiles_x, uint64_t m, const float* __restrict__ grad,
+    int n, int H, int W, int tiles_x, uint64_t m, const float* __restrict__ grad, GradStrides gst,
     const int2* __restrict__ ranges, const int32_t* __restrict__ ids,
     const BlendRec* __restrict__ recs, const float* __restrict__ finalT,
     const int32_t* __restrict__ ncontrib, float* __restrict__ dmean, float* __restrict__ dcov,
@@ -433,7 +435,7 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
 #pragma unroll
     for (int k = 0; k < kPix; ++k) {
         fy[k] = (float)pp.py[k];
-        p[k] = load_bwd_pixel(pp.in[k], pp.px, pp.py[k], W, grad, finalT, ncontrib);
+        p[k] = load_bwd_pixel(pp.in[k], pp.px, pp.py[k], W, grad, gst, finalT, ncontrib);
         my_last = max(my_last, p[k].last);
     }
     int start, end;
@@ -904,7 +906,8 @@ hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num
     return hipGetLastError();
 }
 
-hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_t* ranges,
+hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const GradStrides& gst,
+                            const int32_t* ranges,
                             const int32_t* ids, uint64_t num_pairs, const void* recs,
                             const float* finalT, const int32_t* ncontrib, float* dmean,
                             float* dcov, float* dcol, float* dalpha, const GradSlots& gs,
@@ -923,15 +926,15 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_
                                       &blend_bwd_kernel<2, 64>),
                                   Layout<2>::kThreads))
         hipLaunchKernelGGL((blend_bwd_kernel<2, 64>), dim3(tiles), dim3(Layout<2>::kThreads), 0,
-                           st, n, H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib,
+                           st, n, H, W, tiles_x, num_pairs, grad, gst, r, ids, rc, finalT, ncontrib,
                            dmean, dcov, dcol, dalpha, gs, order);
     else if (bwd_pix() == 2)
         hipLaunchKernelGGL((blend_bwd_kernel<2, 128>), dim3(tiles), dim3(Layout<2>::kThreads), 0,
-                           st, n, H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib,
+                           st, n, H, W, tiles_x, num_pairs, grad, gst, r, ids, rc, finalT, ncontrib,
                            dmean, dcov, dcol, dalpha, gs, order);
     else
         hipLaunchKernelGGL((blend_bwd_kernel<1, 256>), dim3(tiles), dim3(Layout<1>::kThreads), 0,
-                           st, n, H, W, tiles_x, num_pairs, grad, r, ids, rc, finalT, ncontrib,
+                           st, n, H, W, tiles_x, num_pairs, grad, gst, r, ids, rc, finalT, ncontrib,
                            dmean, dcov, dcol, dalpha, gs, order);
     return hipGetLastError();
 }

@@ -635,12 +635,16 @@ size_t gsr_backward_workspace_bytes(int n, int64_t num_pairs, int height, int wi
     return backward_layout(n, num_pairs, height, width).end;
 }
 
-int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
-                           const float* mean2d, const float* cov2d, const float* colors,
-                           const float* alpha, const int32_t* sorted_ids, int64_t num_pairs,
-                           const int32_t* tile_ranges, const float* final_T,
-                           const int32_t* n_contrib, void* ws, size_t ws_bytes, float* d_mean2d,
-                           float* d_cov2d, float* d_colors, float* d_alpha, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int rasterize_backward(int n, int height, int width, const float* grad_img,
+                       const gsr::GradStrides& gst, const float* mean2d, const float* cov2d,
+                       const float* colors, const float* alpha, const int32_t* sorted_ids,
+                       int64_t num_pairs, const int32_t* tile_ranges, const float* final_T,
+                       const int32_t* n_contrib, void* ws, size_t ws_bytes, float* d_mean2d,
+                       float* d_cov2d, float* d_colors, float* d_alpha, void* stream) {
     GSR_REQUIRE(n >= 0, "n must be non-negative");
     if (int rc = check_screen(height, width)) return rc;
     GSR_REQUIRE(num_pairs >= 0 && num_pairs <= kMaxPairs, "num_pairs out of range");
@@ -694,7 +698,7 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
     }
     {
         StageTimer timer("blend_bwd", st);
-        GSR_HIP(gsr::launch_blend_bwd(n, height, width, grad_img, tile_ranges, sorted_ids,
+        GSR_HIP(gsr::launch_blend_bwd(n, height, width, grad_img, gst, tile_ranges, sorted_ids,
                                       (uint64_t)num_pairs, at<void>(ws, L.recs), final_T,
                                       n_contrib, d_mean2d, d_cov2d, d_colors, d_alpha, gs, order,
                                       st),
@@ -705,6 +709,43 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
                                          d_alpha, st),
             "backward: gradient sums");
     return GSR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
+                           const float* mean2d, const float* cov2d, const float* colors,
+                           const float* alpha, const int32_t* sorted_ids, int64_t num_pairs,
+                           const int32_t* tile_ranges, const float* final_T,
+                           const int32_t* n_contrib, void* ws, size_t ws_bytes, float* d_mean2d,
+                           float* d_cov2d, float* d_colors, float* d_alpha, void* stream) {
+    gsr::GradStrides gst;
+    gst.h = 3 * (int64_t)width;
+    gst.w = 3;
+    gst.c = 1;
+    return rasterize_backward(n, height, width, grad_img, gst, mean2d, cov2d, colors, alpha,
+                              sorted_ids, num_pairs, tile_ranges, final_T, n_contrib, ws,
+                              ws_bytes, d_mean2d, d_cov2d, d_colors, d_alpha, stream);
+}
+
+int gsr_rasterize_backward_strided(int n, int height, int width, const float* grad_img,
+                                   int64_t grad_stride_h, int64_t grad_stride_w,
+                                   int64_t grad_stride_c, const float* mean2d,
+                                   const float* cov2d, const float* colors, const float* alpha,
+                                   const int32_t* sorted_ids, int64_t num_pairs,
+                                   const int32_t* tile_ranges, const float* final_T,
+                                   const int32_t* n_contrib, void* ws, size_t ws_bytes,
+                                   float* d_mean2d, float* d_cov2d, float* d_colors,
+                                   float* d_alpha, void* stream) {
+    gsr::GradStrides gst;
+    gst.h = grad_stride_h;
+    gst.w = grad_stride_w;
+    gst.c = grad_stride_c;
+    return rasterize_backward(n, height, width, grad_img, gst, mean2d, cov2d, colors, alpha,
+                              sorted_ids, num_pairs, tile_ranges, final_T, n_contrib, ws,
+                              ws_bytes, d_mean2d, d_cov2d, d_colors, d_alpha, stream);
 }
 
 int gsr_sh_backward(int n, const float* colors_grad, const float* mu, const float* albedo,

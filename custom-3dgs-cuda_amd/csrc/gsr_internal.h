@@ -230,7 +230,14 @@ struct GradSlots {
     uint64_t slots = 0;
 };
 
-hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const int32_t* ranges,
+// Element strides of dL/dimage: pixel (y, x) channel c at grad[y h + x w + c c]
+// ({3 W, 3, 1} for a contiguous [H, W, 3] image).
+struct GradStrides {
+    int64_t h = 0, w = 0, c = 0;
+};
+
+hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const GradStrides& gst,
+                            const int32_t* ranges,
                             const int32_t* ids, uint64_t num_pairs, const void* recs,
                             const float* finalT, const int32_t* ncontrib, float* dmean,
                             float* dcov, float* dcol, float* dalpha, const GradSlots& gs,

@@ -103,8 +103,11 @@ class RasterizeFunction(t.autograd.Function):
             cam_rotation, cam_translation, cam_position,
         ) = ctx.saved_tensors
 
-        mean_2d_grad, cov_2d_grad, colors_grad, alpha_grad = crc.backwards_rasterization(
-            grad_output.contiguous(), mean_2d, cov_2d, colors, alpha,
+        # the reference copies grad_output with .contiguous() (rasterize.py:85-86);
+        # the strided op reads any [H, W, 3] view in place (image.sum() hands
+        # in a broadcast one)
+        mean_2d_grad, cov_2d_grad, colors_grad, alpha_grad = crc.backwards_rasterization_strided(
+            grad_output, mean_2d, cov_2d, colors, alpha,
             sorted_ids, tile_ranges, final_T, n_contrib,
             ctx.num_gaussians, ctx.height, ctx.width,
         )

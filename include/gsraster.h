@@ -120,6 +120,23 @@ int gsr_rasterize_backward(int n, int height, int width, const float* grad_img,
                            const int32_t* n_contrib, void* ws, size_t ws_bytes, float* d_mean2d,
                            float* d_cov2d, float* d_colors, float* d_alpha, void* stream);
 
+/* No counterpart in the reference (its binding requires a contiguous
+ * grad_output, and its glue copies one with .contiguous(),
+ * rasterize.py:85-86): gsr_rasterize_backward with dL/dimage given as a
+ * strided view, pixel (y, x) channel c at grad_img[y * grad_stride_h +
+ * x * grad_stride_w + c * grad_stride_c] (element strides, any sign; all zero
+ * for the broadcast gradient of image.sum()), so no contiguous copy is made.
+ * Results are bit for bit those of gsr_rasterize_backward on the same values. */
+int gsr_rasterize_backward_strided(int n, int height, int width, const float* grad_img,
+                                   int64_t grad_stride_h, int64_t grad_stride_w,
+                                   int64_t grad_stride_c, const float* mean2d,
+                                   const float* cov2d, const float* colors, const float* alpha,
+                                   const int32_t* sorted_ids, int64_t num_pairs,
+                                   const int32_t* tile_ranges, const float* final_T,
+                                   const int32_t* n_contrib, void* ws, size_t ws_bytes,
+                                   float* d_mean2d, float* d_cov2d, float* d_colors,
+                                   float* d_alpha, void* stream);
+
 /* Replaces launch_backward_SH (csrc/backward/delight_backward.h:5,
  * csrc/backward/delight_backward.cu:176-218; bound as `backwards_SH` at
  * csrc/bindings.cpp:102-116,148).  cam_pos is a device pointer; k_j and d_k_j

@@ -267,6 +267,34 @@ def test_rasterize_backward_parity(crc, device, name, kw):
     _backward_case(crc, device, a)
 
 
+def test_rasterize_backward_strided_gradient_views(crc, device):
+    """backwards_rasterization_strided reads dL/dimage views in place: a
+    broadcast (image.sum()'s gradient, strides 0), a transposed image and a
+    channel slice, each bit for bit the contiguous op on .contiguous()."""
+    a = scene_arrays(synthetic.config_scene("c3", requires_grad=False, n=20_000, width=480,
+                                            height=270))
+    fw = gpu_forward(crc, a, device)
+    t, n, H, W = fw["tensors"], a["mu"].shape[0], a["H"], a["W"]
+    G = synthetic.grad_image(H, W, seed=4).to(device)
+    views = {
+        "broadcast": torch.full((1, 1, 1), 1.7, device=device).expand(H, W, 3),
+        "transposed": G.transpose(0, 1).contiguous().transpose(0, 1),
+        "channel_slice": torch.cat([G, G[..., :1]], dim=2)[..., :3],
+    }
+    for name, g in views.items():
+        assert not g.is_contiguous(), name
+        args = (t["mean2d"], t["cov2d"], t["colors"], t["alpha"], t["ids"], t["ranges"],
+                t["final_T"], t["n_contrib"], n, H, W)
+        want = crc.backwards_rasterization(g.contiguous(), *args)
+        got = crc.backwards_rasterization_strided(g, *args)
+        for x, y, nm in zip(got, want, ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")):
+            assert_bitwise(_np(x), _np(y), f"{name}: {nm}")
+    with pytest.raises(RuntimeError, match="contiguous"):
+        crc.backwards_rasterization(views["transposed"], *args)
+    with pytest.raises(RuntimeError, match="shape"):
+        crc.backwards_rasterization_strided(G.reshape(W, H, 3), *args)
+
+
 def test_rasterize_backward_skips_corrupt_ids(crc, device):
     a = scene_arrays(synthetic.config_scene("c1", requires_grad=False, n=2000, width=64, height=48))
     _backward_case(crc, device, a, corrupt=True)
