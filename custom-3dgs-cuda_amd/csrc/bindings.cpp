@@ -107,12 +107,14 @@ Tensor screen_radii(const Tensor cov_2d) {
 }
 
 // The glue's forward head in one kernel (rasterize.py:42-54): (mean_2d,
-// cov_2d, depths, radii, colors, camera_position), bit for bit those of
-// camera_position, project, screen_radii and SH.
-std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> project_sh(
+// cov_2d, depths, radii, colors, camera_position, opacity), bit for bit those
+// of camera_position, project, screen_radii and SH; with alpha_logits also
+// the opacity t.sigmoid(alpha_logits) (rasterize.py:149), else an empty tensor.
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> project_sh(
     int total_gaussians, const Tensor mu3d, const Tensor q3d, const Tensor s3d,
     const Tensor camera_rotation, const Tensor camera_translation, float fx, float fy, float cx,
-    float cy, const Tensor albedo_coeff, const Tensor illumination_coeff) {
+    float cy, const Tensor albedo_coeff, const Tensor illumination_coeff,
+    const c10::optional<Tensor>& alpha_logits) {
     CHECK_INPUT_FP32(mu3d);
     CHECK_INPUT_FP32(q3d);
     CHECK_INPUT_FP32(s3d);
@@ -129,8 +131,14 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> project_sh(
     check_numel(camera_translation, 3, "camera_translation must hold 3 values");
     check_numel(albedo_coeff, 3 * n, "albedo_coeff must hold N x 3 values");
     check_numel(illumination_coeff, 45 * n, "illumination_coeff must hold N x 15 x 3 values");
+    const bool logits = alpha_logits.has_value() && alpha_logits->defined();
+    if (logits) {
+        CHECK_INPUT_FP32(*alpha_logits);
+        TORCH_CHECK(alpha_logits->numel() == n, "alpha_logits must have N elements");
+    }
     c10::hip::HIPGuardMasqueradingAsCUDA guard(mu3d.device());
     auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mu3d.device());
+    Tensor opacity = logits ? torch::empty_like(*alpha_logits) : torch::empty({0}, options);
     Tensor mean_2d = torch::empty({n, 2}, options);
     Tensor cov_2d = torch::empty({n, 3}, options);
     Tensor depths = torch::empty({n}, options);
@@ -142,9 +150,10 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> project_sh(
     check_rc(gsr_project_sh(total_gaussians, cfp(mu3d), cfp(q_al), cfp(s3d), cfp(camera_rotation),
                             cfp(camera_translation), fx, fy, cx, cy, cfp(albedo_coeff),
                             cfp(k_al), fp(mean_2d), fp(cov_2d), fp(depths), fp(radii),
-                            fp(colors), fp(cam), current_stream()),
+                            fp(colors), fp(cam), logits ? cfp(*alpha_logits) : nullptr,
+                            logits ? fp(opacity) : nullptr, current_stream()),
              "project_sh");
-    return {mean_2d, cov_2d, depths, radii, colors, cam};
+    return {mean_2d, cov_2d, depths, radii, colors, cam, opacity};
 }
 
 Tensor camera_position(const Tensor camera_rotation, const Tensor camera_translation) {
@@ -421,13 +430,16 @@ std::tuple<Tensor, Tensor, Tensor> backwards_projection(
 }
 
 // The glue's backward tail in one kernel (rasterize.py:100-117): (mu_grad,
-// q_grad, s_grad, albedo_grad, k_j_grad) with mu_grad = the projection's +
-// the SH's, bit for bit backwards_SH, backwards_projection and that sum.
-std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backwards_project_sh(
+// q_grad, s_grad, albedo_grad, k_j_grad, alpha_logits_grad) with mu_grad =
+// the projection's + the SH's, bit for bit backwards_SH, backwards_projection
+// and that sum; with alpha_grad and opacity also torch's sigmoid backward
+// into alpha_logits_grad (shaped like opacity), else an empty tensor.
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> backwards_project_sh(
     const Tensor mean_2d_grad, const Tensor cov_2d_grad, const Tensor colors_grad,
     const Tensor mu, const Tensor q, const Tensor s, const Tensor camera_rotation,
     const Tensor camera_translation, float fx, float fy, const Tensor albedo, const Tensor k_j,
-    const Tensor camera_position) {
+    const Tensor camera_position, const c10::optional<Tensor>& alpha_grad,
+    const c10::optional<Tensor>& opacity) {
     CHECK_INPUT_FP32(mean_2d_grad);
     CHECK_INPUT_FP32(cov_2d_grad);
     CHECK_INPUT_FP32(colors_grad);
@@ -450,8 +462,18 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backwards_project_sh(
     check_numel(albedo, 3 * n, "albedo must hold N x 3 values");
     check_numel(k_j, 45 * n, "k_j must hold N x 15 x 3 values");
     TORCH_CHECK(camera_position.numel() >= 3, "camera_position must have 3 elements");
+    const bool sig = alpha_grad.has_value() && alpha_grad->defined();
+    TORCH_CHECK(sig == (opacity.has_value() && opacity->defined()),
+                "alpha_grad and opacity go together");
+    if (sig) {
+        CHECK_INPUT_FP32(*alpha_grad);
+        CHECK_INPUT_FP32(*opacity);
+        TORCH_CHECK(alpha_grad->numel() == n && opacity->numel() == n,
+                    "alpha_grad and opacity must have N elements");
+    }
     c10::hip::HIPGuardMasqueradingAsCUDA guard(mu.device());
     auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mu.device());
+    Tensor logit_grad = sig ? torch::empty_like(*opacity) : torch::empty({0}, options);
     Tensor mu_grad = torch::empty({n, 3}, options);
     Tensor q_grad = torch::empty({n, 4}, options);
     Tensor s_grad = torch::empty({n, 3}, options);
@@ -464,9 +486,11 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> backwards_project_sh(
                                      cfp(camera_rotation), cfp(camera_translation), fx, fy,
                                      cfp(albedo), cfp(k_al), cfp(camera_position), fp(mu_grad),
                                      fp(q_grad), fp(s_grad), fp(albedo_grad), fp(k_j_grad),
-                                     current_stream()),
+                                     sig ? cfp(*alpha_grad) : nullptr,
+                                     sig ? cfp(*opacity) : nullptr,
+                                     sig ? fp(logit_grad) : nullptr, current_stream()),
              "backwards_project_sh");
-    return {mu_grad, q_grad, s_grad, albedo_grad, k_j_grad};
+    return {mu_grad, q_grad, s_grad, albedo_grad, k_j_grad, logit_grad};
 }
 
 }  // namespace
@@ -490,9 +514,20 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     m.def("screen_radii", &screen_radii, "glue: approximate screen radii (one kernel)");
     m.def("camera_position", &camera_position, "glue: camera position -R^T t (one kernel)");
     m.def("project_sh", &project_sh,
-          "glue: camera position, project, screen radii and SH in one kernel");
+          "glue: camera position, project, screen radii, SH (and the opacity sigmoid) in one "
+          "kernel",
+          py::arg("total_gaussians"), py::arg("mu3d"), py::arg("q3d"), py::arg("s3d"),
+          py::arg("camera_rotation"), py::arg("camera_translation"), py::arg("fx"), py::arg("fy"),
+          py::arg("cx"), py::arg("cy"), py::arg("albedo_coeff"), py::arg("illumination_coeff"),
+          py::arg("alpha_logits") = py::none());
     m.def("backwards_project_sh", &backwards_project_sh,
-          "glue: backwards_SH, backwards_projection and their dL/dmu sum in one kernel");
+          "glue: backwards_SH, backwards_projection, their dL/dmu sum (and the sigmoid's "
+          "backward) in one kernel",
+          py::arg("mean_2d_grad"), py::arg("cov_2d_grad"), py::arg("colors_grad"), py::arg("mu"),
+          py::arg("q"), py::arg("s"), py::arg("camera_rotation"), py::arg("camera_translation"),
+          py::arg("fx"), py::arg("fy"), py::arg("albedo"), py::arg("k_j"),
+          py::arg("camera_position"), py::arg("alpha_grad") = py::none(),
+          py::arg("opacity") = py::none());
     // Stage timing of libgsraster (HIP events on the launch stream); not part of
     // the reference surface.
     m.def("profile_enable", [](bool on) { gsr_profile_enable(on ? 1 : 0); });

@@ -385,9 +385,11 @@ int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, co
 int gsr_project_sh(int n, const float* mu, const float* q, const float* s, const float* rot,
                    const float* trans, float fx, float fy, float cx, float cy,
                    const float* albedo, const float* k_j, float* mean2d, float* cov2d,
-                   float* depth, float* radii, float* colors, float* cam_pos, void* stream) {
+                   float* depth, float* radii, float* colors, float* cam_pos,
+                   const float* alpha_logits, float* opacity, void* stream) {
     GSR_REQUIRE(n >= 0, "n must be non-negative");
     GSR_REQUIRE(rot && trans && cam_pos, "null pointer");
+    GSR_REQUIRE(!alpha_logits || opacity, "opacity must not be null when alpha_logits is given");
     if (n == 0) return gsr_camera_position(rot, trans, cam_pos, stream);
     GSR_REQUIRE(mu && q && s && albedo && k_j && mean2d && cov2d && depth && radii && colors,
                 "null pointer");
@@ -396,7 +398,7 @@ int gsr_project_sh(int n, const float* mu, const float* q, const float* s, const
     StageTimer timer("project_sh", as_stream(stream));
     GSR_HIP(gsr::launch_project_sh_fwd(n, mu, q, s, rot, trans, fx, fy, cx, cy, albedo, k_j,
                                        mean2d, cov2d, depth, radii, colors, cam_pos,
-                                       as_stream(stream)),
+                                       alpha_logits, opacity, as_stream(stream)),
             "project_sh");
     return GSR_OK;
 }
@@ -769,8 +771,11 @@ int gsr_project_sh_backward(int n, const float* d_mean2d, const float* d_cov2d,
                             const float* s, const float* rot, const float* trans, float fx,
                             float fy, const float* albedo, const float* k_j,
                             const float* cam_pos, float* d_mu, float* d_q, float* d_s,
-                            float* d_albedo, float* d_k_j, void* stream) {
+                            float* d_albedo, float* d_k_j, const float* d_opacity,
+                            const float* opacity, float* d_alpha_logits, void* stream) {
     GSR_REQUIRE(n >= 0, "n must be non-negative");
+    GSR_REQUIRE(!d_opacity || (opacity && d_alpha_logits),
+                "opacity and d_alpha_logits must not be null when d_opacity is given");
     if (n == 0) return GSR_OK;
     GSR_REQUIRE(d_mean2d && d_cov2d && d_colors && mu && q && s && rot && trans && albedo && k_j &&
                     cam_pos && d_mu && d_q && d_s && d_albedo && d_k_j,
@@ -782,7 +787,8 @@ int gsr_project_sh_backward(int n, const float* d_mean2d, const float* d_cov2d,
     StageTimer timer("project_sh_bwd", as_stream(stream));
     GSR_HIP(gsr::launch_project_sh_bwd(n, d_mean2d, d_cov2d, d_colors, mu, q, s, rot, trans, fx,
                                        fy, albedo, k_j, cam_pos, d_mu, d_q, d_s, d_albedo, d_k_j,
-                                       ref_quat_mode(), as_stream(stream)),
+                                       ref_quat_mode(), d_opacity, opacity, d_alpha_logits,
+                                       as_stream(stream)),
             "project_sh_backward");
     return GSR_OK;
 }

@@ -30,19 +30,23 @@ hipError_t launch_sh_bwd(int n, const float* cgrad, const float* mu, const float
                          hipStream_t st);
 
 // Fused per-Gaussian passes: camera position + projection + screen radius +
-// SH colour (cam: 3 floats out), and SH backward + projection backward with
-// dL/dmu summed.  Bit for bit the single-pass kernels' results.
+// SH colour (cam: 3 floats out; with logits also the sigmoid opacity), and
+// SH backward + projection backward with dL/dmu summed (with dop also the
+// sigmoid's backward into dlogits).  Bit for bit the single-pass kernels'
+// (and torch's sigmoid) results.
 hipError_t launch_project_sh_fwd(int n, const float* mu, const float* q, const float* s,
                                  const float* rot, const float* tr, float fx, float fy, float cx,
                                  float cy, const float* albedo, const float* kj, float* mean2d,
                                  float* cov2d, float* depth, float* radii, float* colors,
-                                 float* cam, hipStream_t st);
+                                 float* cam, const float* logits, float* opacity,
+                                 hipStream_t st);
 hipError_t launch_project_sh_bwd(int n, const float* dmean, const float* dcov,
                                  const float* cgrad, const float* mu, const float* q,
                                  const float* s, const float* rot, const float* tr, float fx,
                                  float fy, const float* albedo, const float* kj, const float* cam,
                                  float* dmu, float* dq, float* ds, float* dA, float* dkj,
-                                 int ref_quat, hipStream_t st);
+                                 int ref_quat, const float* dop, const float* op,
+                                 float* dlogits, hipStream_t st);
 
 // ---- radix sort (u32 keys, u32 values), LSD onesweep with 8-bit digits ----
 // Partition size of one onesweep work-group.

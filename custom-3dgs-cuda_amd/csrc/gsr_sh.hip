@@ -58,14 +58,16 @@ __global__ __launch_bounds__(kThreads) void sh_bwd_kernel(
 // position, projection, screen radius and SH colour of each Gaussian, with
 // the operations of camera_position_kernel, project_fwd_kernel,
 // screen_radii_kernel and sh_fwd_kernel, so every output is bit for bit
-// theirs.  Thread 0 of work-group 0 also stores cam.
+// theirs.  Thread 0 of work-group 0 also stores cam.  With logits, also the
+// opacity 1 / (1 + exp(-logit)): torch's fp32 sigmoid, operation for
+// operation (the device expf and a correctly rounded division).
 __global__ __launch_bounds__(kThreads) void project_sh_fwd_kernel(
     int n, const float* __restrict__ mu, const float* __restrict__ q,
     const float* __restrict__ s, const float* __restrict__ rot, const float* __restrict__ tr,
     float fx, float fy, float cx, float cy, const float* __restrict__ albedo,
     const float* __restrict__ kj, float* __restrict__ mean2d, float* __restrict__ cov2d,
     float* __restrict__ depth, float* __restrict__ radii, float* __restrict__ colors,
-    float* __restrict__ cam_out) {
+    float* __restrict__ cam_out, const float* __restrict__ logits, float* __restrict__ opacity) {
     __shared__ __align__(16) float s_k[kThreads * kShCoef];
     const size_t base = (size_t)blockIdx.x * kThreads;
     const int cnt = (int)min((size_t)kThreads, (size_t)n - base);
@@ -88,6 +90,7 @@ __global__ __launch_bounds__(kThreads) void project_sh_fwd_kernel(
         cov2d[3 * i + 2] = p.c;
         depth[i] = p.d;
         radii[i] = screen_radius(p.a, p.b, p.c);
+        if (logits) opacity[i] = 1.0f / (1.0f + expf(-logits[i]));
     }
     __syncthreads();
     if (!live) return;
@@ -100,14 +103,17 @@ __global__ __launch_bounds__(kThreads) void project_sh_fwd_kernel(
 // The glue's backward tail in one pass (rasterize.py:100-125): the SH
 // backward and the projection backward of each Gaussian, with dL/dmu the sum
 // of the two (projection's + SH's, the glue's one fp32 addition), with the
-// operations of sh_bwd_kernel and project_bwd_kernel.
+// operations of sh_bwd_kernel and project_bwd_kernel.  With d_opacity, also
+// dL/dlogit = (d_opacity (1 - s)) s for s = the opacity: torch's fp32 sigmoid
+// backward, operation for operation.
 __global__ __launch_bounds__(kThreads) void project_sh_bwd_kernel(
     int n, const float* __restrict__ dmean, const float* __restrict__ dcov,
     const float* __restrict__ cgrad, const float* __restrict__ mu, const float* __restrict__ q,
     const float* __restrict__ s, const float* __restrict__ rot, const float* __restrict__ tr,
     float fx, float fy, const float* __restrict__ albedo, const float* __restrict__ kj,
     const float* __restrict__ cam, float* __restrict__ dmu, float* __restrict__ dq,
-    float* __restrict__ ds, float* __restrict__ dA, float* __restrict__ dkj, int ref_quat) {
+    float* __restrict__ ds, float* __restrict__ dA, float* __restrict__ dkj, int ref_quat,
+    const float* __restrict__ dop, const float* __restrict__ op, float* __restrict__ dlogits) {
     __shared__ __align__(16) float s_k[kThreads * kShCoef];
     const size_t base = (size_t)blockIdx.x * kThreads;
     const int cnt = (int)min((size_t)kThreads, (size_t)n - base);
@@ -126,6 +132,10 @@ __global__ __launch_bounds__(kThreads) void project_sh_bwd_kernel(
             ds[3 * i + k] = os[k];
         }
         *reinterpret_cast<float4*>(dq + 4 * i) = make_float4(oq[0], oq[1], oq[2], oq[3]);
+        if (dop) {
+            const float sg = op[i];
+            dlogits[i] = (dop[i] * (1.0f - sg)) * sg;
+        }
     }
     __syncthreads();
     unstage_coeffs(dkj, s_k, base, cnt);
@@ -147,11 +157,12 @@ hipError_t launch_project_sh_fwd(int n, const float* mu, const float* q, const f
                                  const float* rot, const float* tr, float fx, float fy, float cx,
                                  float cy, const float* albedo, const float* kj, float* mean2d,
                                  float* cov2d, float* depth, float* radii, float* colors,
-                                 float* cam, hipStream_t st) {
+                                 float* cam, const float* logits, float* opacity,
+                                 hipStream_t st) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(project_sh_fwd_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, n, mu,
                        q, s, rot, tr, fx, fy, cx, cy, albedo, kj, mean2d, cov2d, depth, radii,
-                       colors, cam);
+                       colors, cam, logits, opacity);
     return hipGetLastError();
 }
 
@@ -160,11 +171,12 @@ hipError_t launch_project_sh_bwd(int n, const float* dmean, const float* dcov,
                                  const float* s, const float* rot, const float* tr, float fx,
                                  float fy, const float* albedo, const float* kj, const float* cam,
                                  float* dmu, float* dq, float* ds, float* dA, float* dkj,
-                                 int ref_quat, hipStream_t st) {
+                                 int ref_quat, const float* dop, const float* op,
+                                 float* dlogits, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     hipLaunchKernelGGL(project_sh_bwd_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, n,
                        dmean, dcov, cgrad, mu, q, s, rot, tr, fx, fy, albedo, kj, cam, dmu, dq,
-                       ds, dA, dkj, ref_quat);
+                       ds, dA, dkj, ref_quat, dop, op, dlogits);
     return hipGetLastError();
 }
 

@@ -68,11 +68,15 @@ int gsr_sh(int n, const float* cam_pos, const float* mu, const float* albedo, co
  * pipeline.  Every output is bit for bit what gsr_camera_position,
  * gsr_project, gsr_screen_radii and gsr_sh give: mean2d [N,2], cov2d [N,3],
  * depth [N], radii [N], colors [N,3] and cam_pos [3] (device pointers).
- * q and k_j must be 16-byte aligned. */
+ * alpha_logits (may be NULL): opacity logits [N]; opacity [N] then receives
+ * the glue's t.sigmoid(alpha) (rasterize.py:149), as torch computes it in
+ * fp32 (1 / (1 + exp(-x)) with the device expf).  q and k_j must be 16-byte
+ * aligned. */
 int gsr_project_sh(int n, const float* mu, const float* q, const float* s, const float* rot,
                    const float* trans, float fx, float fy, float cx, float cy,
                    const float* albedo, const float* k_j, float* mean2d, float* cov2d,
-                   float* depth, float* radii, float* colors, float* cam_pos, void* stream);
+                   float* depth, float* radii, float* colors, float* cam_pos,
+                   const float* alpha_logits, float* opacity, void* stream);
 
 /* Replaces launch_rasterization (csrc/forward/rasterize.h:11,
  * csrc/forward/rasterize.cu:284-487; bound as `rasterize` at
@@ -162,14 +166,18 @@ int gsr_project_backward(int n, const float* d_mean2d, const float* d_cov2d, con
  * their dL/dmu) in one kernel.  d_colors is dL/dcolors (the SH input
  * gradient); d_mu = the projection's dL/dmu + the SH's, in one fp32 addition
  * as the glue does; every output is bit for bit what gsr_sh_backward and
- * gsr_project_backward give (GSR_REFERENCE_QUAT_GRAD applies here too).  q,
- * d_q, k_j and d_k_j must be 16-byte aligned. */
+ * gsr_project_backward give (GSR_REFERENCE_QUAT_GRAD applies here too).
+ * d_opacity (may be NULL): dL/dopacity [N] and the forward's opacity [N];
+ * d_alpha_logits [N] then receives the sigmoid's backward, (d_opacity
+ * (1 - opacity)) opacity, as torch's fp32 sigmoid backward.  q, d_q, k_j and
+ * d_k_j must be 16-byte aligned. */
 int gsr_project_sh_backward(int n, const float* d_mean2d, const float* d_cov2d,
                             const float* d_colors, const float* mu, const float* q,
                             const float* s, const float* rot, const float* trans, float fx,
                             float fy, const float* albedo, const float* k_j,
                             const float* cam_pos, float* d_mu, float* d_q, float* d_s,
-                            float* d_albedo, float* d_k_j, void* stream);
+                            float* d_albedo, float* d_k_j, const float* d_opacity,
+                            const float* opacity, float* d_alpha_logits, void* stream);
 
 /* Stage timing (no counterpart in the reference; for benchmarks).  While
  * enabled, each entry point records a pair of HIP events on its stream around

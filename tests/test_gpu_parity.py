@@ -475,6 +475,61 @@ def test_project_sh_matches_the_separate_ops(crc, device, n):
     assert_bitwise(_np(got[4]), orc.sh(_np(got[5]), _np(mu), _np(A), _np(kj)), "colors")
 
 
+def test_project_sh_opacity_is_torch_sigmoid(crc, device):
+    """The fused head's opacity from logits equals t.sigmoid bit for bit, over
+    ±100, tiny and huge values, ±inf and NaN; the fused tail's logit gradient
+    equals torch's sigmoid backward bit for bit."""
+    rng = np.random.default_rng(23)
+    n = 70_001
+    a = scene_arrays(synthetic.config_scene("c3", requires_grad=False, n=n))
+    lg = np.r_[rng.uniform(-100, 100, n - 9),
+               [0.0, -0.0, 1e-30, -1e-30, 88.0, -88.0, np.inf, -np.inf, np.nan]].astype(np.float32)
+    logits = _dev(lg.reshape(n, 1), device)
+    mu, q, s = (_dev(a[k], device) for k in ("mu", "q", "s"))
+    A, kj = _dev(a["A"], device), _dev(a["kj"], device)
+    R, T = _dev(a["R"], device), _dev(a["t"], device)
+    out = crc.project_sh(n, mu, q, s, R, T, a["fx"], a["fy"], a["cx"], a["cy"], A, kj, logits)
+    op = out[6]
+    assert op.shape == logits.shape
+    assert_bitwise(_np(op), _np(torch.sigmoid(logits)), "opacity")
+    dop = _dev(rng.normal(size=(n, 1)), device)
+    z = lambda *sh: torch.zeros(*sh, device=device)
+    got = crc.backwards_project_sh(z(n, 2), z(n, 3), z(n, 3), mu, q, s, R, T, a["fx"], a["fy"],
+                                   A, kj, out[5], dop, op)
+    assert got[5].shape == op.shape
+    assert_bitwise(_np(got[5]), _np(torch.ops.aten.sigmoid_backward(dop, op)), "d logits")
+    assert got[5].numel() == n and crc.backwards_project_sh(
+        z(n, 2), z(n, 3), z(n, 3), mu, q, s, R, T, a["fx"], a["fy"], A, kj, out[5])[5].numel() == 0
+
+
+def test_glue_logits_path_equals_sigmoid_then_rasterize(device):
+    """rasterize() (opacity logits, sigmoid fused) against t.sigmoid +
+    RasterizeFunction: the image and every parameter gradient bit for bit."""
+    import importlib
+    glue = importlib.import_module("gaussian_splatting.rasterizer.rasterize")
+    sc = synthetic.config_scene("c3", device=device, n=20_000, width=480, height=270)
+    g, v = sc.gaussians, sc.view
+    names = ("mu", "q", "s", "alpha", "A", "k_j")
+
+    def run(fused):
+        for nm in names:
+            getattr(g, nm).grad = None
+        if fused:
+            img = glue.rasterize(g, v)
+        else:
+            img = glue.RasterizeFunction.apply(g.mu, g.q, g.s, torch.sigmoid(g.alpha), g.A, g.k_j,
+                                               v["R"], v["T"], v["fx"], v["fy"], v["cx"],
+                                               v["cy"], v["height"], v["width"])
+        (img * torch.linspace(0.5, 1.5, img.numel(), device=device).view_as(img)).sum().backward()
+        return img.detach().clone(), [getattr(g, nm).grad.clone() for nm in names]
+
+    i1, g1 = run(True)
+    i0, g0 = run(False)
+    assert_bitwise(_np(i1), _np(i0), "image")
+    for a_, b_, nm in zip(g1, g0, names):
+        assert_bitwise(_np(a_), _np(b_), f"d {nm}")
+
+
 def test_project_sh_without_gaussians_gives_the_camera(crc, device):
     a = scene_arrays(synthetic.config_scene("c1", requires_grad=False))
     R, T = _dev(a["R"], device), _dev(a["t"], device)
