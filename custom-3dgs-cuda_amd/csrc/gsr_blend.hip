@@ -669,23 +669,35 @@ __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
 // The order changes no result: every tile's pixels are computed by one
 // work-group on their own. ----
 
-// Backward work of a tile: its list entries up to the largest n_contrib.
-__global__ __launch_bounds__(kTilePixels) void tile_work_bwd_kernel(
-    int H, int W, int tiles_x, uint64_t m, const int2* __restrict__ ranges,
-    const int32_t* __restrict__ ncontrib, uint32_t* __restrict__ work) {
-    __shared__ uint32_t s_max[kTilePixels / kWave];
-    const int tile = blockIdx.x, tid = threadIdx.x;
-    const int px = (tile % tiles_x) * kTileSize + (tid & 15);
-    const int py = (tile / tiles_x) * kTileSize + (tid >> 4);
-    const uint32_t c =
-        (px < W && py < H) ? (uint32_t)max(ncontrib[(size_t)py * W + px], 0) : 0u;
-    const uint32_t wm = wave_max_u32(c);
-    if ((tid & 63) == 0) s_max[tid >> 6] = wm;
-    __syncthreads();
-    if (tid == 0) {
+// Backward work of a tile: its list entries up to the largest n_contrib.  One
+// wave per tile, lane l reading row l / 4, columns 4 (l % 4) .. + 3 (one
+// 16-byte load when vec4: the image rows are 16-byte aligned).
+constexpr int kWorkTilesPerBlock = 4;
+
+__global__ __launch_bounds__(kWorkTilesPerBlock * kWave) void tile_work_bwd_kernel(
+    int T, int H, int W, int tiles_x, uint64_t m, const int2* __restrict__ ranges,
+    const int32_t* __restrict__ ncontrib, uint32_t* __restrict__ work, int vec4) {
+    const int lane = threadIdx.x & 63;
+    const int tile = blockIdx.x * kWorkTilesPerBlock + (int)(threadIdx.x >> 6);
+    if (tile >= T) return;  // whole waves; no barriers below
+    const int py = (tile / tiles_x) * kTileSize + (lane >> 2);
+    const int px = (tile % tiles_x) * kTileSize + 4 * (lane & 3);
+    int c = 0;
+    if (py < H) {
+        const int32_t* row = ncontrib + (size_t)py * W;
+        if (vec4 && px + 3 < W) {
+            const int4 v = *reinterpret_cast<const int4*>(row + px);
+            c = max(max(v.x, v.y), max(v.z, v.w));
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (px + k < W) c = max(c, row[px + k]);
+        }
+    }
+    const uint32_t mx = wave_max_u32((uint32_t)max(c, 0));
+    if (lane == 0) {
         int start, end;
         clamp_range(ranges[tile], m, start, end);
-        const uint32_t mx = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
         work[tile] = min(mx, (uint32_t)(end - start));
     }
 }
@@ -899,8 +911,11 @@ hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num
     const unsigned tiles = (unsigned)(tiles_x * ((H + kTileSize - 1) / kTileSize));
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
-    hipLaunchKernelGGL(tile_work_bwd_kernel, dim3(tiles), dim3(kTilePixels), 0, st, H, W, tiles_x,
-                       num_pairs, r, ncontrib, work);
+    const int vec4 = (W % 4 == 0) && ((reinterpret_cast<uintptr_t>(ncontrib) & 15) == 0);
+    hipLaunchKernelGGL(tile_work_bwd_kernel,
+                       dim3((tiles + kWorkTilesPerBlock - 1) / kWorkTilesPerBlock),
+                       dim3(kWorkTilesPerBlock * kWave), 0, st, (int)tiles, H, W, tiles_x,
+                       num_pairs, r, ncontrib, work, vec4);
     hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles,
                        num_pairs, r, work, order);
     return hipGetLastError();
