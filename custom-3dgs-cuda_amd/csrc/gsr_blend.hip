@@ -622,20 +622,37 @@ __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
         const uint64_t base = gs.goff[g];
         const uint64_t end = min(base + (uint64_t)gs.counts[g], gs.slots);
         // flags eight at a time from 8-byte aligned groups (the flag array is
-        // 256-byte aligned and padded to a multiple of 8 bytes)
-        for (uint64_t grp = (base & ~7ull) + 8ull * sub; grp < end;
-             grp += 8ull * kReduceRowLanes) {
-            uint64_t bits = *reinterpret_cast<const uint64_t*>(gs.flags + grp);
+        // 256-byte aligned and padded to a multiple of 8 bytes); each group's
+        // flags are loaded while the group before is summed, and the sums of
+        // two flagged slots are loaded together
+        uint64_t grp = (base & ~7ull) + 8ull * sub;
+        uint64_t bits = (grp < end) ? *reinterpret_cast<const uint64_t*>(gs.flags + grp) : 0ull;
+        while (grp < end) {
+            const uint64_t nxt = grp + 8ull * kReduceRowLanes;
+            const uint64_t nbits =
+                (nxt < end) ? *reinterpret_cast<const uint64_t*>(gs.flags + nxt) : 0ull;
+            // only the flags of [base, end) (flag bytes hold 0 or 1)
+            if (grp < base) bits &= ~0ull << (8 * (base - grp));
+            if (end - grp < 8) bits &= ~(~0ull << (8 * (end - grp)));
             while (bits) {
-                const int b = __builtin_ctzll(bits) >> 3;  // flag bytes hold 0 or 1
+                const uint64_t s0 = grp + (uint64_t)(__builtin_ctzll(bits) >> 3);
                 bits &= bits - 1;
-                const uint64_t slot = grp + (uint64_t)b;
-                if (slot >= base && slot < end) {
-                    const float* d = gs.sums + 9 * slot;
+                const bool two = bits != 0;
+                const uint64_t s1 = two ? grp + (uint64_t)(__builtin_ctzll(bits) >> 3) : s0;
+                if (two) bits &= bits - 1;
+                const float* d0 = gs.sums + 9 * s0;
+                const float* d1 = gs.sums + 9 * s1;
+                float a[kTerms], b[kTerms];
 #pragma unroll
-                    for (int k = 0; k < kTerms; ++k) v[k] += d[k];
+                for (int k = 0; k < kTerms; ++k) {
+                    a[k] = d0[k];
+                    b[k] = d1[k];
                 }
+#pragma unroll
+                for (int k = 0; k < kTerms; ++k) v[k] += two ? a[k] + b[k] : a[k];
             }
+            grp = nxt;
+            bits = nbits;
         }
     }
     // every lane takes part in the row sums (rows past n add zeros)
