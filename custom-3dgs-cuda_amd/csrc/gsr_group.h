@@ -1,5 +1,6 @@
-// gsr_group.h — work-group scans and the "last work-group" hand-off shared by
-// the binning kernels (gfx950, wave64).
+// gsr_group.h — work-group scans, the one-wave decoupled look-back and the
+// "last work-group" hand-off shared by the binning and scan kernels (gfx950,
+// wave64).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -59,6 +60,48 @@ __device__ __forceinline__ bool last_group(uint32_t* done, uint32_t* s_flag) {
         if (threadIdx.x == 0) store_agent_u32(done, 0u);
     }
     return last;
+}
+
+// Decoupled look-back over 64-bit status words (flag in the top two bits,
+// value below), run by one whole wave: publishes agg as partition part's
+// aggregate (its inclusive prefix when part is 0), sums the published values
+// of partitions part - 1 downwards, 64 per step, to the nearest one with an
+// inclusive prefix (waiting only while one of those is unpublished), publishes
+// part's inclusive prefix and returns its exclusive prefix in every lane.  A
+// wait beyond kSpinLimit sets bit 0 of *err and ends it (the prefix is then
+// incomplete), so no wave can hang.
+__device__ inline uint64_t wave_lookback(uint64_t* status, uint64_t part, uint64_t agg,
+                                         int* err) {
+    const int lane = lane_id();
+    uint64_t* mine = status + part;
+    if (lane == 0) store_agent(mine, (part == 0 ? kFlagInclusive : kFlagAggregate) | agg);
+    uint64_t excl = 0;
+    if (part > 0) {
+        int64_t hi = (int64_t)part - 1;
+        uint32_t spins = 0;
+        while (true) {
+            const int64_t q = hi - lane;
+            // below partition 0: an inclusive zero, which ends the walk
+            const uint64_t s = (q >= 0) ? load_agent(status + q) : kFlagInclusive;
+            const uint64_t flag = s & ~kValueMask;
+            const uint64_t incl = ballot(flag == kFlagInclusive);
+            const int last = incl ? (int)__builtin_ctzll(incl) : 63;
+            const uint64_t need = (last == 63) ? ~0ull : ((2ull << last) - 1ull);
+            if (ballot(flag == 0) & need) {
+                if (++spins > kSpinLimit) {
+                    if (lane == 0) atomicOr(err, 1);
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+                continue;
+            }
+            excl += wave_sum_u64(lane <= last ? (s & kValueMask) : 0ull);
+            if (incl) break;
+            hi -= 64;
+        }
+        if (lane == 0) store_agent(mine, kFlagInclusive | (excl + agg));
+    }
+    return excl;
 }
 
 // block_start[b] / seg_start[b] (nb + 1 entries each): exclusive prefixes of

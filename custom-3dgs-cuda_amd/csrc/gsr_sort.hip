@@ -21,6 +21,7 @@
 
 #include "gsr_internal.h"
 #include "gsr_common.h"
+#include "gsr_group.h"
 
 namespace gsr {
 
@@ -468,38 +469,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_counts_kernel(
         if (w < wave) wpre += s_wsum[w];
         btot += s_wsum[w];
     }
-    // Look-back by the first wave, 64 predecessors per step: it sums the
-    // published values of the partitions from part - 1 down to the nearest one
-    // with an inclusive prefix, and waits only while one of those is unpublished.
+    // look-back by the first wave, 64 predecessors per step
     if (wave == 0) {
-        uint64_t* mine = status + part;
-        if (lane == 0) store_agent(mine, (part == 0 ? kFlagInclusive : kFlagAggregate) | (uint64_t)btot);
-        uint64_t excl = 0;
-        if (part > 0) {
-            int64_t hi = (int64_t)part - 1;
-            uint32_t spins = 0;
-            while (true) {
-                const int64_t q = hi - lane;
-                // below partition 0: an inclusive zero, which ends the walk
-                const uint64_t s = (q >= 0) ? load_agent(status + q) : kFlagInclusive;
-                const uint64_t flag = s & ~kValueMask;
-                const uint64_t incl = ballot(flag == kFlagInclusive);
-                const int last = incl ? (int)__builtin_ctzll(incl) : 63;
-                const uint64_t need = (last == 63) ? ~0ull : ((2ull << last) - 1ull);
-                if (ballot(flag == 0) & need) {
-                    if (++spins > kSpinLimit) {
-                        if (lane == 0) atomicOr(err, 1);
-                        break;
-                    }
-                    __builtin_amdgcn_s_sleep(1);
-                    continue;
-                }
-                excl += wave_sum_u64(lane <= last ? (s & kValueMask) : 0ull);
-                if (incl) break;
-                hi -= 64;
-            }
-            if (lane == 0) store_agent(mine, kFlagInclusive | (excl + btot));
-        }
+        const uint64_t excl = wave_lookback(status, part, (uint64_t)btot, err);
         if (lane == 0) {
             s_base = excl;
             const uint64_t pbeg = part * kScanPartition;
