@@ -99,6 +99,49 @@ def test_forward_parity_600k_1080p(crc, device, monkeypatch, binning):
     _check_forward(gpu_forward(crc, a, device), oracle_forward(a))
 
 
+def test_4k_frame_properties(crc, device, monkeypatch):
+    """1M Gaussians at 3840x2160 (32,400 tiles), beyond the oracle's seconds:
+    size-independent properties instead.  Both tile binnings give the same
+    keys, ids, ranges, n_contrib, image and final T bit for bit; every list is
+    sorted by (depth bits, id) and holds only Gaussians whose tile rectangle
+    covers the tile; the ranges tile [0, M); the backward is deterministic and
+    finite."""
+    print("[gpu] 4K frame properties (1M Gaussians, 3840x2160)", flush=True)
+    sc = synthetic.config_scene("c3", requires_grad=False, n=1_000_000, width=3840, height=2160)
+    a = scene_arrays(sc)
+    blocks = gpu_forward(crc, a, device)
+    monkeypatch.setenv("GSR_TILE_BINNING", "sort")
+    srt = gpu_forward(crc, a, device)
+    monkeypatch.delenv("GSR_TILE_BINNING")
+    for k in ("keys", "ids", "ranges", "n_contrib", "img", "final_T"):
+        assert_bitwise(blocks[k], srt[k], f"blocks vs sort: {k}")
+    keys, ids, rng = blocks["keys"], blocks["ids"].astype(np.int64), blocks["ranges"]
+    M = ids.size
+    assert M > 10_000_000
+    tiles = (keys >> np.uint64(32)).astype(np.int64)
+    assert np.all(keys[1:] >= keys[:-1])
+    same = (keys[1:] == keys[:-1])
+    assert np.all(ids[1:][same] > ids[:-1][same]), "equal keys keep the Gaussian order"
+    nz = rng[:, 1] > rng[:, 0]
+    assert rng[nz, 0].min() == 0 and rng[nz, 1].max() == M
+    assert np.array_equal(np.sort(rng[nz, 0]), rng[nz, 0]) and np.all(rng[nz][1:, 0] == rng[nz][:-1, 1])
+    # the tile of each pair lies in its Gaussian's tile rectangle
+    _, rect = orc.bin_count(blocks["mean2d"], blocks["cov2d"], a["H"], a["W"])
+    x0, x1, y0, y1 = (rect[:, k][ids] for k in range(4))
+    tx_n = (a["W"] + 15) // 16
+    tx, ty = tiles % tx_n, tiles // tx_n
+    assert np.all((tx >= x0) & (tx < x1) & (ty >= y0) & (ty < y1))
+    t, n = blocks["tensors"], a["mu"].shape[0]
+    G = synthetic.grad_image(a["H"], a["W"], seed=5).to(device)
+    args = (t["mean2d"], t["cov2d"], t["colors"], t["alpha"], t["ids"], t["ranges"], t["final_T"],
+            t["n_contrib"], n, a["H"], a["W"])
+    r1 = [_np(x) for x in crc.backwards_rasterization(G, *args)]
+    r2 = [_np(x) for x in crc.backwards_rasterization(G, *args)]
+    for x, y, nm in zip(r1, r2, ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")):
+        assert np.isfinite(x).all(), nm
+        assert_bitwise(x, y, nm)
+
+
 @pytest.mark.parametrize("name,kw", [("c3", dict(n=20_000, width=480, height=270)),
                                      ("c5", dict(n=30_000, width=400, height=224))],
                          ids=["c3", "c5"])
