@@ -1,7 +1,7 @@
 """Benchmark of the MI355X rasterizer: fwd+bwd ms/frame and FPS, 100k Gaussians at
 1920x1080, with the dominant kernel's HBM-roofline fraction and a CPU baseline.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-extra] [--no-scale]
 
 A step is one frame of the reference's own benchmark (scripts/bench.py:30-109):
 ``image = rasterize(gaussians, view)`` then ``image.sum().backward()`` on its synthetic
@@ -143,6 +143,118 @@ def pair_count(sc) -> int:
     return int(out[1].numel())
 
 
+def _stage_rates(stages: dict, N: int, M: int, W: int, H: int, keep=None) -> dict:
+    out = {}
+    for name, (count, ms) in stages.items():
+        if keep is not None and name not in keep:
+            continue
+        avg = ms / max(count, 1)
+        b = stage_bytes(name, N, M, W, H)
+        rate = b is not None and avg > 0
+        out[name] = {"ms": round(avg, 4), "calls": int(count),
+                     "GBps": round(b / (avg * 1e-3) / 1e9, 1) if rate else None,
+                     "pct_hbm_peak": round(100 * b / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
+                     if rate else None}
+    return out
+
+
+# The stages that replace the reference's count_overlaps + exclusive scan +
+# key_generation + 64-bit radix sort + tile ranges (rasterize.cu:345-449).
+BINNING_STAGES = ("bin_count", "depth_sort", "scan", "tile_binning", "tile_sort", "ranges")
+
+
+def reference_binning_bytes(N: int, M: int, W: int, H: int) -> int:
+    """The rasterizer baseline's fixed algorithmic bytes for those stages: count +
+    scan + keys 64N + 12M, the sort's passes x 24M with passes = ceil((32 +
+    ceil(log2 T)) / 8) 8-bit digits, ranges 8M + 8T."""
+    T = _tiles(W, H)
+    passes = math.ceil((32 + math.ceil(math.log2(T)) if T > 1 else 32) / 8)
+    return 64 * N + 12 * M + passes * 24 * M + 8 * M + 8 * T
+
+
+def binning_summary(stages: dict, N: int, M: int, W: int, H: int) -> dict:
+    """Time of the binning stages against the reference algorithm's bytes (an
+    equivalent rate: this build moves fewer bytes) and against this build's own."""
+    used = [k for k in BINNING_STAGES if k in stages]
+    ms = sum(stages[k]["ms"] for k in used)
+    own = sum(stage_bytes(k, N, M, W, H) for k in used)
+    ref = reference_binning_bytes(N, M, W, H)
+    if ms <= 0:
+        return {"stages": used, "ms": 0.0}
+    return {"stages": used, "ms": round(ms, 4), "reference_bytes": ref,
+            "reference_equiv_GBps": round(ref / (ms * 1e-3) / 1e9, 1),
+            "reference_equiv_frac": round(ref / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3),
+            "own_bytes": own, "own_GBps": round(own / (ms * 1e-3) / 1e9, 1),
+            "own_frac": round(own / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 3)}
+
+
+def per_gaussian_stages(sc, calls: int = 20) -> dict:
+    """The per-Gaussian stages (project, SH, their backwards and the fused glue
+    kernels) called directly on config ``sc``'s cloud, at sizes where they move
+    hundreds of MB: HIP-event stage times and GB/s from the per-stage byte
+    formulas."""
+    import torch
+    import custom_rasterizer_cuda as crc
+
+    g, v = sc.gaussians, sc.view
+    n = g.mu.shape[0]
+    mu, q, s, A, kj = (x.detach() for x in (g.mu, g.q, g.s, g.A, g.k_j))
+    logits = g.alpha.detach()
+    R, T = v["R"], v["T"]
+    fx, fy, cx, cy = (float(v[k]) for k in ("fx", "fy", "cx", "cy"))
+    gen = torch.Generator(device="cpu").manual_seed(7)
+    dm = torch.randn(n, 2, generator=gen).to(mu.device)
+    dc = torch.randn(n, 3, generator=gen).to(mu.device)
+    dcol = torch.randn(n, 3, generator=gen).to(mu.device)
+    dal = torch.randn(n, 1, generator=gen).to(mu.device)
+    cam = (-(R.T @ T)).contiguous()
+
+    def one_round():
+        crc.project(n, mu, q, s, R, T, fx, fy, cx, cy)
+        crc.SH(n, cam, mu, A, kj)
+        out = crc.project_sh(n, mu, q, s, R, T, fx, fy, cx, cy, A, kj, logits)
+        crc.backwards_SH(dcol, mu, A, kj, cam)
+        crc.backwards_projection(dm, dc, mu, q, s, R, T, fx, fy, cx, cy)
+        crc.backwards_project_sh(dm, dc, dcol, mu, q, s, R, T, fx, fy, A, kj, out[5], dal,
+                                 out[6])
+
+    with torch.no_grad():
+        for _ in range(3):
+            one_round()
+        torch.cuda.synchronize()
+        crc.profile_reset()
+        crc.profile_enable(True)
+        for _ in range(calls):
+            one_round()
+        torch.cuda.synchronize()
+        crc.profile_enable(False)
+        stages = crc.profile_collect()
+    return _stage_rates(stages, n, 0, v["width"], v["height"])
+
+
+def frame_stages(sc, steps: int, binning: str | None = None) -> dict:
+    """fwd+bwd frames of config ``sc`` with the per-stage breakdown; ``binning``
+    "sort" selects the LSD tile sort (GSR_TILE_BINNING) for these frames."""
+    old = os.environ.get("GSR_TILE_BINNING")
+    if binning:
+        os.environ["GSR_TILE_BINNING"] = binning
+    try:
+        M = pair_count(sc)
+        fwd, bwd, total, _ = time_frames(sc, steps, 2, profile=False)
+        _, _, _, stages = time_frames(sc, steps, 1, profile=True)
+    finally:
+        if old is None:
+            os.environ.pop("GSR_TILE_BINNING", None)
+        else:
+            os.environ["GSR_TILE_BINNING"] = old
+    v = sc.view
+    rates = _stage_rates(stages, sc.n, M, v["width"], v["height"])
+    return {"fwd_ms": round(fwd, 4), "bwd_ms": round(bwd, 4), "ms_per_frame": round(total, 4),
+            "fps": round(1000.0 / total, 1), "pairs": M,
+            "binning": binning_summary(rates, sc.n, M, v["width"], v["height"]),
+            "stages": rates}
+
+
 def cpu_baseline(sc, budget_s: float = 30.0) -> dict:
     """The CPU oracle (oracle/gs_oracle.cpp, OpenMP) on the same frame: forward
     (project, SH, key emission, stable sort, ranges, blend) + backward (blend, SH,
@@ -191,8 +303,13 @@ def main() -> int:
     ap.add_argument("--gaussians", type=int, default=100_000)
     ap.add_argument("--width", type=int, default=1920)
     ap.add_argument("--height", type=int, default=1080)
+    ap.add_argument("--scene", default="bench", choices=["bench", "c1", "c2", "c3", "c4", "c5"],
+                    help="the frame to time: the reference's bench scene (default) or a "
+                         "rasterizer baseline config at its own size (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the 720p and c3 side runs")
+    ap.add_argument("--no-scale", action="store_true",
+                    help="skip the per-stage HBM measurements on configs c4 and c5")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -220,22 +337,19 @@ def main() -> int:
                           "launches": 5}), flush=True)
         return 0
     W, H, N = args.width, args.height, args.gaussians
-    sc = synthetic.bench_scene(n=N, width=W, height=H, device=dev)
-    workload = f"bench_{N // 1000}k_{W}x{H}"
+    if args.scene == "bench":
+        sc = synthetic.bench_scene(n=N, width=W, height=H, device=dev)
+        workload = f"bench_{N // 1000}k_{W}x{H}"
+    else:
+        sc = synthetic.config_scene(args.scene, device=dev)
+        N, W, H = sc.n, sc.view["width"], sc.view["height"]
+        workload = sc.name
     M = pair_count(sc)
 
     fwd, bwd, total, _ = time_frames(sc, args.steps, args.warmup, profile=False)
     pf, pb, ptot, stages = time_frames(sc, args.steps, 2, profile=True)
 
-    per_stage = {}
-    for name, (count, ms) in stages.items():
-        avg = ms / max(count, 1)
-        b = stage_bytes(name, N, M, W, H)
-        rate = b is not None and avg > 0
-        per_stage[name] = {"ms": round(avg, 4), "calls": int(count),
-                           "GBps": round(b / (avg * 1e-3) / 1e9, 1) if rate else None,
-                           "pct_hbm_peak": round(100 * b / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
-                           if rate else None}
+    per_stage = _stage_rates(stages, N, M, W, H)
     dominant = max(per_stage, key=lambda k: per_stage[k]["ms"]) if per_stage else None
     roofline = None
     if dominant:
@@ -264,13 +378,16 @@ def main() -> int:
         "vs_baseline": round(value / (1000.0 / REF_FWD_BWD_MS_1080P), 2)
         if (W, H, N) == (1920, 1080, 100_000) else None,
         "dtype": "fp32", "data": "synthetic",
-        "config": {"workload": f"reference scripts/bench.py scene, {N} Gaussians (SH-3 "
-                               f"coefficients, seed 0), {W}x{H}, forward + backward "
+        "config": {"workload": (f"reference scripts/bench.py scene, {N} Gaussians (SH-3 "
+                                f"coefficients, seed 0), {W}x{H}, forward + backward "
+                                f"(loss = image.sum())") if args.scene == "bench" else
+                               f"rasterizer baseline config {sc.name}, forward + backward "
                                f"(loss = image.sum())",
                    "gaussians": N, "width": W, "height": H, "pairs": M, "tiles": _tiles(W, H)},
         "fwd_ms": round(fwd, 4), "bwd_ms": round(bwd, 4),
         "fps_forward": round(1000.0 / fwd, 1),
         "roofline": roofline,
+        "binning": binning_summary(per_stage, N, M, W, H),
         "stages": per_stage,
         "profiled_ms_per_step": round(ptot, 4),
     }
@@ -284,6 +401,18 @@ def main() -> int:
                             "ms_per_frame": round(t2, 4), "fps": round(1000.0 / t2, 1),
                             "pairs": pair_count(scene)}
         out["extra"] = extra
+    if not args.no_scale:
+        # the HBM-bound stages where they move hundreds of MB: the per-Gaussian
+        # kernels on config c5's 5M-Gaussian cloud, the depth sort and the
+        # tile binning / LSD tile sort on config c4's 1M-Gaussian frame
+        c5 = synthetic.config_scene("c5", device=dev, requires_grad=False)
+        scale = {"per_gaussian_c5_5M": per_gaussian_stages(c5)}
+        del c5
+        c4 = synthetic.config_scene("c4", device=dev)
+        scale["c4_1M_1920x1080"] = frame_stages(c4, 5)
+        scale["c4_1M_1920x1080_tile_sort"] = frame_stages(c4, 5, binning="sort")
+        del c4
+        out["scale"] = scale
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(sc)
     print(json.dumps(out), flush=True)

@@ -39,3 +39,25 @@ def test_more_than_one_gpu_is_refused(n):
                        capture_output=True, text=True, timeout=120)
     assert r.returncode != 0
     assert "one GPU" in (r.stdout + r.stderr) or "1 GPU" in (r.stdout + r.stderr)
+
+
+@pytest.mark.parametrize("n, m, w, h, passes", [
+    (10_000, 30_900, 256, 256, 5),          # c1: T = 256, ceil((32 + 8) / 8)
+    (100_000, 1_810_000, 1280, 720, 6),     # c2: T = 3600, ceil((32 + 12) / 8)
+    (100_000, 3_490_000, 1920, 1080, 6),    # c3: T = 8160, ceil((32 + 13) / 8)
+    (1_000_000, 41_600_000, 3840, 2160, 6), # T = 32400, ceil((32 + 15) / 8)
+])
+def test_reference_binning_bytes_follow_the_fixed_formula(n, m, w, h, passes):
+    t = ((w + 15) // 16) * ((h + 15) // 16)
+    want = 64 * n + 12 * m + passes * 24 * m + 8 * m + 8 * t
+    assert bench.reference_binning_bytes(n, m, w, h) == want
+
+
+def test_binning_summary_sums_the_binning_stages_only():
+    st = {"bin_count": {"ms": 0.02}, "depth_sort": {"ms": 0.03},
+          "tile_binning": {"ms": 0.05}, "blend_fwd": {"ms": 0.2}}
+    s = bench.binning_summary(st, 100_000, 13_000_000, 1920, 1080)
+    assert s["stages"] == ["bin_count", "depth_sort", "tile_binning"]
+    assert s["ms"] == pytest.approx(0.1)
+    ref = bench.reference_binning_bytes(100_000, 13_000_000, 1920, 1080)
+    assert s["reference_equiv_GBps"] == pytest.approx(ref / 1e-4 / 1e9, rel=1e-3)
