@@ -93,11 +93,12 @@ def _clear(g):
         getattr(g, name).grad = None
 
 
-def time_frames(sc, steps: int, warmup: int, profile: bool):
+def time_frames(sc, steps: int, warmup: int, profile: bool, render=None):
     import torch
     import custom_rasterizer_cuda as crc
     from gaussian_splatting.rasterizer.rasterize import rasterize
 
+    rasterize = render or rasterize
     g, view = sc.gaussians, sc.view
     for _ in range(warmup):
         _clear(g)
@@ -255,6 +256,38 @@ def frame_stages(sc, steps: int, binning: str | None = None) -> dict:
             "stages": rates}
 
 
+def banded_frame(sc, band_height: int, steps: int) -> dict:
+    """fwd+bwd of a frame beyond the int32 pair lists, rendered as screen bands
+    of ``band_height`` rows through the unchanged surface (rasterize_bands):
+    frame time, the stage breakdown and each band's pair count."""
+    import torch
+    from gaussian_splatting.rasterizer.bands import band_views, rasterize_bands
+    from gaussian_splatting.synthetic import Scene
+
+    render = lambda g, v: rasterize_bands(g, v, band_height)
+    print(f"[bench] {sc.name}: {steps} banded frame(s), bands of {band_height} rows",
+          file=sys.stderr, flush=True)
+    fwd, bwd, total, stages = time_frames(sc, steps, 1, profile=True, render=render)
+    print(f"[bench] {sc.name}: {total:.1f} ms per frame; counting pairs per band",
+          file=sys.stderr, flush=True)
+    pairs = [pair_count(Scene(sc.gaussians, v, f"{sc.name}_band{y0}"))
+             for y0, v in band_views(sc.view, band_height)]
+    torch.cuda.empty_cache()
+    v = sc.view
+    M = sum(pairs)
+    bands = len(pairs)
+    # per-stage rates: a stage's calls cover all bands, so per frame it moves
+    # the bytes of the whole frame (per-Gaussian stages once per band)
+    rates = {}
+    for name, (count, ms) in stages.items():
+        per_frame = ms / max(steps, 1)
+        rates[name] = {"ms_per_frame": round(per_frame, 3), "calls": int(count)}
+    return {"fwd_ms": round(fwd, 3), "bwd_ms": round(bwd, 3), "ms_per_frame": round(total, 3),
+            "fps": round(1000.0 / total, 2), "pairs": M, "bands": bands,
+            "band_height": band_height, "max_band_pairs": max(pairs),
+            "stages": rates, "width": v["width"], "height": v["height"], "gaussians": sc.n}
+
+
 def cpu_baseline(sc, budget_s: float = 30.0) -> dict:
     """The CPU oracle (oracle/gs_oracle.cpp, OpenMP) on the same frame: forward
     (project, SH, key emission, stable sort, ranges, blend) + backward (blend, SH,
@@ -307,6 +340,10 @@ def main() -> int:
                     help="the frame to time: the reference's bench scene (default) or a "
                          "rasterizer baseline config at its own size (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--c5", action="store_true",
+                    help="also time config c5 (5M Gaussians, 3840x2160) in screen bands")
+    ap.add_argument("--band-height", type=int, default=128,
+                    help="rows per screen band of the c5 frame (a multiple of 16)")
     ap.add_argument("--no-extra", action="store_true", help="skip the 720p and c3 side runs")
     ap.add_argument("--no-scale", action="store_true",
                     help="skip the per-stage HBM measurements on configs c4 and c5")
@@ -413,6 +450,12 @@ def main() -> int:
         scale["c4_1M_1920x1080_tile_sort"] = frame_stages(c4, 5, binning="sort")
         del c4
         out["scale"] = scale
+    if args.c5:
+        # config c5 (5M Gaussians, 3840x2160): ~1.1e10 pairs, beyond the int32
+        # lists of the reference's surface, so rendered in screen bands
+        c5 = synthetic.config_scene("c5", device=dev)
+        out["c5_banded"] = banded_frame(c5, args.band_height, max(1, min(args.steps, 3)))
+        del c5
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(sc)
     print(json.dumps(out), flush=True)

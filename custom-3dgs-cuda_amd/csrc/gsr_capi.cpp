@@ -44,7 +44,10 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
 constexpr int kDepthPasses = 4;         // 32-bit depth keys, 8-bit digits
-constexpr int64_t kMaxPairs = 2147483647;  // sorted_ids and offsets are int32
+// sorted_ids and tile ranges are int32, and the kernels add up to two list
+// batches (well under 2^16) to int32 list positions: the pair count stays
+// that far below 2^31.
+constexpr int64_t kMaxPairs = 2147483647 - 65535;
 constexpr size_t kRecBytes = 48;
 
 int tiles_x_of(int W) { return (W + 15) / 16; }

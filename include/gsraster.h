@@ -32,7 +32,7 @@ extern "C" {
 #define GSR_ERR_INVALID_ARGUMENT 1 /* null pointer, bad size, misaligned q */
 #define GSR_ERR_HIP 2              /* a HIP runtime call or launch failed */
 #define GSR_ERR_WORKSPACE 3        /* workspace smaller than the size query */
-#define GSR_ERR_TOO_MANY_PAIRS 4   /* M >= 2^31 (the int32 sorted_ids limit) */
+#define GSR_ERR_TOO_MANY_PAIRS 4   /* M > 2^31 - 2^16 (the int32 sorted_ids limit, less headroom) */
 #define GSR_ERR_DEVICE 5           /* a kernel reported an error (look-back spin limit) */
 
 const char* gsr_last_error(void);
