@@ -298,10 +298,12 @@ def _backward_case(crc, device, a, seed=3, corrupt=False):
     return fw, want, G, (dm, dc, dcol, dal)
 
 
-@pytest.mark.parametrize("name,kw", [("c1", dict()), ("c3", dict(n=20_000, width=480, height=270)),
+@pytest.mark.parametrize("name,kw", [("c1", dict()), ("c2", dict(n=20_000, width=640, height=360)),
+                                     ("c3", dict(n=20_000, width=480, height=270)),
+                                     ("c4", dict(n=50_000, width=480, height=272)),
                                      ("c5", dict(n=20_000, width=320, height=192)),
                                      ("c3_1080p", dict(n=60_000, width=1920, height=1080))],
-                         ids=["c1", "c3", "c5", "c3_1080p"])
+                         ids=["c1", "c2", "c3", "c4", "c5", "c3_1080p"])
 def test_rasterize_backward_parity(crc, device, name, kw):
     """c3_1080p: 8160 tiles, more than fit on the device at once, so the
     backward runs its 64-entry-batch kernel."""
