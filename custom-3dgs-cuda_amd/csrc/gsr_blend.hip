@@ -402,7 +402,74 @@ __device__ __forceinline__ void conic_to_cov_grad(float cx, float cy, float cz, 
     out[2] = -(cy * cy * gx + 2.0f * cy * cz * gy + cz * cz * gz);
 }
 
+// Long tiles' backward runs as two work items (tile_order_kernel picks them).
+// The back part walks entries [mid, maxc) from the final transmittance, as a
+// whole tile does.  The front part walks the same entries first with the
+// pixel state only (state_walk) (the T and accumulated-colour steps of
+// rasterize_backward.cu:141-198, no gradient sums), which hands it the exact
+// state the sequential walk has at mid, then walks [0, mid) in full.  Both
+// parts' gradients are bit for bit the whole tile's.  A state-only step costs
+// about 0.4 of a full one, so mid = 0.37 maxc leaves each part ~0.63 of the
+// tile's walk.
+constexpr int kPartWhole = 0, kPartBack = 1, kPartFront = 2;
+constexpr int kSplitNum = 37, kSplitDen = 100;
+// Most tiles split per backward launch (the launch has this many extra groups).
+constexpr int kSplitMax = 256;
+
+// The pixel state's walk over entries [lo0, hi0), back to front: the same
+// decisions and T / accumulated-colour steps as the full walk, no sums.
 template <int kPix, int kBatch>
+__device__ __forceinline__ void state_walk(int lo0, int hi0, int n, int tile, int tiles_x,
+                                           int start, int wave_last, uint32_t my_bit, float fx,
+                                           const float (&fy)[kPix], BwdPixel (&p)[kPix],
+                                           const int32_t* __restrict__ ids,
+                                           const BlendRec* __restrict__ recs, float4* s_a,
+                                           float4* s_b, float4* s_c) {
+    const int tid = threadIdx.x;
+    for (int hi = hi0; hi > lo0; hi -= kBatch) {
+        const int lo = max(lo0, hi - kBatch);
+        const int cnt = hi - lo;
+        __syncthreads();
+        if (tid < cnt)
+            stage_entry<kPix>(recs, ids[start + lo + tid], n, tile, tiles_x, s_a, s_b, s_c,
+                              nullptr, nullptr, tid);
+        __syncthreads();
+        for (int j = cnt - 1; j >= 0; --j) {
+            const int contributor = lo + j + 1;
+            const float4 Cc = s_c[j];
+            const uint32_t bits = uniform_bits(Cc);
+            if (contributor > wave_last || (bits & my_bit) == 0) continue;
+            const float4 A = s_a[j];
+            const float4 B = s_b[j];
+            const float dx = fx - A.x;
+            const float adxdx = (A.z * dx) * dx;
+            const float bdx = A.w * dx;
+            BwdDecision d[kPix];
+#pragma unroll
+            for (int k = 0; k < kPix; ++k) {
+                d[k].dy = fy[k] - A.y;
+                d[k].power = __builtin_fmaf(B.x * d[k].dy, d[k].dy,
+                                            __builtin_fmaf(bdx, d[k].dy, adxdx));
+            }
+            bool exact = (bits & kFastExpBit) == 0;
+            if (!exact) {
+                bool near = false;
+#pragma unroll
+                for (int k = 0; k < kPix; ++k)
+                    near |= decide_fast(d[k], B.y, contributor, p[k].last);
+                exact = ballot(near) != 0;
+            }
+            if (exact) {
+#pragma unroll
+                for (int k = 0; k < kPix; ++k) decide_exact(d[k], B.y, contributor, p[k].last);
+            }
+#pragma unroll
+            for (int k = 0; k < kPix; ++k) (void)bwd_update(p[k], d[k], B, Cc.x);
+        }
+    }
+}
+
+template <int kPix, int kBatch, bool kSplit>
 __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     int n, int H, int W, int tiles_x, uint64_t m, const float* __restrict__ grad, GradStrides gst,
     const int2* __restrict__ ranges, const int32_t* __restrict__ ids,
@@ -419,10 +486,29 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     __shared__ float s_part[kWaves][kTerms][kBatch + 1];  // +1: the 9 writers hit 9 banks
     __shared__ uint32_t s_max[kWaves];
 
-    const int tile = __builtin_amdgcn_readfirstlane(order ? (int)order[blockIdx.x]
-                                                          : (int)blockIdx.x);
+    // Work item.  kSplit (a schedule is given): items 2i and 2i + 1 (i < K) are
+    // the back and front parts of the schedule's i-th tile, and the later
+    // items its tiles from K on, whole; order[T] holds K (at most kSplitMax).
+    const int T = tiles_x * ((H + kTileSize - 1) / kTileSize);
+    int part = kPartWhole, tile;
+    if constexpr (kSplit) {
+        const int K = (int)min((uint32_t)kSplitMax,
+                               (uint32_t)__builtin_amdgcn_readfirstlane((int)order[T]));
+        const int item = (int)blockIdx.x;
+        if (item < 2 * K) {
+            part = (item & 1) ? kPartFront : kPartBack;
+            tile = (int)order[item >> 1];
+        } else {
+            const int idx = item - K;
+            if (idx >= T) return;
+            tile = (int)order[idx];
+        }
+    } else {
+        tile = order ? (int)order[blockIdx.x] : (int)blockIdx.x;
+    }
+    tile = __builtin_amdgcn_readfirstlane(tile);
     // a launch order is a permutation of the tiles; nothing else is touched
-    if ((unsigned)tile >= (unsigned)(tiles_x * ((H + kTileSize - 1) / kTileSize))) return;
+    if ((unsigned)tile >= (unsigned)T) return;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: uniform branches
     const uint32_t my_bit = 1u << wave;
@@ -449,18 +535,31 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     const int maxc = __builtin_amdgcn_readfirstlane(min((int)tile_last, end - start));
     start = __builtin_amdgcn_readfirstlane(start);
     const int my_value = reduce9_value_of_lane(lane);
+    // the entries [lo0, hi0) this item walks with gradients; the front part
+    // first walks [mid, maxc) for the pixel state only
+    int lo0 = 0, hi0 = maxc;
+    if constexpr (kSplit) {
+        const int mid = (int)(((int64_t)maxc * kSplitNum) / kSplitDen);
+        if (part == kPartBack) lo0 = mid;
+        if (part == kPartFront) {
+            hi0 = mid;
+            state_walk<kPix, kBatch>(mid, maxc, n, tile, tiles_x, start, wave_last, my_bit, fx,
+                                     fy, p, ids, recs, s_a, s_b, s_c);
+        }
+    }
 
     // each batch's ids are loaded while the batch after it is walked
-    int next_id = (tid < min(maxc, kBatch)) ? ids[start + max(0, maxc - kBatch) + tid] : -1;
-    for (int hi = maxc; hi > 0; hi -= kBatch) {
-        const int lo = max(0, hi - kBatch);
+    int next_id =
+        (tid < min(hi0 - lo0, kBatch)) ? ids[start + max(lo0, hi0 - kBatch) + tid] : -1;
+    for (int hi = hi0; hi > lo0; hi -= kBatch) {
+        const int lo = max(lo0, hi - kBatch);
         const int cnt = hi - lo;
         const int g = next_id;
         __syncthreads();
         if (tid < cnt)
             stage_entry<kPix>(recs, g, n, tile, tiles_x, s_a, s_b, s_c, nullptr, s_id, tid);
-        if (lo > 0) {
-            const int nlo = max(0, lo - kBatch);
+        if (lo > lo0) {
+            const int nlo = max(lo0, lo - kBatch);
             if (tid < lo - nlo) next_id = ids[start + nlo + tid];
         }
         __syncthreads();
@@ -796,14 +895,22 @@ __device__ __forceinline__ uint32_t work_bucket(uint32_t w) {
 }
 
 constexpr int kOrderThreads = 1024;
+constexpr uint32_t kSplitBuckets = 5;
+constexpr uint32_t kSplitMinWork = 256;
+// A tile alone on a CU runs at roughly a quarter of the CU's rate.
+constexpr uint64_t kSplitLoad = 4;
 
-// order[i] = tiles by descending work bucket (one work-group).  work == null:
+// order[i] = tiles by descending work bucket (one work-group); with split_max
+// >= 0 also order[T], the backward's split count (below).  work == null:
 // the forward's estimate, the tile's list length.
 __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
     int T, uint64_t m, const int2* __restrict__ ranges, const uint32_t* __restrict__ work,
-    uint32_t* __restrict__ order) {
+    uint32_t* __restrict__ order, int split_max, int cus) {
     __shared__ uint32_t s_cnt[256];
     __shared__ uint32_t s_scan[4];
+    __shared__ uint32_t s_top;
+    __shared__ unsigned long long s_sum;
+    __shared__ uint32_t s_wmax;
     const int tid = threadIdx.x;
     auto bucket_of = [&](int t) -> uint32_t {
         uint32_t w;
@@ -817,8 +924,30 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
         return 255u - work_bucket(w);  // descending work
     };
     if (tid < 256) s_cnt[tid] = 0;
+    if (tid == 0) {
+        s_sum = 0ull;
+        s_wmax = 0u;
+    }
     __syncthreads();
-    for (int t = tid; t < T; t += kOrderThreads) atomicAdd(&s_cnt[bucket_of(t)], 1u);
+    uint64_t wsum = 0;
+    uint32_t wmax = 0;
+    for (int t = tid; t < T; t += kOrderThreads) {
+        atomicAdd(&s_cnt[bucket_of(t)], 1u);
+        if (split_max > 0) {
+            const uint32_t w = work[t];
+            wsum += w;
+            wmax = max(wmax, w);
+        }
+    }
+    if (split_max > 0) {
+        // one atomic per wave
+        const uint64_t ws = wave_sum_u64(wsum);
+        const uint32_t wm = wave_max_u32(wmax);
+        if ((tid & 63) == 0) {
+            atomicAdd(&s_sum, (unsigned long long)ws);
+            atomicMax(&s_wmax, wm);
+        }
+    }
     __syncthreads();
     uint32_t c = 0, inc = 0;
     if (tid < 256) {
@@ -836,6 +965,28 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
     for (int t = tid; t < T; t += kOrderThreads) {
         const uint32_t pos = atomicAdd(&s_cnt[bucket_of(t)], 1u);
         if (pos < (uint32_t)T) order[pos] = (uint32_t)t;
+    }
+    if (split_max == 0 && tid == 0) order[T] = 0u;
+    if (split_max > 0) {
+        // order[T] = how many of the first tiles the backward splits: those
+        // within kSplitBuckets sub-buckets (a factor 2^(5/8) ~ 1.5) of the
+        // longest, if it has kSplitMinWork entries or more and a long tail
+        // (below).  s_cnt[b] now holds the end of bucket b, so the first
+        // non-zero one is the top.
+        if (tid == 0) s_top = 256u;
+        __syncthreads();
+        if (tid < 256 && s_cnt[tid] > 0u) atomicMin(&s_top, (uint32_t)tid);
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t top = s_top;
+            uint32_t k = 0;
+            // only when the longest tile outlasts the balanced share of the
+            // work: kSplitLoad x its work x the CUs against the total
+            const bool tail = (uint64_t)s_wmax * (uint64_t)max(cus, 1) * kSplitLoad >= s_sum;
+            if (tail && top < 256u && 255u - top >= work_bucket(kSplitMinWork))
+                k = min(s_cnt[min(top + kSplitBuckets, 255u)], (uint32_t)split_max);
+            order[T] = k;
+        }
     }
 }
 
@@ -862,6 +1013,12 @@ int bwd_pix() {
     static const int p = pix_setting("GSR_BLEND_BWD_PIX", 2);
     return p;
 }
+// Splitting the backward's longest tiles in two (on unless GSR_BWD_SPLIT=0;
+// read on every call, so a test can compare both).
+bool bwd_split() {
+    const char* v = std::getenv("GSR_BWD_SPLIT");
+    return !(v && v[0] == '0');
+}
 
 // Work-groups of `kernel` (with `threads` threads, no dynamic LDS) that fit on
 // the current device at once: per-CU occupancy times the CU count, cached.
@@ -883,6 +1040,29 @@ unsigned resident_groups(const void* kernel, int threads) {
     return g;
 }
 
+// Compute units of the current device, cached per device.
+int cu_count() {
+    static std::mutex mu;
+    static std::map<int, int> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = cache.find(dev);
+    if (it != cache.end()) return it->second;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        return 1;
+    cache.emplace(dev, std::max(1, cus));
+    return std::max(1, cus);
+}
+
+// Whether the backward's whole grid of tiles is resident on the device at once.
+bool bwd_grid_fits(unsigned tiles) {
+    return tiles <= resident_groups(
+                        reinterpret_cast<const void*>(&blend_bwd_kernel<2, 64, false>),
+                        Layout<2>::kThreads);
+}
+
 }  // namespace
 
 bool launch_order_enabled() { return tile_order_enabled(); }
@@ -899,7 +1079,7 @@ hipError_t launch_fwd_schedule(int n, int H, int W, const int32_t* ranges, const
                        dim3(kEstTilesPerBlock * kWave), 0, st, (int)tiles, tiles_x, n, m, r, ids,
                        static_cast<const BlendRec*>(recs), work);
     hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles, m, r,
-                       work, order);
+                       work, order, -1, 1);
     return hipGetLastError();
 }
 
@@ -934,7 +1114,9 @@ hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num
                        dim3(kWorkTilesPerBlock * kWave), 0, st, (int)tiles, H, W, tiles_x,
                        num_pairs, r, ncontrib, work, vec4);
     hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles,
-                       num_pairs, r, work, order);
+                       num_pairs, r, work, order,
+                       (bwd_split() && bwd_pix() == 2 && bwd_grid_fits(tiles)) ? kSplitMax : 0,
+                       cu_count());
     return hipGetLastError();
 }
 
@@ -950,24 +1132,32 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const GradSt
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
     const auto* rc = static_cast<const BlendRec*>(recs);
+    // With a schedule and the whole grid resident at once, the longest tiles
+    // set the kernel's length: up to kSplitMax of them run as two items each.
+    // When the grid does not fit, the total work does, and the split's extra
+    // state-only walk costs more than it saves.
+    const bool fits = bwd_grid_fits(tiles);
+    const bool split = order && bwd_split() && fits && bwd_pix() == 2;
     // The 64-entry batch halves the work-group's LDS (8 KB), so registers, not
     // LDS, bound the resident waves; it pays when the grid does not fit on the
     // device at once.  When it would, the 128-entry batch leaves part of the
     // grid to be placed as CUs free up, which balances the long tiles better.
-    if (bwd_pix() == 2 && tiles > resident_groups(reinterpret_cast<const void*>(
-                                      &blend_bwd_kernel<2, 64>),
-                                  Layout<2>::kThreads))
-        hipLaunchKernelGGL((blend_bwd_kernel<2, 64>), dim3(tiles), dim3(Layout<2>::kThreads), 0,
-                           st, n, H, W, tiles_x, num_pairs, grad, gst, r, ids, rc, finalT, ncontrib,
-                           dmean, dcov, dcol, dalpha, gs, order);
+    if (bwd_pix() == 2 && !fits)
+        hipLaunchKernelGGL((blend_bwd_kernel<2, 64, false>), dim3(tiles),
+                           dim3(Layout<2>::kThreads), 0, st, n, H, W, tiles_x, num_pairs, grad, gst,
+                           r, ids, rc, finalT, ncontrib, dmean, dcov, dcol, dalpha, gs, order);
+    else if (split)
+        hipLaunchKernelGGL((blend_bwd_kernel<2, 128, true>), dim3(tiles + kSplitMax),
+                           dim3(Layout<2>::kThreads), 0, st, n, H, W, tiles_x, num_pairs, grad, gst,
+                           r, ids, rc, finalT, ncontrib, dmean, dcov, dcol, dalpha, gs, order);
     else if (bwd_pix() == 2)
-        hipLaunchKernelGGL((blend_bwd_kernel<2, 128>), dim3(tiles), dim3(Layout<2>::kThreads), 0,
-                           st, n, H, W, tiles_x, num_pairs, grad, gst, r, ids, rc, finalT, ncontrib,
-                           dmean, dcov, dcol, dalpha, gs, order);
+        hipLaunchKernelGGL((blend_bwd_kernel<2, 128, false>), dim3(tiles),
+                           dim3(Layout<2>::kThreads), 0, st, n, H, W, tiles_x, num_pairs, grad, gst,
+                           r, ids, rc, finalT, ncontrib, dmean, dcov, dcol, dalpha, gs, order);
     else
-        hipLaunchKernelGGL((blend_bwd_kernel<1, 256>), dim3(tiles), dim3(Layout<1>::kThreads), 0,
-                           st, n, H, W, tiles_x, num_pairs, grad, gst, r, ids, rc, finalT, ncontrib,
-                           dmean, dcov, dcol, dalpha, gs, order);
+        hipLaunchKernelGGL((blend_bwd_kernel<1, 256, false>), dim3(tiles),
+                           dim3(Layout<1>::kThreads), 0, st, n, H, W, tiles_x, num_pairs, grad, gst,
+                           r, ids, rc, finalT, ncontrib, dmean, dcov, dcol, dalpha, gs, order);
     return hipGetLastError();
 }
 

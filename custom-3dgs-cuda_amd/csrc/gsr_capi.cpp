@@ -194,7 +194,7 @@ BwdLayout backward_layout(int n, int64_t m, int height, int width) {
                          : 0;
     L.recs = take(kRecBytes * un);
     L.work = take(4 * T);
-    L.order = take(4 * T);
+    L.order = take(4 * (T + 1));  // the tile order, then the backward's split count
     L.counts = take(4 * un);
     L.rects = take(8 * un);
     L.goff = take(4 * un);

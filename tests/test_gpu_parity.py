@@ -312,6 +312,24 @@ def test_rasterize_backward_parity(crc, device, name, kw):
     _backward_case(crc, device, a)
 
 
+def test_rasterize_backward_split_tiles(crc, device, monkeypatch):
+    """The backward runs its longest tiles as two work items: a back part from
+    the final transmittance, and a front part that walks the back part's
+    entries with the pixel state only before its own.  On c4's clustered
+    cloud (long lists; the largest tiles split) the gradients are within the
+    oracle bar and bit for bit the unsplit backward's (GSR_BWD_SPLIT=0)."""
+    a = scene_arrays(synthetic.config_scene("c4", requires_grad=False, n=50_000, width=480,
+                                            height=272))
+    fw, want, G, split = _backward_case(crc, device, a)
+    t, n = fw["tensors"], a["mu"].shape[0]
+    monkeypatch.setenv("GSR_BWD_SPLIT", "0")
+    whole = crc.backwards_rasterization(
+        _dev(G, device), t["mean2d"], t["cov2d"], t["colors"], t["alpha"], t["ids"], t["ranges"],
+        t["final_T"], t["n_contrib"], n, a["H"], a["W"])
+    for x, y, nm in zip(split, whole, ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")):
+        assert_bitwise(_np(x), _np(y), f"split vs whole: {nm}")
+
+
 def test_rasterize_backward_strided_gradient_views(crc, device):
     """backwards_rasterization_strided reads dL/dimage views in place: a
     broadcast (image.sum()'s gradient, strides 0), a transposed image and a
