@@ -256,13 +256,34 @@ def frame_stages(sc, steps: int, binning: str | None = None) -> dict:
             "stages": rates}
 
 
+def band_pair_counts(sc, band_height: int) -> list[int]:
+    """Each screen band's pair count, the bands rendered as rasterize_bands does
+    (the frame's projection, means moved up by the band's first row)."""
+    import torch
+    import custom_rasterizer_cuda as crc
+    from gaussian_splatting.rasterizer.bands import band_rows
+
+    g, v = sc.gaussians, sc.view
+    out = []
+    with torch.no_grad():
+        n = g.mu.shape[0]
+        m2, c2, d = crc.project(n, g.mu.detach(), g.q.detach(), g.s.detach(), v["R"], v["T"],
+                                float(v["fx"]), float(v["fy"]), float(v["cx"]), float(v["cy"]))
+        col = crc.SH(n, (-(v["R"].T @ v["T"])).contiguous(), g.mu.detach(), g.A.detach(),
+                     g.k_j.detach())
+        op = torch.sigmoid(g.alpha.detach())
+        for y0, h in band_rows(int(v["height"]), band_height):
+            mb = m2 - m2.new_tensor([0.0, float(y0)])
+            out.append(int(crc.rasterize(n, d, mb, c2, col, op, h, int(v["width"]))[1].numel()))
+    return out
+
+
 def banded_frame(sc, band_height: int, steps: int) -> dict:
     """fwd+bwd of a frame beyond the int32 pair lists, rendered as screen bands
     of ``band_height`` rows through the unchanged surface (rasterize_bands):
     frame time, the stage breakdown and each band's pair count."""
     import torch
-    from gaussian_splatting.rasterizer.bands import band_views, rasterize_bands
-    from gaussian_splatting.synthetic import Scene
+    from gaussian_splatting.rasterizer.bands import rasterize_bands
 
     render = lambda g, v: rasterize_bands(g, v, band_height)
     print(f"[bench] {sc.name}: {steps} banded frame(s), bands of {band_height} rows",
@@ -270,8 +291,7 @@ def banded_frame(sc, band_height: int, steps: int) -> dict:
     fwd, bwd, total, stages = time_frames(sc, steps, 1, profile=True, render=render)
     print(f"[bench] {sc.name}: {total:.1f} ms per frame; counting pairs per band",
           file=sys.stderr, flush=True)
-    pairs = [pair_count(Scene(sc.gaussians, v, f"{sc.name}_band{y0}"))
-             for y0, v in band_views(sc.view, band_height)]
+    pairs = band_pair_counts(sc, band_height)
     torch.cuda.empty_cache()
     v = sc.view
     M = sum(pairs)

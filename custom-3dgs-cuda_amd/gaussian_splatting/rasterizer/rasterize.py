@@ -79,7 +79,6 @@ def _forward(ctx, logits, mu, q, s, alpha_in, albedo, k_j, cam_rotation, cam_tra
         cam_rotation, cam_translation, cam_position,
     )
     ctx.logits = logits
-    ctx.band = RasterizeFunction.band_accumulate
     ctx.num_gaussians = num_gaussians
     ctx.height = img_h
     ctx.width = img_w
@@ -106,12 +105,7 @@ def _backward(ctx, grad_output):
         sorted_ids, tile_ranges, final_T, n_contrib,
         ctx.num_gaussians, ctx.height, ctx.width,
     )
-    prev = RasterizeFunction.last_mean2d_grad
-    if ctx.band and prev is not None and prev.shape == mean_2d_grad.shape:
-        # a band of a banded frame: the frame's dL/d mean2d is the bands' sum
-        RasterizeFunction.last_mean2d_grad = prev + mean_2d_grad.detach()
-    else:
-        RasterizeFunction.last_mean2d_grad = mean_2d_grad.detach()
+    RasterizeFunction.last_mean2d_grad = mean_2d_grad.detach()
 
     # backwards_SH, backwards_projection and mu_grad + mu_sh_grad
     # (rasterize.py:100-117) in one kernel; with logits also the sigmoid's
@@ -137,9 +131,6 @@ class RasterizeFunction(t.autograd.Function):
 
     last_mean2d_grad: t.Tensor | None = None
     last_radii2d: t.Tensor | None = None
-    # set while rasterize_bands (bands.py) renders: the backward then adds each
-    # band's dL/d mean2d into last_mean2d_grad
-    band_accumulate: bool = False
 
     @staticmethod
     def forward(ctx, mu, q, s, alpha, albedo, k_j, cam_rotation, cam_translation, fx, fy, cx, cy,

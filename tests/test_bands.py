@@ -1,5 +1,5 @@
 """Screen bands (gaussian_splatting/rasterizer/bands.py) without a GPU: the band
-cameras, and the banded oracle frame against the whole oracle frame."""
+rows and cameras, and the banded oracle frame against the whole oracle frame."""
 
 from __future__ import annotations
 
@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from gaussian_splatting import synthetic
-from gaussian_splatting.rasterizer.bands import band_views
+from gaussian_splatting.rasterizer.bands import band_rows, band_views
 from helpers import oracle_forward, scene_arrays
 
 
@@ -29,24 +29,35 @@ def test_band_height_must_be_whole_tiles(h):
         band_views(view, h)
 
 
-def test_banded_oracle_frame_matches_the_whole_frame(orc):
-    """Config c1 rendered by the oracle in 64-row bands (cy - y0, height 64)
-    and stacked equals the whole frame: n_contrib identical and the image
-    within 1e-5.  A sign slip in the moved principal point, a wrong band
-    height or a wrong stacking order fails it."""
-    sc = synthetic.config_scene("c1", requires_grad=False)
+def test_band_rows_cover_the_frame():
+    assert band_rows(100, 32) == [(0, 32), (32, 32), (64, 32), (96, 4)]
+    assert band_rows(64, 64) == [(0, 64)]
+    assert band_rows(0, 16) == []
+
+
+@pytest.mark.parametrize("name,bh,kw", [("c1", 64, dict()),
+                                        ("c3", 48, dict(n=20_000, width=480, height=270))])
+def test_banded_oracle_frame_matches_the_whole_frame(orc, name, bh, kw):
+    """The oracle frame rendered in bands the way rasterize_bands renders them
+    (the frame's projection, means moved up by y0, each band through
+    rasterize) and stacked equals the whole frame bit for bit: image, final T
+    and n_contrib, and each band's pairs are the frame's pairs of its tile
+    rows.  A sign slip in the shift, a wrong band height or a wrong stacking
+    order fails it."""
+    sc = synthetic.config_scene(name, requires_grad=False, **kw)
     a = scene_arrays(sc)
     whole = oracle_forward(a)
-    imgs, ncs, fts = [], [], []
-    for y0, v in band_views(sc.view, 64):
-        b = dict(a, cy=float(v["cy"]), H=int(v["height"]))
-        out = oracle_forward(b)
-        imgs.append(out["img"])
-        ncs.append(out["n_contrib"])
-        fts.append(out["final_T"])
-    img, nc, ft = np.concatenate(imgs), np.concatenate(ncs), np.concatenate(fts)
-    assert img.shape == whole["img"].shape
-    assert np.array_equal(nc, whole["n_contrib"])
-    assert np.abs(img - whole["img"]).max() <= 1e-5
-    assert np.abs(ft - whole["final_T"]).max() <= 1e-5
+    imgs, ncs, fts, pairs = [], [], [], 0
+    for y0, h in band_rows(a["H"], bh):
+        mb = (whole["mean2d"] - np.array([0.0, y0], np.float32)).astype(np.float32)
+        img, ids, ranges, fT, nc, _ = orc.rasterize(whole["depth"], mb, whole["cov2d"],
+                                                    whole["colors"], a["alpha"], h, a["W"])
+        imgs.append(img)
+        ncs.append(nc)
+        fts.append(fT)
+        pairs += ids.size
+    assert np.array_equal(np.concatenate(imgs), whole["img"])
+    assert np.array_equal(np.concatenate(fts), whole["final_T"])
+    assert np.array_equal(np.concatenate(ncs), whole["n_contrib"])
+    assert pairs == whole["ids"].size
     assert whole["n_contrib"].max() > 0

@@ -1,8 +1,9 @@
 """GPU: frames rendered in screen bands (gaussian_splatting/rasterizer/bands.py).
 
-Each band is a frame of its own through the unchanged surface, so each is held
-to the forward parity bar against the oracle on the band's camera.  The glue
-stacks the bands and sums their gradients.  Config c5 at its full size (5M
+Each band is rasterized through the unchanged surface from the frame's
+projection with the means moved up by the band's first row, so each band is
+held to the forward parity bar against the oracle on the same inputs, and the
+stacked frame to a whole-frame render.  Config c5 at its full size (5M
 Gaussians at 3840x2160, ~1.1e10 pairs) is beyond the int32 pair lists of the
 reference's surface (rasterize.cu:382-390): the whole frame is refused with an
 error, and the banded frame is checked by size-independent properties.
@@ -16,9 +17,10 @@ import torch
 
 from gaussian_splatting import synthetic
 from gaussian_splatting.rasterizer import RasterizeFunction, rasterize, rasterize_bands
-from gaussian_splatting.rasterizer.bands import band_views
+from gaussian_splatting.rasterizer.bands import band_rows
 from helpers import assert_bitwise, oracle_forward, scene_arrays
-from test_gpu_parity import _check_forward, _np, gpu_forward
+from oracle import oracle as orc
+from test_gpu_parity import _np, gpu_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -27,50 +29,52 @@ NAMES = ("mu", "q", "s", "alpha", "A", "k_j")
 
 def test_each_band_matches_the_oracle(crc, device):
     """c5's distributions at 30k Gaussians, 400x224, in 64-row bands (the last
-    one 32 rows): every band bit-exact against the oracle on its camera."""
+    one 32 rows): each band's keys, ids, ranges, n_contrib, image and final T
+    bit-exact against the oracle rasterizing the same moved means."""
     sc = synthetic.config_scene("c5", requires_grad=False, n=30_000, width=400, height=224)
     a = scene_arrays(sc)
-    for y0, v in band_views(sc.view, 64):
-        print(f"[gpu] band at row {y0}, {v['height']} rows", flush=True)
-        b = dict(a, cy=float(v["cy"]), H=int(v["height"]))
-        _check_forward(gpu_forward(crc, b, device), oracle_forward(b))
+    fw, want = gpu_forward(crc, a, device), oracle_forward(a)
+    t, n = fw["tensors"], a["mu"].shape[0]
+    depth = torch.from_numpy(fw["depth"]).to(device)
+    for y0, h in band_rows(a["H"], 64):
+        print(f"[gpu] band at row {y0}, {h} rows", flush=True)
+        mb = t["mean2d"] - t["mean2d"].new_tensor([0.0, float(y0)])
+        img, ids, rng, fT, nc, keys = crc.rasterize_with_keys(n, depth, mb, t["cov2d"], t["colors"],
+                                                              t["alpha"], h, a["W"])
+        mb_np = (want["mean2d"] - np.array([0.0, y0], np.float32)).astype(np.float32)
+        wi, wids, wr, wfT, wnc, wkeys = orc.rasterize(want["depth"], mb_np, want["cov2d"],
+                                                      want["colors"], a["alpha"], h, a["W"])
+        assert_bitwise(_np(keys).view(np.uint64), wkeys, "sorted keys")
+        assert_bitwise(_np(ids), wids, "sorted_ids")
+        assert_bitwise(_np(rng), wr, "tile_ranges")
+        assert_bitwise(_np(nc), wnc, "n_contrib")
+        assert_bitwise(_np(img), wi, "img")
+        assert_bitwise(_np(fT), wfT, "final_T")
 
 
-def test_banded_glue_stacks_bands_and_sums_their_gradients(device):
-    """rasterize_bands: the image is the bands' images stacked (bit for bit
-    rasterize on each band's view); the parameter gradients are the sums of
-    the bands' gradients (fp32 sums in another order: 1e-6 relative), and
-    last_mean2d_grad is the sum of the bands' dL/d mean2d."""
+def test_banded_glue_equals_the_whole_frame(device):
+    """rasterize_bands against rasterize on a frame that fits: the image bit
+    for bit, the parameter gradients and last_mean2d_grad within 1e-6
+    relative (the same terms, summed per band first), the radii identical."""
     sc = synthetic.config_scene("c3", device=device, n=20_000, width=480, height=272)
     g, view = sc.gaussians, sc.view
     w = torch.linspace(0.5, 1.5, 480 * 272 * 3, device=device).view(272, 480, 3)
 
-    def clear():
+    def run(render):
         for nm in NAMES:
             getattr(g, nm).grad = None
+        img = render()
+        (img * w).sum().backward()
+        return (img.detach().clone(), [getattr(g, nm).grad.clone() for nm in NAMES],
+                RasterizeFunction.last_mean2d_grad.clone(), RasterizeFunction.last_radii2d.clone())
 
-    clear()
-    img = rasterize_bands(g, view, 96)
-    (img * w).sum().backward()
-    banded = [getattr(g, nm).grad.clone() for nm in NAMES]
-    banded_m2 = RasterizeFunction.last_mean2d_grad.clone()
-
-    sums = [torch.zeros_like(x) for x in banded]
-    m2_sum = None
-    for y0, v in band_views(view, 96):
-        clear()
-        part = rasterize(g, v)
-        assert_bitwise(_np(img[y0:y0 + v["height"]]), _np(part), f"band at row {y0}")
-        (part * w[y0:y0 + v["height"]]).sum().backward()
-        for acc, nm in zip(sums, NAMES):
-            acc += getattr(g, nm).grad
-        m = RasterizeFunction.last_mean2d_grad
-        m2_sum = m.clone() if m2_sum is None else m2_sum + m
-    for got, want, nm in zip(banded, sums, NAMES):
+    bi, bg, bm, br = run(lambda: rasterize_bands(g, view, 96))
+    wi, wg, wm, wr = run(lambda: rasterize(g, view))
+    assert_bitwise(_np(bi), _np(wi), "image")
+    assert_bitwise(_np(br), _np(wr), "radii")
+    for got, want, nm in zip(bg + [bm], wg + [wm], NAMES + ("last_mean2d_grad",)):
         err = (got - want).norm() / want.norm().clamp_min(1e-30)
         assert err <= 1e-6, f"d {nm}: {err:.2e}"
-    err = (banded_m2 - m2_sum).norm() / m2_sum.norm()
-    assert err <= 1e-6, f"last_mean2d_grad: {err:.2e}"
 
 
 def test_c5_full_size_in_screen_bands(crc, device):
@@ -86,12 +90,13 @@ def test_c5_full_size_in_screen_bands(crc, device):
     pairs = []
     with torch.no_grad():
         n = g.mu.shape[0]
-        for _, v in band_views(view, 256):
-            m2, c2, d = crc.project(n, g.mu, g.q, g.s, v["R"], v["T"], v["fx"], v["fy"],
-                                    v["cx"], v["cy"])
-            col = crc.SH(n, (-(v["R"].T @ v["T"])).contiguous(), g.mu, g.A, g.k_j)
-            out = crc.rasterize(n, d, m2, c2, col, torch.sigmoid(g.alpha), v["height"],
-                                v["width"])
+        m2, c2, d = crc.project(n, g.mu, g.q, g.s, view["R"], view["T"], view["fx"], view["fy"],
+                                view["cx"], view["cy"])
+        col = crc.SH(n, (-(view["R"].T @ view["T"])).contiguous(), g.mu, g.A, g.k_j)
+        op = torch.sigmoid(g.alpha)
+        for y0, h in band_rows(view["height"], 256):
+            mb = m2 - m2.new_tensor([0.0, float(y0)])
+            out = crc.rasterize(n, d, mb, c2, col, op, h, view["width"])
             pairs.append(out[1].numel())
             del out
     print(f"[gpu] c5 pairs per band: {pairs}", flush=True)
