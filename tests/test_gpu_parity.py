@@ -317,7 +317,8 @@ def test_rasterize_backward_split_tiles(crc, device, monkeypatch):
     the final transmittance, and a front part that walks the back part's
     entries with the pixel state only before its own.  On c4's clustered
     cloud (long lists; the largest tiles split) the gradients are within the
-    oracle bar and bit for bit the unsplit backward's (GSR_BWD_SPLIT=0)."""
+    oracle bar and bit for bit the unsplit backward's (GSR_BWD_SPLIT=0), also
+    with ids the forward did not produce in the lists."""
     a = scene_arrays(synthetic.config_scene("c4", requires_grad=False, n=50_000, width=480,
                                             height=272))
     fw, want, G, split = _backward_case(crc, device, a)
@@ -328,6 +329,19 @@ def test_rasterize_backward_split_tiles(crc, device, monkeypatch):
         t["final_T"], t["n_contrib"], n, a["H"], a["W"])
     for x, y, nm in zip(split, whole, ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")):
         assert_bitwise(_np(x), _np(y), f"split vs whole: {nm}")
+    # ids the forward did not produce (skipped entries) on both paths
+    ids = _np(t["ids"]).copy()
+    pos = np.random.default_rng(1).choice(ids.size, 64, replace=False)
+    ids[pos[:32]] = -1
+    ids[pos[32:]] = n + 7
+    bad = _dev(ids, device, torch.int32)
+    args = (_dev(G, device), t["mean2d"], t["cov2d"], t["colors"], t["alpha"], bad, t["ranges"],
+            t["final_T"], t["n_contrib"], n, a["H"], a["W"])
+    whole = crc.backwards_rasterization(*args)
+    monkeypatch.setenv("GSR_BWD_SPLIT", "1")
+    split = crc.backwards_rasterization(*args)
+    for x, y, nm in zip(split, whole, ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")):
+        assert_bitwise(_np(x), _np(y), f"split vs whole, corrupt ids: {nm}")
 
 
 def test_rasterize_backward_strided_gradient_views(crc, device):
