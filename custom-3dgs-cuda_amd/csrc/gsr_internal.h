@@ -142,6 +142,7 @@ struct TileBinning {
     const uint32_t* seg_start = nullptr;    // nb + 1
     uint32_t* bcount = nullptr;             // nb * block_count_stride(n)
     uint32_t* lists = nullptr;              // block lists (m)
+    uint16_t* lrects = nullptr;             // each list entry's rectangle in its block (m)
     uint32_t* seg_owner = nullptr;          // segment_bound(m)
     uint32_t* tcount = nullptr;             // 64 * segment_bound(m)
     uint32_t* ttotal = nullptr;             // tiles

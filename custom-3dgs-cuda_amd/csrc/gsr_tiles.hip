@@ -65,17 +65,27 @@ struct RankLane {
     int bx0, by0;
     uint32_t bw, bh;
     bool has;
+    Rect t;  // the tile rectangle
 };
+
+// A tile rectangle clipped to the 8x8-tile block at tile (ox, oy), which it
+// meets, in 12 bits: x0 and y0 in [0, 8) and the extents less one.
+__device__ __forceinline__ uint16_t local_rect(const Rect& t, int ox, int oy) {
+    const int lx0 = max(t.x0 - ox, 0), lx1 = min(t.x1 - ox, 8);
+    const int ly0 = max(t.y0 - oy, 0), ly1 = min(t.y1 - oy, 8);
+    return (uint16_t)(lx0 | ((lx1 - lx0 - 1) << 3) | (ly0 << 6) | ((ly1 - ly0 - 1) << 9));
+}
 
 __device__ __forceinline__ RankLane rank_lane(int n, const uint32_t* __restrict__ perm,
                                               const uint2* __restrict__ rects, int64_t r) {
-    RankLane L{0u, 0, 0, 0u, 0u, false};
+    RankLane L{0u, 0, 0, 0u, 0u, false, Rect{0, 0, 0, 0}};
     if (r < n) {
         const uint32_t g = perm[r];
         if (g < (uint32_t)n) {
             const Rect t = unpack_rect(rects[g]);
             if (t.x1 > t.x0 && t.y1 > t.y0) {
                 L.g = g;
+                L.t = t;
                 L.bx0 = t.x0 >> 3;
                 L.by0 = t.y0 >> 3;
                 L.bw = (uint32_t)(((t.x1 + 7) >> 3) - L.bx0);
@@ -208,7 +218,7 @@ __global__ __launch_bounds__(kThreads) void block_scan_kernel(
 __global__ __launch_bounds__(kThreads) void block_scatter_kernel(
     int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects, BlockGrid bg,
     int chunks, int windows, int cstride, const uint32_t* __restrict__ pos,
-    uint32_t* __restrict__ lists, uint64_t cap) {
+    uint32_t* __restrict__ lists, uint16_t* __restrict__ lrects, uint64_t cap) {
     __shared__ uint64_t s_row[kWavesPer][kWave];
     __shared__ uint64_t s_col[kWavesPer][kWave];
     __shared__ uint32_t s_base[kWavesPer][kWave];
@@ -232,7 +242,10 @@ __global__ __launch_bounds__(kThreads) void block_scatter_kernel(
             if (s < W.s0 || s >= W.s1) continue;
             const uint64_t m = rm & s_col[wave][window_col(W, bg, sx)];
             const uint64_t p = (uint64_t)s_base[wave][s - W.s0] + (uint64_t)popc64(m & below);
-            if (p < cap) lists[p] = L.g;
+            if (p < cap) {
+                lists[p] = L.g;
+                lrects[p] = local_rect(L.t, sx * 8, sy * 8);
+            }
         }
     }
 }
@@ -248,24 +261,25 @@ struct SegLane {
     uint32_t lw, lh;
 };
 
+// The entry's id (with_id) and its local rectangle, written beside it by the
+// level-1 scatter, so level 2 reads both in list order.
+template <bool with_id>
 __device__ __forceinline__ SegLane seg_lane(const uint32_t* __restrict__ lists,
-                                            const uint2* __restrict__ rects, uint32_t first,
-                                            uint32_t end, int ox, int oy, uint64_t cap, int n) {
+                                            const uint16_t* __restrict__ lrects, uint32_t first,
+                                            uint32_t end, uint64_t cap, int n) {
     SegLane S{0u, 0, 0, 0u, 0u};
     const uint32_t e = first + (uint32_t)lane_id();
     if (e < end && e < cap) {
-        const uint32_t g = lists[e];
-        if (g >= (uint32_t)n) return S;
-        const Rect t = unpack_rect(rects[g]);
-        const int lx0 = min(max(t.x0 - ox, 0), 8), lx1 = min(max(t.x1 - ox, 0), 8);
-        const int ly0 = min(max(t.y0 - oy, 0), 8), ly1 = min(max(t.y1 - oy, 0), 8);
-        S.g = g;
-        if (lx1 > lx0 && ly1 > ly0) {
-            S.lx0 = lx0;
-            S.ly0 = ly0;
-            S.lw = (uint32_t)(lx1 - lx0);
-            S.lh = (uint32_t)(ly1 - ly0);
+        if constexpr (with_id) {
+            const uint32_t g = lists[e];
+            if (g >= (uint32_t)n) return S;
+            S.g = g;
         }
+        const uint32_t lr = lrects[e];
+        S.lx0 = (int)(lr & 7u);
+        S.lw = ((lr >> 3) & 7u) + 1u;
+        S.ly0 = (int)((lr >> 6) & 7u);
+        S.lh = ((lr >> 9) & 7u) + 1u;
     }
     return S;
 }
@@ -303,7 +317,7 @@ __device__ __forceinline__ SegInfo seg_info(uint32_t k, const uint32_t* __restri
 __global__ __launch_bounds__(kThreads) void tile_count_kernel(
     int n, BlockGrid bg, const uint32_t* __restrict__ seg_owner,
     const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ block_start,
-    const uint32_t* __restrict__ lists, uint64_t cap, const uint2* __restrict__ rects,
+    const uint32_t* __restrict__ lists, uint64_t cap, const uint16_t* __restrict__ lrects,
     uint32_t seg_cap, uint32_t* __restrict__ tcount) {
     const uint32_t nseg = min(uniform(seg_start[bg.nb]), seg_cap);
     const uint32_t stride = gridDim.x * kWavesPer;
@@ -311,7 +325,7 @@ __global__ __launch_bounds__(kThreads) void tile_count_kernel(
     for (uint32_t k = uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6)); k < nseg;
          k += stride) {
         const SegInfo I = seg_info(k, seg_owner, seg_start, block_start, bg.bw, bg.nb);
-        const SegLane S = seg_lane(lists, rects, I.first, I.end, I.ox, I.oy, cap, n);
+        const SegLane S = seg_lane<false>(lists, lrects, I.first, I.end, cap, n);
         uint64_t rowv = 0, colv = 0;
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -378,7 +392,7 @@ __global__ __launch_bounds__(kStartsThreads) void tile_starts_kernel(
 __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
     int n, BlockGrid bg, const uint32_t* __restrict__ seg_owner,
     const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ block_start,
-    const uint32_t* __restrict__ lists, uint64_t cap, const uint2* __restrict__ rects,
+    const uint32_t* __restrict__ lists, uint64_t cap, const uint16_t* __restrict__ lrects,
     uint32_t seg_cap, const uint32_t* __restrict__ tcount, const int2* __restrict__ ranges,
     uint64_t m, uint32_t* __restrict__ ids) {
     const uint32_t nseg = min(uniform(seg_start[bg.nb]), seg_cap);
@@ -388,7 +402,7 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
     for (uint32_t k = uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6)); k < nseg;
          k += stride) {
         const SegInfo I = seg_info(k, seg_owner, seg_start, block_start, bg.bw, bg.nb);
-        const SegLane S = seg_lane(lists, rects, I.first, I.end, I.ox, I.oy, cap, n);
+        const SegLane S = seg_lane<true>(lists, lrects, I.first, I.end, cap, n);
         // lane t: where segment k's entries of tile t begin
         const int tx = I.ox + (lane & 7), ty = I.oy + (lane >> 3);
         uint32_t base = 0;
@@ -481,10 +495,10 @@ hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(block_scatter_kernel, dim3(groups_for(l1_waves)), dim3(kThreads), 0, st,
                        tb.n, tb.perm, tb.rects, bg, chunks, windows, cstride, tb.bcount, tb.lists,
-                       tb.m);
+                       tb.lrects, tb.m);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(tile_count_kernel, dim3(seg_groups(segs)), dim3(kThreads), 0, st, tb.n, bg,
-                       tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.rects,
+                       tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.lrects,
                        seg_cap, tb.tcount);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(tile_scan_kernel, dim3(bg.nb), dim3(kThreads), 0, st, bg, tb.seg_start,
@@ -495,7 +509,7 @@ hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
                        reinterpret_cast<int2*>(tb.ranges), tb.err);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(tile_scatter_kernel, dim3(seg_groups(segs)), dim3(kThreads), 0, st, tb.n,
-                       bg, tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.rects,
+                       bg, tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.lrects,
                        seg_cap, tb.tcount, reinterpret_cast<const int2*>(tb.ranges), tb.m,
                        tb.ids);
     return hipGetLastError();
