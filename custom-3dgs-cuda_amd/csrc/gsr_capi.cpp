@@ -136,7 +136,7 @@ BinLayout bin_layout(int n, int H, int W) {
 // size serves both; the schedule's work and order arrays follow.
 struct SortLayout {
     size_t ctl, part_rank, ctl_end, tk0, tk1, vbuf;
-    size_t bcount, lists, lrects, seg_owner, tcount, ttotal;
+    size_t bcount, lists, lrects, drects, seg_owner, tcount, ttotal;
     size_t work, order, end;
 };
 
@@ -163,6 +163,7 @@ SortLayout sort_layout(int64_t m, int passes, int64_t T, int n, int H, int W) {
     L.bcount = take(4 * (size_t)bg.nb * gsr::block_count_stride(n));
     L.lists = take(4 * um);
     L.lrects = take(2 * um);
+    L.drects = take(8 * (size_t)(n > 0 ? n : 0));
     L.seg_owner = take(4 * (size_t)segs);
     L.tcount = take(4 * 64 * (size_t)segs);
     L.ttotal = take(4 * (size_t)(T > 0 ? T : 0));
@@ -561,6 +562,9 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                 tb.bcount = at<uint32_t>(sort_ws, SL.bcount);
                 tb.lists = at<uint32_t>(sort_ws, SL.lists);
                 tb.lrects = at<uint16_t>(sort_ws, SL.lrects);
+                // gathering the rectangles into depth order pays once the
+                // level-1 passes' lookups by id are bandwidth-bound
+                if (n >= (1 << 19)) tb.drects = at<uint2>(sort_ws, SL.drects);
                 tb.seg_owner = at<uint32_t>(sort_ws, SL.seg_owner);
                 tb.tcount = at<uint32_t>(sort_ws, SL.tcount);
                 tb.ttotal = at<uint32_t>(sort_ws, SL.ttotal);

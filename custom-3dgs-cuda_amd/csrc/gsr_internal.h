@@ -137,6 +137,7 @@ struct TileBinning {
     BlockGrid grid;
     const uint32_t* perm = nullptr;         // depth order (n)
     const uint2* rects = nullptr;           // packed tile rectangles (n)
+    uint2* drects = nullptr;                // optional: rects in depth order (n), gathered once
     const uint32_t* block_hist = nullptr;   // Gaussians per block (nb)
     const uint32_t* block_start = nullptr;  // nb + 1
     const uint32_t* seg_start = nullptr;    // nb + 1

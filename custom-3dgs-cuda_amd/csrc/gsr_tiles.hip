@@ -76,13 +76,16 @@ __device__ __forceinline__ uint16_t local_rect(const Rect& t, int ox, int oy) {
     return (uint16_t)(lx0 | ((lx1 - lx0 - 1) << 3) | (ly0 << 6) | ((ly1 - ly0 - 1) << 9));
 }
 
+// drects: the rectangles already in depth order (rank_rects_kernel), read in
+// rank order instead of by Gaussian id.
 __device__ __forceinline__ RankLane rank_lane(int n, const uint32_t* __restrict__ perm,
-                                              const uint2* __restrict__ rects, int64_t r) {
+                                              const uint2* __restrict__ rects,
+                                              const uint2* __restrict__ drects, int64_t r) {
     RankLane L{0u, 0, 0, 0u, 0u, false, Rect{0, 0, 0, 0}};
     if (r < n) {
         const uint32_t g = perm[r];
         if (g < (uint32_t)n) {
-            const Rect t = unpack_rect(rects[g]);
+            const Rect t = unpack_rect(drects ? drects[r] : rects[g]);
             if (t.x1 > t.x0 && t.y1 > t.y0) {
                 L.g = g;
                 L.t = t;
@@ -163,12 +166,13 @@ __device__ __forceinline__ int window_col(const WindowMasks& W, const BlockGrid&
 // counts[b * cstride + c] = how many of chunk c's 64 ranks meet block b, for
 // every block (zeros included); lane l counts block 64 w + l.
 __global__ __launch_bounds__(kThreads) void block_count_kernel(
-    int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects, BlockGrid bg,
+    int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects,
+    const uint2* __restrict__ drects, BlockGrid bg,
     int chunks, int windows, int cstride, uint32_t* __restrict__ counts) {
     const int lane = lane_id();
     const ChunkWindow cw = chunk_window(windows);
     if (cw.chunk >= chunks) return;
-    const RankLane L = rank_lane(n, perm, rects, (int64_t)cw.chunk * kWave + lane);
+    const RankLane L = rank_lane(n, perm, rects, drects, (int64_t)cw.chunk * kWave + lane);
     const WindowMasks W = window_masks(L, bg, cw.window);
     const int s = W.s0 + lane;
     const int sy = (W.sx_a + lane) / bg.bw;  // rows below sy_a
@@ -216,7 +220,8 @@ __global__ __launch_bounds__(kThreads) void block_scan_kernel(
 // meeting the block.  Each lane walks its own blocks in the window.  Positions
 // at or beyond cap are dropped.
 __global__ __launch_bounds__(kThreads) void block_scatter_kernel(
-    int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects, BlockGrid bg,
+    int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects,
+    const uint2* __restrict__ drects, BlockGrid bg,
     int chunks, int windows, int cstride, const uint32_t* __restrict__ pos,
     uint32_t* __restrict__ lists, uint16_t* __restrict__ lrects, uint64_t cap) {
     __shared__ uint64_t s_row[kWavesPer][kWave];
@@ -225,7 +230,7 @@ __global__ __launch_bounds__(kThreads) void block_scatter_kernel(
     const int lane = lane_id(), wave = threadIdx.x >> 6;
     const ChunkWindow cw = chunk_window(windows);
     if (cw.chunk >= chunks) return;
-    const RankLane L = rank_lane(n, perm, rects, (int64_t)cw.chunk * kWave + lane);
+    const RankLane L = rank_lane(n, perm, rects, drects, (int64_t)cw.chunk * kWave + lane);
     const WindowMasks W = window_masks(L, bg, cw.window);
     const int b = W.s0 + lane;
     s_row[wave][lane] = W.rowv;
@@ -248,6 +253,18 @@ __global__ __launch_bounds__(kThreads) void block_scatter_kernel(
             }
         }
     }
+}
+
+// drects[r] = rects[perm[r]]: the depth order's rectangles, gathered once so
+// that both level-1 passes read them in rank order.
+__global__ __launch_bounds__(kThreads) void rank_rects_kernel(int n,
+                                                              const uint32_t* __restrict__ perm,
+                                                              const uint2* __restrict__ rects,
+                                                              uint2* __restrict__ drects) {
+    const int r = blockIdx.x * kThreads + threadIdx.x;
+    if (r >= n) return;
+    const uint32_t g = perm[r];
+    drects[r] = (g < (uint32_t)n) ? rects[g] : make_uint2(0u, 0u);
 }
 
 // ---- level 2: block lists -> tile lists ------------------------------------
@@ -486,16 +503,22 @@ hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
     const uint32_t seg_cap = (uint32_t)segs;
     hipError_t e;
     const uint64_t l1_waves = (uint64_t)chunks * (uint64_t)windows;
+    if (tb.drects) {
+        hipLaunchKernelGGL(rank_rects_kernel, dim3(groups_for(((uint64_t)tb.n + kWave - 1) / kWave)),
+                           dim3(kThreads), 0, st, tb.n, tb.perm, tb.rects, tb.drects);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
+    }
     hipLaunchKernelGGL(block_count_kernel, dim3(groups_for(l1_waves)), dim3(kThreads), 0, st,
-                       tb.n, tb.perm, tb.rects, bg, chunks, windows, cstride, tb.bcount);
+                       tb.n, tb.perm, tb.rects, tb.drects, bg, chunks, windows, cstride,
+                       tb.bcount);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(block_scan_kernel, dim3(bg.nb), dim3(kThreads), 0, st, chunks, cstride,
                        tb.bcount, tb.block_hist, tb.block_start, tb.seg_start, tb.seg_owner,
                        seg_cap, tb.err);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(block_scatter_kernel, dim3(groups_for(l1_waves)), dim3(kThreads), 0, st,
-                       tb.n, tb.perm, tb.rects, bg, chunks, windows, cstride, tb.bcount, tb.lists,
-                       tb.lrects, tb.m);
+                       tb.n, tb.perm, tb.rects, tb.drects, bg, chunks, windows, cstride, tb.bcount,
+                       tb.lists, tb.lrects, tb.m);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(tile_count_kernel, dim3(seg_groups(segs)), dim3(kThreads), 0, st, tb.n, bg,
                        tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.lrects,
