@@ -699,21 +699,25 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
 // One 16-lane row per Gaussian (four per wave): the nine sums of its flagged
 // slots, the conic part converted to the covariance gradient, added to the
 // outputs (which hold zeros and any fallback atomics from the blend).
-constexpr int kReduceRowLanes = 16;
-constexpr int kReduceGaussiansPerBlock = 256 / kReduceRowLanes;
-
-// Sum over the 16 lanes of each row, result in every lane of the row.
-__device__ __forceinline__ float row_sum16(float x) {
-    x += dpp_move<kDppRowRor8>(x);
+// Sum over the kLanes (16 or 8) lanes of each row, result in every lane of
+// the row.
+template <int kLanes>
+__device__ __forceinline__ float row_sum(float x) {
+    if constexpr (kLanes == 16) x += dpp_move<kDppRowRor8>(x);
     x += lane_xor4(x);
     x += dpp_move<kDppQuadXor2>(x);
     x += dpp_move<kDppQuadXor1>(x);
     return x;
 }
 
+// kLanes per Gaussian: 16, or 8 when Gaussians have few slots (a row then
+// covers 64 slots per flag load; half the waves wait on the dependent loads).
+template <int kReduceRowLanes>
 __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
     int n, const BlendRec* __restrict__ recs, GradSlots gs, float* __restrict__ dmean,
     float* __restrict__ dcov, float* __restrict__ dcol, float* __restrict__ dalpha) {
+    static_assert(kReduceRowLanes == 16 || kReduceRowLanes == 8, "rows of 16 or 8 lanes");
+    constexpr int kReduceGaussiansPerBlock = 256 / kReduceRowLanes;
     const int sub = threadIdx.x & (kReduceRowLanes - 1);
     const int g = blockIdx.x * kReduceGaussiansPerBlock + (int)(threadIdx.x / kReduceRowLanes);
     float v[kTerms] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
@@ -757,7 +761,7 @@ __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
     // every lane takes part in the row sums (rows past n add zeros)
     float t[kTerms];
 #pragma unroll
-    for (int k = 0; k < kTerms; ++k) t[k] = row_sum16(v[k]);
+    for (int k = 0; k < kTerms; ++k) t[k] = row_sum<kReduceRowLanes>(v[k]);
     if (g < n && sub == 0) {
         const BlendRec r = recs[g];
         float dc[3];
@@ -1164,10 +1168,14 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const GradSt
 hipError_t launch_pair_grad_reduce(int n, const void* recs, const GradSlots& gs, float* dmean,
                                    float* dcov, float* dcol, float* dalpha, hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(pair_grad_reduce_kernel,
-                       dim3((unsigned)((n + kReduceGaussiansPerBlock - 1) / kReduceGaussiansPerBlock)),
-                       dim3(256), 0, st, n, static_cast<const BlendRec*>(recs), gs, dmean, dcov,
-                       dcol, dalpha);
+    const auto* rc = static_cast<const BlendRec*>(recs);
+    // 8-lane rows when a Gaussian averages at most 64 slots (one flag load per lane)
+    if (gs.slots <= 64ull * (uint64_t)n)
+        hipLaunchKernelGGL(pair_grad_reduce_kernel<8>, dim3((unsigned)((n + 31) / 32)), dim3(256),
+                           0, st, n, rc, gs, dmean, dcov, dcol, dalpha);
+    else
+        hipLaunchKernelGGL(pair_grad_reduce_kernel<16>, dim3((unsigned)((n + 15) / 16)), dim3(256),
+                           0, st, n, rc, gs, dmean, dcov, dcol, dalpha);
     return hipGetLastError();
 }
 
