@@ -296,11 +296,13 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
     const BlockGrid bg = block_grid((W + 15) / 16, (H + 15) / 16);
     if (block_hist && (bg.nb > kMaxBlocks || !pair_total || !block_start || !seg_start || !done))
         return hipErrorInvalidValue;
-    // few work-groups: the histogram flush costs one global atomic per bin and
-    // work-group.  One per two CUs up to 2^19 Gaussians; beyond, two per CU, so
-    // that each thread's grid-strided loop stays short (its loads are not
-    // overlapped across iterations)
-    const unsigned blocks = std::min(blocks_for(n), n >= (1 << 19) ? 512u : 128u);
+    // few work-groups: each flushes its histograms with one global atomic per
+    // bin and counts itself in behind a device-wide release.  One per two CUs
+    // up to 2^19 Gaussians; beyond, one per CU, so that each thread's
+    // grid-strided loop stays short (its loads are not overlapped across
+    // iterations).  At 1M Gaussians: 128 groups 170 us, 256 150 us, 512 157 us,
+    // 1024 199 us (bin_count + depth sort).
+    const unsigned blocks = std::min(blocks_for(n), n >= (1 << 19) ? 256u : 128u);
     hipLaunchKernelGGL(bin_count_kernel, dim3(blocks), dim3(kThreads), 0, st, n, mean2d, cov2d,
                        depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist,
                        depth_hist, bg, block_hist, pair_total, block_start, seg_start, done,
