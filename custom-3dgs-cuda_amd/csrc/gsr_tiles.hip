@@ -357,16 +357,18 @@ __global__ __launch_bounds__(kThreads) void tile_count_kernel(
 
 // Per block: each tile's segment counts replaced by their exclusive prefix
 // over the block's segments, and the tile's total to ttotal (tiles on the
-// screen only).  Four waves split the segments into consecutive runs.
-__global__ __launch_bounds__(kThreads) void tile_scan_kernel(
+// screen only).  kScanWaves waves split the segments into consecutive runs
+// (one work-group per block: a block's run is the serial part).
+constexpr int kScanWaves = 16;
+__global__ __launch_bounds__(kScanWaves * kWave) void tile_scan_kernel(
     BlockGrid bg, const uint32_t* __restrict__ seg_start, uint32_t seg_cap,
     uint32_t* __restrict__ tcount, uint32_t* __restrict__ ttotal) {
-    __shared__ uint32_t s_sum[kWavesPer][kWave];
+    __shared__ uint32_t s_sum[kScanWaves][kWave];
     const int b = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t k0 = min(seg_start[b], seg_cap);
     const uint32_t R = min(seg_start[b + 1], seg_cap) - k0;
-    const uint32_t per = (R + kWavesPer - 1) / kWavesPer;
+    const uint32_t per = (R + kScanWaves - 1) / kScanWaves;
     const uint32_t r0 = k0 + min(R, (uint32_t)wave * per);
     const uint32_t r1 = k0 + min(R, (uint32_t)(wave + 1) * per);
     uint32_t sum = 0;
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void tile_scan_kernel(
     __syncthreads();
     uint32_t run = 0, total = 0;
 #pragma unroll
-    for (int w = 0; w < kWavesPer; ++w) {
+    for (int w = 0; w < kScanWaves; ++w) {
         run += (w < wave) ? s_sum[w][lane] : 0u;
         total += s_sum[w][lane];
     }
@@ -524,8 +526,8 @@ hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
                        tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.lrects,
                        seg_cap, tb.tcount);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(tile_scan_kernel, dim3(bg.nb), dim3(kThreads), 0, st, bg, tb.seg_start,
-                       seg_cap, tb.tcount, tb.ttotal);
+    hipLaunchKernelGGL(tile_scan_kernel, dim3(bg.nb), dim3(kScanWaves * kWave), 0, st, bg,
+                       tb.seg_start, seg_cap, tb.tcount, tb.ttotal);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(tile_starts_kernel, dim3(1), dim3(kStartsThreads), 0, st,
                        bg.tiles_x * bg.tiles_y, tb.ttotal, tb.m,
