@@ -312,6 +312,18 @@ def test_rasterize_backward_parity(crc, device, name, kw):
     _backward_case(crc, device, a)
 
 
+def test_rasterize_backward_parity_large_splats(crc, device):
+    """Gaussians covering hundreds of tiles each (c3's cloud with log-scales
+    raised by 3): more than 256 gradient slots per Gaussian, so each row of
+    the gradient reduce walks several flag groups; against the oracle as every
+    backward case."""
+    a = scene_arrays(synthetic.config_scene("c3", requires_grad=False, n=2000, width=640,
+                                            height=368))
+    a["s"] = (a["s"] + 3.0).astype(np.float32)
+    fw, want, G, _ = _backward_case(crc, device, a)
+    assert fw["ids"].size > 256 * a["mu"].shape[0]
+
+
 def test_rasterize_backward_split_tiles(crc, device, monkeypatch):
     """The backward runs its longest tiles as two work items: a back part from
     the final transmittance, and a front part that walks the back part's
