@@ -77,6 +77,33 @@ def test_banded_glue_equals_the_whole_frame(device):
         assert err <= 1e-6, f"d {nm}: {err:.2e}"
 
 
+def test_bands_without_gaussians(device):
+    """Every Gaussian above row 130 of a 272-row frame: of the 64-row bands,
+    the last two hold no pair at all (empty lists through rasterize and its
+    backward).  The stacked image is the whole frame's bit for bit, those
+    bands are zero, and the gradients match rasterize's within 1e-6."""
+    sc = synthetic.config_scene("c3", device=device, n=2000, width=480, height=272)
+    g, view = sc.gaussians, sc.view
+    with torch.no_grad():
+        g.mu[:, 1] = -0.5 - 0.5 * g.mu[:, 1].abs()  # y in [-1, -0.5]: projected near the top
+    w = torch.linspace(0.5, 1.5, 480 * 272 * 3, device=device).view(272, 480, 3)
+
+    def run(render):
+        for nm in NAMES:
+            getattr(g, nm).grad = None
+        img = render()
+        (img * w).sum().backward()
+        return img.detach().clone(), [getattr(g, nm).grad.clone() for nm in NAMES]
+
+    bi, bg = run(lambda: rasterize_bands(g, view, 64))
+    wi, wg = run(lambda: rasterize(g, view))
+    assert_bitwise(_np(bi), _np(wi), "image")
+    assert float(bi[192:].abs().max()) == 0.0 and float(bi[:64].abs().max()) > 0.0
+    for got, want, nm in zip(bg, wg, NAMES):
+        err = (got - want).norm() / want.norm().clamp_min(1e-30)
+        assert err <= 1e-6, f"d {nm}: {err:.2e}"
+
+
 def test_c5_full_size_in_screen_bands(crc, device):
     """Config c5 at full size.  The whole frame needs more pairs than int32
     lists hold and is refused; in 256-row bands every band fits, the pairs add
