@@ -4,9 +4,11 @@
 
 libgsraster.so: every csrc/*.hip plus csrc/gsr_capi.cpp, compiled by hipcc with
 --offload-arch=gfx950, -ffp-contract=off (the fp32 forward keeps the reference's
-operation order; see csrc/gsr_common.h), hardware float atomics and packed-fp32
-instructions disabled.  custom_rasterizer_cuda*.so: csrc/bindings.cpp compiled
-against torch's headers and linked to libgsraster.so (rpath $ORIGIN).
+operation order; see csrc/gsr_common.h), packed-fp32 instructions disabled, and
+-munsafe-fp-atomics: the backward's few float atomics (list entries without a
+gradient slot of their own) use the hardware's float add.
+custom_rasterizer_cuda*.so: csrc/bindings.cpp compiled against torch's headers and
+linked to libgsraster.so (rpath $ORIGIN).
 """
 
 from __future__ import annotations

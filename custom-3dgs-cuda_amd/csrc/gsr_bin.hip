@@ -93,7 +93,7 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     int passes, uint32_t* __restrict__ tile_hist, uint32_t* __restrict__ depth_hist,
     BlockGrid bg, uint32_t* __restrict__ block_hist, uint64_t* __restrict__ pair_total,
     uint32_t* __restrict__ block_start, uint32_t* __restrict__ seg_start,
-    uint32_t* __restrict__ done, uint64_t* __restrict__ host_total) {
+    uint32_t* __restrict__ done, uint64_t* __restrict__ host_total, int* __restrict__ status) {
     __shared__ int s_d0[kRadixBins + 1];
     __shared__ uint32_t s_h[3][kRadixBins];
     __shared__ uint32_t s_dh[4][kRadixBins];
@@ -172,6 +172,11 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
             if (tid == 0 && host_total) {
                 const uint64_t total = __hip_atomic_load(pair_total, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT);
+                // the device status word goes to the host with the count, and
+                // is cleared: each error is reported once
+                const int stat = status ? atomicExch(status, 0) : 0;
+                __hip_atomic_store(host_total + 1, (uint64_t)(uint32_t)stat, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_SYSTEM);
                 __hip_atomic_store(host_total, total, __ATOMIC_RELAXED,
                                    __HIP_MEMORY_SCOPE_SYSTEM);
                 __threadfence_system();
@@ -290,7 +295,7 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
                             uint32_t* block_start, uint32_t* seg_start, uint32_t* done,
-                            uint64_t* host_total, hipStream_t st) {
+                            uint64_t* host_total, int* status, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     if (tile_passes < 0 || tile_passes > 4) return hipErrorInvalidValue;
     const BlockGrid bg = block_grid((W + 15) / 16, (H + 15) / 16);
@@ -306,7 +311,7 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
     hipLaunchKernelGGL(bin_count_kernel, dim3(blocks), dim3(kThreads), 0, st, n, mean2d, cov2d,
                        depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist,
                        depth_hist, bg, block_hist, pair_total, block_start, seg_start, done,
-                       block_hist ? host_total : nullptr);
+                       block_hist ? host_total : nullptr, status);
     return hipGetLastError();
 }
 

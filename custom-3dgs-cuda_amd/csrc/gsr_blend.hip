@@ -27,13 +27,17 @@
 // and each wave skips entries beyond its own max n_contrib; each entry's nine
 // gradient sums are formed in the lane, summed across the wave (one
 // transposed permlane/DPP reduction) and across the waves through LDS, then
-// added to HBM with one set of 9 float atomics per (tile, entry).
+// stored with plain stores into the (Gaussian, tile) pair's own gradient slot
+// (nine floats and a claim flag).  pair_grad_reduce_kernel adds each
+// Gaussian's claimed slots.  Float atomics are used only for list entries
+// that have no slot of their own: pairs outside the Gaussian's tile
+// rectangle, and a repeated id within one tile's list (caller-supplied lists).
 //
 // Work-groups take their tile from a launch order, longest estimated work
 // first (tile_order_kernel), so long tiles do not start last.
+#include <algorithm>
 #include <cstdlib>
 
-#include <map>
 #include <mutex>
 
 #include "gsr_internal.h"
@@ -351,11 +355,17 @@ __device__ __forceinline__ BwdTerms bwd_update(BwdPixel& p, const BwdDecision& d
     BwdTerms t;
     const float ae = d.act ? d.alpha : 0.0f;
     // T / (1 - alpha) with 1 - alpha in [0.01, 1]: the reference's 1e-4 floor
-    // never applies.  The hardware reciprocal (1 ulp) and a multiply: T drifts
-    // by ~1.5 ulp per entry where a division drifts by 0.5, about 1e-6
-    // relative over a few hundred entries, and every term scales with T.
+    // never applies.  The hardware reciprocal (1 ulp) times T, then one
+    // correction from the exact residual T - q (1 - alpha) (a fused
+    // multiply-add): the quotient is within ~0.5 ulp, as a division's.  Without
+    // the correction T drifts by ~1.5 ulp per entry, and over the two thousand
+    // entries of a long list the drift reaches 1e-5 of the terms that a
+    // Gaussian's gradient sums (every term scales with T).  A skipped entry
+    // (alpha 0) leaves T unchanged: the reciprocal of 1 is exact.
     const float den = 1.0f - ae;
-    const float Tb = p.T * __builtin_amdgcn_rcpf(den);
+    const float rd = __builtin_amdgcn_rcpf(den);
+    const float q0 = p.T * rd;
+    const float Tb = __builtin_fmaf(__builtin_fmaf(-q0, den, p.T), rd, q0);
     const float cg = B.z * p.g0 + B.w * p.g1 + cb * p.g2;
     const float diff = cg - p.accg;
     const float dal = diff * Tb;
@@ -670,13 +680,23 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                 const int ry0 = (int)(rc.y & 0xffffu), ry1 = (int)(rc.y >> 16);
                 const uint64_t slot = (uint64_t)gs.goff[g] +
                                       (uint64_t)((ty - ry0) * (rx1 - rx0) + (tx - rx0));
-                if (tx >= rx0 && tx < rx1 && ty >= ry0 && ty < ry1 && slot < gs.slots) {
+                bool own = tx >= rx0 && tx < rx1 && ty >= ry0 && ty < ry1 && slot < gs.slots;
+                if (own) {
+                    // claim the slot: its flag byte, through the 32-bit word
+                    // holding it (the flag array is padded to 8-byte groups).
+                    // Only an id repeated within this tile's list finds it
+                    // claimed already.
+                    const uint32_t bit = 1u << (8u * (uint32_t)(slot & 3u));
+                    own = (atomicOr(reinterpret_cast<uint32_t*>(gs.flags + (slot & ~3ull)), bit) &
+                           bit) == 0u;
+                }
+                if (own) {
                     float* d = gs.sums + 9 * slot;
 #pragma unroll
                     for (int k = 0; k < kTerms; ++k) d[k] = t[k];
-                    gs.flags[slot] = 1;
                 } else {
-                    // not a pair of the rectangles: straight to the outputs
+                    // no slot of its own (outside the rectangles, or a repeated
+                    // id): straight to the outputs
                     const float cx = -2.0f * s_a[tid].z, cy = -2.0f * s_c[tid].y,
                                 cz = -2.0f * s_b[tid].x;
                     float dc[3];
@@ -994,29 +1014,6 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
     }
 }
 
-bool tile_order_enabled() {
-    static const bool on = [] {
-        const char* v = std::getenv("GSR_TILE_ORDER");
-        return !(v && v[0] == '0');
-    }();
-    return on;
-}
-
-// Pixels per lane for each kernel: the measured defaults, overridable for
-// tuning with GSR_BLEND_FWD_PIX / GSR_BLEND_BWD_PIX = 1 or 2.
-int pix_setting(const char* env, int dflt) {
-    const char* v = std::getenv(env);
-    if (v && (v[0] == '1' || v[0] == '2') && v[1] == '\0') return v[0] - '0';
-    return dflt;
-}
-int fwd_pix() {
-    static const int p = pix_setting("GSR_BLEND_FWD_PIX", 1);
-    return p;
-}
-int bwd_pix() {
-    static const int p = pix_setting("GSR_BLEND_BWD_PIX", 2);
-    return p;
-}
 // Splitting the backward's longest tiles in two (on unless GSR_BWD_SPLIT=0;
 // read on every call, so a test can compare both).
 bool bwd_split() {
@@ -1024,52 +1021,42 @@ bool bwd_split() {
     return !(v && v[0] == '0');
 }
 
-// Work-groups of `kernel` (with `threads` threads, no dynamic LDS) that fit on
-// the current device at once: per-CU occupancy times the CU count, cached.
-unsigned resident_groups(const void* kernel, int threads) {
+// Per-device launch facts, looked up once per device and kept in a fixed
+// table (no allocation after the first call): the compute units, and how many
+// work-groups of the 64-entry-batch backward kernel fit on the device at once.
+constexpr int kMaxDevices = 64;
+struct DeviceFacts {
+    int cus = 0;
+    unsigned bwd_resident = 0;
+};
+DeviceFacts device_facts() {
     static std::mutex mu;
-    static std::map<std::pair<int, const void*>, unsigned> cache;
+    static DeviceFacts table[kMaxDevices];
     int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+        return DeviceFacts{1, 1};
     std::lock_guard<std::mutex> lock(mu);
-    const auto key = std::make_pair(dev, kernel);
-    auto it = cache.find(key);
-    if (it != cache.end()) return it->second;
-    int per_cu = 0, cus = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, threads, 0) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return 1;
-    const unsigned g = (unsigned)std::max(1, per_cu * cus);
-    cache.emplace(key, g);
-    return g;
+    DeviceFacts& f = table[dev];
+    if (f.cus == 0) {
+        int per_cu = 0, cus = 0;
+        if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) !=
+                hipSuccess ||
+            hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                &per_cu, reinterpret_cast<const void*>(&blend_bwd_kernel<2, 64, false>),
+                Layout<2>::kThreads, 0) != hipSuccess)
+            return DeviceFacts{1, 1};
+        f.cus = std::max(1, cus);
+        f.bwd_resident = (unsigned)std::max(1, per_cu * f.cus);
+    }
+    return f;
 }
 
-// Compute units of the current device, cached per device.
-int cu_count() {
-    static std::mutex mu;
-    static std::map<int, int> cache;
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess) return 1;
-    std::lock_guard<std::mutex> lock(mu);
-    auto it = cache.find(dev);
-    if (it != cache.end()) return it->second;
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-        return 1;
-    cache.emplace(dev, std::max(1, cus));
-    return std::max(1, cus);
-}
+int cu_count() { return device_facts().cus; }
 
 // Whether the backward's whole grid of tiles is resident on the device at once.
-bool bwd_grid_fits(unsigned tiles) {
-    return tiles <= resident_groups(
-                        reinterpret_cast<const void*>(&blend_bwd_kernel<2, 64, false>),
-                        Layout<2>::kThreads);
-}
+bool bwd_grid_fits(unsigned tiles) { return tiles <= device_facts().bwd_resident; }
 
 }  // namespace
-
-bool launch_order_enabled() { return tile_order_enabled(); }
 
 hipError_t launch_fwd_schedule(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
                                uint64_t m, const void* recs, uint32_t* work, uint32_t* order,
@@ -1096,12 +1083,8 @@ hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const in
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
     const auto* rc = static_cast<const BlendRec*>(recs);
-    if (fwd_pix() == 2)
-        hipLaunchKernelGGL(blend_fwd_kernel<2>, dim3(tiles), dim3(Layout<2>::kThreads), 0, st, n,
-                           H, W, tiles_x, m, r, ids, rc, img, finalT, ncontrib, order);
-    else
-        hipLaunchKernelGGL(blend_fwd_kernel<1>, dim3(tiles), dim3(Layout<1>::kThreads), 0, st, n,
-                           H, W, tiles_x, m, r, ids, rc, img, finalT, ncontrib, order);
+    hipLaunchKernelGGL(blend_fwd_kernel<1>, dim3(tiles), dim3(Layout<1>::kThreads), 0, st, n, H,
+                       W, tiles_x, m, r, ids, rc, img, finalT, ncontrib, order);
     return hipGetLastError();
 }
 
@@ -1119,7 +1102,7 @@ hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num
                        num_pairs, r, ncontrib, work, vec4);
     hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles,
                        num_pairs, r, work, order,
-                       (bwd_split() && bwd_pix() == 2 && bwd_grid_fits(tiles)) ? kSplitMax : 0,
+                       (bwd_split() && bwd_grid_fits(tiles)) ? kSplitMax : 0,
                        cu_count());
     return hipGetLastError();
 }
@@ -1141,12 +1124,12 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const GradSt
     // When the grid does not fit, the total work does, and the split's extra
     // state-only walk costs more than it saves.
     const bool fits = bwd_grid_fits(tiles);
-    const bool split = order && bwd_split() && fits && bwd_pix() == 2;
+    const bool split = order && bwd_split() && fits;
     // The 64-entry batch halves the work-group's LDS (8 KB), so registers, not
     // LDS, bound the resident waves; it pays when the grid does not fit on the
     // device at once.  When it would, the 128-entry batch leaves part of the
     // grid to be placed as CUs free up, which balances the long tiles better.
-    if (bwd_pix() == 2 && !fits)
+    if (!fits)
         hipLaunchKernelGGL((blend_bwd_kernel<2, 64, false>), dim3(tiles),
                            dim3(Layout<2>::kThreads), 0, st, n, H, W, tiles_x, num_pairs, grad, gst,
                            r, ids, rc, finalT, ncontrib, dmean, dcov, dcol, dalpha, gs, order);
@@ -1154,13 +1137,9 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const GradSt
         hipLaunchKernelGGL((blend_bwd_kernel<2, 128, true>), dim3(tiles + kSplitMax),
                            dim3(Layout<2>::kThreads), 0, st, n, H, W, tiles_x, num_pairs, grad, gst,
                            r, ids, rc, finalT, ncontrib, dmean, dcov, dcol, dalpha, gs, order);
-    else if (bwd_pix() == 2)
+    else
         hipLaunchKernelGGL((blend_bwd_kernel<2, 128, false>), dim3(tiles),
                            dim3(Layout<2>::kThreads), 0, st, n, H, W, tiles_x, num_pairs, grad, gst,
-                           r, ids, rc, finalT, ncontrib, dmean, dcov, dcol, dalpha, gs, order);
-    else
-        hipLaunchKernelGGL((blend_bwd_kernel<1, 256, false>), dim3(tiles),
-                           dim3(Layout<1>::kThreads), 0, st, n, H, W, tiles_x, num_pairs, grad, gst,
                            r, ids, rc, finalT, ncontrib, dmean, dcov, dcol, dalpha, gs, order);
     return hipGetLastError();
 }

@@ -67,7 +67,7 @@ int tile_passes(int64_t T) {
 constexpr int kMaxTilePasses = 4;
 
 // Bits of a Gaussian id in the packed tile-sort word, or 0 for the two-word
-// form (tile and id do not fit in 32 bits together, or GSR_PACKED_SORT=0).
+// form (tile and id do not fit in 32 bits together).
 int packed_id_bits(int n, int64_t T);
 
 // Significant bits of tile ids in [0, T).
@@ -77,12 +77,23 @@ int tile_key_bits(int64_t T) {
     return bits;
 }
 
-// Misc block at the head of the bin workspace.
+// Misc block at the head of the bin workspace.  In the host's pinned copy,
+// `status` receives the device status word.
 struct Misc {
     uint64_t total;       // pair count
-    int err;              // set by a kernel that hit its spin bound or found bad counts
+    int status;           // host copy only: the device status word
     uint32_t bin_done;    // bin_count's finished work-groups (left at zero)
 };
+
+// The message for a non-zero device status word.
+std::string status_message(int bits) {
+    std::string m = "a kernel on this device";
+    if (bits & gsr::kStatusSpin) m += " reached its look-back spin bound";
+    if ((bits & gsr::kStatusSpin) && (bits & gsr::kStatusCounts)) m += " and one";
+    if (bits & gsr::kStatusCounts) m += " found counts inconsistent with the binning";
+    return m + " (status " + std::to_string(bits) +
+           "; reported by the first forward or status call after it); its outputs are invalid";
+}
 
 // Which tile binning a frame uses: the two-level block binning, unless the
 // grid has more 8x8-tile blocks than its histogram holds or GSR_TILE_BINNING
@@ -263,12 +274,11 @@ hipEvent_t count_event() {
     return e;
 }
 
+// The quaternion gradient's mode, read on every call: 1 (GSR_REFERENCE_QUAT_GRAD
+// set to 1) is the reference's literal formula, 0 the derivative of the forward.
 int ref_quat_mode() {
-    static const int mode = [] {
-        const char* v = std::getenv("GSR_REFERENCE_QUAT_GRAD");
-        return (v && v[0] == '1') ? 1 : 0;
-    }();
-    return mode;
+    const char* v = std::getenv("GSR_REFERENCE_QUAT_GRAD");
+    return (v && v[0] == '1' && v[1] == '\0') ? 1 : 0;
 }
 
 // ---- optional per-stage timing (gsr_profile_*): a pair of HIP events on the
@@ -322,11 +332,6 @@ class StageTimer {
 };
 
 int packed_id_bits(int n, int64_t T) {
-    static const bool off = [] {
-        const char* v = std::getenv("GSR_PACKED_SORT");
-        return v && v[0] == '0';
-    }();
-    if (off) return 0;
     int gb = 0;
     for (uint32_t v = (uint32_t)(n > 1 ? n - 1 : 1); v; v >>= 1) ++gb;
     return gb + tile_key_bits(T) <= 32 ? gb : 0;
@@ -427,15 +432,20 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
     GSR_HIP(gsr::zero_fill(bin_ws, L.ctl_end, st), "rasterize: clear");
     if (n == 0 || height == 0 || width == 0) return GSR_OK;
     GSR_REQUIRE(depth && mean2d && cov2d, "null pointer");
+    gsr::DeviceGlobals dg;
+    GSR_HIP(gsr::device_globals(&dg), "rasterize: device globals");
     Misc* misc = at<Misc>(bin_ws, L.misc);
-    int* err = &misc->err;
+    int* err = dg.status;
     uint32_t* counts = at<uint32_t>(bin_ws, L.counts);
     uint32_t* dk0 = at<uint32_t>(bin_ws, L.dk0);
     uint32_t* dv0 = at<uint32_t>(bin_ws, L.dv0);
     const bool blocks = block_binning(height, width);
     const HostCount hc = blocks ? host_count() : HostCount{};
     if (blocks && !hc.host) return fail(GSR_ERR_HIP, "rasterize: host-mapped count allocation failed");
-    if (blocks) *hc.host = kNoCount;
+    if (blocks) {
+        hc.host[0] = kNoCount;
+        hc.host[1] = 0;
+    }
     {
         StageTimer timer("bin_count", st);
         const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
@@ -448,7 +458,7 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
                                       blocks ? &misc->total : nullptr,
                                       at<uint32_t>(bin_ws, L.block_start),
                                       at<uint32_t>(bin_ws, L.seg_start), &misc->bin_done,
-                                      hc.dev, st),
+                                      hc.dev, dg.status, st),
                 "rasterize: count");
     }
     Misc* host = pinned_misc();
@@ -466,15 +476,18 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
         // The pair count is final after bin_count, whose last work-group
         // stores it to host-mapped memory: queue the depth sort behind
         // bin_count and wait only for bin_count, so the sort runs while the
-        // host returns and queues the render.  A spin-bound error of the sort
-        // stays in the status word (gsr_rasterize_status).
+        // host returns and queues the render.  bin_count also hands over the
+        // device status word: errors of every earlier kernel on the device
+        // (an earlier frame's sorts, binning and backward) are reported here;
+        // this frame's own, at the next forward or gsr_rasterize_status.
         hipEvent_t ev = count_event();
         if (!ev) return fail(GSR_ERR_HIP, "rasterize: event creation failed");
         GSR_HIP(hipEventRecord(ev, st), "rasterize: record");
         if (int rc = depth_sort()) return rc;
         GSR_HIP(hipEventSynchronize(ev), "rasterize: synchronize");
-        const uint64_t total = *hc.host;
+        const uint64_t total = hc.host[0];
         if (total == kNoCount) return fail(GSR_ERR_DEVICE, "rasterize: pair count not stored");
+        if (const int bits = (int)hc.host[1]) return fail(GSR_ERR_DEVICE, status_message(bits));
         if (total > (uint64_t)kMaxPairs)
             return fail(GSR_ERR_TOO_MANY_PAIRS,
                         "rasterize: " + std::to_string(total) +
@@ -490,9 +503,12 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
                 "rasterize: scan");
         GSR_HIP(hipMemcpyAsync(host, misc, sizeof(Misc), hipMemcpyDeviceToHost, st),
                 "rasterize: read pair count");
+        GSR_HIP(hipMemcpyAsync(&host->status, dg.status, sizeof(int), hipMemcpyDeviceToHost, st),
+                "rasterize: read status");
+        GSR_HIP(gsr::zero_fill(dg.status, sizeof(int), st), "rasterize: clear status");
         GSR_HIP(hipStreamSynchronize(st), "rasterize: synchronize");
     }
-    if (host->err) return fail(GSR_ERR_DEVICE, "rasterize: look-back spin bound reached");
+    if (host->status) return fail(GSR_ERR_DEVICE, status_message(host->status));
     if (host->total > (uint64_t)kMaxPairs)
         return fail(GSR_ERR_TOO_MANY_PAIRS,
                     "rasterize: " + std::to_string(host->total) +
@@ -540,13 +556,14 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
         GSR_REQUIRE(sort_ws && sorted_ids, "null pointer");
         if (sort_ws_bytes < SL.end) return fail(GSR_ERR_WORKSPACE, "sort workspace too small");
         GSR_REQUIRE(mean2d && cov2d && colors && alpha && depth, "null pointer");
-        Misc* misc = at<Misc>(bin_ws, BL.misc);
         {
             StageTimer timer("records", st);
             GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, recs, st),
                     "rasterize: records");
         }
         uint32_t* ids = reinterpret_cast<uint32_t*>(sorted_ids);
+        gsr::DeviceGlobals dg;
+        GSR_HIP(gsr::device_globals(&dg), "rasterize: device globals");
         if (blocks) {
             {
                 StageTimer timer("tile_binning", st);
@@ -570,7 +587,7 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                 tb.ttotal = at<uint32_t>(sort_ws, SL.ttotal);
                 tb.ranges = tile_ranges;
                 tb.ids = ids;
-                tb.err = &misc->err;
+                tb.err = dg.status;
                 GSR_HIP(gsr::launch_tile_binning(tb, st), "rasterize: tile binning");
             }
             if (sorted_keys)
@@ -601,7 +618,7 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                                               at<uint32_t>(bin_ws, BL.tilehist),
                                               at<void>(sort_ws, SL.ctl), tk0, tk1,
                                               at<uint32_t>(sort_ws, SL.vbuf), ids, ktiles,
-                                              &misc->err, st),
+                                              dg.status, st),
                         "rasterize: tile sort");
             }
             {
@@ -615,8 +632,7 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                         "rasterize: keys");
         }
     }
-    uint32_t* order = (m > 0 && gsr::launch_order_enabled()) ? at<uint32_t>(sort_ws, SL.order)
-                                                               : nullptr;
+    uint32_t* order = m > 0 ? at<uint32_t>(sort_ws, SL.order) : nullptr;
     if (order) {
         StageTimer timer("fwd_schedule", st);
         GSR_HIP(gsr::launch_fwd_schedule(n, height, width, tile_ranges, sorted_ids, m, recs,
@@ -631,14 +647,26 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
 }
 
 int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream) {
-    GSR_REQUIRE(bin_ws && bin_ws_bytes >= sizeof(Misc), "bin workspace must not be null");
+    (void)bin_ws;
+    (void)bin_ws_bytes;
     hipStream_t st = as_stream(stream);
+    gsr::DeviceGlobals dg;
+    GSR_HIP(gsr::device_globals(&dg), "status: device globals");
     Misc* host = pinned_misc();
     if (!host) return fail(GSR_ERR_HIP, "pinned host buffer allocation failed");
-    GSR_HIP(hipMemcpyAsync(host, at<Misc>(bin_ws, 0), sizeof(Misc), hipMemcpyDeviceToHost, st),
+    GSR_HIP(hipMemcpyAsync(&host->status, dg.status, sizeof(int), hipMemcpyDeviceToHost, st),
             "status: read");
+    GSR_HIP(gsr::zero_fill(dg.status, sizeof(int), st), "status: clear");
     GSR_HIP(hipStreamSynchronize(st), "status: synchronize");
-    if (host->err) return fail(GSR_ERR_DEVICE, "a sort or scan kernel reached its spin bound");
+    if (host->status) return fail(GSR_ERR_DEVICE, status_message(host->status));
+    return GSR_OK;
+}
+
+int gsr_debug_raise_status(int bits, void* stream) {
+    GSR_REQUIRE(bits > 0, "bits must be positive");
+    gsr::DeviceGlobals dg;
+    GSR_HIP(gsr::device_globals(&dg), "raise status: device globals");
+    GSR_HIP(gsr::launch_raise_status(dg.status, bits, as_stream(stream)), "raise status");
     return GSR_OK;
 }
 
@@ -677,6 +705,8 @@ int rasterize_backward(int n, int height, int width, const float* grad_img,
     if (work) clear.add(at<void>(ws, L.ctl), L.ctl_end - L.ctl);
     GSR_HIP(gsr::zero_fill(clear, st), "backward: clear");
     if (!work) return GSR_OK;
+    gsr::DeviceGlobals dg;
+    GSR_HIP(gsr::device_globals(&dg), "backward: device globals");
     Misc* misc = at<Misc>(ws, L.misc);
     uint32_t* counts = at<uint32_t>(ws, L.counts);
     uint2* rects = at<uint2>(ws, L.rects);
@@ -690,7 +720,7 @@ int rasterize_backward(int n, int height, int width, const float* grad_img,
     {
         StageTimer timer("bwd_slots", st);
         GSR_HIP(gsr::launch_scan_counts(n, nullptr, counts, goff, &misc->total,
-                                        at<void>(ws, L.scanctl), &misc->err, st),
+                                        at<void>(ws, L.scanctl), dg.status, st),
                 "backward: slot layout");
     }
     gsr::GradSlots gs;
@@ -700,8 +730,8 @@ int rasterize_backward(int n, int height, int width, const float* grad_img,
     gs.sums = at<float>(ws, L.sums);
     gs.flags = at<uint8_t>(ws, L.flags);
     gs.slots = (uint64_t)num_pairs;
-    uint32_t* order = gsr::launch_order_enabled() ? at<uint32_t>(ws, L.order) : nullptr;
-    if (order) {
+    uint32_t* order = at<uint32_t>(ws, L.order);
+    {
         StageTimer timer("bwd_schedule", st);
         GSR_HIP(gsr::launch_bwd_schedule(height, width, tile_ranges, (uint64_t)num_pairs, n_contrib,
                                          at<uint32_t>(ws, L.work), order, st),

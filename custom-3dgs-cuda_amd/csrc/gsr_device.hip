@@ -1,0 +1,58 @@
+// gsr_device.hip — the library's per-device globals:
+//   - the device status word: kernels that reach their look-back spin bound
+//     or find inconsistent counts OR an error bit into it (bit 0: spin
+//     bound, bit 2: inconsistent counts).  bin_count's last work-group moves
+//     it to the host with the pair count, so the next forward call reports
+//     what any earlier kernel on the device found, without a synchronisation
+//     of its own;
+// Each device holds its own copy at its own address.  Host code takes that
+// address from hipGetSymbolAddress, once per device with that device current,
+// and passes it to kernels as an argument; the symbol's name is a host-side
+// stand-in and is never used as a device address.
+#include <hip/hip_runtime.h>
+
+#include <mutex>
+
+#include "gsr_internal.h"
+
+namespace gsr {
+
+// Word 0 is the status; the rest pads the word to its own 256-byte block.
+static __device__ __align__(256) int status_word[64];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_mu;
+DeviceGlobals g_table[kMaxDevices];  // by device ordinal; null until set up
+
+__global__ void raise_status_kernel(int* __restrict__ status, int bits) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) atomicOr(status, bits);
+}
+
+}  // namespace
+
+hipError_t device_globals(DeviceGlobals* out) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_mu);
+    DeviceGlobals& g = g_table[dev];
+    if (!g.status) {
+        void* st = nullptr;
+        e = hipGetSymbolAddress(&st, HIP_SYMBOL(status_word));
+        if (e != hipSuccess) return e;
+        if (!st) return hipErrorInvalidSymbol;
+        g.status = static_cast<int*>(st);
+    }
+    *out = g;
+    return hipSuccess;
+}
+
+hipError_t launch_raise_status(int* status, int bits, hipStream_t st) {
+    hipLaunchKernelGGL(raise_status_kernel, dim3(1), dim3(64), 0, st, status, bits);
+    return hipGetLastError();
+}
+
+}  // namespace gsr

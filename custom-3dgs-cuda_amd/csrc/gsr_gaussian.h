@@ -280,7 +280,7 @@ __device__ __forceinline__ void project_backward_one(
 #pragma unroll
     for (int r = 0; r < 3; ++r)
         omu[r] = Rct.m[r][0] * dmc[0] + Rct.m[r][1] * dmc[1] + Rct.m[r][2] * dmc[2];
-    // quaternion (projection_backward.cu:334-344); L[i][j] is the value the
+    // quaternion (projection_backward.cu:116-127); L[i][j] is the value the
     // reference reads as dL_dRt[i][j].
     float L[3][3];
 #pragma unroll
@@ -296,7 +296,7 @@ __device__ __forceinline__ void project_backward_one(
                      2.0f * qz * (L[1][2] + L[2][1]) - 4.0f * qy * (L[2][2] + L[0][0]);
     const float gz = 2.0f * qw * (L[0][1] - L[1][0]) + 2.0f * qx * (L[2][0] + L[0][2]) +
                      2.0f * qy * (L[1][2] + L[2][1]) - 4.0f * qz * (L[1][1] + L[0][0]);
-    // through normalize (projection_backward.cu:346-356)
+    // through normalize (projection_backward.cu:129-138)
     const float inv_norm =
         1.0f / __builtin_sqrtf(qq.x * qq.x + qq.y * qq.y + qq.z * qq.z + qq.w * qq.w + 1e-8f);
     const float qdot = qw * gw + qx * gx + qy * gy + qz * gz;

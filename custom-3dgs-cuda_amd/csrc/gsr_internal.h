@@ -9,6 +9,19 @@
 
 namespace gsr {
 
+// ---- per-device globals (gsr_device.hip) ----
+// Status-word bits set by kernels.
+constexpr int kStatusSpin = 1;    // a look-back wait reached its spin bound
+constexpr int kStatusCounts = 2;  // a scan found counts that disagree with the binning's
+struct DeviceGlobals {
+    int* status = nullptr;  // device address of the current device's status word
+};
+// The current device's globals: their addresses are looked up once per
+// device (hipGetSymbolAddress, with that device current) and kept.
+hipError_t device_globals(DeviceGlobals* out);
+// ORs bits into a status word from a one-thread kernel (a test hook).
+hipError_t launch_raise_status(int* status, int bits, hipStream_t st);
+
 hipError_t launch_project_fwd(int n, const float* mu, const float* q, const float* s,
                               const float* rot, const float* tr, float fx, float fy, float cx,
                               float cy, float* mean2d, float* cov2d, float* depth,
@@ -165,13 +178,14 @@ hipError_t launch_range_keys(int T, const int32_t* ranges, const int32_t* ids, c
 // the pair count added to *pair_total and, by the last work-group, the block
 // and segment starts (block_start / seg_start, nb + 1 entries each; `done` a
 // zero counter, left at zero) and, when host_total is not null, the final pair
-// count stored to that host-mapped coherent word (block histogram mode only).
+// count stored to that host-mapped coherent word (block histogram mode only),
+// and the device status word (status, read and cleared) to host_total[1].
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
                             uint32_t* block_start, uint32_t* seg_start, uint32_t* done,
-                            uint64_t* host_total, hipStream_t st);
+                            uint64_t* host_total, int* status, hipStream_t st);
 
 // Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r] (perm null:
 // the identity); the total (u64) is written to *total.
@@ -204,9 +218,6 @@ hipError_t launch_blend_records(int n, const float* mean2d, const float* cov2d,
                                 hipStream_t st, int H = 0, int W = 0, uint32_t* counts = nullptr,
                                 uint2* rects = nullptr);
 
-// Whether the blends take their tiles in a longest-first order (on unless
-// GSR_TILE_ORDER=0).
-bool launch_order_enabled();
 // Forward schedule: per-tile work estimates (work, T entries) and the launch
 // order (order, T entries).
 hipError_t launch_fwd_schedule(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
@@ -223,10 +234,11 @@ hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num
 
 // Gradient slots: the (Gaussian, tile) pairs in Gaussian-major order, pair
 // (g, t) at goff[g] + its index in g's tile rectangle (row-major); the backward
-// writes each processed pair's nine sums to sums[9 slot ..] and sets
-// flags[slot], and pair_grad_reduce adds each Gaussian's flagged slots to the
-// gradient outputs.  Pairs outside the layout (inputs that disagree with the
-// rectangles) fall back to atomics on the outputs.
+// claims each processed pair's slot (flags[slot] = 1, an atomic OR on the
+// 32-bit word holding the byte) and writes its nine sums to sums[9 slot ..],
+// and pair_grad_reduce adds each Gaussian's claimed slots to the gradient
+// outputs.  Pairs without a slot of their own (outside the rectangles, or an
+// id repeated within one tile's list) fall back to atomics on the outputs.
 struct GradSlots {
     const uint32_t* goff = nullptr;
     const uint32_t* counts = nullptr;

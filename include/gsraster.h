@@ -17,6 +17,14 @@
  * Every entry point returns GSR_OK or an error code; gsr_last_error() gives
  * the calling thread's message for the last failure.  Outputs are fully
  * written by the call (no zero-initialisation by the caller is needed).
+ *
+ * Device errors.  A kernel that reaches its bounded look-back wait, or finds
+ * counts that disagree with the binning, exits normally and ORs a bit into
+ * its device's status word (its outputs are then invalid).  Calls do not
+ * synchronize to look at it: gsr_rasterize_bin reads and clears it with the
+ * pair count it waits for anyway, so it reports GSR_ERR_DEVICE for every
+ * kernel queued on the device before it (an earlier frame's sorts, binning or
+ * backward); gsr_rasterize_status synchronizes and reports the rest.
  */
 #ifndef GSRASTER_H
 #define GSRASTER_H
@@ -33,7 +41,7 @@ extern "C" {
 #define GSR_ERR_HIP 2              /* a HIP runtime call or launch failed */
 #define GSR_ERR_WORKSPACE 3        /* workspace smaller than the size query */
 #define GSR_ERR_TOO_MANY_PAIRS 4   /* M > 2^31 - 2^16 (the int32 sorted_ids limit, less headroom) */
-#define GSR_ERR_DEVICE 5           /* a kernel reported an error (look-back spin limit) */
+#define GSR_ERR_DEVICE 5           /* a kernel reported an error (spin bound, bad counts) */
 
 const char* gsr_last_error(void);
 const char* gsr_version(void);
@@ -101,10 +109,17 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                          size_t sort_ws_bytes, int32_t* sorted_ids, int32_t* tile_ranges,
                          float* img, float* final_T, int32_t* n_contrib, uint64_t* sorted_keys,
                          void* stream);
-/* Synchronizes `stream` and reports GSR_ERR_DEVICE if a kernel of the last
- * bin/render calls on this bin_ws hit its look-back spin bound or found
- * inconsistent counts. */
+/* Synchronizes `stream`, then reads and clears the current device's status
+ * word: GSR_ERR_DEVICE if a kernel queued on the device since the status was
+ * last read hit its look-back spin bound or found inconsistent counts.
+ * bin_ws is not read (it may be NULL); the status is per device. */
 int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream);
+
+/* Test hook (no counterpart in the reference): ORs `bits` (> 0) into the
+ * current device's status word from a one-thread kernel on `stream`, as a
+ * kernel that hit its spin bound would, so that callers can test their
+ * handling of GSR_ERR_DEVICE. */
+int gsr_debug_raise_status(int bits, void* stream);
 
 /* Replaces launch_backward_rasterization (csrc/backward/rasterize_backward.h:5,
  * csrc/backward/rasterize_backward.cu:239-309; bound as
@@ -153,9 +168,11 @@ int gsr_sh_backward(int n, const float* colors_grad, const float* mu, const floa
  * csrc/backward/projection_backward.cu:142-187; bound as
  * `backwards_projection` at csrc/bindings.cpp:118-138,149).  cx, cy are
  * accepted and unused, as in the reference.  The quaternion gradient is the
- * derivative of the rotation the forward builds; set the environment
- * variable GSR_REFERENCE_QUAT_GRAD=1 before the first call to get the
- * reference's literal formula (projection_backward.cu:334-344) instead. */
+ * derivative of the rotation the forward builds; with the environment
+ * variable GSR_REFERENCE_QUAT_GRAD=1 (read on every call) d_q is the
+ * reference's literal formula instead (projection_backward.cu:116-127, whose
+ * w-multiplied terms carry the opposite sign), bit for bit; d_mu and d_s do
+ * not depend on the setting. */
 int gsr_project_backward(int n, const float* d_mean2d, const float* d_cov2d, const float* mu,
                          const float* q, const float* s, const float* rot, const float* trans,
                          float fx, float fy, float cx, float cy, float* d_mu, float* d_q,

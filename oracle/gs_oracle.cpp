@@ -570,7 +570,7 @@ void sh_bwd_all(int n, const T* cgrad, const T* mu, const T* A, const T* kj, con
 
 // ----- a12: projection backward (projection_backward.cu:33-138) ------------
 // ref_quat = 1 evaluates the reference's quaternion formula literally
-// (projection_backward.cu:334-344): it indexes transpose(dL/dR) with the
+// (projection_backward.cu:116-127): it indexes transpose(dL/dR) with the
 // index pattern of a formula derived for dL/dR itself, so every term that
 // multiplies w changes sign and the result fails finite differences (the
 // reference's own test_projection_backward_matches_finite_differences).
@@ -654,7 +654,7 @@ void proj_bwd_all(int n, const T* dmean, const T* dcov, const T* mu, const T* q,
                 T(2) * qz * (L[1][2] + L[2][1]) - T(4) * qy * (L[2][2] + L[0][0]);
         T gzq = T(2) * qw * (L[0][1] - L[1][0]) + T(2) * qx * (L[2][0] + L[0][2]) +
                 T(2) * qy * (L[1][2] + L[2][1]) - T(4) * qz * (L[1][1] + L[0][0]);
-        // through normalize (projection_backward.cu:346-356)
+        // through normalize (projection_backward.cu:129-138)
         const T* qr = q + 4 * (size_t)i;
         T inv_norm = T(1) / M<T>::sqrt(qr[0] * qr[0] + qr[1] * qr[1] + qr[2] * qr[2] +
                                        qr[3] * qr[3] + T(1e-8f));

@@ -221,7 +221,7 @@ def project_bwd(dmean, dcov, mu, q, s, R, t, fx, fy, cx, cy, dtype=np.float32, r
     """csrc/backward/projection_backward.cu:11-140 -> (dmu [N,3], dq [N,4], ds [N,3]).
 
     ``ref_quat=True`` evaluates the reference's quaternion formula literally
-    (projection_backward.cu:334-344), which fails finite differences; the default
+    (projection_backward.cu:116-127), which fails finite differences; the default
     is the derivative of glm::toMat3 that the reference's own test demands.
     """
     dmean, dcov, mu, q, s, R, t = (_c(a, dtype) for a in (dmean, dcov, mu, q, s, R, t))

@@ -53,7 +53,8 @@ def assert_bitwise(got, want, what: str) -> None:
             f"got {got[first]!r} want {want[first]!r}")
 
 
-def assert_grad_close(got, want, absum, what: str, rel: float = 1e-4) -> None:
+def assert_grad_close(got, want, absum, what: str, rel: float = 1e-4,
+                      want64=None, floor: float = 0.05) -> tuple[float, float]:
     """fp32 gradient vs float64 oracle sum.
 
     Bar: |got - want| <= rel * max(|want|, absum_floor) per element, where the
@@ -61,19 +62,44 @@ def assert_grad_close(got, want, absum, what: str, rel: float = 1e-4) -> None:
     an fp32 sum of k terms in any order is accurate to ~k*eps*sum|terms|, so
     elements whose terms cancel are held to the conditioning of their sum, and
     every other element to 1e-4 relative.
+
+    floor: the fraction of absum below which |want| does not shrink the bar
+    (0.05: errors up to 5e-6 of sum|terms| pass).  Every term of a pixel's
+    gradient scales with its transmittance T, which the backward unwinds from
+    final_T through the list; over the ~2000-entry lists of the benchmark scene
+    T's relative rounding error at the front of a list reaches ~1e-5 in any
+    fp32 evaluation, the reference's own arithmetic included (measured against
+    its float64 twin), so those tests pass floor=0.25.
+
+    want64 (optional): the same oracle with float64 per-pixel arithmetic.  The
+    fp32 per-pixel arithmetic in the reference's operation order (want) then
+    has a measured error of its own on each element, |want - want64|; an
+    element also passes when got lies within twice that of want (two fp32
+    evaluations of one sum, each with its own rounding).
+
+    Returns (max scaled error over the elements held to the first bar, tensor
+    relative error); the tensor relative error is always held to rel.
     """
     got = np.asarray(got, dtype=np.float64).reshape(np.shape(want))
     want = np.asarray(want, dtype=np.float64)
     absum = np.asarray(absum, dtype=np.float64).reshape(want.shape)
-    scale = np.maximum(np.abs(want), 0.05 * absum)
+    scale = np.maximum(np.abs(want), floor * absum)
     scale = np.maximum(scale, 1e-30)
-    err = np.abs(got - want) / scale
+    diff = np.abs(got - want)
+    err = diff / scale
+    if want64 is not None:
+        own = np.abs(want - np.asarray(want64, dtype=np.float64).reshape(want.shape))
+        err = np.where(diff <= 2.0 * own, 0.0, err)
     worst = np.unravel_index(np.argmax(err), err.shape) if err.size else None
     assert err.size == 0 or err.max() <= rel, (
         f"{what}: max scaled error {err.max():.3e} > {rel} at {worst}: got {got[worst]!r} "
-        f"want {want[worst]!r} absum {absum[worst]!r}")
+        f"want {want[worst]!r} absum {absum[worst]!r}"
+        + (f" want64 {np.asarray(want64).reshape(want.shape)[worst]!r}" if want64 is not None
+           else ""))
     # tensor-level relative error, the plain 1e-4 rel bar
     den = np.linalg.norm(want.ravel())
+    tot = 0.0
     if den > 0:
-        tot = np.linalg.norm((got - want).ravel()) / den
+        tot = float(np.linalg.norm((got - want).ravel()) / den)
         assert tot <= rel, f"{what}: tensor relative error {tot:.3e} > {rel}"
+    return (float(err.max()) if err.size else 0.0), tot

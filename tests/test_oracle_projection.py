@@ -132,7 +132,7 @@ def test_backward_matches_finite_differences_fp64(orc):
 
 
 def test_reference_literal_quaternion_formula_fails_finite_differences(orc):
-    """projection_backward.cu:334-344 read literally (ref_quat=True) is not the
+    """projection_backward.cu:116-127 read literally (ref_quat=True) is not the
     derivative of the forward rotation; it fails the same finite-difference check."""
     rng = np.random.default_rng(3)
     mu, q, s = _inputs(rng, n=8)
