@@ -789,6 +789,38 @@ int gsr_rasterize_backward_strided(int n, int height, int width, const float* gr
                               ws_bytes, d_mean2d, d_cov2d, d_colors, d_alpha, stream);
 }
 
+int gsr_rasterize_backward_noalloc(int n, int height, int width, const float* grad_img,
+                                   const float* mean2d, const float* cov2d, const float* colors,
+                                   const float* alpha, const int32_t* sorted_ids,
+                                   int64_t num_pairs, const int32_t* tile_ranges,
+                                   const float* final_T, const int32_t* n_contrib,
+                                   float* d_mean2d, float* d_cov2d, float* d_colors,
+                                   float* d_alpha, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (int rc = check_screen(height, width)) return rc;
+    GSR_REQUIRE(num_pairs >= 0 && num_pairs <= kMaxPairs, "num_pairs out of range");
+    const size_t need = backward_layout(n, num_pairs, height, width).end;
+    static_assert(gsr::kNoAllocScratchBytes == (size_t)GSR_NOALLOC_SCRATCH_BYTES,
+                  "the header's scratch size is the array's");
+    if (need > gsr::kNoAllocScratchBytes)
+        return fail(GSR_ERR_WORKSPACE,
+                    "backward (no allocation): the frame needs " + std::to_string(need) +
+                        " bytes of workspace (about 37 per pair and 68 per Gaussian), more than "
+                        "the fixed scratch's " +
+                        std::to_string(gsr::kNoAllocScratchBytes) +
+                        "; use gsr_rasterize_backward with a workspace");
+    gsr::DeviceGlobals dg;
+    GSR_HIP(gsr::device_globals(&dg), "backward (no allocation): device globals");
+    gsr::GradStrides gst;
+    gst.h = 3 * (int64_t)width;
+    gst.w = 3;
+    gst.c = 1;
+    return rasterize_backward(n, height, width, grad_img, gst, mean2d, cov2d, colors, alpha,
+                              sorted_ids, num_pairs, tile_ranges, final_T, n_contrib, dg.scratch,
+                              gsr::kNoAllocScratchBytes, d_mean2d, d_cov2d, d_colors, d_alpha,
+                              stream);
+}
+
 int gsr_sh_backward(int n, const float* colors_grad, const float* mu, const float* albedo,
                     const float* k_j, const float* cam_pos, float* d_albedo, float* d_k_j,
                     float* d_mu, void* stream) {

@@ -5,10 +5,12 @@
 //     it to the host with the pair count, so the next forward call reports
 //     what any earlier kernel on the device found, without a synchronisation
 //     of its own;
-// Each device holds its own copy at its own address.  Host code takes that
-// address from hipGetSymbolAddress, once per device with that device current,
-// and passes it to kernels as an argument; the symbol's name is a host-side
-// stand-in and is never used as a device address.
+//   - `scratch`, the fixed workspace of the allocation-free backward entry
+//     point (gsr_rasterize_backward_noalloc).
+// Each device holds its own copy of both at its own address.  Host code takes
+// those addresses from hipGetSymbolAddress, once per device with that device
+// current, and passes them to kernels as arguments; the symbols' names are
+// host-side stand-ins and are never used as device addresses.
 #include <hip/hip_runtime.h>
 
 #include <mutex>
@@ -19,6 +21,8 @@ namespace gsr {
 
 // Word 0 is the status; the rest pads the word to its own 256-byte block.
 static __device__ __align__(256) int status_word[64];
+
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
 
 namespace {
 
@@ -39,12 +43,16 @@ hipError_t device_globals(DeviceGlobals* out) {
     if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
     std::lock_guard<std::mutex> lock(g_mu);
     DeviceGlobals& g = g_table[dev];
-    if (!g.status) {
+    if (!g.status || !g.scratch) {
         void* st = nullptr;
+        void* sc = nullptr;
         e = hipGetSymbolAddress(&st, HIP_SYMBOL(status_word));
         if (e != hipSuccess) return e;
-        if (!st) return hipErrorInvalidSymbol;
+        e = hipGetSymbolAddress(&sc, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        if (!st || !sc) return hipErrorInvalidSymbol;
         g.status = static_cast<int*>(st);
+        g.scratch = sc;
     }
     *out = g;
     return hipSuccess;

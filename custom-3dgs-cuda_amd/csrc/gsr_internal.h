@@ -10,11 +10,14 @@
 namespace gsr {
 
 // ---- per-device globals (gsr_device.hip) ----
+// Bytes of the fixed scratch array of gsr_rasterize_backward_noalloc.
+constexpr size_t kNoAllocScratchBytes = (size_t)256 << 20;
 // Status-word bits set by kernels.
 constexpr int kStatusSpin = 1;    // a look-back wait reached its spin bound
 constexpr int kStatusCounts = 2;  // a scan found counts that disagree with the binning's
 struct DeviceGlobals {
-    int* status = nullptr;  // device address of the current device's status word
+    int* status = nullptr;    // device address of the current device's status word
+    void* scratch = nullptr;  // device address of its scratch array
 };
 // The current device's globals: their addresses are looked up once per
 // device (hipGetSymbolAddress, with that device current) and kept.

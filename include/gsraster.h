@@ -156,6 +156,26 @@ int gsr_rasterize_backward_strided(int n, int height, int width, const float* gr
                                    float* d_mean2d, float* d_cov2d, float* d_colors,
                                    float* d_alpha, void* stream);
 
+/* No counterpart in the reference: gsr_rasterize_backward for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  It takes no workspace: its
+ * kernels use a fixed array of GSR_NOALLOC_SCRATCH_BYTES in the library's
+ * device memory, one per GPU, held until the process ends.  A frame whose
+ * workspace (gsr_backward_workspace_bytes: about 37 B per pair plus 68 B per
+ * Gaussian) exceeds it is rejected with GSR_ERR_WORKSPACE.  The call
+ * allocates nothing.  Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (other streams, other threads) race; calls queued
+ * in order on one stream do not.  Results are bit for bit those of
+ * gsr_rasterize_backward. */
+#define GSR_NOALLOC_SCRATCH_BYTES (256u << 20)
+int gsr_rasterize_backward_noalloc(int n, int height, int width, const float* grad_img,
+                                   const float* mean2d, const float* cov2d, const float* colors,
+                                   const float* alpha, const int32_t* sorted_ids,
+                                   int64_t num_pairs, const int32_t* tile_ranges,
+                                   const float* final_T, const int32_t* n_contrib,
+                                   float* d_mean2d, float* d_cov2d, float* d_colors,
+                                   float* d_alpha, void* stream);
+
 /* Replaces launch_backward_SH (csrc/backward/delight_backward.h:5,
  * csrc/backward/delight_backward.cu:176-218; bound as `backwards_SH` at
  * csrc/bindings.cpp:102-116,148).  cam_pos is a device pointer; k_j and d_k_j
