@@ -69,6 +69,10 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
         "project_bwd": 100 * N,
         # the two backwards in one pass: mu read once, dL/dmu written once
         "project_sh_bwd": 496 * N,
+        # the trainer's loss: both images in, the SSIM index's three derivative
+        # maps out (fwd); maps and images in, dL/dimage out (bwd)
+        "loss": 60 * P,
+        "loss_bwd": 72 * P,
     }.get(stage)
 
 
@@ -93,16 +97,27 @@ def _clear(g):
         getattr(g, name).grad = None
 
 
-def time_frames(sc, steps: int, warmup: int, profile: bool, render=None):
+def time_frames(sc, steps: int, warmup: int, profile: bool, render=None, grad=None):
+    """Mean forward, backward and whole-frame ms of ``steps`` frames.  The
+    backward is ``image.sum().backward()`` (the reference's bench.py:94-96), or
+    ``image.backward(grad)`` for a given dL/dimage (the baseline configs'
+    seeded N(0, 1))."""
     import torch
     import custom_rasterizer_cuda as crc
     from gaussian_splatting.rasterizer.rasterize import rasterize
 
     rasterize = render or rasterize
     g, view = sc.gaussians, sc.view
+
+    def backward(img):
+        if grad is None:
+            img.sum().backward()
+        else:
+            img.backward(grad)
+
     for _ in range(warmup):
         _clear(g)
-        rasterize(g, view).sum().backward()
+        backward(rasterize(g, view))
     torch.cuda.synchronize()
     crc.profile_reset()
     crc.profile_enable(profile)
@@ -116,7 +131,7 @@ def time_frames(sc, steps: int, warmup: int, profile: bool, render=None):
         e0.record()
         img = rasterize(g, view)
         e1.record()
-        img.sum().backward()
+        backward(img)
         e2.record()
     t_end.record()
     torch.cuda.synchronize()
@@ -233,16 +248,27 @@ def per_gaussian_stages(sc, calls: int = 20) -> dict:
     return _stage_rates(stages, n, 0, v["width"], v["height"])
 
 
+def config_grad(sc):
+    """The baseline configs' dL/dimage: N(0, 1), seeded, resident on the device."""
+    from gaussian_splatting import synthetic
+
+    v = sc.view
+    return synthetic.grad_image(int(v["height"]), int(v["width"]), seed=3).to(
+        sc.gaussians.mu.device)
+
+
 def frame_stages(sc, steps: int, binning: str | None = None) -> dict:
-    """fwd+bwd frames of config ``sc`` with the per-stage breakdown; ``binning``
-    "sort" selects the LSD tile sort (GSR_TILE_BINNING) for these frames."""
+    """fwd+bwd frames of config ``sc`` (dL/dimage N(0, 1)) with the per-stage
+    breakdown; ``binning`` "sort" selects the LSD tile sort (GSR_TILE_BINNING)
+    for these frames."""
     old = os.environ.get("GSR_TILE_BINNING")
     if binning:
         os.environ["GSR_TILE_BINNING"] = binning
     try:
         M = pair_count(sc)
-        fwd, bwd, total, _ = time_frames(sc, steps, 2, profile=False)
-        _, _, _, stages = time_frames(sc, steps, 1, profile=True)
+        G = config_grad(sc)
+        fwd, bwd, total, _ = time_frames(sc, steps, 2, profile=False, grad=G)
+        _, _, _, stages = time_frames(sc, steps, 1, profile=True, grad=G)
     finally:
         if old is None:
             os.environ.pop("GSR_TILE_BINNING", None)
@@ -288,7 +314,9 @@ def banded_frame(sc, band_height: int, steps: int) -> dict:
     render = lambda g, v: rasterize_bands(g, v, band_height)
     print(f"[bench] {sc.name}: {steps} banded frame(s), bands of {band_height} rows",
           file=sys.stderr, flush=True)
-    fwd, bwd, total, stages = time_frames(sc, steps, 1, profile=True, render=render)
+    G = config_grad(sc)
+    fwd, bwd, total, _ = time_frames(sc, steps, 1, profile=False, render=render, grad=G)
+    _, _, _, stages = time_frames(sc, 1, 0, profile=True, render=render, grad=G)
     print(f"[bench] {sc.name}: {total:.1f} ms per frame; counting pairs per band",
           file=sys.stderr, flush=True)
     pairs = band_pair_counts(sc, band_height)
@@ -299,9 +327,8 @@ def banded_frame(sc, band_height: int, steps: int) -> dict:
     # per-stage rates: a stage's calls cover all bands, so per frame it moves
     # the bytes of the whole frame (per-Gaussian stages once per band)
     rates = {}
-    for name, (count, ms) in stages.items():
-        per_frame = ms / max(steps, 1)
-        rates[name] = {"ms_per_frame": round(per_frame, 3), "calls": int(count)}
+    for name, (count, ms) in stages.items():  # one profiled frame
+        rates[name] = {"ms_per_frame": round(ms, 3), "calls": int(count)}
     return {"fwd_ms": round(fwd, 3), "bwd_ms": round(bwd, 3), "ms_per_frame": round(total, 3),
             "fps": round(1000.0 / total, 2), "pairs": M, "bands": bands,
             "band_height": band_height, "max_band_pairs": max(pairs),
@@ -383,8 +410,8 @@ def main() -> int:
                     help="the frame to time: the reference's bench scene (default) or a "
                          "rasterizer baseline config at its own size (for profiling)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--c5", action="store_true",
-                    help="also time config c5 (5M Gaussians, 3840x2160) in screen bands")
+    ap.add_argument("--no-c5", action="store_true",
+                    help="skip config c5 (5M Gaussians, 3840x2160, timed in screen bands)")
     ap.add_argument("--band-height", type=int, default=128,
                     help="rows per screen band of the c5 frame (a multiple of 16)")
     ap.add_argument("--no-extra", action="store_true", help="skip the 720p and c3 side runs")
@@ -473,13 +500,24 @@ def main() -> int:
     }
     if not args.no_extra:
         extra = {}
-        for label, scene in (
-                ("bench_100k_1280x720", synthetic.bench_scene(n=N, width=1280, height=720, device=dev)),
-                ("c3_100k_1920x1080", synthetic.config_scene("c3", device=dev))):
-            f2, b2, t2, _ = time_frames(scene, max(10, args.steps // 2), 5, profile=False)
+        # the 720p bench scene (image.sum(), as the reference's bench.py), the
+        # 1080p bench scene with a seeded N(0, 1) dL/dimage, and configs c2 and
+        # c3 (N(0, 1) dL/dimage, as the baseline states)
+        b1080 = synthetic.bench_scene(n=N, width=1920, height=1080, device=dev)
+        for label, scene, grad in (
+                ("bench_100k_1280x720",
+                 synthetic.bench_scene(n=N, width=1280, height=720, device=dev), None),
+                ("bench_100k_1920x1080_randn_grad", b1080, config_grad(b1080)),
+                ("c2_100k_1280x720", synthetic.config_scene("c2", device=dev), "randn"),
+                ("c3_100k_1920x1080", synthetic.config_scene("c3", device=dev), "randn")):
+            if isinstance(grad, str):
+                grad = config_grad(scene)
+            f2, b2, t2, _ = time_frames(scene, max(10, args.steps // 2), 5, profile=False,
+                                        grad=grad)
             extra[label] = {"fwd_ms": round(f2, 4), "bwd_ms": round(b2, 4),
                             "ms_per_frame": round(t2, 4), "fps": round(1000.0 / t2, 1),
-                            "pairs": pair_count(scene)}
+                            "pairs": pair_count(scene),
+                            "loss": "image.sum()" if grad is None else "dL/dimage N(0,1)"}
         out["extra"] = extra
     if not args.no_scale:
         # the HBM-bound stages where they move hundreds of MB: the per-Gaussian
@@ -493,7 +531,7 @@ def main() -> int:
         scale["c4_1M_1920x1080_tile_sort"] = frame_stages(c4, 5, binning="sort")
         del c4
         out["scale"] = scale
-    if args.c5:
+    if not args.no_c5:
         # config c5 (5M Gaussians, 3840x2160): ~1.1e10 pairs, beyond the int32
         # lists of the reference's surface, so rendered in screen bands
         c5 = synthetic.config_scene("c5", device=dev)

@@ -493,6 +493,61 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> backwards_project_sh(
     return {mu_grad, q_grad, s_grad, albedo_grad, k_j_grad, logit_grad};
 }
 
+// ---- the trainer's loss (gaussian_splatting/utils/loss.py:12-33) ----
+void check_image_pair(const Tensor& a, const Tensor& b, const char* an, const char* bn) {
+    CHECK_INPUT_FP32(a);
+    CHECK_INPUT_FP32(b);
+    TORCH_CHECK(a.dim() == 3 && a.size(2) == 3, an, " must have shape (H, W, 3)");
+    TORCH_CHECK(a.sizes() == b.sizes(), "Shape mismatch: gt ", b.sizes(), " vs rendered ",
+                a.sizes());
+    (void)bn;
+}
+
+// (out, ws): out = [loss, SSIM, L1 mean] on the device; ws feeds the backward.
+std::tuple<Tensor, Tensor> l1_dssim(const Tensor rendered, const Tensor gt, double lambda_dssim) {
+    check_image_pair(rendered, gt, "rendered", "gt");
+    const int H = (int)rendered.size(0), W = (int)rendered.size(1);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(rendered.device());
+    Tensor ws = workspace((int64_t)gsr_loss_workspace_bytes(H, W), rendered);
+    Tensor out = torch::empty({3}, rendered.options());
+    check_rc(gsr_l1_dssim(H, W, cfp(rendered), cfp(gt), (float)lambda_dssim, ws.data_ptr(),
+                          (size_t)ws.numel(), fp(out), current_stream()),
+             "l1_dssim");
+    return {out, ws};
+}
+
+Tensor l1_dssim_backward(const Tensor rendered, const Tensor gt, double lambda_dssim,
+                         const Tensor ws, const c10::optional<Tensor>& grad_loss) {
+    check_image_pair(rendered, gt, "rendered", "gt");
+    const int H = (int)rendered.size(0), W = (int)rendered.size(1);
+    const bool g = grad_loss.has_value() && grad_loss->defined();
+    if (g) {
+        CHECK_INPUT_FP32(*grad_loss);
+        TORCH_CHECK(grad_loss->numel() == 1, "grad_loss must hold one value");
+    }
+    TORCH_CHECK(ws.is_cuda() && ws.scalar_type() == torch::kUInt8, "ws must be the forward's");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(rendered.device());
+    Tensor d = torch::empty_like(rendered);
+    check_rc(gsr_l1_dssim_backward(H, W, cfp(rendered), cfp(gt), (float)lambda_dssim,
+                                   ws.data_ptr(), (size_t)ws.numel(), g ? cfp(*grad_loss) : nullptr,
+                                   fp(d), current_stream()),
+             "l1_dssim_backward");
+    return d;
+}
+
+// [1 - SSIM, SSIM, mean|a - b|] on the device (scripts/eval.py:60)
+Tensor ssim(const Tensor a, const Tensor b) {
+    check_image_pair(a, b, "a", "b");
+    const int H = (int)a.size(0), W = (int)a.size(1);
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(a.device());
+    Tensor ws = workspace((int64_t)gsr_loss_workspace_bytes(H, W), a);
+    Tensor out = torch::empty({3}, a.options());
+    check_rc(gsr_ssim(H, W, cfp(a), cfp(b), ws.data_ptr(), (size_t)ws.numel(), fp(out),
+                      current_stream()),
+             "ssim");
+    return out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(custom_rasterizer_cuda, m) {
@@ -528,6 +583,12 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
           py::arg("fx"), py::arg("fy"), py::arg("albedo"), py::arg("k_j"),
           py::arg("camera_position"), py::arg("alpha_grad") = py::none(),
           py::arg("opacity") = py::none());
+    m.def("l1_dssim", &l1_dssim,
+          "trainer loss (1 - l) L1 + l (1 - SSIM): (tensor [loss, SSIM, L1], workspace)");
+    m.def("l1_dssim_backward", &l1_dssim_backward, "dloss/drendered, scaled by grad_loss",
+          py::arg("rendered"), py::arg("gt"), py::arg("lambda_dssim"), py::arg("ws"),
+          py::arg("grad_loss") = py::none());
+    m.def("ssim", &ssim, "SSIM of two (H, W, 3) images: tensor [1 - SSIM, SSIM, L1]");
     // Stage timing of libgsraster (HIP events on the launch stream); not part of
     // the reference surface.
     m.def("profile_enable", [](bool on) { gsr_profile_enable(on ? 1 : 0); });

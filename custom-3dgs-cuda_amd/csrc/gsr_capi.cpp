@@ -883,6 +883,61 @@ int gsr_project_backward(int n, const float* d_mean2d, const float* d_cov2d, con
     return GSR_OK;
 }
 
+size_t gsr_loss_workspace_bytes(int height, int width) {
+    if (height < 11 || width < 11) return 0;
+    const size_t parts = align_up(8 * gsr::loss_partial_count(height, width), 256);
+    return parts + 3 * 12 * (size_t)height * (size_t)width;
+}
+
+namespace {
+int check_loss_args(int height, int width, const void* a, const void* b, const void* ws,
+                    size_t ws_bytes) {
+    GSR_REQUIRE(height >= 11 && width >= 11,
+                "the SSIM needs images of at least 11 x 11 pixels (its window)");
+    GSR_REQUIRE((int64_t)height * width <= ((int64_t)1 << 31) / 3, "image too large");
+    GSR_REQUIRE(a && b, "null pointer");
+    if (!ws || ws_bytes < gsr_loss_workspace_bytes(height, width))
+        return fail(GSR_ERR_WORKSPACE, "loss workspace too small");
+    return GSR_OK;
+}
+}  // namespace
+
+int gsr_l1_dssim(int height, int width, const float* rendered, const float* gt,
+                 float lambda_dssim, void* ws, size_t ws_bytes, float* out, void* stream) {
+    if (int rc = check_loss_args(height, width, rendered, gt, ws, ws_bytes)) return rc;
+    GSR_REQUIRE(out, "null pointer");
+    const size_t parts = align_up(8 * gsr::loss_partial_count(height, width), 256);
+    StageTimer timer("loss", as_stream(stream));
+    GSR_HIP(gsr::launch_l1_dssim_fwd(height, width, rendered, gt, lambda_dssim,
+                                     at<float>(ws, parts), ws, out, as_stream(stream)),
+            "l1_dssim");
+    return GSR_OK;
+}
+
+int gsr_l1_dssim_backward(int height, int width, const float* rendered, const float* gt,
+                          float lambda_dssim, const void* ws, size_t ws_bytes,
+                          const float* grad_loss, float* d_rendered, void* stream) {
+    if (int rc = check_loss_args(height, width, rendered, gt, ws, ws_bytes)) return rc;
+    GSR_REQUIRE(d_rendered, "null pointer");
+    const size_t parts = align_up(8 * gsr::loss_partial_count(height, width), 256);
+    StageTimer timer("loss_bwd", as_stream(stream));
+    GSR_HIP(gsr::launch_l1_dssim_bwd(height, width, rendered, gt, lambda_dssim,
+                                     at<float>(const_cast<void*>(ws), parts), grad_loss,
+                                     d_rendered, as_stream(stream)),
+            "l1_dssim_backward");
+    return GSR_OK;
+}
+
+int gsr_ssim(int height, int width, const float* a, const float* b, void* ws, size_t ws_bytes,
+             float* out, void* stream) {
+    if (int rc = check_loss_args(height, width, a, b, ws, ws_bytes)) return rc;
+    GSR_REQUIRE(out, "null pointer");
+    GSR_HIP(gsr::launch_l1_dssim_fwd(height, width, a, b, 1.0f, nullptr, ws, out,
+                                     as_stream(stream)),
+            "ssim");
+    return GSR_OK;
+}
+
 void gsr_profile_enable(int on) {
     ProfState& P = prof();
     std::lock_guard<std::mutex> lk(P.mu);

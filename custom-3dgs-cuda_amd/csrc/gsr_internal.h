@@ -269,4 +269,18 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const GradSt
 hipError_t launch_pair_grad_reduce(int n, const void* recs, const GradSlots& gs, float* dmean,
                                    float* dcov, float* dcol, float* dalpha, hipStream_t st);
 
+// ---- training loss (gsr_loss.hip) ----
+// Work-group partial sums of the loss's forward kernel for an H x W image
+// (float2 each).
+size_t loss_partial_count(int H, int W);
+// (1 - lambda) mean|gt - img| + lambda (1 - SSIM): out[0] = loss, out[1] =
+// SSIM, out[2] = the L1 mean (device floats); gmaps (3 planes of H W 3 floats,
+// or null) receives the SSIM index's derivatives for the backward.
+hipError_t launch_l1_dssim_fwd(int H, int W, const float* img, const float* gt, float lambda,
+                               float* gmaps, void* partial, float* out, hipStream_t st);
+// dL/dimg, scaled by *grad_loss (a device float; null reads as 1).
+hipError_t launch_l1_dssim_bwd(int H, int W, const float* img, const float* gt, float lambda,
+                               const float* gmaps, const float* grad_loss, float* dimg,
+                               hipStream_t st);
+
 }  // namespace gsr

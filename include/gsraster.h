@@ -216,12 +216,36 @@ int gsr_project_sh_backward(int n, const float* d_mean2d, const float* d_cov2d,
                             float* d_albedo, float* d_k_j, const float* d_opacity,
                             const float* opacity, float* d_alpha_logits, void* stream);
 
+/* Replaces the trainer's loss, calculate_loss (gaussian_splatting/utils/
+ * loss.py:12-33): (1 - lambda_dssim) mean|gt - rendered| + lambda_dssim
+ * (1 - SSIM(clamp(rendered, 0, 1), clamp(gt, 0, 1))), with torchmetrics'
+ * SSIM (loss.py:2, the reference's torchmetrics >= 1.0: 11 x 11 Gaussian
+ * window, sigma 1.5, K1 0.01, K2 0.03, data range 1, the windows that lie
+ * inside the image).  rendered and gt are [H,W,3] fp32, H and W >= 11 (the
+ * window).  gsr_l1_dssim writes out[0] = loss, out[1] = SSIM, out[2] = the L1
+ * mean (device floats) and keeps in ws what gsr_l1_dssim_backward needs;
+ * the backward writes d_rendered [H,W,3] = *grad_loss * dloss/drendered
+ * (grad_loss a device float, NULL for 1), zero through the clamp outside
+ * [0, 1] as torch's clamp backward.  ws (gsr_loss_workspace_bytes: 36 B per
+ * pixel) must stay untouched between the two calls.  gsr_ssim gives the SSIM
+ * alone (out[0] = 1 - SSIM, out[1] = SSIM, out[2] = mean|a - b|; the
+ * reference's scripts/eval.py:60). */
+size_t gsr_loss_workspace_bytes(int height, int width);
+int gsr_l1_dssim(int height, int width, const float* rendered, const float* gt,
+                 float lambda_dssim, void* ws, size_t ws_bytes, float* out, void* stream);
+int gsr_l1_dssim_backward(int height, int width, const float* rendered, const float* gt,
+                          float lambda_dssim, const void* ws, size_t ws_bytes,
+                          const float* grad_loss, float* d_rendered, void* stream);
+int gsr_ssim(int height, int width, const float* a, const float* b, void* ws, size_t ws_bytes,
+             float* out, void* stream);
+
 /* Stage timing (no counterpart in the reference; for benchmarks).  While
  * enabled, each entry point records a pair of HIP events on its stream around
  * its stage's kernels: "project", "sh", "project_sh", "bin_count",
  * "depth_sort", "scan", "records", "tile_binning", "tile_sort", "ranges",
  * "fwd_schedule", "blend_fwd", "bwd_records", "bwd_slots", "bwd_schedule",
- * "blend_bwd", "grad_reduce", "sh_bwd", "project_bwd", "project_sh_bwd".
+ * "blend_bwd", "grad_reduce", "sh_bwd", "project_bwd", "project_sh_bwd",
+ * "loss", "loss_bwd".
  * gsr_profile_collect waits for the recorded events
  * and adds their durations to per-stage totals read by gsr_profile_get;
  * gsr_profile_stage(i) names the i-th stage with a total (NULL past the end). */
