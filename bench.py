@@ -73,6 +73,9 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
         # maps out (fwd); maps and images in, dL/dimage out (bwd)
         "loss": 60 * P,
         "loss_bwd": 72 * P,
+        # the fused optimizer step over the 59 fp32 parameters of a Gaussian:
+        # parameter, gradient and both moments in, parameter and moments out
+        "adam": 28 * 59 * N,
     }.get(stage)
 
 
@@ -225,7 +228,18 @@ def per_gaussian_stages(sc, calls: int = 20) -> dict:
     dal = torch.randn(n, 1, generator=gen).to(mu.device)
     cam = (-(R.T @ T)).contiguous()
 
+    # the optimizer step over the cloud's six parameter tensors (values are
+    # arbitrary: the kernel's work does not depend on them)
+    params = [x.clone() for x in (mu, q, s, logits, A, kj)]
+    grads = [torch.randn_like(x) for x in params]
+    moms = [torch.zeros_like(x) for x in params]
+    vars_ = [torch.zeros_like(x) for x in params]
+    lrs = [1.6e-4, 1e-3, 5e-3, 5e-2, 2.5e-3, 6.25e-4]
+    inf = float("inf")
+
     def one_round():
+        crc.adam_step(params, grads, moms, vars_, lrs, [1] * 6, [-inf] * 6, [inf] * 6, 0.9,
+                      0.999, 1e-15)
         crc.project(n, mu, q, s, R, T, fx, fy, cx, cy)
         crc.SH(n, cam, mu, A, kj)
         out = crc.project_sh(n, mu, q, s, R, T, fx, fy, cx, cy, A, kj, logits)
@@ -246,6 +260,53 @@ def per_gaussian_stages(sc, calls: int = 20) -> dict:
         crc.profile_enable(False)
         stages = crc.profile_collect()
     return _stage_rates(stages, n, 0, v["width"], v["height"])
+
+
+def train_steps(sc, steps: int, warmup: int = 3) -> dict:
+    """The reference trainer's step (scripts/train.py:148-178) on scene ``sc``:
+    rasterize, the L1 + D-SSIM loss against a fixed target image, backward,
+    the fused Adam step with the opacity and log-scale clamps; ms per step and
+    the per-stage breakdown."""
+    import torch
+    import custom_rasterizer_cuda as crc
+    from gaussian_splatting.rasterizer.rasterize import rasterize
+    from gaussian_splatting.utils.loss import calculate_loss
+    from gaussian_splatting.utils.optim import setup_optimizer, set_trainer_clamps
+
+    g, v = sc.gaussians, sc.view
+    H, W = int(v["height"]), int(v["width"])
+    gen = torch.Generator(device="cpu").manual_seed(11)
+    target = torch.rand(H, W, 3, generator=gen).to(g.mu.device)
+    lrs = {"mu": 1.6e-4, "q": 1e-3, "s": 5e-3, "alpha": 5e-2, "A": 2.5e-3, "k_j": 6.25e-4}
+    opt = setup_optimizer(g, lrs)
+    set_trainer_clamps(opt, scene_extent=5.0)
+
+    def step():
+        opt.zero_grad(set_to_none=True)
+        loss = calculate_loss(target, rasterize(g, v))
+        loss.backward()
+        opt.step()
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        step()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / steps
+    crc.profile_reset()
+    crc.profile_enable(True)
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    crc.profile_enable(False)
+    stages = crc.profile_collect()
+    M = pair_count(sc)
+    return {"ms_per_step": round(ms, 4), "steps_per_s": round(1000.0 / ms, 1), "pairs": M,
+            "stages": _stage_rates(stages, sc.n, M, W, H)}
 
 
 def config_grad(sc):
@@ -519,6 +580,9 @@ def main() -> int:
                             "pairs": pair_count(scene),
                             "loss": "image.sum()" if grad is None else "dL/dimage N(0,1)"}
         out["extra"] = extra
+        # the trainer's whole step on the 1080p bench scene
+        out["train_step_bench_100k_1920x1080"] = train_steps(
+            synthetic.bench_scene(n=N, width=1920, height=1080, device=dev), max(10, args.steps // 2))
     if not args.no_scale:
         # the HBM-bound stages where they move hundreds of MB: the per-Gaussian
         # kernels on config c5's 5M-Gaussian cloud, the depth sort and the

@@ -10,6 +10,7 @@
 #include <ATen/hip/impl/HIPStreamMasqueradingAsCUDA.h>
 
 #include <tuple>
+#include <vector>
 
 #include "../../include/gsraster.h"
 
@@ -548,6 +549,40 @@ Tensor ssim(const Tensor a, const Tensor b) {
     return out;
 }
 
+// ---- the trainer's optimizer step (utils/optim.py:12-31, train.py:171-176) ----
+void adam_step(const std::vector<Tensor>& params, const std::vector<Tensor>& grads,
+               const std::vector<Tensor>& exp_avgs, const std::vector<Tensor>& exp_avg_sqs,
+               const std::vector<double>& lrs, const std::vector<int64_t>& steps,
+               const std::vector<double>& clamp_min, const std::vector<double>& clamp_max,
+               double beta1, double beta2, double eps) {
+    const size_t n = params.size();
+    TORCH_CHECK(grads.size() == n && exp_avgs.size() == n && exp_avg_sqs.size() == n &&
+                    lrs.size() == n && steps.size() == n && clamp_min.size() == n &&
+                    clamp_max.size() == n,
+                "adam_step: one gradient, state pair, lr, step and clamp pair per parameter");
+    if (n == 0) return;
+    std::vector<gsr_adam_tensor> t(n);
+    for (size_t i = 0; i < n; ++i) {
+        const Tensor& p = params[i];
+        CHECK_INPUT_FP32(p);
+        CHECK_INPUT_FP32(grads[i]);
+        CHECK_INPUT_FP32(exp_avgs[i]);
+        CHECK_INPUT_FP32(exp_avg_sqs[i]);
+        TORCH_CHECK(grads[i].numel() == p.numel() && exp_avgs[i].numel() == p.numel() &&
+                        exp_avg_sqs[i].numel() == p.numel(),
+                    "adam_step: gradient and state must match the parameter's size");
+        TORCH_CHECK(grads[i].device() == p.device() && exp_avgs[i].device() == p.device() &&
+                        exp_avg_sqs[i].device() == p.device() &&
+                        p.device() == params[0].device(),
+                    "adam_step: all tensors must be on one device");
+        t[i] = gsr_adam_tensor{fp(p),         cfp(grads[i]), fp(exp_avgs[i]), fp(exp_avg_sqs[i]),
+                               p.numel(),     lrs[i],        steps[i],        (float)clamp_min[i],
+                               (float)clamp_max[i]};
+    }
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(params[0].device());
+    check_rc(gsr_adam_step((int)n, t.data(), beta1, beta2, eps, current_stream()), "adam_step");
+}
+
 }  // namespace
 
 PYBIND11_MODULE(custom_rasterizer_cuda, m) {
@@ -589,6 +624,11 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
           py::arg("rendered"), py::arg("gt"), py::arg("lambda_dssim"), py::arg("ws"),
           py::arg("grad_loss") = py::none());
     m.def("ssim", &ssim, "SSIM of two (H, W, 3) images: tensor [1 - SSIM, SSIM, L1]");
+    m.def("adam_step", &adam_step,
+          "fused Adam step (torch.optim.Adam arithmetic) with per-tensor clamps, in place",
+          py::arg("params"), py::arg("grads"), py::arg("exp_avgs"), py::arg("exp_avg_sqs"),
+          py::arg("lrs"), py::arg("steps"), py::arg("clamp_min"), py::arg("clamp_max"),
+          py::arg("beta1"), py::arg("beta2"), py::arg("eps"));
     // Stage timing of libgsraster (HIP events on the launch stream); not part of
     // the reference surface.
     m.def("profile_enable", [](bool on) { gsr_profile_enable(on ? 1 : 0); });

@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -935,6 +936,36 @@ int gsr_ssim(int height, int width, const float* a, const float* b, void* ws, si
     GSR_HIP(gsr::launch_l1_dssim_fwd(height, width, a, b, 1.0f, nullptr, ws, out,
                                      as_stream(stream)),
             "ssim");
+    return GSR_OK;
+}
+
+int gsr_adam_step(int count, const gsr_adam_tensor* tensors, double beta1, double beta2,
+                  double eps, void* stream) {
+    GSR_REQUIRE(count >= 0, "count must be non-negative");
+    if (count == 0) return GSR_OK;
+    GSR_REQUIRE(tensors, "null pointer");
+    GSR_REQUIRE(beta1 >= 0.0 && beta1 < 1.0 && beta2 >= 0.0 && beta2 < 1.0,
+                "betas must lie in [0, 1)");
+    std::vector<gsr::AdamTensor> t((size_t)count);
+    std::vector<gsr::AdamHostScalars> h((size_t)count);
+    for (int i = 0; i < count; ++i) {
+        const gsr_adam_tensor& a = tensors[i];
+        GSR_REQUIRE(a.numel >= 0, "numel must be non-negative");
+        GSR_REQUIRE(a.numel == 0 || (a.param && a.grad && a.exp_avg && a.exp_avg_sq),
+                    "null pointer");
+        GSR_REQUIRE(a.step >= 1, "step must be at least 1");
+        t[(size_t)i] = gsr::AdamTensor{a.param, a.grad, a.exp_avg, a.exp_avg_sq,
+                                       (uint64_t)a.numel};
+        // torch forms these in Python floats (double) and rounds each to fp32
+        const double bc1 = 1.0 - std::pow(beta1, (double)a.step);
+        const double bc2 = 1.0 - std::pow(beta2, (double)a.step);
+        h[(size_t)i] = gsr::AdamHostScalars{(float)(1.0 - beta1),     (float)beta2,
+                                            (float)(1.0 - beta2),     (float)std::sqrt(bc2),
+                                            (float)(-(a.lr / bc1)),   (float)eps,
+                                            a.clamp_min,              a.clamp_max};
+    }
+    StageTimer timer("adam", as_stream(stream));
+    GSR_HIP(gsr::launch_adam(count, t.data(), h.data(), as_stream(stream)), "adam_step");
     return GSR_OK;
 }
 

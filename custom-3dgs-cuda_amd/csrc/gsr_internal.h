@@ -283,4 +283,21 @@ hipError_t launch_l1_dssim_bwd(int H, int W, const float* img, const float* gt, 
                                const float* gmaps, const float* grad_loss, float* dimg,
                                hipStream_t st);
 
+// ---- optimizer step (gsr_optim.hip) ----
+constexpr int kAdamMaxTensors = 8;  // tensors per launch
+struct AdamTensor {
+    float* param;
+    const float* grad;
+    float* exp_avg;
+    float* exp_avg_sq;
+    uint64_t numel;
+};
+// A tensor's fp32 scalars, each rounded once from the host's double: 1 - b1,
+// b2, 1 - b2, sqrt(1 - b2^t), -lr / (1 - b1^t), eps, and the clamp bounds.
+struct AdamHostScalars {
+    float w1, b2, w2, bc2s, neg_step, eps, lo, hi;
+};
+hipError_t launch_adam(int count, const AdamTensor* tensors, const AdamHostScalars* hs,
+                       hipStream_t st);
+
 }  // namespace gsr

@@ -1,0 +1,139 @@
+// gsr_optim.hip — the trainer's optimizer step: Adam over the six parameter
+// groups (gaussian_splatting/utils/optim.py:12-31 of kmurungi/custom-3dgs-cuda:
+// torch.optim.Adam, eps 1e-15, default betas) with the trainer's clamps of the
+// updated parameters fused in (scripts/train.py:171-176: opacity logits;
+// utils/adc.py:90-93: log-scales).  One launch covers up to kAdamMaxTensors
+// tensors; each work-group takes a 4096-element chunk of one of them and
+// streams parameter, gradient and both moments through registers in 16-byte
+// loads: 16 B in and 12 B out per element, nothing else.
+//
+// Arithmetic per element, fp32, in torch's order (torch/optim/adam.py,
+// _single_tensor_adam), every scalar rounded to fp32 once from the host's
+// double as torch does with a Python scalar:
+//   m = fma(1 - b1, g - m, m)             (lerp_)
+//   v = fma((1 - b2) g, g, v b2)          (mul_ then addcmul_)
+//   p = p + (-step_size m) / (sqrt(v) / sqrt(bc2) + eps)   (addcdiv_)
+//   p = clamp(p, lo, hi), NaN kept        (clamp_)
+// with correctly rounded sqrt (sqrt_rn below) and division (__fdiv_rn: the
+// div_scale / div_fmas / div_fixup sequence) and no other contraction (the
+// library is built with -ffp-contract=off).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "gsr_internal.h"
+
+namespace gsr {
+
+namespace {
+
+constexpr int kAdamThreads = 256;
+constexpr int kAdamVec = 4;  // float4 per load
+constexpr int kAdamChunk = kAdamThreads * kAdamVec * 4;  // elements per work-group
+
+struct AdamScalars {
+    float w1, b2, w2, bc2s, neg_step, eps, lo, hi;
+};
+
+// sqrt rounded to nearest, as the CPU's: the hardware square root (within
+// 1 ulp; inputs below 2^-96 scaled by 2^32 first, the result by 2^-16), then
+// a step to the neighbour on the side the exact residual x - s' s points to
+// (the residual of a neighbour s' against s, one fused multiply-add each).
+// Zero, infinity and NaN pass unchanged (their residuals are NaN or zero).
+__device__ __forceinline__ float sqrt_rn(float x) {
+    const bool small = x < 0x1p-96f;
+    const float xs = small ? x * 0x1p+32f : x;
+    float s = __builtin_amdgcn_sqrtf(xs);
+    const float down = __int_as_float(__float_as_int(s) - 1);
+    const float up = __int_as_float(__float_as_int(s) + 1);
+    const float rd = __builtin_fmaf(-down, s, xs);
+    const float ru = __builtin_fmaf(-up, s, xs);
+    s = (rd <= 0.0f) ? down : s;
+    s = (ru > 0.0f) ? up : s;
+    return small ? s * 0x1p-16f : s;
+}
+
+__device__ __forceinline__ void adam_update(float& p, float g, float& m, float& v,
+                                            const AdamScalars& s) {
+    m = __builtin_fmaf(s.w1, g - m, m);
+    v = __builtin_fmaf(s.w2 * g, g, v * s.b2);
+    const float d = __fdiv_rn(sqrt_rn(v), s.bc2s) + s.eps;
+    float q = __fdiv_rn(s.neg_step * m, d);
+    float x = p + q;
+    x = (x < s.lo) ? s.lo : x;
+    x = (x > s.hi) ? s.hi : x;
+    p = x;
+}
+
+struct AdamBatch {
+    AdamTensor t[kAdamMaxTensors];
+    AdamScalars s[kAdamMaxTensors];
+    uint32_t chunk0[kAdamMaxTensors + 1];
+    int count;
+};
+
+__global__ __launch_bounds__(kAdamThreads) void adam_kernel(AdamBatch b) {
+    // the tensor of this work-group's chunk (uniform: a scalar loop)
+    int i = 0;
+    while (i + 1 < b.count && blockIdx.x >= b.chunk0[i + 1]) ++i;
+    const AdamTensor t = b.t[i];
+    const AdamScalars s = b.s[i];
+    const uint64_t base = (uint64_t)(blockIdx.x - b.chunk0[i]) * kAdamChunk;
+    const uint64_t n = t.numel;
+    const bool vec = ((reinterpret_cast<uintptr_t>(t.param) | reinterpret_cast<uintptr_t>(t.grad) |
+                       reinterpret_cast<uintptr_t>(t.exp_avg) |
+                       reinterpret_cast<uintptr_t>(t.exp_avg_sq)) & 15) == 0;
+#pragma unroll
+    for (int k = 0; k < kAdamChunk / (kAdamThreads * kAdamVec); ++k) {
+        const uint64_t e = base + ((uint64_t)k * kAdamThreads + threadIdx.x) * kAdamVec;
+        if (vec && e + kAdamVec <= n) {
+            float4 p = *reinterpret_cast<const float4*>(t.param + e);
+            const float4 g = *reinterpret_cast<const float4*>(t.grad + e);
+            float4 m = *reinterpret_cast<const float4*>(t.exp_avg + e);
+            float4 v = *reinterpret_cast<const float4*>(t.exp_avg_sq + e);
+            adam_update(p.x, g.x, m.x, v.x, s);
+            adam_update(p.y, g.y, m.y, v.y, s);
+            adam_update(p.z, g.z, m.z, v.z, s);
+            adam_update(p.w, g.w, m.w, v.w, s);
+            *reinterpret_cast<float4*>(t.param + e) = p;
+            *reinterpret_cast<float4*>(t.exp_avg + e) = m;
+            *reinterpret_cast<float4*>(t.exp_avg_sq + e) = v;
+        } else {
+            for (uint64_t j = e; j < e + kAdamVec && j < n; ++j) {
+                float p = t.param[j], m = t.exp_avg[j], v = t.exp_avg_sq[j];
+                adam_update(p, t.grad[j], m, v, s);
+                t.param[j] = p;
+                t.exp_avg[j] = m;
+                t.exp_avg_sq[j] = v;
+            }
+        }
+    }
+}
+
+}  // namespace
+
+hipError_t launch_adam(int count, const AdamTensor* tensors, const AdamHostScalars* hs,
+                       hipStream_t st) {
+    for (int first = 0; first < count; first += kAdamMaxTensors) {
+        AdamBatch b{};
+        b.count = std::min(kAdamMaxTensors, count - first);
+        uint64_t chunks = 0;
+        for (int i = 0; i < b.count; ++i) {
+            const AdamTensor& t = tensors[first + i];
+            const AdamHostScalars& h = hs[first + i];
+            b.t[i] = t;
+            b.s[i] = AdamScalars{h.w1, h.b2, h.w2, h.bc2s, h.neg_step, h.eps, h.lo, h.hi};
+            b.chunk0[i] = (uint32_t)chunks;
+            chunks += (t.numel + kAdamChunk - 1) / kAdamChunk;
+        }
+        b.chunk0[b.count] = (uint32_t)chunks;
+        if (chunks == 0) continue;
+        if (chunks > 0x7fffffffull) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(adam_kernel, dim3((unsigned)chunks), dim3(kAdamThreads), 0, st, b);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+}  // namespace gsr

@@ -239,13 +239,38 @@ int gsr_l1_dssim_backward(int height, int width, const float* rendered, const fl
 int gsr_ssim(int height, int width, const float* a, const float* b, void* ws, size_t ws_bytes,
              float* out, void* stream);
 
+/* Replaces the trainer's optimizer step and its clamps: torch.optim.Adam
+ * (gaussian_splatting/utils/optim.py:12-31: six parameter groups, eps 1e-15,
+ * default betas) followed by the clamps of the updated parameters
+ * (scripts/train.py:171-176, opacity logits; utils/adc.py:90-93,
+ * log-scales), in one pass per element: 16 B read and 12 B written.  Each
+ * tensor is fp32 and contiguous on the device; exp_avg / exp_avg_sq are its
+ * Adam moments (updated in place), `step` the step number after this update
+ * (1 for the first), lr its group's learning rate; clamp_min / clamp_max bound
+ * the updated parameter (-INFINITY / INFINITY for none; NaN stays NaN).
+ * The arithmetic is torch's single-tensor Adam's for fp32 tensors: the moments
+ * come out bit for bit, the parameter within a few ulps of its operands. */
+typedef struct gsr_adam_tensor {
+    float* param;
+    const float* grad;
+    float* exp_avg;
+    float* exp_avg_sq;
+    int64_t numel;
+    double lr;
+    int64_t step;
+    float clamp_min;
+    float clamp_max;
+} gsr_adam_tensor;
+int gsr_adam_step(int count, const gsr_adam_tensor* tensors, double beta1, double beta2,
+                  double eps, void* stream);
+
 /* Stage timing (no counterpart in the reference; for benchmarks).  While
  * enabled, each entry point records a pair of HIP events on its stream around
  * its stage's kernels: "project", "sh", "project_sh", "bin_count",
  * "depth_sort", "scan", "records", "tile_binning", "tile_sort", "ranges",
  * "fwd_schedule", "blend_fwd", "bwd_records", "bwd_slots", "bwd_schedule",
  * "blend_bwd", "grad_reduce", "sh_bwd", "project_bwd", "project_sh_bwd",
- * "loss", "loss_bwd".
+ * "loss", "loss_bwd", "adam".
  * gsr_profile_collect waits for the recorded events
  * and adds their durations to per-stage totals read by gsr_profile_get;
  * gsr_profile_stage(i) names the i-th stage with a total (NULL past the end). */

@@ -834,3 +834,40 @@ ORC_EXPORT void orc_project_bwd_f64(int n, const double* dmean, const double* dc
     proj_bwd_all<double>(n, dmean, dcov, mu, q, s, rot, tr, fx, fy, cx, cy, dmu, dq, ds,
                          ref_quat);
 }
+
+// ---- the trainer's optimizer step: torch.optim.Adam (the reference's
+// utils/optim.py:12-31, eps 1e-15, default betas), as torch's single-tensor
+// path evaluates it for an fp32 tensor (torch/optim/adam.py,
+// _single_tensor_adam), followed by the trainer's clamps of the updated
+// parameter (scripts/train.py:171-176, utils/adc.py:90-93):
+//   m = fma(1 - b1, g - m, m)                 exp_avg.lerp_(grad, 1 - b1)
+//   v = fma((1 - b2) g, g, v b2)              exp_avg_sq.mul_(b2).addcmul_(grad, grad, 1 - b2)
+//   d = sqrt(v) / sqrt(1 - b2^t) + eps        (exp_avg_sq.sqrt() / bc2_sqrt).add_(eps)
+//   p = p + (-(lr / (1 - b1^t)) m) / d        param.addcdiv_(exp_avg, denom, -step_size)
+//   p = min(max(p, lo), hi), NaN kept         param.clamp_(lo, hi)
+// The scalars are formed in double (Python floats) and rounded to fp32 once,
+// as torch does when it applies a Python scalar to an fp32 tensor; the fused
+// multiply-adds are the ones torch's CPU lerp and addcmul kernels form.
+ORC_EXPORT void orc_adam_step_f32(int64_t n, float* p, const float* g, float* m, float* v,
+                                  double lr, double beta1, double beta2, double eps, int64_t step,
+                                  float lo, float hi) {
+    const float w1 = (float)(1.0 - beta1), b2 = (float)beta2, w2 = (float)(1.0 - beta2);
+    const double bc1 = 1.0 - std::pow(beta1, (double)step);
+    const double bc2 = 1.0 - std::pow(beta2, (double)step);
+    const float neg_step = (float)(-(lr / bc1));
+    const float bc2s = (float)std::sqrt(bc2);
+    const float e = (float)eps;
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) {
+        const float gi = g[i];
+        const float mi = std::fma(w1, gi - m[i], m[i]);
+        const float vi = std::fma(w2 * gi, gi, v[i] * b2);
+        const float d = std::sqrt(vi) / bc2s + e;
+        float pi = p[i] + (neg_step * mi) / d;
+        pi = (pi < lo) ? lo : pi;
+        pi = (pi > hi) ? hi : pi;
+        m[i] = mi;
+        v[i] = vi;
+        p[i] = pi;
+    }
+}
