@@ -76,6 +76,8 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
         # the fused optimizer step over the 59 fp32 parameters of a Gaussian:
         # parameter, gradient and both moments in, parameter and moments out
         "adam": 28 * 59 * N,
+        # the PLY export's records: 59 parameters in, 62-float records out
+        "ply_pack": 236 * N + 248 * N,
     }.get(stage)
 
 
@@ -240,6 +242,7 @@ def per_gaussian_stages(sc, calls: int = 20) -> dict:
     def one_round():
         crc.adam_step(params, grads, moms, vars_, lrs, [1] * 6, [-inf] * 6, [inf] * 6, 0.9,
                       0.999, 1e-15)
+        crc.ply_records(mu, q, s, logits, A, kj, False)
         crc.project(n, mu, q, s, R, T, fx, fy, cx, cy)
         crc.SH(n, cam, mu, A, kj)
         out = crc.project_sh(n, mu, q, s, R, T, fx, fy, cx, cy, A, kj, logits)

@@ -583,6 +583,33 @@ void adam_step(const std::vector<Tensor>& params, const std::vector<Tensor>& gra
     check_rc(gsr_adam_step((int)n, t.data(), beta1, beta2, eps, current_stream()), "adam_step");
 }
 
+// ---- the PLY export's vertex records (scripts/run.py:66-165) ----
+Tensor ply_records(const Tensor mu, const Tensor q, const Tensor s, const Tensor alpha,
+                   const Tensor albedo, const Tensor k_j, bool opacity_from_probability) {
+    CHECK_INPUT_FP32(mu);
+    CHECK_INPUT_FP32(q);
+    CHECK_INPUT_FP32(s);
+    CHECK_INPUT_FP32(alpha);
+    CHECK_INPUT_FP32(albedo);
+    CHECK_INPUT_FP32(k_j);
+    const int64_t n = mu.size(0);
+    TORCH_CHECK(k_j.dim() == 3 && k_j.size(0) == n && k_j.size(2) == 3,
+                "Expected k_j shape (N, K, 3), got ", k_j.sizes());
+    const int64_t K = k_j.size(1);
+    check_numel(mu, 3 * n, "mu must hold N x 3 values");
+    check_numel(q, 4 * n, "q must hold N x 4 values");
+    check_numel(s, 3 * n, "s must hold N x 3 values");
+    check_numel(alpha, n, "alpha must hold N values");
+    check_numel(albedo, 3 * n, "albedo must hold N x 3 values");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(mu.device());
+    Tensor out = torch::empty({n, 17 + 3 * K}, mu.options());
+    const Tensor q_al = aligned16(q);
+    check_rc(gsr_ply_pack((int)n, (int)K, cfp(mu), cfp(q_al), cfp(s), cfp(alpha), cfp(albedo),
+                          cfp(k_j), opacity_from_probability ? 1 : 0, fp(out), current_stream()),
+             "ply_records");
+    return out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(custom_rasterizer_cuda, m) {
@@ -624,6 +651,8 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
           py::arg("rendered"), py::arg("gt"), py::arg("lambda_dssim"), py::arg("ws"),
           py::arg("grad_loss") = py::none());
     m.def("ssim", &ssim, "SSIM of two (H, W, 3) images: tensor [1 - SSIM, SSIM, L1]");
+    m.def("ply_records", &ply_records,
+          "Inria 3DGS PLY vertex records [N, 17 + 3K] of a Gaussian cloud (run.py:66-165)");
     m.def("adam_step", &adam_step,
           "fused Adam step (torch.optim.Adam arithmetic) with per-tensor clamps, in place",
           py::arg("params"), py::arg("grads"), py::arg("exp_avgs"), py::arg("exp_avg_sqs"),

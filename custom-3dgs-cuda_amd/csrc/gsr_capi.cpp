@@ -969,6 +969,21 @@ int gsr_adam_step(int count, const gsr_adam_tensor* tensors, double beta1, doubl
     return GSR_OK;
 }
 
+int gsr_ply_pack(int n, int rest_coeffs, const float* mu, const float* q, const float* s,
+                 const float* alpha, const float* albedo, const float* k_j,
+                 int opacity_from_probability, float* records, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    GSR_REQUIRE(rest_coeffs >= 1 && rest_coeffs <= 63, "rest_coeffs must lie in [1, 63]");
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(mu && q && s && alpha && albedo && k_j && records, "null pointer");
+    GSR_REQUIRE(((uintptr_t)q & 15) == 0, "q must be 16-byte aligned");
+    StageTimer timer("ply_pack", as_stream(stream));
+    GSR_HIP(gsr::launch_ply_pack(n, rest_coeffs, mu, q, s, alpha, albedo, k_j,
+                                 opacity_from_probability ? 1 : 0, records, as_stream(stream)),
+            "ply_pack");
+    return GSR_OK;
+}
+
 void gsr_profile_enable(int on) {
     ProfState& P = prof();
     std::lock_guard<std::mutex> lk(P.mu);

@@ -74,6 +74,24 @@ __device__ __forceinline__ int f2i_sat(float x) {
     return (int)x;
 }
 
+// sqrt rounded to nearest, as the CPU's: the hardware square root (within
+// 1 ulp; inputs below 2^-96 scaled by 2^32 first, the result by 2^-16), then
+// a step to the neighbour on the side the exact residual x - s' s points to
+// (the residual of a neighbour s' against s, one fused multiply-add each).
+// Zero, infinity and NaN pass unchanged (their residuals are NaN or zero).
+__device__ __forceinline__ float sqrt_rn(float x) {
+    const bool small = x < 0x1p-96f;
+    const float xs = small ? x * 0x1p+32f : x;
+    float s = __builtin_amdgcn_sqrtf(xs);
+    const float down = __int_as_float(__float_as_int(s) - 1);
+    const float up = __int_as_float(__float_as_int(s) + 1);
+    const float rd = __builtin_fmaf(-down, s, xs);
+    const float ru = __builtin_fmaf(-up, s, xs);
+    s = (rd <= 0.0f) ? down : s;
+    s = (ru > 0.0f) ? up : s;
+    return small ? s * 0x1p-16f : s;
+}
+
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
 __device__ __forceinline__ uint64_t ballot(bool p) { return __builtin_amdgcn_ballot_w64(p); }

@@ -300,4 +300,11 @@ struct AdamHostScalars {
 hipError_t launch_adam(int count, const AdamTensor* tensors, const AdamHostScalars* hs,
                        hipStream_t st);
 
+// ---- PLY export (gsr_export.hip) ----
+// Inria 3DGS vertex records [n, 17 + 3K] of n Gaussians with K rest SH
+// coefficients per channel (q 16-byte aligned).
+hipError_t launch_ply_pack(int n, int K, const float* mu, const float* q, const float* s,
+                           const float* alpha, const float* A, const float* kj,
+                           int from_probability, float* out, hipStream_t st);
+
 }  // namespace gsr

@@ -14,13 +14,14 @@
 //   v = fma((1 - b2) g, g, v b2)          (mul_ then addcmul_)
 //   p = p + (-step_size m) / (sqrt(v) / sqrt(bc2) + eps)   (addcdiv_)
 //   p = clamp(p, lo, hi), NaN kept        (clamp_)
-// with correctly rounded sqrt (sqrt_rn below) and division (__fdiv_rn: the
+// with correctly rounded sqrt (sqrt_rn, gsr_common.h) and division (__fdiv_rn: the
 // div_scale / div_fmas / div_fixup sequence) and no other contraction (the
 // library is built with -ffp-contract=off).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 
+#include "gsr_common.h"
 #include "gsr_internal.h"
 
 namespace gsr {
@@ -34,24 +35,6 @@ constexpr int kAdamChunk = kAdamThreads * kAdamVec * 4;  // elements per work-gr
 struct AdamScalars {
     float w1, b2, w2, bc2s, neg_step, eps, lo, hi;
 };
-
-// sqrt rounded to nearest, as the CPU's: the hardware square root (within
-// 1 ulp; inputs below 2^-96 scaled by 2^32 first, the result by 2^-16), then
-// a step to the neighbour on the side the exact residual x - s' s points to
-// (the residual of a neighbour s' against s, one fused multiply-add each).
-// Zero, infinity and NaN pass unchanged (their residuals are NaN or zero).
-__device__ __forceinline__ float sqrt_rn(float x) {
-    const bool small = x < 0x1p-96f;
-    const float xs = small ? x * 0x1p+32f : x;
-    float s = __builtin_amdgcn_sqrtf(xs);
-    const float down = __int_as_float(__float_as_int(s) - 1);
-    const float up = __int_as_float(__float_as_int(s) + 1);
-    const float rd = __builtin_fmaf(-down, s, xs);
-    const float ru = __builtin_fmaf(-up, s, xs);
-    s = (rd <= 0.0f) ? down : s;
-    s = (ru > 0.0f) ? up : s;
-    return small ? s * 0x1p-16f : s;
-}
 
 __device__ __forceinline__ void adam_update(float& p, float g, float& m, float& v,
                                             const AdamScalars& s) {

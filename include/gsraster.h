@@ -264,13 +264,26 @@ typedef struct gsr_adam_tensor {
 int gsr_adam_step(int count, const gsr_adam_tensor* tensors, double beta1, double beta2,
                   double eps, void* stream);
 
+/* Replaces the record assembly of the reference's PLY export, save_ply
+ * (scripts/run.py:66-165, the official Inria 3DGS point_cloud.ply layout):
+ * records [N, 17 + 3K] fp32 on the device, one per Gaussian: x y z, nx ny nz
+ * (0), f_dc_0..2 (albedo), f_rest_0..3K-1 channel-major (f_rest[c K + k] =
+ * k_j[n][k][c], run.py:98-108), opacity, scale_0..2 (the log-scales), rot_0..3
+ * (q / max(|q|, 1e-8), w x y z).  opacity is the stored logit, or with
+ * opacity_from_probability log(a / (1 - a)) of a clamped to [1e-6, 1 - 1e-6]
+ * (run.py:110-118, a legacy checkpoint holding probabilities).  k_j is
+ * [N,K,3], 1 <= K <= 63; q must be 16-byte aligned. */
+int gsr_ply_pack(int n, int rest_coeffs, const float* mu, const float* q, const float* s,
+                 const float* alpha, const float* albedo, const float* k_j,
+                 int opacity_from_probability, float* records, void* stream);
+
 /* Stage timing (no counterpart in the reference; for benchmarks).  While
  * enabled, each entry point records a pair of HIP events on its stream around
  * its stage's kernels: "project", "sh", "project_sh", "bin_count",
  * "depth_sort", "scan", "records", "tile_binning", "tile_sort", "ranges",
  * "fwd_schedule", "blend_fwd", "bwd_records", "bwd_slots", "bwd_schedule",
  * "blend_bwd", "grad_reduce", "sh_bwd", "project_bwd", "project_sh_bwd",
- * "loss", "loss_bwd", "adam".
+ * "loss", "loss_bwd", "adam", "ply_pack".
  * gsr_profile_collect waits for the recorded events
  * and adds their durations to per-stage totals read by gsr_profile_get;
  * gsr_profile_stage(i) names the i-th stage with a total (NULL past the end). */
