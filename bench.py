@@ -78,6 +78,14 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
         "adam": 28 * 59 * N,
         # the PLY export's records: 59 parameters in, 62-float records out
         "ply_pack": 236 * N + 248 * N,
+        # densification statistics: mean2d gradient and radius in, the three
+        # buffers read and written
+        "adc_stats": 12 * N + 24 * N,
+        # the densify / prune plan: buffers, log-scales and opacity in, flags out
+        "adc_plan": 29 * N,
+        # the gather: every parameter and both moments read and written once
+        # (counted for a pass that keeps each Gaussian once)
+        "adc_apply": 2 * 3 * 236 * N,
     }.get(stage)
 
 
@@ -268,11 +276,13 @@ def per_gaussian_stages(sc, calls: int = 20) -> dict:
 def train_steps(sc, steps: int, warmup: int = 3) -> dict:
     """The reference trainer's step (scripts/train.py:148-178) on scene ``sc``:
     rasterize, the L1 + D-SSIM loss against a fixed target image, backward,
-    the fused Adam step with the opacity and log-scale clamps; ms per step and
-    the per-stage breakdown."""
+    the densification statistics, the fused Adam step with the opacity and
+    log-scale clamps; ms per step and the per-stage breakdown."""
     import torch
     import custom_rasterizer_cuda as crc
     from gaussian_splatting.rasterizer.rasterize import rasterize
+    from gaussian_splatting.rasterizer.rasterize import RasterizeFunction
+    from gaussian_splatting.utils.adc import densification_stats
     from gaussian_splatting.utils.loss import calculate_loss
     from gaussian_splatting.utils.optim import setup_optimizer, set_trainer_clamps
 
@@ -288,6 +298,8 @@ def train_steps(sc, steps: int, warmup: int = 3) -> dict:
         opt.zero_grad(set_to_none=True)
         loss = calculate_loss(target, rasterize(g, v))
         loss.backward()
+        densification_stats(g, RasterizeFunction.last_mean2d_grad, RasterizeFunction.last_radii2d,
+                            width=W, height=H)
         opt.step()
 
     for _ in range(warmup):
@@ -310,6 +322,57 @@ def train_steps(sc, steps: int, warmup: int = 3) -> dict:
     M = pair_count(sc)
     return {"ms_per_step": round(ms, 4), "steps_per_s": round(1000.0 / ms, 1), "pairs": M,
             "stages": _stage_rates(stages, sc.n, M, W, H)}
+
+
+def adc_pass(sc, calls: int = 3) -> dict:
+    """The densify / prune pass (utils/adc.py:316-393) on config ``sc``'s cloud
+    with Adam state, statistics that select about a tenth of the Gaussians
+    for densification: ms per pass and the per-stage breakdown (the cloud is
+    rebuilt from the same inputs each call)."""
+    import torch
+    import custom_rasterizer_cuda as crc
+    from gaussian_splatting.scene.gaussian import gaussian
+    from gaussian_splatting.utils.adc import adaptive_density_control
+    from gaussian_splatting.utils.optim import setup_optimizer
+
+    src = sc.gaussians
+    n = src.mu.shape[0]
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    accum = (torch.rand(n, 1, generator=gen) * 1.1e-4).to(src.mu.device)
+    lrs = {"mu": 1.6e-4, "q": 1e-3, "s": 5e-3, "alpha": 5e-2, "A": 2.5e-3, "k_j": 6.25e-4}
+
+    def fresh():
+        g = gaussian(n)
+        for k in ("mu", "q", "s", "alpha", "A", "k_j"):
+            setattr(g, k, getattr(src, k).detach().clone())
+        opt = setup_optimizer(g, lrs)
+        for p in opt.param_groups:
+            par = p["params"][0]
+            opt.state[par] = {"step": torch.tensor(1.0), "exp_avg": torch.zeros_like(par),
+                              "exp_avg_sq": torch.zeros_like(par)}
+        g.xyz_grad_accum = accum.clone()
+        g.denom = torch.ones_like(accum)
+        g.max_radii2D = torch.zeros(n, device=src.mu.device)
+        return g, opt
+
+    g, opt = fresh()
+    adaptive_density_control(g, opt, scene_extent=5.0, max_screen_size=200.0)
+    times, stats = [], None
+    crc.profile_reset()
+    crc.profile_enable(True)
+    for _ in range(calls):
+        g, opt = fresh()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g, opt, stats = adaptive_density_control(g, opt, scene_extent=5.0, max_screen_size=200.0)
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b))
+    crc.profile_enable(False)
+    stages = crc.profile_collect()
+    return {"ms_per_pass": round(sorted(times)[len(times) // 2], 3), "gaussians": n,
+            "result": stats, "stages": _stage_rates(stages, n, 0, 0, 0)}
 
 
 def config_grad(sc):
@@ -595,6 +658,7 @@ def main() -> int:
         del c5
         c4 = synthetic.config_scene("c4", device=dev)
         scale["c4_1M_1920x1080"] = frame_stages(c4, 5)
+        scale["adc_pass_c4_1M"] = adc_pass(c4)
         scale["c4_1M_1920x1080_tile_sort"] = frame_stages(c4, 5, binning="sort")
         del c4
         out["scale"] = scale

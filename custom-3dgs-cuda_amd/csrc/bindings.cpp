@@ -610,6 +610,140 @@ Tensor ply_records(const Tensor mu, const Tensor q, const Tensor s, const Tensor
     return out;
 }
 
+// ---- adaptive density control (gaussian_splatting/utils/adc.py) ----
+void adc_stats(const c10::optional<Tensor>& mean2d_grad, int width, int height,
+               const c10::optional<Tensor>& radii, const Tensor grad_accum, const Tensor denom,
+               const Tensor max_radii2d) {
+    CHECK_INPUT_FP32(grad_accum);
+    CHECK_INPUT_FP32(denom);
+    CHECK_INPUT_FP32(max_radii2d);
+    const int64_t n = grad_accum.numel();
+    TORCH_CHECK(denom.numel() == n && max_radii2d.numel() == n,
+                "densification buffers must have N elements");
+    const bool g = mean2d_grad.has_value() && mean2d_grad->defined();
+    const bool r = radii.has_value() && radii->defined();
+    if (g) {
+        CHECK_INPUT_FP32(*mean2d_grad);
+        TORCH_CHECK(mean2d_grad->numel() == 2 * n, "mean2d_grad must have shape (N, 2)");
+    }
+    if (r) {
+        CHECK_INPUT_FP32(*radii);
+        TORCH_CHECK(radii->numel() == n, "radii must have N elements");
+    }
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(grad_accum.device());
+    check_rc(gsr_adc_stats((int)n, g ? cfp(*mean2d_grad) : nullptr, width, height,
+                           r ? cfp(*radii) : nullptr, fp(grad_accum), fp(denom), fp(max_radii2d),
+                           current_stream()),
+             "adc_stats");
+}
+
+gsr_adc_config adc_cfg(double grad_threshold, double percent_dense, double scene_extent,
+                       double min_opacity, c10::optional<double> max_screen_size, bool densify,
+                       bool prune, bool reset_opacity) {
+    gsr_adc_config c;
+    c.grad_threshold = grad_threshold;
+    c.percent_dense = percent_dense;
+    c.scene_extent = scene_extent;
+    c.min_opacity = min_opacity;
+    c.has_max_screen_size = max_screen_size.has_value() ? 1 : 0;
+    c.max_screen_size = max_screen_size.value_or(0.0);
+    c.densify = densify ? 1 : 0;
+    c.prune = prune ? 1 : 0;
+    c.reset_opacity = reset_opacity ? 1 : 0;
+    return c;
+}
+
+const int64_t kAdcWidths[6] = {3, 4, 3, 1, 3, 45};
+
+void check_cloud(const std::vector<Tensor>& p, int64_t n) {
+    TORCH_CHECK(p.size() == 6, "the cloud is six tensors: mu, q, s, alpha, A, k_j");
+    for (int a = 0; a < 6; ++a) {
+        CHECK_INPUT_FP32(p[a]);
+        TORCH_CHECK(p[a].numel() == n * kAdcWidths[a], "cloud tensor ", a, " must hold N x ",
+                    kAdcWidths[a], " values");
+    }
+}
+
+// (counts[5], ws): the plan of the densify / prune pass
+std::tuple<std::vector<int64_t>, Tensor> adc_plan(
+    const std::vector<Tensor>& params, const Tensor grad_accum, const Tensor denom,
+    const c10::optional<Tensor>& max_radii2d, double grad_threshold, double percent_dense,
+    double scene_extent, double min_opacity, c10::optional<double> max_screen_size,
+    bool densify, bool prune, bool reset_opacity) {
+    const int64_t n = params.empty() ? 0 : params[0].size(0);
+    check_cloud(params, n);
+    CHECK_INPUT_FP32(grad_accum);
+    CHECK_INPUT_FP32(denom);
+    TORCH_CHECK(grad_accum.numel() == n && denom.numel() == n,
+                "densification buffers must have N elements");
+    const bool r = max_radii2d.has_value() && max_radii2d->defined();
+    if (r) {
+        CHECK_INPUT_FP32(*max_radii2d);
+        TORCH_CHECK(max_radii2d->numel() == n, "max_radii2D must have N elements");
+    }
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(params[0].device());
+    Tensor ws = workspace((int64_t)gsr_adc_workspace_bytes((int)n), params[0]);
+    const gsr_adc_config c = adc_cfg(grad_threshold, percent_dense, scene_extent, min_opacity,
+                                     max_screen_size, densify, prune, reset_opacity);
+    float* pp[6];
+    for (int a = 0; a < 6; ++a) pp[a] = fp(params[a]);
+    std::vector<int64_t> counts(5, 0);
+    check_rc(gsr_adc_plan((int)n, pp, cfp(grad_accum), cfp(denom),
+                          r ? cfp(*max_radii2d) : nullptr, &c, ws.data_ptr(), (size_t)ws.numel(),
+                          counts.data(), current_stream()),
+             "adc_plan");
+    return {counts, ws};
+}
+
+// the new cloud (6 tensors) and its moments (12, undefined where the input's are)
+std::tuple<std::vector<Tensor>, std::vector<c10::optional<Tensor>>> adc_apply(
+    const std::vector<Tensor>& params, const std::vector<c10::optional<Tensor>>& moments,
+    const Tensor noise, const Tensor ws, int64_t n_out, double grad_threshold,
+    double percent_dense, double scene_extent, double min_opacity,
+    c10::optional<double> max_screen_size, bool densify, bool prune, bool reset_opacity) {
+    const int64_t n = params.empty() ? 0 : params[0].size(0);
+    check_cloud(params, n);
+    TORCH_CHECK(moments.size() == 12, "moments: exp_avg of each tensor, then exp_avg_sq");
+    CHECK_INPUT_FP32(noise);
+    TORCH_CHECK(ws.is_cuda() && ws.scalar_type() == torch::kUInt8 &&
+                    ws.numel() >= (int64_t)gsr_adc_workspace_bytes((int)n),
+                "ws must be the plan's");
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(params[0].device());
+    std::vector<Tensor> out(6);
+    std::vector<c10::optional<Tensor>> mout(12);
+    float* pin[6];
+    float* pout[6];
+    float* min_[12];
+    float* mo[12];
+    for (int a = 0; a < 6; ++a) {
+        std::vector<int64_t> shape = params[a].sizes().vec();
+        shape[0] = n_out;
+        out[a] = torch::empty(shape, params[a].options());
+        pin[a] = fp(params[a]);
+        pout[a] = fp(out[a]);
+    }
+    for (int a = 0; a < 12; ++a) {
+        const auto& mt = moments[a];
+        if (mt.has_value() && mt->defined()) {
+            CHECK_INPUT_FP32(*mt);
+            TORCH_CHECK(mt->numel() == n * kAdcWidths[a % 6], "moment ", a, " must match its tensor");
+            min_[a] = fp(*mt);
+            mout[a] = torch::empty(out[a % 6].sizes(), mt->options());
+            mo[a] = fp(*mout[a]);
+        } else {
+            min_[a] = nullptr;
+            mo[a] = nullptr;
+        }
+    }
+    const gsr_adc_config c = adc_cfg(grad_threshold, percent_dense, scene_extent, min_opacity,
+                                     max_screen_size, densify, prune, reset_opacity);
+    if (n_out > 0)  // an empty new cloud has nothing to write
+        check_rc(gsr_adc_apply((int)n, pin, min_, cfp(noise), &c, ws.data_ptr(),
+                               (size_t)ws.numel(), pout, mo, current_stream()),
+                 "adc_apply");
+    return {out, mout};
+}
+
 }  // namespace
 
 PYBIND11_MODULE(custom_rasterizer_cuda, m) {
@@ -653,6 +787,11 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     m.def("ssim", &ssim, "SSIM of two (H, W, 3) images: tensor [1 - SSIM, SSIM, L1]");
     m.def("ply_records", &ply_records,
           "Inria 3DGS PLY vertex records [N, 17 + 3K] of a Gaussian cloud (run.py:66-165)");
+    m.def("adc_stats", &adc_stats, "densification statistics (adc.py:58-87)",
+          py::arg("mean2d_grad"), py::arg("width"), py::arg("height"), py::arg("radii"),
+          py::arg("grad_accum"), py::arg("denom"), py::arg("max_radii2d"));
+    m.def("adc_plan", &adc_plan, "densify / prune plan: (counts[5], workspace)");
+    m.def("adc_apply", &adc_apply, "densify / prune gather: (new cloud, new moments)");
     m.def("adam_step", &adam_step,
           "fused Adam step (torch.optim.Adam arithmetic) with per-tensor clamps, in place",
           py::arg("params"), py::arg("grads"), py::arg("exp_avgs"), py::arg("exp_avg_sqs"),

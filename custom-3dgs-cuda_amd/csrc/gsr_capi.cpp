@@ -984,6 +984,100 @@ int gsr_ply_pack(int n, int rest_coeffs, const float* mu, const float* q, const 
     return GSR_OK;
 }
 
+int gsr_adc_stats(int n, const float* mean2d_grad, int width, int height, const float* radii,
+                  float* grad_accum, float* denom, float* max_radii2d, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(!mean2d_grad || (grad_accum && denom), "null pointer");
+    GSR_REQUIRE(!radii || max_radii2d, "null pointer");
+    const bool scale = width > 0 && height > 0;
+    StageTimer timer("adc_stats", as_stream(stream));
+    // (width / 2.0, height / 2.0) as an fp32 tensor (adc.py:70-71)
+    GSR_HIP(gsr::launch_adc_stats(n, mean2d_grad, (float)(width / 2.0), (float)(height / 2.0),
+                                  scale ? 1 : 0, radii, grad_accum, denom, max_radii2d,
+                                  as_stream(stream)),
+            "adc_stats");
+    return GSR_OK;
+}
+
+size_t gsr_adc_workspace_bytes(int n) { return gsr::adc_workspace_bytes(n > 0 ? n : 0); }
+
+namespace {
+gsr::AdcConfig adc_config(const gsr_adc_config& c) {
+    gsr::AdcConfig a;
+    a.grad_threshold = (float)c.grad_threshold;
+    a.dense_scale = (float)(c.percent_dense * c.scene_extent);
+    a.max_scale = (float)(0.1 * c.scene_extent);
+    a.min_opacity = (float)c.min_opacity;
+    a.max_screen = (float)c.max_screen_size;
+    a.split_scale = (float)1.6;                          // adc.py:217 scale_factor
+    a.reset_logit = (float)std::log(0.01 / (1.0 - 0.01));  // adc.py:297-298
+    a.densify = c.densify ? 1 : 0;
+    a.prune = c.prune ? 1 : 0;
+    a.has_screen = c.has_max_screen_size ? 1 : 0;
+    a.reset_opacity = c.reset_opacity ? 1 : 0;
+    return a;
+}
+}  // namespace
+
+int gsr_adc_plan(int n, float* const params[6], const float* grad_accum, const float* denom,
+                 const float* max_radii2d, const gsr_adc_config* cfg, void* ws, size_t ws_bytes,
+                 int64_t counts[5], void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    GSR_REQUIRE(cfg && counts, "null pointer");
+    for (int k = 0; k < 5; ++k) counts[k] = 0;
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(params && grad_accum && denom, "null pointer");
+    for (int a = 0; a < 6; ++a) GSR_REQUIRE(params[a], "null parameter array");
+    if (!ws || ws_bytes < gsr::adc_workspace_bytes(n))
+        return fail(GSR_ERR_WORKSPACE, "adc workspace too small");
+    gsr::AdcCloud in;
+    for (int a = 0; a < 6; ++a) in.p[a] = params[a];
+    hipStream_t st = as_stream(stream);
+    uint64_t* totals = static_cast<uint64_t*>(ws);
+    {
+        StageTimer timer("adc_plan", st);
+        GSR_HIP(gsr::launch_adc_plan(n, in, grad_accum, denom, max_radii2d, adc_config(*cfg), ws,
+                                     totals, st),
+                "adc_plan");
+    }
+    uint64_t host[5];
+    GSR_HIP(hipMemcpyAsync(host, totals, sizeof(host), hipMemcpyDeviceToHost, st), "adc_plan: read");
+    GSR_HIP(hipStreamSynchronize(st), "adc_plan: synchronize");
+    for (int k = 0; k < 5; ++k) counts[k] = (int64_t)host[k];
+    return GSR_OK;
+}
+
+int gsr_adc_apply(int n, float* const params[6], float* const moments[12],
+                  const float* split_noise, const gsr_adc_config* cfg, const void* ws,
+                  size_t ws_bytes, float* const out_params[6], float* const out_moments[12],
+                  void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(params && out_params && cfg, "null pointer");
+    GSR_REQUIRE(split_noise || !cfg->densify,
+                "split_noise must not be null when densifying (2 counts[3] rows of 3 floats)");
+    for (int a = 0; a < 6; ++a) GSR_REQUIRE(params[a] && out_params[a], "null parameter array");
+    if (!ws || ws_bytes < gsr::adc_workspace_bytes(n))
+        return fail(GSR_ERR_WORKSPACE, "adc workspace too small");
+    gsr::AdcCloud in, out;
+    gsr::AdcMoments min_{}, mout{};
+    for (int a = 0; a < 6; ++a) {
+        in.p[a] = params[a];
+        out.p[a] = out_params[a];
+    }
+    for (int a = 0; a < 12; ++a) {
+        min_.p[a] = moments ? moments[a] : nullptr;
+        mout.p[a] = out_moments ? out_moments[a] : nullptr;
+    }
+    StageTimer timer("adc_apply", as_stream(stream));
+    GSR_HIP(gsr::launch_adc_gather(n, in, min_, split_noise, adc_config(*cfg), ws,
+                                   static_cast<const uint64_t*>(ws), out, mout,
+                                   as_stream(stream)),
+            "adc_apply");
+    return GSR_OK;
+}
+
 void gsr_profile_enable(int on) {
     ProfState& P = prof();
     std::lock_guard<std::mutex> lk(P.mu);

@@ -307,4 +307,39 @@ hipError_t launch_ply_pack(int n, int K, const float* mu, const float* q, const 
                            const float* alpha, const float* A, const float* kj,
                            int from_probability, float* out, hipStream_t st);
 
+// ---- adaptive density control (gsr_adc.hip) ----
+// A cloud's six parameter arrays: mu [N,3], q [N,4], s [N,3], alpha [N],
+// A [N,3], k_j [N,15,3]; its Adam moments: exp_avg of each, then exp_avg_sq
+// of each (null entries: no state, read as zeros / not written).
+struct AdcCloud {
+    float* p[6];
+};
+struct AdcMoments {
+    float* p[12];
+};
+// fp32 thresholds (the reference compares fp32 tensors with Python floats).
+struct AdcConfig {
+    float grad_threshold, dense_scale, max_scale, min_opacity, max_screen, split_scale,
+        reset_logit;
+    int densify, prune, has_screen, reset_opacity;
+};
+// Densification statistics: with mean2d_grad, its norm (the gradient scaled
+// by (sx, sy) when `scale`) added to accum and 1 to denom where it is > 0;
+// with radii, maxr = max(maxr, radii).
+hipError_t launch_adc_stats(int n, const float* mean2d_grad, float sx, float sy, int scale,
+                            const float* radii, float* accum, float* denom, float* maxr,
+                            hipStream_t st);
+size_t adc_workspace_bytes(int n);
+// Flags and counts per source, then totals_dev[5] (device u64): kept
+// originals, kept clones, kept split sources (two copies each), all split
+// sources (noise rows: two per source), all clone sources.  The workspace's
+// first 256 bytes are free for totals_dev.
+hipError_t launch_adc_plan(int n, const AdcCloud& in, const float* accum, const float* denom,
+                           const float* maxr, const AdcConfig& c, void* ws, uint64_t* totals_dev,
+                           hipStream_t st);
+hipError_t launch_adc_gather(int n, const AdcCloud& in, const AdcMoments& min_,
+                             const float* noise, const AdcConfig& c, const void* ws,
+                             const uint64_t* totals_dev, const AdcCloud& out,
+                             const AdcMoments& mout, hipStream_t st);
+
 }  // namespace gsr

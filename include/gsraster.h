@@ -277,13 +277,56 @@ int gsr_ply_pack(int n, int rest_coeffs, const float* mu, const float* q, const 
                  const float* alpha, const float* albedo, const float* k_j,
                  int opacity_from_probability, float* records, void* stream);
 
+/* Replaces the reference's densification statistics
+ * (gaussian_splatting/utils/adc.py:58-87, accumulate_densification_stats and
+ * update_max_radii2d): with mean2d_grad [N,2] (may be NULL), its norm, scaled
+ * by (width / 2, height / 2) when both are positive, is added to
+ * grad_accum [N] and 1 to denom [N] where it is above 0; with radii [N] (may be
+ * NULL), max_radii2d = max(max_radii2d, radii), NaN propagating. */
+int gsr_adc_stats(int n, const float* mean2d_grad, int width, int height, const float* radii,
+                  float* grad_accum, float* denom, float* max_radii2d, void* stream);
+
+/* Replaces the reference's densify / prune pass (utils/adc.py:316-393 with
+ * :209-294 and :122-165).  params: the six arrays mu [N,3], q [N,4], s [N,3],
+ * alpha [N,1], A [N,3], k_j [N,15,3]; moments: exp_avg of each, then exp_avg_sq
+ * of each (NULL entries: no optimizer state yet).  gsr_adc_plan decides every
+ * Gaussian's fate and synchronizes to return counts[5]: kept originals, kept
+ * clones, kept split sources (two copies each), all split sources, all clone
+ * sources; the new cloud holds counts[0] + counts[1] + 2 counts[2] Gaussians.
+ * gsr_adc_apply writes it to out_params / out_moments in the reference's order
+ * (kept originals, kept clones, kept first split copies, kept second split
+ * copies).  split_noise holds 2 counts[3] rows of 3 N(0, 1) values, the draws
+ * of the reference's torch.normal (row k counts[3] + j: copy k of the j-th
+ * split source).  ws (gsr_adc_workspace_bytes) must stay untouched between the
+ * two calls.  Thresholds are rounded to fp32 as torch compares an fp32 tensor
+ * with a Python float. */
+typedef struct gsr_adc_config {
+    double grad_threshold;   /* 0.00005 */
+    double percent_dense;    /* 0.01 */
+    double scene_extent;
+    double min_opacity;      /* 0.01 */
+    double max_screen_size;  /* used when has_max_screen_size */
+    int has_max_screen_size;
+    int densify;             /* allow_densify and N < max_gaussians */
+    int prune;               /* allow_densify */
+    int reset_opacity;       /* reset_opacity and allow_densify */
+} gsr_adc_config;
+size_t gsr_adc_workspace_bytes(int n);
+int gsr_adc_plan(int n, float* const params[6], const float* grad_accum, const float* denom,
+                 const float* max_radii2d, const gsr_adc_config* cfg, void* ws, size_t ws_bytes,
+                 int64_t counts[5], void* stream);
+int gsr_adc_apply(int n, float* const params[6], float* const moments[12],
+                  const float* split_noise, const gsr_adc_config* cfg, const void* ws,
+                  size_t ws_bytes, float* const out_params[6], float* const out_moments[12],
+                  void* stream);
+
 /* Stage timing (no counterpart in the reference; for benchmarks).  While
  * enabled, each entry point records a pair of HIP events on its stream around
  * its stage's kernels: "project", "sh", "project_sh", "bin_count",
  * "depth_sort", "scan", "records", "tile_binning", "tile_sort", "ranges",
  * "fwd_schedule", "blend_fwd", "bwd_records", "bwd_slots", "bwd_schedule",
  * "blend_bwd", "grad_reduce", "sh_bwd", "project_bwd", "project_sh_bwd",
- * "loss", "loss_bwd", "adam", "ply_pack".
+ * "loss", "loss_bwd", "adam", "ply_pack", "adc_stats", "adc_plan", "adc_apply".
  * gsr_profile_collect waits for the recorded events
  * and adds their durations to per-stage totals read by gsr_profile_get;
  * gsr_profile_stage(i) names the i-th stage with a total (NULL past the end). */
