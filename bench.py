@@ -356,7 +356,8 @@ def adc_pass(sc, calls: int = 3) -> dict:
         return g, opt
 
     g, opt = fresh()
-    adaptive_density_control(g, opt, scene_extent=5.0, max_screen_size=200.0)
+    kw = dict(scene_extent=5.0, max_screen_size=200.0, max_gaussians=4 * n)
+    adaptive_density_control(g, opt, **kw)
     times, stats = [], None
     crc.profile_reset()
     crc.profile_enable(True)
@@ -365,7 +366,7 @@ def adc_pass(sc, calls: int = 3) -> dict:
         torch.cuda.synchronize()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         a.record()
-        g, opt, stats = adaptive_density_control(g, opt, scene_extent=5.0, max_screen_size=200.0)
+        g, opt, stats = adaptive_density_control(g, opt, **kw)
         b.record()
         torch.cuda.synchronize()
         times.append(a.elapsed_time(b))

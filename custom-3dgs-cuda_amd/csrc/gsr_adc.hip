@@ -175,27 +175,40 @@ __global__ __launch_bounds__(1024) void adc_scan_kernel(int blocks, uint32_t* __
         }
 }
 
-__device__ __forceinline__ void copy_params(const AdcCloud& in, const AdcCloud& out, size_t src,
-                                            size_t dst) {
-#pragma unroll
-    for (int a = 0; a < 6; ++a) {
-        const int w = kWidths[a];
-        const float* s = in.p[a] + (size_t)w * src;
-        float* d = out.p[a] + (size_t)w * dst;
-        for (int k = 0; k < w; ++k) d[k] = s[k];
-    }
-}
+// Destinations of a block's Gaussians in the new cloud (row indices, or
+// kNoRow): itself, its clone, its two split copies.
+constexpr uint32_t kNoRow = 0xffffffffu;
 
-__device__ __forceinline__ void copy_moments(const AdcMoments& in, const AdcMoments& out,
-                                             size_t src, size_t dst, bool zero) {
+// Copies one [N, W] array of the block's Gaussians to their destinations,
+// element-parallel: the block's source rows are contiguous, so the loads are
+// coalesced, and each destination kind's rows are contiguous too (the order
+// is kept), so are the stores up to the dropped rows.  mode 0: a parameter
+// (every destination gets the value; with `skip_split` the split copies are
+// left to the caller; with `clamp` the value is min(v, clamp_hi), NaN kept);
+// mode 1: a moment (the Gaussian's own row gets the value, new rows zero;
+// `zero_all` zeroes every row).
+template <int W>
+__device__ __forceinline__ void copy_rows(const float* __restrict__ src, float* __restrict__ dst,
+                                          int g0, int cnt, const uint32_t (*s_dst)[kAdcThreads],
+                                          int mode, bool skip_split, bool clamp, float clamp_hi,
+                                          bool zero_all) {
+    const float* sp = src ? src + (size_t)g0 * W : nullptr;
+    for (int e = threadIdx.x; e < cnt * W; e += kAdcThreads) {
+        const int g = e / W, k = e - g * W;
+        const float v = sp ? sp[e] : 0.0f;
 #pragma unroll
-    for (int a = 0; a < 12; ++a) {
-        float* d = out.p[a];
-        if (!d) continue;
-        const int w = kWidths[a % 6];
-        d += (size_t)w * dst;
-        const float* s = in.p[a];
-        for (int k = 0; k < w; ++k) d[k] = (zero || !s) ? 0.0f : s[(size_t)w * src + k];
+        for (int d = 0; d < 4; ++d) {
+            const uint32_t row = s_dst[d][g];
+            if (row == kNoRow) continue;
+            if (mode == 0) {
+                if (skip_split && d >= 2) continue;
+                float x = v;
+                if (clamp) x = isnan_f(x) ? x : fminf(x, clamp_hi);
+                dst[(size_t)row * W + k] = x;
+            } else {
+                dst[(size_t)row * W + k] = (d == 0 && !zero_all) ? v : 0.0f;
+            }
+        }
     }
 }
 
@@ -204,7 +217,10 @@ __global__ __launch_bounds__(kAdcThreads) void adc_gather_kernel(
     const uint32_t* __restrict__ offs, const uint64_t* __restrict__ totals,
     const float* __restrict__ noise, AdcConfig c, AdcCloud out, AdcMoments mout) {
     __shared__ uint32_t s_w[4][kAdcThreads / kWave];
-    const int i = blockIdx.x * kAdcThreads + threadIdx.x;
+    __shared__ uint32_t s_dst[4][kAdcThreads];
+    const int g0 = blockIdx.x * kAdcThreads;
+    const int cnt = min(kAdcThreads, n - g0);
+    const int i = g0 + threadIdx.x;
     const uint8_t f = (i < n) ? flags[i] : 0;
     const int w = threadIdx.x / kWave;
     uint32_t rank[4];
@@ -215,7 +231,6 @@ __global__ __launch_bounds__(kAdcThreads) void adc_gather_kernel(
         if ((threadIdx.x & (kWave - 1)) == 0) s_w[k][w] = (uint32_t)popc64(b);
     }
     __syncthreads();
-    if (i >= n) return;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         uint32_t pre = offs[kKinds * (size_t)blockIdx.x + k];
@@ -224,20 +239,37 @@ __global__ __launch_bounds__(kAdcThreads) void adc_gather_kernel(
     }
     const uint64_t n_orig = totals[0], n_clone = totals[1], n_split = totals[2];
     const uint64_t n_src = totals[3];
-    if (f & kKeepOrig) {
-        const size_t d = (size_t)rank[0];
-        copy_params(in, out, (size_t)i, d);
-        copy_moments(min_, mout, (size_t)i, d, false);
+    s_dst[0][threadIdx.x] = (f & kKeepOrig) ? (uint32_t)rank[0] : kNoRow;
+    s_dst[1][threadIdx.x] = (f & kKeepClone) ? (uint32_t)(n_orig + rank[1]) : kNoRow;
+    s_dst[2][threadIdx.x] = (f & kKeepSplit) ? (uint32_t)(n_orig + n_clone + rank[2]) : kNoRow;
+    s_dst[3][threadIdx.x] =
+        (f & kKeepSplit) ? (uint32_t)(n_orig + n_clone + n_split + rank[2]) : kNoRow;
+    __syncthreads();
+    if (cnt <= 0) return;
+    const bool reset = c.reset_opacity != 0;
+    // the parameters (the split copies' mu and s below), then the moments
+    copy_rows<3>(in.p[0], out.p[0], g0, cnt, s_dst, 0, true, false, 0.0f, false);
+    copy_rows<4>(in.p[1], out.p[1], g0, cnt, s_dst, 0, false, false, 0.0f, false);
+    copy_rows<3>(in.p[2], out.p[2], g0, cnt, s_dst, 0, true, false, 0.0f, false);
+    copy_rows<1>(in.p[3], out.p[3], g0, cnt, s_dst, 0, false, reset, c.reset_logit, false);
+    copy_rows<3>(in.p[4], out.p[4], g0, cnt, s_dst, 0, false, false, 0.0f, false);
+    copy_rows<45>(in.p[5], out.p[5], g0, cnt, s_dst, 0, false, false, 0.0f, false);
+    for (int m = 0; m < 2; ++m) {
+        const int o = 6 * m;
+        if (mout.p[o + 0]) copy_rows<3>(min_.p[o + 0], mout.p[o + 0], g0, cnt, s_dst, 1, false, false, 0.0f, false);
+        if (mout.p[o + 1]) copy_rows<4>(min_.p[o + 1], mout.p[o + 1], g0, cnt, s_dst, 1, false, false, 0.0f, false);
+        if (mout.p[o + 2]) copy_rows<3>(min_.p[o + 2], mout.p[o + 2], g0, cnt, s_dst, 1, false, false, 0.0f, false);
+        if (mout.p[o + 3]) copy_rows<1>(min_.p[o + 3], mout.p[o + 3], g0, cnt, s_dst, 1, false, false, 0.0f, reset);
+        if (mout.p[o + 4]) copy_rows<3>(min_.p[o + 4], mout.p[o + 4], g0, cnt, s_dst, 1, false, false, 0.0f, false);
+        if (mout.p[o + 5]) copy_rows<45>(min_.p[o + 5], mout.p[o + 5], g0, cnt, s_dst, 1, false, false, 0.0f, false);
     }
-    if (f & kKeepClone) {
-        const size_t d = (size_t)(n_orig + rank[1]);
-        copy_params(in, out, (size_t)i, d);
-        copy_moments(min_, mout, (size_t)i, d, true);
-    }
+    if (i >= n) return;
+    // the kept original's and clone's mu and s were copied above; the split
+    // copies' are the perturbed ones
     if (f & kKeepSplit) {
         const float* q = in.p[1] + 4 * (size_t)i;
-        const float* s = in.p[2] + 3 * (size_t)i;
-        const float* m = in.p[0] + 3 * (size_t)i;
+        const float* sv = in.p[2] + 3 * (size_t)i;
+        const float* mu = in.p[0] + 3 * (size_t)i;
         // R of the normalized quaternion (adc.py:103-119: F.normalize, eps
         // 1e-12, then the rotation matrix)
         const float len = fmaxf(
@@ -250,11 +282,9 @@ __global__ __launch_bounds__(kAdcThreads) void adc_gather_kernel(
              2.0f * (qy * qz - qw * qx)},
             {2.0f * (qx * qz - qw * qy), 2.0f * (qy * qz + qw * qx),
              1.0f - 2.0f * (qx * qx + qy * qy)}};
-        const float sc[3] = {exp_gs(s[0]), exp_gs(s[1]), exp_gs(s[2])};
+        const float sc[3] = {exp_gs(sv[0]), exp_gs(sv[1]), exp_gs(sv[2])};
         for (int copy = 0; copy < 2; ++copy) {
-            const size_t d = (size_t)(n_orig + n_clone + (uint64_t)copy * n_split + rank[2]);
-            copy_params(in, out, (size_t)i, d);
-            copy_moments(min_, mout, (size_t)i, d, true);
+            const size_t d = (size_t)s_dst[2 + copy][threadIdx.x];
             // the split source's noise row: copy k of source j is row k n_src + j
             const float* z = noise + 3 * ((size_t)copy * n_src + rank[3]);
             float smp[3];
@@ -262,24 +292,9 @@ __global__ __launch_bounds__(kAdcThreads) void adc_gather_kernel(
             float* om = out.p[0] + 3 * d;
             float* os = out.p[2] + 3 * d;
             for (int a = 0; a < 3; ++a) {
-                om[a] = ((r[a][0] * smp[0] + r[a][1] * smp[1]) + r[a][2] * smp[2]) + m[a];
+                om[a] = ((r[a][0] * smp[0] + r[a][1] * smp[1]) + r[a][2] * smp[2]) + mu[a];
                 os[a] = logf(sc[a] / c.split_scale);
             }
-        }
-    }
-    if (c.reset_opacity) {
-        // adc.py:297-313: clamp_max to logit(0.01), the moments zeroed
-        const size_t dsts[4] = {
-            (f & kKeepOrig) ? (size_t)rank[0] : ~(size_t)0,
-            (f & kKeepClone) ? (size_t)(n_orig + rank[1]) : ~(size_t)0,
-            (f & kKeepSplit) ? (size_t)(n_orig + n_clone + rank[2]) : ~(size_t)0,
-            (f & kKeepSplit) ? (size_t)(n_orig + n_clone + n_split + rank[2]) : ~(size_t)0};
-        for (int k = 0; k < 4; ++k) {
-            if (dsts[k] == ~(size_t)0) continue;
-            float& a = out.p[3][dsts[k]];
-            a = isnan_f(a) ? a : fminf(a, c.reset_logit);
-            if (mout.p[3]) mout.p[3][dsts[k]] = 0.0f;
-            if (mout.p[9]) mout.p[9][dsts[k]] = 0.0f;
         }
     }
 }
