@@ -302,58 +302,83 @@ struct BwdPixel {
     int last;
 };
 
-// dL/dpower = alpha dL/dalpha = opacity * (G dL/dalpha) = opacity * dL/dopacity
-// for an unclamped entry, and both are 0 for a clamped or skipped one
-// (rasterize_backward.cu:155-161), so only dL/dopacity is formed per pixel and
-// the power terms are scaled by the entry's opacity once, at the flush.
+// Per pixel and list entry the walk forms dL/dpower = alpha dL/dalpha
+// (rasterize_backward.cu:155-161: 0 for a clamped or skipped entry) and the
+// colour weight alpha T; dL/dopacity = G dL/dalpha is dL/dpower / opacity,
+// formed once per (tile, entry) at the flush.
 struct BwdTerms {
     float aT;   // alpha * T_before: dL/dcolour = aT * dL/dpixel
-    float dop;  // dL/dopacity
+    float dpw;  // dL/dpower
 };
 
 // One pixel's decision for one list entry (rasterize_backward.cu:117-140):
 // G = exp(power), alpha = min(0.99, opacity G), and whether the entry blends
 // (within n_contrib, power <= 0, alpha >= 1/255) and passes gradient through
-// the clamp.
+// the clamp.  ae = alpha if it blends, else 0; ag = alpha if it also passes
+// gradient (then alpha = opacity G unclamped), else 0.
 struct BwdDecision {
-    float dy, power, G, alpha;
-    bool act, unc;
+    float dy, power, alpha, ae, ag;
+    bool act;
 };
 
 // The forward's own evaluation: exp_blend and the same fp32 operations, so
 // every skip agrees with the forward bit for bit.
 __device__ __forceinline__ void decide_exact(BwdDecision& d, float o, int contributor, int last) {
-    d.G = exp_blend(d.power);
-    const float araw = o * d.G;
+    const float araw = o * exp_blend(d.power);
     d.alpha = fminf(kAlphaMax, araw);
     d.act = (contributor <= last) & !(d.power > 0.0f) & !(d.alpha < kAlphaMin);
-    d.unc = d.act & (araw < kAlphaMax);
+    d.ae = d.act ? d.alpha : 0.0f;
+    d.ag = (d.act & (araw < kAlphaMax)) ? d.alpha : 0.0f;
 }
 
 // For an entry with opacity in [0, 0.99): G from the hardware exp2, which is
 // within 1e-6 relative of exp_blend wherever alpha can reach 1/255 (power in
 // [-5.6, 0]), so the alpha >= 1/255 test agrees with the exact one unless
 // alpha lies within kNearAlpha of 1/255; alpha <= opacity < 0.99 is never
-// clamped.  Returns true when the lane needs the exact evaluation (near the
-// threshold, or a NaN alpha).
+// clamped.  near_fast says whether the lane needs the exact evaluation (near
+// the threshold, or a NaN alpha).
 constexpr float kNearAlpha = kAlphaMin * 2e-5f;
-__device__ __forceinline__ bool decide_fast(BwdDecision& d, float o, int contributor, int last) {
-    d.G = __builtin_amdgcn_exp2f(d.power * 1.44269504088896341f);
-    d.alpha = o * d.G;
+__device__ __forceinline__ void decide_fast(BwdDecision& d, float o, int contributor, int last) {
+    d.alpha = o * __builtin_amdgcn_exp2f(d.power * 1.44269504088896341f);
     d.act = (contributor <= last) & !(d.power > 0.0f) & !(d.alpha < kAlphaMin);
-    d.unc = d.act;
+    d.ae = d.act ? d.alpha : 0.0f;
+    d.ag = d.ae;
+}
+__device__ __forceinline__ bool near_fast(const BwdDecision& d) {
     return !(fabsf(d.alpha - kAlphaMin) > kNearAlpha);
 }
 
+// The wave's decisions for one entry: the fast evaluation where the record
+// allows it, the exact one for the whole wave when any lane is near the
+// threshold (one ballot per pixel of a single compare: no lane-mask
+// materialisation).
+template <int kPix>
+__device__ __forceinline__ void decide_entry(BwdDecision (&d)[kPix], float o, uint32_t bits,
+                                             int contributor, const BwdPixel (&p)[kPix]) {
+    bool exact = (bits & kFastExpBit) == 0;
+    if (!exact) {
+        uint64_t near = 0;
+#pragma unroll
+        for (int k = 0; k < kPix; ++k) {
+            decide_fast(d[k], o, contributor, p[k].last);
+            near |= ballot(near_fast(d[k]));
+        }
+        exact = near != 0;
+    }
+    if (exact) {
+#pragma unroll
+        for (int k = 0; k < kPix; ++k) decide_exact(d[k], o, contributor, p[k].last);
+    }
+}
+
 // One pixel's gradient step for a decided entry (rasterize_backward.cu:
-// 141-198).  A skipped entry enters with alpha 0, which leaves T (x / 1) and
-// accg unchanged and gives zero terms.  This arithmetic only has to meet the
-// fp32 gradient tolerance and may use fused multiply-adds.
+// 141-198).  A skipped entry enters with ae = ag = 0, which leaves T (x / 1)
+// and accg unchanged and gives zero terms.  This arithmetic only has to meet
+// the fp32 gradient tolerance and may use fused multiply-adds.
 __device__ __forceinline__ BwdTerms bwd_update(BwdPixel& p, const BwdDecision& d,
                                                const float4& B, float cb) {
 #pragma clang fp contract(fast)
     BwdTerms t;
-    const float ae = d.act ? d.alpha : 0.0f;
     // T / (1 - alpha) with 1 - alpha in [0.01, 1]: the reference's 1e-4 floor
     // never applies.  The hardware reciprocal (1 ulp) times T, then one
     // correction from the exact residual T - q (1 - alpha) (a fused
@@ -362,16 +387,15 @@ __device__ __forceinline__ BwdTerms bwd_update(BwdPixel& p, const BwdDecision& d
     // entries of a long list the drift reaches 1e-5 of the terms that a
     // Gaussian's gradient sums (every term scales with T).  A skipped entry
     // (alpha 0) leaves T unchanged: the reciprocal of 1 is exact.
-    const float den = 1.0f - ae;
+    const float den = 1.0f - d.ae;
     const float rd = __builtin_amdgcn_rcpf(den);
     const float q0 = p.T * rd;
     const float Tb = __builtin_fmaf(__builtin_fmaf(-q0, den, p.T), rd, q0);
     const float cg = B.z * p.g0 + B.w * p.g1 + cb * p.g2;
     const float diff = cg - p.accg;
-    const float dal = diff * Tb;
-    t.aT = ae * Tb;
-    t.dop = (d.unc ? d.G : 0.0f) * dal;
-    p.accg = __builtin_fmaf(ae, diff, p.accg);
+    t.aT = d.ae * Tb;
+    t.dpw = d.ag * (diff * Tb);
+    p.accg = __builtin_fmaf(d.ae, diff, p.accg);
     p.T = Tb;
     return t;
 }
@@ -394,12 +418,15 @@ __device__ __forceinline__ BwdPixel load_bwd_pixel(bool in, int px, int py, int 
     return p;
 }
 
-// Per (tile, entry) the wave sums nine values.  A lane's pixels share dx, so
-// the reference's per-pixel mean and conic terms (rasterize_backward.cu:
-// 163-176) summed over the lane follow from S0 = sum dop, P1 = dx S0,
-// P2 = sum dop dy and P5 = sum dop dy^2 (dop = dL/dopacity, dL/dpower being
-// opacity * dop): dL/dmean = o (cx P1 + cy P2, cy P1 + cz P2), dL/dconic =
-// o (-P1 dx / 2, -P2 dx, -P5 / 2); then dL/dcolour (3) and dL/dopacity (S0).
+// Per (tile, entry) the wave sums nine values.  A lane's pixels share dx
+// (column lane & 15), so the reference's per-pixel mean and conic terms
+// (rasterize_backward.cu:163-176) follow from per-lane sums of dpw = dL/dpower:
+// S0 = sum dpw, P2 = sum dpw dy, P5 = sum dpw dy^2, with dx applied once the
+// lanes of a column are summed (wave_reduce_columns): P1 = sum dx S0,
+// Q1 = sum dx^2 S0, Q2 = sum dx P2.  Then dL/dmean = (cx P1 + cy P2,
+// cy P1 + cz P2), dL/dconic = (-Q1 / 2, -Q2, -P5 / 2), dL/dcolour the sums of
+// alpha T dL/dpixel and dL/dopacity = S0 / opacity.  Value k sits in slot
+// kCol* of the reduction's result.
 constexpr int kTerms = 9;
 
 // dL/dcov2d (a, b, c) from dL/dconic (x, y full off-diagonal, z) for conic =
@@ -461,18 +488,7 @@ __device__ __forceinline__ void state_walk(int lo0, int hi0, int n, int tile, in
                 d[k].power = __builtin_fmaf(B.x * d[k].dy, d[k].dy,
                                             __builtin_fmaf(bdx, d[k].dy, adxdx));
             }
-            bool exact = (bits & kFastExpBit) == 0;
-            if (!exact) {
-                bool near = false;
-#pragma unroll
-                for (int k = 0; k < kPix; ++k)
-                    near |= decide_fast(d[k], B.y, contributor, p[k].last);
-                exact = ballot(near) != 0;
-            }
-            if (exact) {
-#pragma unroll
-                for (int k = 0; k < kPix; ++k) decide_exact(d[k], B.y, contributor, p[k].last);
-            }
+            decide_entry<kPix>(d, B.y, bits, contributor, p);
 #pragma unroll
             for (int k = 0; k < kPix; ++k) (void)bwd_update(p[k], d[k], B, Cc.x);
         }
@@ -544,7 +560,7 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
     for (int w = 0; w < kWaves; ++w) tile_last = max(tile_last, s_max[w]);
     const int maxc = __builtin_amdgcn_readfirstlane(min((int)tile_last, end - start));
     start = __builtin_amdgcn_readfirstlane(start);
-    const int my_value = reduce9_value_of_lane(lane);
+    const int my_value = columns_value_of_lane(lane);
     // the entries [lo0, hi0) this item walks with gradients; the front part
     // first walks [mid, maxc) for the pixel state only
     int lo0 = 0, hi0 = maxc;
@@ -594,58 +610,36 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                     d[k].power = __builtin_fmaf(B.x * d[k].dy, d[k].dy,
                                                 __builtin_fmaf(bdx, d[k].dy, adxdx));
                 }
-                bool exact = (bits & kFastExpBit) == 0;
-                if (!exact) {
-                    bool near = false;
-#pragma unroll
-                    for (int k = 0; k < kPix; ++k)
-                        near |= decide_fast(d[k], B.y, contributor, p[k].last);
-                    exact = ballot(near) != 0;
-                }
-                if (exact) {
-#pragma unroll
-                    for (int k = 0; k < kPix; ++k) decide_exact(d[k], B.y, contributor, p[k].last);
-                }
+                decide_entry<kPix>(d, B.y, bits, contributor, p);
                 // per-lane sums over its pixels, started from the first pixel's terms
                 float S0, P2, P5, c0, c1, c2;
-                bool act;
                 {
                     const BwdTerms t = bwd_update(p[0], d[0], B, Cc.x);
-                    const float e = t.dop * d[0].dy;
-                    S0 = t.dop;
+                    const float e = t.dpw * d[0].dy;
+                    S0 = t.dpw;
                     P2 = e;
                     P5 = e * d[0].dy;
                     c0 = t.aT * p[0].g0;
                     c1 = t.aT * p[0].g1;
                     c2 = t.aT * p[0].g2;
-                    act = d[0].act;
                 }
 #pragma unroll
                 for (int k = 1; k < kPix; ++k) {
                     const BwdTerms t = bwd_update(p[k], d[k], B, Cc.x);
                     {
 #pragma clang fp contract(fast)
-                        const float e = t.dop * d[k].dy;
-                        S0 += t.dop;
+                        const float e = t.dpw * d[k].dy;
+                        S0 += t.dpw;
                         P2 += e;
                         P5 += e * d[k].dy;
                         c0 += t.aT * p[k].g0;
                         c1 += t.aT * p[k].g1;
                         c2 += t.aT * p[k].g2;
                     }
-                    act |= d[k].act;
                 }
-                if (ballot(act) != 0) {
-                    const float P1 = dx * S0;
-                    // mean terms formed in the lane, before the wide sum, as the
-                    // per-pixel dpw (conic.x dx + conic.y dy) is; with the
-                    // record's -cx/2, -cy/2 (Cc.y), -cz/2 they are -1/2 of
-                    // (cx P1 + cy P2, cy P1 + cz P2), rescaled at the flush
-                    const float hy = Cc.y;
-                    const float vals[kTerms] = {A.z * P1 + hy * P2, hy * P1 + B.x * P2, dx * P1,
-                                                dx * P2, P5, c0, c1, c2, S0};
-                    w9 = wave_reduce9(vals);
-                }
+                // a wave with no blending pixel (2% of the strip-passing
+                // wave-entries on the bench scene) sums zeros
+                w9 = wave_reduce_columns(S0, P2, P5, c0, c1, c2, dx);
             }
             if (my_value >= 0) s_part[wave][my_value][j] = w9;
         }
@@ -664,16 +658,20 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
             }
             if (g >= 0 && any) {
                 float t[kTerms];
-                const float o = s_b[tid].y;  // the power terms carry dL/dopacity
-                t[0] = (-2.0f * o) * tot[0];  // dL/dmean.x
-                t[1] = (-2.0f * o) * tot[1];  // dL/dmean.y
-                t[2] = (-0.5f * o) * tot[2];  // dL/dconic.x
-                t[3] = -o * tot[3];           // dL/dconic.y (full off-diagonal)
-                t[4] = (-0.5f * o) * tot[4];  // dL/dconic.z
-                t[5] = tot[5];         // dL/dcolour
-                t[6] = tot[6];
-                t[7] = tot[7];
-                t[8] = tot[8];         // dL/dopacity
+                // the record's -cx/2 (A.z), -cy/2 (C.y), -cz/2 (B.x), opacity (B.y)
+                const float ha = s_a[tid].z, hb = s_c[tid].y, hc = s_b[tid].x, o = s_b[tid].y;
+                const float S0 = tot[kColS0], P1 = tot[kColP1], P2 = tot[kColP2];
+                t[0] = -2.0f * (ha * P1 + hb * P2);  // dL/dmean.x = cx P1 + cy P2
+                t[1] = -2.0f * (hb * P1 + hc * P2);  // dL/dmean.y = cy P1 + cz P2
+                t[2] = -0.5f * tot[kColQ1];          // dL/dconic.x
+                t[3] = -tot[kColQ2];                 // dL/dconic.y (full off-diagonal)
+                t[4] = -0.5f * tot[kColP5];          // dL/dconic.z
+                t[5] = tot[kColC0];                  // dL/dcolour
+                t[6] = tot[kColC1];
+                t[7] = tot[kColC2];
+                // dL/dopacity: every dpw carries a factor opacity (no pixel
+                // blends the entry when the opacity is 0)
+                t[8] = (S0 == 0.0f) ? 0.0f : S0 / o;
                 // the pair's slot: goff[g] + this tile's index in g's rectangle
                 const uint2 rc = gs.rects[g];
                 const int rx0 = (int)(rc.x & 0xffffu), rx1 = (int)(rc.x >> 16);

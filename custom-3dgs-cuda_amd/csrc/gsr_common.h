@@ -123,9 +123,12 @@ constexpr int kDppRowShl4 = 0x104;
 constexpr int kDppRowShr4 = 0x114;
 constexpr int kDppRowRor8 = 0x128;  // lane i <- lane i ^ 8 within the row
 
-// lane i <- lane i ^ 4 within the row: two bank-masked moves.
+// lane i <- lane i ^ 4 within the row: two bank-masked moves (the first
+// writes banks 1 and 3, the second banks 0 and 2, so no lane keeps the
+// destination's old value).
 __device__ __forceinline__ float lane_xor4(float x) {
-    const float t = dpp_move<kDppRowShr4, 0xa>(x);
+    const float t = __int_as_float(
+        __builtin_amdgcn_mov_dpp(__float_as_int(x), kDppRowShr4, 0xf, 0xa, false));
     return dpp_move<kDppRowShl4, 0x5>(x, t);
 }
 
@@ -144,27 +147,35 @@ __device__ __forceinline__ float fold16(float a, float b) {
     return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Sums nine per-lane values over the whole wave with a transposed reduction:
-// each level halves the number of live registers while doubling the lanes
-// summed (32: permlane32 swap, 16: permlane16 swap, 8: row_ror, 4: bank-masked
-// row shifts, 2 and 1: quad permutes), ~30 VALU instead of 9 x 6 shuffles.
-// Value k's wave total ends in lane kReduce9Lane[k] of the result.  All 64
-// lanes must be active.
-constexpr int kReduce9Lane[9] = {0, 32, 16, 48, 8, 40, 24, 56, 4};
+// The backward's nine wave sums from six per-lane sums, for the blend layout
+// where lanes l, l ^ 16, l ^ 32 and l ^ 48 hold the same pixel column (lane &
+// 15, one dx per lane).  A transposed reduction: each level halves the live
+// registers while doubling the lanes summed.  The 32- and 16-lane levels
+// (permlane swaps) run on the six column-free sums only (S0, P2, P5, c0, c1,
+// c2) and leave column totals; then dx S0, dx^2 S0 and dx P2 are formed per
+// column and the 8-, 4-, 2- and 1-lane levels (row_ror, bank-masked row
+// shifts, quad permutes) finish four registers.  ~27 VALU.  Value k's wave
+// total ends in lane kColLane[k] of the result (and in the lanes of its quad).
+// All 64 lanes must be active.
+constexpr int kColS0 = 0, kColP1 = 1, kColQ1 = 2, kColP2 = 3, kColQ2 = 4, kColP5 = 5,
+              kColC0 = 6, kColC1 = 7, kColC2 = 8;
+constexpr int kColLane[9] = {0, 8, 4, 16, 24, 12, 32, 48, 44};
 
-__device__ __forceinline__ float wave_reduce9(const float v[9]) {
-    const float r0 = fold32(v[0], v[1]);  // lanes 0-31: v0, 32-63: v1
-    const float r1 = fold32(v[2], v[3]);
-    const float r2 = fold32(v[4], v[5]);
-    const float r3 = fold32(v[6], v[7]);
-    const float r4 = fold32(v[8], v[8]);
-    const float s0 = fold16(r0, r1);      // rows: v0, v2, v1, v3
-    const float s1 = fold16(r2, r3);      // rows: v4, v6, v5, v7
-    const float s2 = fold16(r4, r4);      // rows: v8
+__device__ __forceinline__ float wave_reduce_columns(float s0, float p2, float p5, float c0,
+                                                     float c1, float c2, float dx) {
+    // lanes 0-31 (rows 0, 1) hold S0, P2, P5; lanes 32-63 (rows 2, 3) c0, c1, c2
+    const float r0 = fold32(s0, c0);
+    const float r1 = fold32(p2, c1);
+    const float r2 = fold32(p5, c2);
+    // column totals: a = (S0, P2, c0, c1) in rows 0-3, b = (P5, P5, c2, c2)
+    const float a = fold16(r0, r1);
+    const float b = fold16(r2, r2);
+    const float t1 = dx * a;   // row 0: dx S0, row 1: dx P2
+    const float t2 = dx * t1;  // row 0: dx^2 S0
     const int l = lane_id();
     const bool b3 = (l & 8) != 0;
-    const float u0 = (b3 ? s1 : s0) + dpp_move<kDppRowRor8>(b3 ? s0 : s1);
-    const float u1 = s2 + dpp_move<kDppRowRor8>(s2);
+    const float u0 = (b3 ? t1 : a) + dpp_move<kDppRowRor8>(b3 ? a : t1);
+    const float u1 = (b3 ? b : t2) + dpp_move<kDppRowRor8>(b3 ? t2 : b);
     const bool b2 = (l & 4) != 0;
     float w = (b2 ? u1 : u0) + lane_xor4(b2 ? u0 : u1);
     w = w + dpp_move<kDppQuadXor2>(w);
@@ -172,13 +183,14 @@ __device__ __forceinline__ float wave_reduce9(const float v[9]) {
     return w;
 }
 
-// Which of the nine values lane l holds after wave_reduce9 (-1: a duplicate).
-__device__ __forceinline__ int reduce9_value_of_lane(int l) {
+// Which of the nine values lane l holds after wave_reduce_columns (-1: none).
+// Lane l with l & 3 == 0 holds, in row l >> 4, register (l >> 2) & 3 of the
+// last levels: 0 a, 1 t2, 2 t1, 3 b.
+__device__ __forceinline__ int columns_value_of_lane(int l) {
     if (l & 3) return -1;
-    const int row = l >> 4, sub = (l >> 2) & 3;
-    if (sub == 0) return (row == 0) ? 0 : (row == 1) ? 2 : (row == 2) ? 1 : 3;
-    if (sub == 2) return (row == 0) ? 4 : (row == 1) ? 6 : (row == 2) ? 5 : 7;
-    return (l == 4) ? 8 : -1;
+    for (int k = 0; k < 9; ++k)
+        if (kColLane[k] == l) return k;
+    return -1;
 }
 
 __device__ __forceinline__ uint32_t wave_sum_u32(uint32_t v) {
