@@ -89,20 +89,77 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
     }.get(stage)
 
 
-# Highest wave64 VALU issue rate measured on MI355X (v_add_f32 / v_mul_f32 chains,
-# 8 independent per lane, 16 waves per SIMD; SQ_INSTS_VALU-calibrated): 945 G/s.
-# v_fma_f32 issues at ~600 G/s (one per CU per 2.4 GHz cycle).
-VALU_PEAK_GINST = 945.0
+# VALU issue ceiling from MI355X's published figures: 256 CUs x 4 SIMDs, each
+# SIMD issuing one wave64 VALU instruction per 4-cycle quad-cycle, at the
+# 2.4 GHz peak engine clock: 614.4 G issue quad-cycles/s.  The same figure is
+# the published 157.3 TFLOP/s fp32 vector peak divided by the 256 flops of a
+# wave64 packed FMA.  Two VALU instructions can share a quad-cycle (rocprofv3's
+# SQ_ACTIVE_INST_VALU2), so a kernel's issue quad-cycles are SQ_ACTIVE_INST_VALU
+# - SQ_ACTIVE_INST_VALU2 (transcendentals and lane permutes take two).
+VALU_PEAK_GISSUE = 256 * 4 * 2.4 / 4
+# The blends are bound by VALU issue, not by HBM: their pct_hbm_peak comes only
+# from measured FETCH_SIZE + WRITE_SIZE traffic, never from a byte formula.
+VALU_BOUND_STAGES = ("blend_fwd", "blend_bwd")
+# Calibration kinds of gsr_calibrate_valu (one instruction kind per kernel).
+VALU_CALIBRATION_KINDS = ("add", "fma", "exp", "permlane_swap", "dpp_add")
 
 
-def _profile_json(kind: str, kernel: str, workload: str):
-    p = ROOT / "profiles" / f"{kind}_{kernel}_{workload}.json"
+def _profile_json(kind: str, workload: str):
+    """profiles/<kind>_<workload>.json (committed summaries of rocprofv3 runs)."""
+    p = ROOT / "profiles" / f"{kind}_{workload}.json"
     if p.exists():
         try:
             return json.loads(p.read_text())
         except (OSError, ValueError):
             return None
     return None
+
+
+def dominant_roofline(stage: str, per_stage: dict, N: int, M: int, W: int, H: int,
+                      workload: str) -> dict:
+    """The roofline object of the frame's dominant stage, its average launch
+    time measured live (HIP events around each launch on the launch stream).
+
+    VALU-bound blends: achieved = the kernel's VALU issue quad-cycles per launch
+    (SQ_ACTIVE_INST_VALU - SQ_ACTIVE_INST_VALU2, profiles/valu_<workload>.json)
+    / launch time, against VALU_PEAK_GISSUE; the issue utilisation at the
+    measured clock and the calibration kernels' utilisation (the practical
+    ceiling of one instruction kind) come from the same profile.  The HBM side
+    is the measured FETCH_SIZE + WRITE_SIZE traffic; the per-pair byte formula
+    is kept as a labelled equivalent.  Other stages: HBM-bound, achieved =
+    their formula bytes / launch time."""
+    avg_s = per_stage[stage]["ms"] * 1e-3
+    alg = stage_bytes(stage, N, M, W, H)
+    tr = (_profile_json("traffic", workload) or {}).get("stages", {}).get(stage)
+    traffic = tr.get("bytes_per_call") if tr else None
+    va = (_profile_json("valu", workload) or {})
+    vk = va.get("kernels", {}).get(stage)
+    if stage in VALU_BOUND_STAGES and vk:
+        ach = vk["issue_quads_per_launch"] / avg_s / 1e9
+        out = {"bound": "valu", "kernel": stage, "achieved": round(ach, 1),
+               "peak": VALU_PEAK_GISSUE, "unit": "G VALU issue quad-cycles/s",
+               "frac": round(ach / VALU_PEAK_GISSUE, 4), "traffic": traffic,
+               "avg_launch_ms": per_stage[stage]["ms"],
+               "issue_quads_per_launch": vk["issue_quads_per_launch"],
+               "valu_insts_per_launch": vk.get("insts_per_launch"),
+               "issue_util_at_measured_clock": vk.get("issue_util"),
+               "measured_clock_mhz": vk.get("clock_mhz"),
+               "calibration_issue_util": {k: c.get("issue_util")
+                                          for k, c in va.get("calibration", {}).items()}}
+        if traffic:
+            gbs = traffic / avg_s / 1e9
+            out["hbm_measured"] = {"GBps": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        if alg:
+            gbs = alg / avg_s / 1e9
+            out["equivalent"] = {"what": "the rasterizer baseline's per-pair byte formula",
+                                 "bytes": alg, "GBps": round(gbs, 1),
+                                 "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        return out
+    b = traffic or alg
+    ach = (b / avg_s / 1e9) if b else 0.0
+    return {"bound": "hbm", "kernel": stage, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+            "algorithmic_bytes": alg, "avg_launch_ms": per_stage[stage]["ms"]}
 
 
 def _clear(g):
@@ -172,18 +229,33 @@ def pair_count(sc) -> int:
     return int(out[1].numel())
 
 
-def _stage_rates(stages: dict, N: int, M: int, W: int, H: int, keep=None) -> dict:
+def _stage_rates(stages: dict, N: int, M: int, W: int, H: int, keep=None,
+                 workload: str | None = None) -> dict:
+    """Per-stage ms and HBM rate.  The bytes are the stage's measured
+    FETCH_SIZE + WRITE_SIZE per call where profiles/traffic_<workload>.json
+    holds them ("bytes": "measured"), else the per-stage formula
+    ("bytes": "formula"); the VALU-bound blends get no formula rate."""
+    measured = (_profile_json("traffic", workload) or {}).get("stages", {}) if workload else {}
     out = {}
     for name, (count, ms) in stages.items():
         if keep is not None and name not in keep:
             continue
         avg = ms / max(count, 1)
-        b = stage_bytes(name, N, M, W, H)
-        rate = b is not None and avg > 0
-        out[name] = {"ms": round(avg, 4), "calls": int(count),
-                     "GBps": round(b / (avg * 1e-3) / 1e9, 1) if rate else None,
-                     "pct_hbm_peak": round(100 * b / (avg * 1e-3) / 1e9 / HBM_PEAK_GBS, 2)
-                     if rate else None}
+        entry = {"ms": round(avg, 4), "calls": int(count)}
+        b, src = None, None
+        if name in measured and measured[name].get("bytes_per_call"):
+            b, src = float(measured[name]["bytes_per_call"]), "measured"
+        elif name not in VALU_BOUND_STAGES:
+            b, src = stage_bytes(name, N, M, W, H), "formula"
+        if b is not None and avg > 0:
+            gbs = b / (avg * 1e-3) / 1e9
+            entry.update({"GBps": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+                          "bytes": src})
+        else:
+            entry.update({"GBps": None, "pct_hbm_peak": None, "bytes": None})
+        if name in VALU_BOUND_STAGES:
+            entry["bound"] = "valu"
+        out[name] = entry
     return out
 
 
@@ -403,7 +475,8 @@ def frame_stages(sc, steps: int, binning: str | None = None) -> dict:
         else:
             os.environ["GSR_TILE_BINNING"] = old
     v = sc.view
-    rates = _stage_rates(stages, sc.n, M, v["width"], v["height"])
+    rates = _stage_rates(stages, sc.n, M, v["width"], v["height"],
+                         workload=None if binning else sc.name + "_randn_grad")
     return {"fwd_ms": round(fwd, 4), "bwd_ms": round(bwd, 4), "ms_per_frame": round(total, 4),
             "fps": round(1000.0 / total, 1), "pairs": M,
             "binning": binning_summary(rates, sc.n, M, v["width"], v["height"]),
@@ -537,6 +610,9 @@ def main() -> int:
     ap.add_argument("--scene", default="bench", choices=["bench", "c1", "c2", "c3", "c4", "c5"],
                     help="the frame to time: the reference's bench scene (default) or a "
                          "rasterizer baseline config at its own size (for profiling)")
+    ap.add_argument("--grad", default="sum", choices=["sum", "randn"],
+                    help="dL/dimage of the timed frames: image.sum() (the reference's "
+                         "bench.py, default) or the baseline configs' seeded N(0, 1)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-c5", action="store_true",
                     help="skip config c5 (5M Gaussians, 3840x2160, timed in screen bands)")
@@ -545,6 +621,9 @@ def main() -> int:
     ap.add_argument("--no-extra", action="store_true", help="skip the 720p and c3 side runs")
     ap.add_argument("--no-scale", action="store_true",
                     help="skip the per-stage HBM measurements on configs c4 and c5")
+    ap.add_argument("--calibrate-valu", action="store_true",
+                    help="only run the VALU issue-rate calibration kernels (one per "
+                         "instruction kind, 3 launches each) and print their rates")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 256 MiB device copy 5 times (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -571,6 +650,25 @@ def main() -> int:
         print(json.dumps({"copy_bytes_read": src.numel() * 4, "copy_bytes_written": dst.numel() * 4,
                           "launches": 5}), flush=True)
         return 0
+    if args.calibrate_valu:
+        import custom_rasterizer_cuda as crc
+
+        iters, res = 4096, {}
+        for kind, name in enumerate(VALU_CALIBRATION_KINDS):
+            best = None
+            for _ in range(3):
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                a.record()
+                out = crc.calibrate_valu(kind, iters)
+                b.record()
+                torch.cuda.synchronize()
+                ms = a.elapsed_time(b)
+                best = ms if best is None else min(best, ms)
+            insts = out.numel() // 64 * iters * 8  # wave64 instructions of the kind
+            res[name] = {"ms": round(best, 4), "wave64_insts": insts,
+                         "G_insts_per_s": round(insts / (best * 1e-3) / 1e9, 1)}
+        print(json.dumps({"calibrate_valu": res}), flush=True)
+        return 0
     W, H, N = args.width, args.height, args.gaussians
     if args.scene == "bench":
         sc = synthetic.bench_scene(n=N, width=W, height=H, device=dev)
@@ -581,29 +679,15 @@ def main() -> int:
         workload = sc.name
     M = pair_count(sc)
 
-    fwd, bwd, total, _ = time_frames(sc, args.steps, args.warmup, profile=False)
-    pf, pb, ptot, stages = time_frames(sc, args.steps, 2, profile=True)
+    G = config_grad(sc) if args.grad == "randn" else None
+    if G is not None:
+        workload += "_randn_grad"
+    fwd, bwd, total, _ = time_frames(sc, args.steps, args.warmup, profile=False, grad=G)
+    pf, pb, ptot, stages = time_frames(sc, args.steps, 2, profile=True, grad=G)
 
-    per_stage = _stage_rates(stages, N, M, W, H)
+    per_stage = _stage_rates(stages, N, M, W, H, workload=workload)
     dominant = max(per_stage, key=lambda k: per_stage[k]["ms"]) if per_stage else None
-    roofline = None
-    if dominant:
-        avg_s = per_stage[dominant]["ms"] * 1e-3
-        alg = stage_bytes(dominant, N, M, W, H)
-        ach = alg / avg_s / 1e9
-        tr = _profile_json("traffic", dominant, workload)
-        roofline = {"bound": "hbm", "kernel": dominant, "achieved": round(ach, 1),
-                    "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4),
-                    "traffic": tr.get("bytes_per_launch") if tr else None,
-                    "algorithmic_bytes": alg, "avg_launch_ms": per_stage[dominant]["ms"]}
-        va = _profile_json("valu", dominant, workload)
-        if va and va.get("valu_insts_per_launch"):
-            g = va["valu_insts_per_launch"] / avg_s / 1e9
-            # the blends issue VALU, not HBM, at their limit: issue rate against
-            # the chip's wave64 instruction rate
-            roofline["valu"] = {"insts_per_launch": va["valu_insts_per_launch"],
-                                "achieved_ginst_s": round(g, 1), "peak_ginst_s": VALU_PEAK_GINST,
-                                "frac": round(g / VALU_PEAK_GINST, 4)}
+    roofline = dominant_roofline(dominant, per_stage, N, M, W, H, workload) if dominant else None
 
     value = 1000.0 / total
     out = {
@@ -617,7 +701,7 @@ def main() -> int:
                                 f"coefficients, seed 0), {W}x{H}, forward + backward "
                                 f"(loss = image.sum())") if args.scene == "bench" else
                                f"rasterizer baseline config {sc.name}, forward + backward "
-                               f"(loss = image.sum())",
+                               f"(loss = {'image.sum()' if G is None else 'dL/dimage N(0,1)'})",
                    "gaussians": N, "width": W, "height": H, "pairs": M, "tiles": _tiles(W, H)},
         "fwd_ms": round(fwd, 4), "bwd_ms": round(bwd, 4),
         "fps_forward": round(1000.0 / fwd, 1),

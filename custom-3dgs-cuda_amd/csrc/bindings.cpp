@@ -801,6 +801,14 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     // the reference surface.
     m.def("profile_enable", [](bool on) { gsr_profile_enable(on ? 1 : 0); });
     m.def("profile_reset", []() { gsr_profile_reset(); });
+    // VALU issue-rate calibration kernels (measurement support for bench.py)
+    m.def("calibrate_valu", [](int kind, int iters) {
+        auto out = torch::empty({(int64_t)gsr_calibrate_valu_out_floats()},
+                                torch::dtype(torch::kFloat32).device(torch::kCUDA));
+        check_rc(gsr_calibrate_valu(kind, iters, out.data_ptr<float>(), current_stream()),
+                 "calibrate_valu");
+        return out;
+    }, py::arg("kind"), py::arg("iters"));
     m.def("profile_collect", []() {
         check_rc(gsr_profile_collect(), "profile_collect");
         py::dict out;

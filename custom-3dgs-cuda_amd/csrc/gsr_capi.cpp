@@ -671,6 +671,18 @@ int gsr_debug_raise_status(int bits, void* stream) {
     return GSR_OK;
 }
 
+size_t gsr_calibrate_valu_out_floats(void) {
+    return (size_t)gsr::calibrate_valu_blocks() * 256;
+}
+
+int gsr_calibrate_valu(int kind, int iters, float* out, void* stream) {
+    GSR_REQUIRE(kind >= 0 && kind <= 4, "kind must be 0..4");
+    GSR_REQUIRE(iters >= 1 && iters <= 65536, "iters must be 1..65536");
+    GSR_REQUIRE(out != nullptr, "out is null");
+    GSR_HIP(gsr::launch_calibrate_valu(kind, iters, out, as_stream(stream)), "calibrate valu");
+    return GSR_OK;
+}
+
 size_t gsr_backward_workspace_bytes(int n, int64_t num_pairs, int height, int width) {
     return backward_layout(n, num_pairs, height, width).end;
 }

@@ -25,6 +25,12 @@ hipError_t device_globals(DeviceGlobals* out);
 // ORs bits into a status word from a one-thread kernel (a test hook).
 hipError_t launch_raise_status(int* status, int bits, hipStream_t st);
 
+// VALU issue-rate calibration kernels (gsr_calibrate.hip): kind 0 add, 1 fma,
+// 2 exp, 3 permlane swaps, 4 DPP add; calibrate_valu_blocks() work-groups of
+// 256 threads, one float of `out` per thread.
+int calibrate_valu_blocks();
+hipError_t launch_calibrate_valu(int kind, int iters, float* out, hipStream_t st);
+
 hipError_t launch_project_fwd(int n, const float* mu, const float* q, const float* s,
                               const float* rot, const float* tr, float fx, float fy, float cx,
                               float cy, float* mean2d, float* cov2d, float* depth,

@@ -121,6 +121,17 @@ int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream);
  * handling of GSR_ERR_DEVICE. */
 int gsr_debug_raise_status(int bits, void* stream);
 
+/* Measurement support (no counterpart in the reference): launches one VALU
+ * issue-rate calibration kernel on `stream`.  kind: 0 v_add_f32, 1 v_fma_f32,
+ * 2 v_exp_f32, 3 v_permlane32/16_swap, 4 v_add_f32 with a DPP row rotate;
+ * every lane runs 8 independent chains of `iters` (1..65536) steps, and the
+ * grid is gsr_calibrate_valu_out_floats() / 256 work-groups of 256 threads,
+ * each thread storing one float to `out`.  rocprofv3 issue counters of these
+ * kernels give the practical VALU ceiling that bench.py reads the blends
+ * against. */
+size_t gsr_calibrate_valu_out_floats(void);
+int gsr_calibrate_valu(int kind, int iters, float* out, void* stream);
+
 /* Replaces launch_backward_rasterization (csrc/backward/rasterize_backward.h:5,
  * csrc/backward/rasterize_backward.cu:239-309; bound as
  * `backwards_rasterization` at csrc/bindings.cpp:72-100,147).  num_pairs is

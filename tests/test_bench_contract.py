@@ -61,3 +61,57 @@ def test_binning_summary_sums_the_binning_stages_only():
     assert s["ms"] == pytest.approx(0.1)
     ref = bench.reference_binning_bytes(100_000, 13_000_000, 1920, 1080)
     assert s["reference_equiv_GBps"] == pytest.approx(ref / 1e-4 / 1e9, rel=1e-3)
+
+
+def test_valu_peak_is_the_published_fp32_figure_per_packed_wave64_fma():
+    # 157.3 TFLOP/s fp32 / (64 lanes x 2 flops x 2 packed) = 614.4 G issues/s
+    assert bench.VALU_PEAK_GISSUE == pytest.approx(157.3e12 / 256 / 1e9, rel=1e-3)
+
+
+def _fake_profiles(monkeypatch, traffic=None, valu=None):
+    def fake(kind, workload):
+        return {"traffic": traffic, "valu": valu}.get(kind)
+    monkeypatch.setattr(bench, "_profile_json", fake)
+
+
+def test_stage_rates_use_measured_bytes_and_never_a_formula_for_the_blends(monkeypatch):
+    _fake_profiles(monkeypatch, traffic={"stages": {"blend_bwd": {"bytes_per_call": 1.5e8},
+                                                    "tile_binning": {"bytes_per_call": 1.1e8}}})
+    st = {"blend_bwd": (10, 2.5), "blend_fwd": (10, 1.8), "tile_binning": (10, 0.5),
+          "bin_count": (10, 0.2)}
+    r = bench._stage_rates(st, 100_000, 13_000_000, 1920, 1080, workload="w")
+    assert r["blend_bwd"]["bytes"] == "measured" and r["blend_bwd"]["bound"] == "valu"
+    assert r["blend_bwd"]["GBps"] == pytest.approx(1.5e8 / 0.25e-3 / 1e9, rel=1e-3)
+    # no measured traffic for the forward blend: no HBM rate at all
+    assert r["blend_fwd"]["pct_hbm_peak"] is None and r["blend_fwd"]["bound"] == "valu"
+    assert r["tile_binning"]["bytes"] == "measured"
+    assert r["bin_count"]["bytes"] == "formula"
+    assert r["bin_count"]["GBps"] == pytest.approx(
+        bench.stage_bytes("bin_count", 100_000, 13_000_000, 1920, 1080) / 0.02e-3 / 1e9, rel=1e-3)
+
+
+def test_blend_roofline_is_valu_issue_from_the_profile(monkeypatch):
+    _fake_profiles(monkeypatch, traffic={"stages": {"blend_bwd": {"bytes_per_call": 1.46e8}}},
+                   valu={"kernels": {"blend_bwd": {"issue_quads_per_launch": 1.255e8,
+                                                   "insts_per_launch": 1.55e8,
+                                                   "issue_util": 0.816, "clock_mhz": 2253}},
+                         "calibration": {"fma": {"issue_util": 0.938}}})
+    per = {"blend_bwd": {"ms": 0.257}}
+    r = bench.dominant_roofline("blend_bwd", per, 100_000, 13_482_333, 1920, 1080, "w")
+    assert r["bound"] == "valu" and r["peak"] == bench.VALU_PEAK_GISSUE
+    assert r["achieved"] == pytest.approx(1.255e8 / 0.257e-3 / 1e9, rel=1e-3)
+    assert r["frac"] == pytest.approx(r["achieved"] / bench.VALU_PEAK_GISSUE, rel=1e-3)
+    assert r["traffic"] == 1.46e8 and r["hbm_measured"]["frac"] < 0.2
+    assert r["equivalent"]["bytes"] == bench.stage_bytes("blend_bwd", 100_000, 13_482_333,
+                                                          1920, 1080)
+    assert r["calibration_issue_util"] == {"fma": 0.938}
+
+
+def test_committed_profiles_cover_the_bench_roofline():
+    t = bench._profile_json("traffic", "bench_100k_1920x1080")
+    v = bench._profile_json("valu", "bench_100k_1920x1080")
+    assert t and t["stages"]["blend_bwd"]["bytes_per_call"] > 0
+    assert v and v["kernels"]["blend_bwd"]["issue_quads_per_launch"] > 0
+    assert 0 < v["kernels"]["blend_bwd"]["issue_util"] <= 1.0
+    for c in v["calibration"].values():
+        assert 0.8 < c["issue_util"] <= 1.0
