@@ -483,56 +483,52 @@ def frame_stages(sc, steps: int, binning: str | None = None) -> dict:
             "stages": rates}
 
 
-def band_pair_counts(sc, band_height: int) -> list[int]:
-    """Each screen band's pair count, the bands rendered as rasterize_bands does
-    (the frame's projection, means moved up by the band's first row)."""
+def band_plan(sc, band_height: int | None):
+    """The bands rasterize_bands renders config ``sc``'s frame in, and each
+    band's pair count (the frame's pairs per tile row summed over the band)."""
     import torch
     import custom_rasterizer_cuda as crc
-    from gaussian_splatting.rasterizer.bands import band_rows
+    from gaussian_splatting.rasterizer.bands import band_rows, plan_bands
 
     g, v = sc.gaussians, sc.view
-    out = []
+    H, W = int(v["height"]), int(v["width"])
     with torch.no_grad():
         n = g.mu.shape[0]
-        m2, c2, d = crc.project(n, g.mu.detach(), g.q.detach(), g.s.detach(), v["R"], v["T"],
+        m2, c2, _ = crc.project(n, g.mu.detach(), g.q.detach(), g.s.detach(), v["R"], v["T"],
                                 float(v["fx"]), float(v["fy"]), float(v["cx"]), float(v["cy"]))
-        col = crc.SH(n, (-(v["R"].T @ v["T"])).contiguous(), g.mu.detach(), g.A.detach(),
-                     g.k_j.detach())
-        op = torch.sigmoid(g.alpha.detach())
-        for y0, h in band_rows(int(v["height"]), band_height):
-            mb = m2 - m2.new_tensor([0.0, float(y0)])
-            out.append(int(crc.rasterize(n, d, mb, c2, col, op, h, int(v["width"]))[1].numel()))
-    return out
+        rows = crc.tile_row_pairs(n, m2, c2, H, W).cpu().tolist()
+    plan = plan_bands(rows, H) if band_height is None else band_rows(H, band_height)
+    return plan, [sum(rows[y0 // 16:(y0 + h + 15) // 16]) for y0, h in plan]
 
 
-def banded_frame(sc, band_height: int, steps: int) -> dict:
+def banded_frame(sc, band_height: int | None, steps: int) -> dict:
     """fwd+bwd of a frame beyond the int32 pair lists, rendered as screen bands
-    of ``band_height`` rows through the unchanged surface (rasterize_bands):
+    through the unchanged surface (rasterize_bands): bands planned from the
+    frame's pairs per tile row (band_height None) or of ``band_height`` rows;
     frame time, the stage breakdown and each band's pair count."""
     import torch
     from gaussian_splatting.rasterizer.bands import rasterize_bands
 
     render = lambda g, v: rasterize_bands(g, v, band_height)
-    print(f"[bench] {sc.name}: {steps} banded frame(s), bands of {band_height} rows",
+    plan, pairs = band_plan(sc, band_height)
+    print(f"[bench] {sc.name}: {steps} banded frame(s), {len(plan)} bands "
+          f"({'planned' if band_height is None else f'{band_height} rows'})",
           file=sys.stderr, flush=True)
     G = config_grad(sc)
     fwd, bwd, total, _ = time_frames(sc, steps, 1, profile=False, render=render, grad=G)
     _, _, _, stages = time_frames(sc, 1, 0, profile=True, render=render, grad=G)
-    print(f"[bench] {sc.name}: {total:.1f} ms per frame; counting pairs per band",
-          file=sys.stderr, flush=True)
-    pairs = band_pair_counts(sc, band_height)
+    print(f"[bench] {sc.name}: {total:.1f} ms per frame", file=sys.stderr, flush=True)
     torch.cuda.empty_cache()
     v = sc.view
-    M = sum(pairs)
-    bands = len(pairs)
-    # per-stage rates: a stage's calls cover all bands, so per frame it moves
-    # the bytes of the whole frame (per-Gaussian stages once per band)
     rates = {}
     for name, (count, ms) in stages.items():  # one profiled frame
         rates[name] = {"ms_per_frame": round(ms, 3), "calls": int(count)}
     return {"fwd_ms": round(fwd, 3), "bwd_ms": round(bwd, 3), "ms_per_frame": round(total, 3),
-            "fps": round(1000.0 / total, 2), "pairs": M, "bands": bands,
-            "band_height": band_height, "max_band_pairs": max(pairs),
+            "fps": round(1000.0 / total, 2), "pairs": sum(pairs), "bands": len(plan),
+            "band_rows": [h for _, h in plan], "band_pairs": pairs,
+            "band_plan": "pairs per tile row, at most (2^31 - 2^16) x 127/128 per band"
+            if band_height is None else f"{band_height} rows",
+            "max_band_pairs": max(pairs),
             "stages": rates, "width": v["width"], "height": v["height"], "gaussians": sc.n}
 
 
@@ -616,8 +612,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-c5", action="store_true",
                     help="skip config c5 (5M Gaussians, 3840x2160, timed in screen bands)")
-    ap.add_argument("--band-height", type=int, default=128,
-                    help="rows per screen band of the c5 frame (a multiple of 16)")
+    ap.add_argument("--band-height", type=int, default=0,
+                    help="rows per screen band of the c5 frame (a multiple of 16); 0 (default): "
+                         "bands planned from the frame's pairs per tile row")
     ap.add_argument("--no-extra", action="store_true", help="skip the 720p and c3 side runs")
     ap.add_argument("--no-scale", action="store_true",
                     help="skip the per-stage HBM measurements on configs c4 and c5")
@@ -751,7 +748,7 @@ def main() -> int:
         # config c5 (5M Gaussians, 3840x2160): ~1.1e10 pairs, beyond the int32
         # lists of the reference's surface, so rendered in screen bands
         c5 = synthetic.config_scene("c5", device=dev)
-        out["c5_banded"] = banded_frame(c5, args.band_height, max(1, min(args.steps, 3)))
+        out["c5_banded"] = banded_frame(c5, args.band_height or None, max(1, min(args.steps, 3)))
         del c5
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(sc)

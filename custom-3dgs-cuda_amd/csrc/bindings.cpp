@@ -288,7 +288,7 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization_impl(
     const Tensor& grad_output, const Tensor& mean_2d, const Tensor& cov_2d, const Tensor& colors,
     const Tensor& alpha, const Tensor& sorted_ids, const Tensor& tile_ranges,
     const Tensor& final_T, const Tensor& n_contrib, int num_gaussians, int height, int width,
-    bool strided) {
+    bool strided, const std::vector<Tensor>* accumulate = nullptr) {
     if (strided) {
         CHECK_CUDA(grad_output);
         CHECK_FP32(grad_output);
@@ -322,15 +322,42 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization_impl(
 
     c10::hip::HIPGuardMasqueradingAsCUDA guard(mean_2d.device());
     auto options = torch::TensorOptions().dtype(torch::kFloat32).device(mean_2d.device());
-    Tensor grad_mean_2d = torch::empty({num_gaussians, 2}, options);
-    Tensor grad_cov_2d = torch::empty({num_gaussians, 3}, options);
-    Tensor grad_colors = torch::empty({num_gaussians, 3}, options);
-    Tensor grad_alpha = torch::empty({num_gaussians, 1}, options);
+    Tensor grad_mean_2d, grad_cov_2d, grad_colors, grad_alpha;
+    if (accumulate) {
+        TORCH_CHECK(accumulate->size() == 4, "accumulate_into must hold 4 tensors");
+        const int64_t widths[4] = {2, 3, 3, 1};
+        for (int k = 0; k < 4; ++k) {
+            const Tensor& a = (*accumulate)[k];
+            CHECK_INPUT_FP32(a);
+            TORCH_CHECK(a.numel() == widths[k] * num_gaussians && a.device() == mean_2d.device(),
+                        "accumulate_into tensors must be d mean2d [N,2], d cov2d [N,3], "
+                        "d colors [N,3], d alpha [N,1] on the inputs' device");
+        }
+        grad_mean_2d = (*accumulate)[0];
+        grad_cov_2d = (*accumulate)[1];
+        grad_colors = (*accumulate)[2];
+        grad_alpha = (*accumulate)[3];
+    } else {
+        grad_mean_2d = torch::empty({num_gaussians, 2}, options);
+        grad_cov_2d = torch::empty({num_gaussians, 3}, options);
+        grad_colors = torch::empty({num_gaussians, 3}, options);
+        grad_alpha = torch::empty({num_gaussians, 1}, options);
+    }
     Tensor ws =
         workspace((int64_t)gsr_backward_workspace_bytes(num_gaussians, sorted_ids.numel(),
                                                          height, width),
                   mean_2d);
-    if (strided) {
+    if (accumulate) {
+        check_rc(gsr_rasterize_backward_accumulate(
+                     num_gaussians, height, width, cfp(grad_output), grad_output.stride(0),
+                     grad_output.stride(1), grad_output.stride(2), cfp(mean_2d), cfp(cov_2d),
+                     cfp(colors), cfp(alpha), sorted_ids.data_ptr<int32_t>(), sorted_ids.numel(),
+                     tile_ranges.data_ptr<int32_t>(), cfp(final_T),
+                     n_contrib.data_ptr<int32_t>(), ws.data_ptr(), (size_t)ws.numel(),
+                     fp(grad_mean_2d), fp(grad_cov_2d), fp(grad_colors), fp(grad_alpha),
+                     current_stream()),
+                 "backwards_rasterization_accumulate");
+    } else if (strided) {
         check_rc(gsr_rasterize_backward_strided(
                      num_gaussians, height, width, cfp(grad_output), grad_output.stride(0),
                      grad_output.stride(1), grad_output.stride(2), cfp(mean_2d), cfp(cov_2d),
@@ -369,6 +396,17 @@ std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization_strided(
     return backwards_rasterization_impl(grad_output, mean_2d, cov_2d, colors, alpha, sorted_ids,
                                         tile_ranges, final_T, n_contrib, num_gaussians, height,
                                         width, true);
+}
+
+// strided, adding into the four given gradient tensors (screen bands)
+std::tuple<Tensor, Tensor, Tensor, Tensor> backwards_rasterization_accumulate(
+    const Tensor grad_output, const Tensor mean_2d, const Tensor cov_2d, const Tensor colors,
+    const Tensor alpha, const Tensor sorted_ids, const Tensor tile_ranges, const Tensor final_T,
+    const Tensor n_contrib, int num_gaussians, int height, int width,
+    std::vector<Tensor> accumulate_into) {
+    return backwards_rasterization_impl(grad_output, mean_2d, cov_2d, colors, alpha, sorted_ids,
+                                        tile_ranges, final_T, n_contrib, num_gaussians, height,
+                                        width, true, &accumulate_into);
 }
 
 // ---- backwards_SH (bindings.cpp:102-116 / delight_backward.cu:176-218) ----
@@ -756,6 +794,9 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
           "3DGS backward rasterization (HIP, gfx950)");
     m.def("backwards_rasterization_strided", &backwards_rasterization_strided,
           "glue: backwards_rasterization with grad_output any (H, W, 3) view, no copy");
+    m.def("backwards_rasterization_accumulate", &backwards_rasterization_accumulate,
+          "glue: backwards_rasterization_strided adding into accumulate_into "
+          "(d mean2d, d cov2d, d colors, d alpha) in place; returns them");
     m.def("backwards_SH", &backwards_SH, "3DGS backward spherical harmonics (HIP, gfx950)");
     m.def("backwards_projection", &backwards_projection,
           "3DGS backward projection (HIP, gfx950)");
@@ -801,6 +842,20 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     // the reference surface.
     m.def("profile_enable", [](bool on) { gsr_profile_enable(on ? 1 : 0); });
     m.def("profile_reset", []() { gsr_profile_reset(); });
+    // pairs per tile row, for planning screen bands (no reference counterpart)
+    m.def("tile_row_pairs", [](int64_t n, const Tensor& mean_2d, const Tensor& cov_2d,
+                               int64_t height, int64_t width) {
+        CHECK_INPUT_FP32(mean_2d);
+        CHECK_INPUT_FP32(cov_2d);
+        const int64_t ty = (height + 15) / 16;
+        auto rows = torch::empty({ty + 1}, mean_2d.options().dtype(torch::kInt64));
+        check_rc(gsr_tile_row_pairs((int)n, mean_2d.data_ptr<float>(), cov_2d.data_ptr<float>(),
+                                    (int)height, (int)width,
+                                    reinterpret_cast<uint64_t*>(rows.data_ptr<int64_t>()),
+                                    current_stream()),
+                 "tile_row_pairs");
+        return rows.narrow(0, 0, ty);
+    }, py::arg("n"), py::arg("mean_2d"), py::arg("cov_2d"), py::arg("height"), py::arg("width"));
     // VALU issue-rate calibration kernels (measurement support for bench.py)
     m.def("calibrate_valu", [](int kind, int iters) {
         auto out = torch::empty({(int64_t)gsr_calibrate_valu_out_floats()},

@@ -191,6 +191,65 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     }
 }
 
+// Pairs per tile row of the frame, for planning screen bands: each Gaussian's
+// rectangle (tile_rect, as bin_count_kernel forms it) adds its width to the
+// rows it spans, through a per-work-group difference array in LDS flushed
+// with one 64-bit atomic per non-zero entry into diff[0 .. tiles_y].
+constexpr int kMaxRowTiles = 4096;  // 65535 rows / 16
+__global__ __launch_bounds__(kThreads) void row_pairs_kernel(int n,
+                                                             const float* __restrict__ mean2d,
+                                                             const float* __restrict__ cov2d,
+                                                             int H, int W,
+                                                             unsigned long long* __restrict__ diff) {
+    __shared__ unsigned long long s_diff[kMaxRowTiles + 1];
+    const int tiles_y = (H + 15) / 16;
+    for (int j = threadIdx.x; j <= tiles_y; j += kThreads) s_diff[j] = 0ull;
+    __syncthreads();
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
+        const TileRect r = tile_rect(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1],
+                                     cov2d[3 * (size_t)i], cov2d[3 * (size_t)i + 1],
+                                     cov2d[3 * (size_t)i + 2], W, H);
+        const int w = r.ok ? max(0, r.x1 - r.x0) : 0;
+        if (w > 0 && r.y1 > r.y0) {
+            atomicAdd(&s_diff[r.y0], (unsigned long long)w);
+            atomicAdd(&s_diff[r.y1], (unsigned long long)(-(long long)w));
+        }
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j <= tiles_y; j += kThreads) {
+        const unsigned long long v = s_diff[j];
+        if (v) atomicAdd(&diff[j], v);
+    }
+}
+
+// In place: diff[0 .. tiles_y) becomes its inclusive prefix sums (the pairs of
+// each tile row).  One work-group.
+__global__ __launch_bounds__(kThreads) void row_pairs_scan_kernel(
+    int tiles_y, unsigned long long* __restrict__ rows) {
+    __shared__ unsigned long long s_carry;
+    __shared__ unsigned long long s_w[kThreads / kWave];
+    if (threadIdx.x == 0) s_carry = 0ull;
+    __syncthreads();
+    for (int b = 0; b < tiles_y; b += kThreads) {
+        const int j = b + (int)threadIdx.x;
+        unsigned long long v = j < tiles_y ? rows[j] : 0ull;
+        // inclusive scan over the work-group: waves, then wave totals
+        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+        for (int off = 1; off < 64; off <<= 1) {
+            const unsigned long long o = __shfl_up(v, off, kWave);
+            if (lane >= off) v += o;
+        }
+        if (lane == 63) s_w[wave] = v;
+        __syncthreads();
+        unsigned long long pre = s_carry;
+        for (int k = 0; k < wave; ++k) pre += s_w[k];
+        if (j < tiles_y) rows[j] = pre + v;
+        __syncthreads();
+        if (threadIdx.x == kThreads - 1) s_carry = pre + v;
+        __syncthreads();
+    }
+}
+
 // part_rank[p] = the depth rank whose pairs include sort slot p * kSortPartition;
 // part_rank[nparts] = one past the last rank with pairs.
 __global__ __launch_bounds__(kThreads) void partition_starts_kernel(
@@ -312,6 +371,24 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
                        depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist,
                        depth_hist, bg, block_hist, pair_total, block_start, seg_start, done,
                        block_hist ? host_total : nullptr, status);
+    return hipGetLastError();
+}
+
+hipError_t launch_row_pairs(int n, const float* mean2d, const float* cov2d, int H, int W,
+                            uint64_t* rows, hipStream_t st) {
+    const int tiles_y = (H + 15) / 16;
+    if (tiles_y > kMaxRowTiles) return hipErrorInvalidValue;
+    hipError_t e = zero_fill(rows, (size_t)(tiles_y + 1) * sizeof(uint64_t), st);
+    if (e != hipSuccess) return e;
+    if (n > 0) {
+        const unsigned blocks = std::min(blocks_for(n), 1024u);
+        hipLaunchKernelGGL(row_pairs_kernel, dim3(blocks), dim3(kThreads), 0, st, n, mean2d,
+                           cov2d, H, W, reinterpret_cast<unsigned long long*>(rows));
+        e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    hipLaunchKernelGGL(row_pairs_scan_kernel, dim3(1), dim3(kThreads), 0, st, tiles_y,
+                       reinterpret_cast<unsigned long long*>(rows));
     return hipGetLastError();
 }
 

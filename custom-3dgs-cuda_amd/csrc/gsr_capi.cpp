@@ -647,6 +647,18 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
     return GSR_OK;
 }
 
+int gsr_tile_row_pairs(int n, const float* mean2d, const float* cov2d, int height, int width,
+                       uint64_t* rows, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (int rc = check_screen(height, width)) return rc;
+    GSR_REQUIRE(tiles_y_of(height) <= 4096, "height must be at most 65536");
+    GSR_REQUIRE(rows != nullptr, "rows is null");
+    GSR_REQUIRE(n == 0 || (mean2d && cov2d), "null pointer");
+    GSR_HIP(gsr::launch_row_pairs(n, mean2d, cov2d, height, width, rows, as_stream(stream)),
+            "tile row pairs");
+    return GSR_OK;
+}
+
 int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream) {
     (void)bin_ws;
     (void)bin_ws_bytes;
@@ -696,7 +708,8 @@ int rasterize_backward(int n, int height, int width, const float* grad_img,
                        const float* colors, const float* alpha, const int32_t* sorted_ids,
                        int64_t num_pairs, const int32_t* tile_ranges, const float* final_T,
                        const int32_t* n_contrib, void* ws, size_t ws_bytes, float* d_mean2d,
-                       float* d_cov2d, float* d_colors, float* d_alpha, void* stream) {
+                       float* d_cov2d, float* d_colors, float* d_alpha, void* stream,
+                       bool accumulate = false) {
     GSR_REQUIRE(n >= 0, "n must be non-negative");
     if (int rc = check_screen(height, width)) return rc;
     GSR_REQUIRE(num_pairs >= 0 && num_pairs <= kMaxPairs, "num_pairs out of range");
@@ -711,10 +724,12 @@ int rasterize_backward(int n, int height, int width, const float* grad_img,
     if (work)
         GSR_REQUIRE(grad_img && sorted_ids && tile_ranges && final_T && n_contrib, "null pointer");
     gsr::FillList clear;
-    clear.add(d_mean2d, 8 * (size_t)n);
-    clear.add(d_cov2d, 12 * (size_t)n);
-    clear.add(d_colors, 12 * (size_t)n);
-    clear.add(d_alpha, 4 * (size_t)n);
+    if (!accumulate) {
+        clear.add(d_mean2d, 8 * (size_t)n);
+        clear.add(d_cov2d, 12 * (size_t)n);
+        clear.add(d_colors, 12 * (size_t)n);
+        clear.add(d_alpha, 4 * (size_t)n);
+    }
     if (work) clear.add(at<void>(ws, L.ctl), L.ctl_end - L.ctl);
     GSR_HIP(gsr::zero_fill(clear, st), "backward: clear");
     if (!work) return GSR_OK;
@@ -800,6 +815,25 @@ int gsr_rasterize_backward_strided(int n, int height, int width, const float* gr
     return rasterize_backward(n, height, width, grad_img, gst, mean2d, cov2d, colors, alpha,
                               sorted_ids, num_pairs, tile_ranges, final_T, n_contrib, ws,
                               ws_bytes, d_mean2d, d_cov2d, d_colors, d_alpha, stream);
+}
+
+int gsr_rasterize_backward_accumulate(int n, int height, int width, const float* grad_img,
+                                      int64_t grad_stride_h, int64_t grad_stride_w,
+                                      int64_t grad_stride_c, const float* mean2d,
+                                      const float* cov2d, const float* colors,
+                                      const float* alpha, const int32_t* sorted_ids,
+                                      int64_t num_pairs, const int32_t* tile_ranges,
+                                      const float* final_T, const int32_t* n_contrib, void* ws,
+                                      size_t ws_bytes, float* d_mean2d, float* d_cov2d,
+                                      float* d_colors, float* d_alpha, void* stream) {
+    gsr::GradStrides gst;
+    gst.h = grad_stride_h;
+    gst.w = grad_stride_w;
+    gst.c = grad_stride_c;
+    return rasterize_backward(n, height, width, grad_img, gst, mean2d, cov2d, colors, alpha,
+                              sorted_ids, num_pairs, tile_ranges, final_T, n_contrib, ws,
+                              ws_bytes, d_mean2d, d_cov2d, d_colors, d_alpha, stream,
+                              /*accumulate=*/true);
 }
 
 int gsr_rasterize_backward_noalloc(int n, int height, int width, const float* grad_img,

@@ -189,6 +189,10 @@ hipError_t launch_range_keys(int T, const int32_t* ranges, const int32_t* ids, c
 // zero counter, left at zero) and, when host_total is not null, the final pair
 // count stored to that host-mapped coherent word (block histogram mode only),
 // and the device status word (status, read and cleared) to host_total[1].
+// Pairs per tile row of an H x W frame (rows[tiles_y], needs tiles_y + 1
+// entries of room; tiles_y <= 4096).
+hipError_t launch_row_pairs(int n, const float* mean2d, const float* cov2d, int H, int W,
+                            uint64_t* rows, hipStream_t st);
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,

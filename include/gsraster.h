@@ -132,6 +132,15 @@ int gsr_debug_raise_status(int bits, void* stream);
 size_t gsr_calibrate_valu_out_floats(void);
 int gsr_calibrate_valu(int kind, int iters, float* out, void* stream);
 
+/* No counterpart in the reference (whose frames are limited to int32 pair
+ * lists): the (Gaussian, tile) pairs of each tile row of a height x width
+ * frame, rows[r] for r < ceil(height / 16), counted from each Gaussian's tile
+ * rectangle exactly as gsr_rasterize_bin counts them; for planning screen
+ * bands of at most a given number of pairs.  `rows` (device) needs
+ * ceil(height / 16) + 1 entries of room; height <= 65535. */
+int gsr_tile_row_pairs(int n, const float* mean2d, const float* cov2d, int height, int width,
+                       uint64_t* rows, void* stream);
+
 /* Replaces launch_backward_rasterization (csrc/backward/rasterize_backward.h:5,
  * csrc/backward/rasterize_backward.cu:239-309; bound as
  * `backwards_rasterization` at csrc/bindings.cpp:72-100,147).  num_pairs is
@@ -166,6 +175,24 @@ int gsr_rasterize_backward_strided(int n, int height, int width, const float* gr
                                    const int32_t* n_contrib, void* ws, size_t ws_bytes,
                                    float* d_mean2d, float* d_cov2d, float* d_colors,
                                    float* d_alpha, void* stream);
+
+/* No counterpart in the reference (whose frames are limited to int32 pair
+ * lists): gsr_rasterize_backward_strided that adds its gradients to what
+ * d_mean2d, d_cov2d, d_colors and d_alpha hold instead of overwriting them,
+ * for frames rendered as screen bands (one call per band into one set of
+ * outputs).  Each Gaussian's band total is added once, so the result is bit
+ * for bit the sum of the separate calls' outputs, added band by band, unless
+ * list entries without a gradient slot (pairs outside the Gaussian's tile
+ * rectangle, repeated ids) fall back to float atomics. */
+int gsr_rasterize_backward_accumulate(int n, int height, int width, const float* grad_img,
+                                      int64_t grad_stride_h, int64_t grad_stride_w,
+                                      int64_t grad_stride_c, const float* mean2d,
+                                      const float* cov2d, const float* colors,
+                                      const float* alpha, const int32_t* sorted_ids,
+                                      int64_t num_pairs, const int32_t* tile_ranges,
+                                      const float* final_T, const int32_t* n_contrib, void* ws,
+                                      size_t ws_bytes, float* d_mean2d, float* d_cov2d,
+                                      float* d_colors, float* d_alpha, void* stream);
 
 /* No counterpart in the reference: gsr_rasterize_backward for callers that
  * cannot allocate device memory (code under HIP graph capture, tight serving

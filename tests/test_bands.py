@@ -7,7 +7,7 @@ import numpy as np
 import pytest
 
 from gaussian_splatting import synthetic
-from gaussian_splatting.rasterizer.bands import band_rows, band_views
+from gaussian_splatting.rasterizer.bands import band_rows, band_views, plan_bands
 from helpers import oracle_forward, scene_arrays
 
 
@@ -61,3 +61,40 @@ def test_banded_oracle_frame_matches_the_whole_frame(orc, name, bh, kw):
     assert np.array_equal(np.concatenate(ncs), whole["n_contrib"])
     assert pairs == whole["ids"].size
     assert whole["n_contrib"].max() > 0
+
+
+def _band_pairs(rows, plan):
+    return [sum(rows[y0 // 16:(y0 + h + 15) // 16]) for y0, h in plan]
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_planned_bands_cover_the_frame_within_the_budget(seed):
+    """Planned bands are whole tile rows, contiguous, top to bottom, each
+    within the pair budget, as few as the budget allows (the total over the
+    budget, rounded up, or one more), and balanced: no band below a third of
+    an equal share unless it is the only way to meet the budget."""
+    rng = np.random.default_rng(seed)
+    H = 2160
+    rows = list(rng.integers(0, 2000, size=(H + 15) // 16) * rng.integers(1, 50))
+    budget = max(max(rows), sum(rows) // 5)
+    plan = plan_bands(rows, H, budget)
+    assert plan[0][0] == 0 and sum(h for _, h in plan) == H
+    for (a, ha), (b, _) in zip(plan, plan[1:]):
+        assert a + ha == b and ha % 16 == 0
+    bp = _band_pairs(rows, plan)
+    assert sum(bp) == sum(rows) and max(bp) <= budget
+    k = -(-sum(rows) // budget)
+    assert k <= len(plan) <= k + 1
+    assert min(bp) >= sum(rows) / len(plan) / 3
+
+
+def test_planned_bands_small_cases():
+    assert plan_bands([5, 5, 5, 5], 64, 100) == [(0, 64)]
+    assert plan_bands([5, 5, 5, 5], 60, 10) == [(0, 32), (32, 28)]
+    assert plan_bands([], 0, 10) == []
+    assert plan_bands([0, 0, 0], 48, 1) == [(0, 48)]
+    # a row over the budget cannot be split
+    with pytest.raises(ValueError):
+        plan_bands([3, 12, 3], 48, 10)
+    # uneven rows: bands cut where the running total reaches its share
+    assert _band_pairs([9, 1, 1, 9], plan_bands([9, 1, 1, 9], 64, 12)) == [10, 10]

@@ -17,7 +17,8 @@ import torch
 
 from gaussian_splatting import synthetic
 from gaussian_splatting.rasterizer import RasterizeFunction, rasterize, rasterize_bands
-from gaussian_splatting.rasterizer.bands import band_rows
+from gaussian_splatting.rasterizer.bands import (BAND_PAIR_BUDGET, MAX_BAND_PAIRS, band_rows,
+                                                  plan_bands)
 from helpers import assert_bitwise, oracle_forward, scene_arrays
 from oracle import oracle as orc
 from test_gpu_parity import _np, gpu_forward
@@ -77,6 +78,93 @@ def test_banded_glue_equals_the_whole_frame(device):
         assert err <= 1e-6, f"d {nm}: {err:.2e}"
 
 
+def _project(crc, g, view):
+    n = g.mu.shape[0]
+    with torch.no_grad():
+        m2, c2, d = crc.project(n, g.mu.detach(), g.q.detach(), g.s.detach(), view["R"],
+                                view["T"], view["fx"], view["fy"], view["cx"], view["cy"])
+        col = crc.SH(n, (-(view["R"].T @ view["T"])).contiguous(), g.mu.detach(), g.A.detach(),
+                     g.k_j.detach())
+    return n, m2, c2, d, col
+
+
+@pytest.mark.parametrize("name,kw", [("c3", dict(n=20_000, width=480, height=272)),
+                                     ("c5", dict(n=200_000, width=1000, height=600)),
+                                     ("bench", dict())])
+def test_tile_row_pairs_count_the_rasterizers_pairs(crc, device, name, kw):
+    """Pairs per tile row (the band planner's input) equal the row sums of the
+    tile ranges rasterize builds for the whole frame."""
+    sc = (synthetic.bench_scene(n=30_000, width=640, height=360, device=device)
+          if name == "bench" else synthetic.config_scene(name, device=device, **kw))
+    g, view = sc.gaussians, sc.view
+    H, W = int(view["height"]), int(view["width"])
+    n, m2, c2, d, col = _project(crc, g, view)
+    rows = crc.tile_row_pairs(n, m2, c2, H, W).cpu().numpy()
+    out = crc.rasterize(n, d, m2, c2, col, torch.sigmoid(g.alpha.detach()), H, W)
+    rng = _np(out[2]).reshape(-1, 2).astype(np.int64)
+    tx = (W + 15) // 16
+    want = (rng[:, 1] - rng[:, 0]).reshape(-1, tx).sum(axis=1)
+    assert rows.shape == want.shape and np.array_equal(rows, want)
+    assert rows.sum() == out[1].numel()
+    empty = crc.tile_row_pairs(0, m2[:0], c2[:0], H, W).cpu().numpy()
+    assert empty.shape == want.shape and not empty.any()
+
+
+def test_planned_bands_equal_the_whole_frame(crc, device):
+    """rasterize_bands with its planned bands (a pair budget of a third of the
+    frame's pairs: three or four bands) against rasterize: the image bit for
+    bit, the gradients within 1e-6 relative."""
+    sc = synthetic.config_scene("c3", device=device, n=20_000, width=480, height=272)
+    g, view = sc.gaussians, sc.view
+    n, m2, c2, d, col = _project(crc, g, view)
+    rows = crc.tile_row_pairs(n, m2, c2, 272, 480).cpu().tolist()
+    budget = max(max(rows), sum(rows) // 3)
+    plan = plan_bands(rows, 272, budget)
+    assert len(plan) >= 3
+    w = torch.linspace(0.5, 1.5, 480 * 272 * 3, device=device).view(272, 480, 3)
+
+    def run(render):
+        for nm in NAMES:
+            getattr(g, nm).grad = None
+        img = render()
+        (img * w).sum().backward()
+        return img.detach().clone(), [getattr(g, nm).grad.clone() for nm in NAMES]
+
+    bi, bg = run(lambda: rasterize_bands(g, view, max_pairs=budget))
+    wi, wg = run(lambda: rasterize(g, view))
+    assert_bitwise(_np(bi), _np(wi), "image")
+    for got, want, nm in zip(bg, wg, NAMES):
+        err = (got - want).norm() / want.norm().clamp_min(1e-30)
+        assert err <= 1e-6, f"d {nm}: {err:.2e}"
+
+
+def test_backward_accumulate_equals_the_band_sums(crc, device):
+    """backwards_rasterization_accumulate (one set of outputs, each band
+    added in place) against each band's own backward summed in torch in the
+    same order: bit for bit."""
+    sc = synthetic.config_scene("c3", device=device, n=20_000, width=480, height=272)
+    g, view = sc.gaussians, sc.view
+    n, m2, c2, d, col = _project(crc, g, view)
+    op = torch.sigmoid(g.alpha.detach())
+    G = synthetic.grad_image(272, 480, seed=3).to(device)
+    sums, acc = None, None
+    for y0, h in band_rows(272, 96):
+        mb = m2 - m2.new_tensor([0.0, float(y0)])
+        img, ids, rng, fT, nc = crc.rasterize(n, d, mb, c2, col, op, h, 480)
+        args = (G[y0:y0 + h], mb, c2, col, op, ids, rng, fT, nc, n, h, 480)
+        part = crc.backwards_rasterization_strided(*args)
+        sums = [x.clone() for x in part] if sums is None else [a + b for a, b in zip(sums, part)]
+        if acc is None:
+            acc = [x.clone() for x in part]
+        else:
+            out = crc.backwards_rasterization_accumulate(*args, acc)
+            assert all(o.data_ptr() == a.data_ptr() for o, a in zip(out, acc))
+    for a, b, nm in zip(acc, sums, ("mean2d", "cov2d", "colors", "alpha")):
+        assert_bitwise(_np(a), _np(b), f"d {nm}")
+    with pytest.raises(RuntimeError, match="accumulate_into"):
+        crc.backwards_rasterization_accumulate(*args, acc[:3])
+
+
 def test_bands_without_gaussians(device):
     """Every Gaussian above row 130 of a 272-row frame: of the 64-row bands,
     the last two hold no pair at all (empty lists through rasterize and its
@@ -106,9 +194,11 @@ def test_bands_without_gaussians(device):
 
 def test_c5_full_size_in_screen_bands(crc, device):
     """Config c5 at full size.  The whole frame needs more pairs than int32
-    lists hold and is refused; in 256-row bands every band fits, the pairs add
-    up to more than 2^31, the image is finite and in [0, 1], and the
-    gradients are finite and deterministic."""
+    lists hold and is refused; in 256-row bands every band fits and the pairs
+    add up to more than 2^31; the pairs per tile row add up to each band's;
+    the planned bands are fewer and each within the limit; the planned frame's
+    image is finite and in [0, 1], and its gradients are finite and
+    deterministic."""
     print("[gpu] c5 full size: 5M Gaussians, 3840x2160", flush=True)
     sc = synthetic.config_scene("c5", device=device)
     g, view = sc.gaussians, sc.view
@@ -128,11 +218,23 @@ def test_c5_full_size_in_screen_bands(crc, device):
             del out
     print(f"[gpu] c5 pairs per band: {pairs}", flush=True)
     assert sum(pairs) > 2**31 and max(pairs) < 2**31 - 65535
+    # the planned bands: the same pairs in fewer bands, each within the limit
+    # (a band below the first is rasterized from moved means, whose rounding
+    # can shift a far-away Gaussian's footprint: its count may differ by a few)
+    rows = crc.tile_row_pairs(n, m2, c2, view["height"], view["width"]).cpu().tolist()
+    assert sum(rows[:16]) == pairs[0]
+    for (y0, h), p in zip(band_rows(view["height"], 256), pairs):
+        assert abs(sum(rows[y0 // 16:(y0 + h + 15) // 16]) - p) <= 1e-6 * p
+    plan = plan_bands(rows, view["height"])
+    planned = [sum(rows[y0 // 16:(y0 + h + 15) // 16]) for y0, h in plan]
+    print(f"[gpu] c5 planned bands: {plan}, pairs {planned}", flush=True)
+    assert max(planned) <= BAND_PAIR_BUDGET < MAX_BAND_PAIRS and len(plan) < len(pairs)
+    del m2, c2, d, col
 
     def frame():
         for nm in NAMES:
             getattr(g, nm).grad = None
-        img = rasterize_bands(g, view, 256)
+        img = rasterize_bands(g, view)
         img.sum().backward()
         torch.cuda.synchronize()
         return img.detach(), [getattr(g, nm).grad.clone() for nm in NAMES]
