@@ -242,7 +242,7 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
     const int tile = order ? (int)order[blockIdx.x] : (int)blockIdx.x;
     // a launch order is a permutation of the tiles; nothing else is touched
     if ((unsigned)tile >= (unsigned)(tiles_x * ((H + kTileSize - 1) / kTileSize))) return;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // scalar: uniform branches
     const uint32_t my_bit = 1u << wave;
     const Pixels<kPix> pp = pixels_of<kPix>(tile, tiles_x, W, H);
@@ -256,11 +256,15 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
     }
     int start, end;
     clamp_range(ranges[tile], m, start, end);
+    // the range is the work-group's: scalar, so the loop counters are scalar
+    start = __builtin_amdgcn_readfirstlane(start);
+    end = __builtin_amdgcn_readfirstlane(end);
 
     // each batch's ids are loaded while the batch before it is blended
     int next_id = (start + tid < end) ? ids[start + tid] : -1;
     for (int b0 = start; b0 < end; b0 += kBatch) {
-        const int cnt = min(kBatch, end - b0);
+        // scalar, so the entry loop's counter is scalar
+        const int cnt = __builtin_amdgcn_readfirstlane(min(kBatch, end - b0));
         const int g = next_id;
         __syncthreads();
         if (tid < cnt)
@@ -269,14 +273,26 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
         __syncthreads();
         if (ballot(any_live(p)) != 0) {
             const int cbase = b0 - start + 1;
-            for (int j = 0; j < cnt; ++j) {
-                if ((uniform_bits(s_bits, j) & my_bit) == 0) continue;  // strip culled
-                const float4 A = s_a[j];
-                const float4 B = s_b[j];
-                const float cb = s_c[j].x;
+            // 64 entries at a time: one ballot gives the entries this wave's
+            // strip meets (lane e holds entry c0 + e), walked in order with a
+            // scalar find-first; strip-culled entries cost nothing
+            bool done = false;
+            for (int c0 = 0; c0 < cnt && !done; c0 += kWave) {
+                const int e = c0 + lane;
+                uint64_t todo = ballot(e < cnt && (s_bits[min(e, kBatch - 1)] & my_bit) != 0u);
+                while (todo) {
+                    const int j = c0 + (int)__builtin_ctzll(todo);
+                    todo &= todo - 1;
+                    const float4 A = s_a[j];
+                    const float4 B = s_b[j];
+                    const float cb = s_c[j].x;
 #pragma unroll
-                for (int k = 0; k < kPix; ++k) fwd_step(p[k], fx, fy[k], A, B, cb, cbase + j);
-                if (ballot(any_live(p)) == 0) break;
+                    for (int k = 0; k < kPix; ++k) fwd_step(p[k], fx, fy[k], A, B, cb, cbase + j);
+                    if (ballot(any_live(p)) == 0) {
+                        done = true;
+                        break;
+                    }
+                }
             }
         }
         if (__syncthreads_and(!any_live(p))) break;
@@ -353,9 +369,9 @@ __device__ __forceinline__ bool near_fast(const BwdDecision& d) {
 // threshold (one ballot per pixel of a single compare: no lane-mask
 // materialisation).
 template <int kPix>
-__device__ __forceinline__ void decide_entry(BwdDecision (&d)[kPix], float o, uint32_t bits,
+__device__ __forceinline__ void decide_entry(BwdDecision (&d)[kPix], float o, bool fast,
                                              int contributor, const BwdPixel (&p)[kPix]) {
-    bool exact = (bits & kFastExpBit) == 0;
+    bool exact = !fast;
     if (!exact) {
         uint64_t near = 0;
 #pragma unroll
@@ -453,6 +469,23 @@ constexpr int kSplitNum = 37, kSplitDen = 100;
 // Most tiles split per backward launch (the launch has this many extra groups).
 constexpr int kSplitMax = 256;
 
+// The entries of one 64-entry chunk of a staged batch [lo, lo + cnt) that a
+// wave walks, one ballot each: bit e of `walk` for entry c0 + e when it is in
+// the batch, within the wave's largest n_contrib and its strip bit is set;
+// bit e of `fast` for its fast-exp flag.  Lane e reads entry c0 + e's bits.
+struct ChunkMasks {
+    uint64_t walk, fast;
+};
+template <int kBatch>
+__device__ __forceinline__ ChunkMasks chunk_masks(const float4* s_c, int c0, int cnt, int lo,
+                                                  int wave_last, uint32_t my_bit) {
+    const int e = c0 + (int)(threadIdx.x & 63);
+    const bool in = e < cnt;
+    const uint32_t b = in ? __float_as_uint(s_c[min(e, kBatch - 1)].w) : 0u;
+    return ChunkMasks{ballot(in && lo + e + 1 <= wave_last && (b & my_bit) != 0u),
+                      ballot((b & kFastExpBit) != 0u)};
+}
+
 // The pixel state's walk over entries [lo0, hi0), back to front: the same
 // decisions and T / accumulated-colour steps as the full walk, no sums.
 template <int kPix, int kBatch>
@@ -471,26 +504,30 @@ __device__ __forceinline__ void state_walk(int lo0, int hi0, int n, int tile, in
             stage_entry<kPix>(recs, ids[start + lo + tid], n, tile, tiles_x, s_a, s_b, s_c,
                               nullptr, nullptr, tid);
         __syncthreads();
-        for (int j = cnt - 1; j >= 0; --j) {
-            const int contributor = lo + j + 1;
-            const float4 Cc = s_c[j];
-            const uint32_t bits = uniform_bits(Cc);
-            if (contributor > wave_last || (bits & my_bit) == 0) continue;
-            const float4 A = s_a[j];
-            const float4 B = s_b[j];
-            const float dx = fx - A.x;
-            const float adxdx = (A.z * dx) * dx;
-            const float bdx = A.w * dx;
-            BwdDecision d[kPix];
+        for (int chunk = ((cnt - 1) / kWave) * kWave; chunk >= 0; chunk -= kWave) {
+            const ChunkMasks cm = chunk_masks<kBatch>(s_c, chunk, cnt, lo, wave_last, my_bit);
+            for (uint64_t todo = cm.walk; todo != 0;) {
+                const int jj = 63 - (int)__builtin_clzll(todo);  // back to front
+                todo ^= 1ull << jj;
+                const int j = chunk + jj;
+                const int contributor = lo + j + 1;
+                const float4 A = s_a[j];
+                const float4 B = s_b[j];
+                const float cb = s_c[j].x;
+                const float dx = fx - A.x;
+                const float adxdx = (A.z * dx) * dx;
+                const float bdx = A.w * dx;
+                BwdDecision d[kPix];
 #pragma unroll
-            for (int k = 0; k < kPix; ++k) {
-                d[k].dy = fy[k] - A.y;
-                d[k].power = __builtin_fmaf(B.x * d[k].dy, d[k].dy,
-                                            __builtin_fmaf(bdx, d[k].dy, adxdx));
+                for (int k = 0; k < kPix; ++k) {
+                    d[k].dy = fy[k] - A.y;
+                    d[k].power = __builtin_fmaf(B.x * d[k].dy, d[k].dy,
+                                                __builtin_fmaf(bdx, d[k].dy, adxdx));
+                }
+                decide_entry<kPix>(d, B.y, ((cm.fast >> jj) & 1u) != 0u, contributor, p);
+#pragma unroll
+                for (int k = 0; k < kPix; ++k) (void)bwd_update(p[k], d[k], B, cb);
             }
-            decide_entry<kPix>(d, B.y, bits, contributor, p);
-#pragma unroll
-            for (int k = 0; k < kPix; ++k) (void)bwd_update(p[k], d[k], B, Cc.x);
         }
     }
 }
@@ -589,14 +626,24 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
             if (tid < lo - nlo) next_id = ids[start + nlo + tid];
         }
         __syncthreads();
-        for (int j = cnt - 1; j >= 0; --j) {
-            const int contributor = lo + j + 1;
-            float w9 = 0.0f;
-            // wave-uniform skips: beyond every pixel's n_contrib, or culled
-            const float4 Cc = s_c[j];  // (b, conic.y, qthr, strip bits)
-            const uint32_t bits = uniform_bits(Cc);
-            if (contributor <= wave_last && (bits & my_bit) != 0) {
+        // this wave's partial sums of the batch start at zero: entries it does
+        // not walk (culled, or beyond its largest n_contrib) add nothing
+        for (int e = lane; e < cnt; e += kWave)
+#pragma unroll
+            for (int k = 0; k < kTerms; ++k) s_part[wave][k][e] = 0.0f;
+        // 64 entries at a time, back to front, the walked ones found with a
+        // scalar find-last over one ballot
+        for (int chunk = ((cnt - 1) / kWave) * kWave; chunk >= 0; chunk -= kWave) {
+            const ChunkMasks cm = chunk_masks<kBatch>(s_c, chunk, cnt, lo, wave_last, my_bit);
+            for (uint64_t todo = cm.walk; todo != 0;) {
+                const int jj = 63 - (int)__builtin_clzll(todo);
+                todo ^= 1ull << jj;
+                const int j = chunk + jj;
+                const int contributor = lo + j + 1;
+                float w9;
                 const float4 A = s_a[j];
+                const float4 Cc = s_c[j];  // (b, -cy/2, qthr, strip bits)
+                const float cb = Cc.x;
                 const float4 B = s_b[j];
                 const float dx = fx - A.x;
                 // blend_power's shared column terms: (a dx) dx and b dx
@@ -610,11 +657,11 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                     d[k].power = __builtin_fmaf(B.x * d[k].dy, d[k].dy,
                                                 __builtin_fmaf(bdx, d[k].dy, adxdx));
                 }
-                decide_entry<kPix>(d, B.y, bits, contributor, p);
+                decide_entry<kPix>(d, B.y, ((cm.fast >> jj) & 1u) != 0u, contributor, p);
                 // per-lane sums over its pixels, started from the first pixel's terms
                 float S0, P2, P5, c0, c1, c2;
                 {
-                    const BwdTerms t = bwd_update(p[0], d[0], B, Cc.x);
+                    const BwdTerms t = bwd_update(p[0], d[0], B, cb);
                     const float e = t.dpw * d[0].dy;
                     S0 = t.dpw;
                     P2 = e;
@@ -625,7 +672,7 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                 }
 #pragma unroll
                 for (int k = 1; k < kPix; ++k) {
-                    const BwdTerms t = bwd_update(p[k], d[k], B, Cc.x);
+                    const BwdTerms t = bwd_update(p[k], d[k], B, cb);
                     {
 #pragma clang fp contract(fast)
                         const float e = t.dpw * d[k].dy;
@@ -640,8 +687,8 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                 // a wave with no blending pixel (2% of the strip-passing
                 // wave-entries on the bench scene) sums zeros
                 w9 = wave_reduce_columns(S0, P2, P5, c0, c1, c2, dx);
+                if (my_value >= 0) s_part[wave][my_value][j] = w9;
             }
-            if (my_value >= 0) s_part[wave][my_value][j] = w9;
         }
         __syncthreads();
         if (tid < cnt) {
