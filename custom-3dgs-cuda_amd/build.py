@@ -78,7 +78,9 @@ def _hip_objects(jobs: int) -> list[Path]:
 def build_library(jobs: int = 8) -> Path:
     objs = _hip_objects(jobs)
     tmp = LIB.with_suffix(".so.tmp")
-    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)])
+    # -z defs: an undefined symbol fails the link, not the first import
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *map(str, objs),
+          "-o", str(tmp)])
     os.replace(tmp, LIB)
     return LIB
 

@@ -91,17 +91,13 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     const float* __restrict__ depth, int H, int W, uint32_t* __restrict__ counts,
     uint2* __restrict__ rects, uint32_t* __restrict__ dkeys, uint32_t* __restrict__ dvals,
     int passes, uint32_t* __restrict__ tile_hist, uint32_t* __restrict__ depth_hist,
-    BlockGrid bg, uint32_t* __restrict__ block_hist, uint64_t* __restrict__ pair_total,
-    uint32_t* __restrict__ block_start, uint32_t* __restrict__ seg_start,
-    uint32_t* __restrict__ done, uint64_t* __restrict__ host_total, int* __restrict__ status) {
+    BlockGrid bg, uint32_t* __restrict__ block_hist, uint64_t* __restrict__ pair_total) {
     __shared__ int s_d0[kRadixBins + 1];
     __shared__ uint32_t s_h[3][kRadixBins];
     __shared__ uint32_t s_dh[4][kRadixBins];
     __shared__ uint32_t s_bh[kMaxBlocks];
     __shared__ uint32_t s_full[kThreads / kWave];
     __shared__ uint32_t s_scan[kThreads / kWave];
-    __shared__ uint32_t s_v[kThreads / kWave];
-    __shared__ uint32_t s_flag;
     const int tid = threadIdx.x;
     const bool blocks = block_hist != nullptr;
     for (int j = tid; j <= kRadixBins; j += kThreads) s_d0[j] = 0;
@@ -166,29 +162,36 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
         const uint64_t wp = wave_sum_u64(pairs);
         if ((tid & 63) == 0 && wp) atomicAdd(reinterpret_cast<unsigned long long*>(pair_total),
                                              (unsigned long long)wp);
-        // the last work-group to finish turns the histogram into the starts
-        // and hands the final pair count to the host
-        if (last_group(done, &s_flag)) {
-            if (tid == 0 && host_total) {
-                const uint64_t total = __hip_atomic_load(pair_total, __ATOMIC_RELAXED,
-                                                         __HIP_MEMORY_SCOPE_AGENT);
-                // the device status word goes to the host with the count, and
-                // is cleared: each error is reported once
-                const int stat = status ? atomicExch(status, 0) : 0;
-                __hip_atomic_store(host_total + 1, (uint64_t)(uint32_t)stat, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_SYSTEM);
-                __hip_atomic_store(host_total, total, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_SYSTEM);
-                __threadfence_system();
-            }
-            block_starts_body<kThreads>(bg.nb, block_hist, block_start, seg_start, s_scan, s_v);
-        }
     }
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
         const uint32_t v = s_dh[p][tid];
         if (v) atomicAdd(&depth_hist[p * kRadixBins + tid], v);
     }
+}
+
+// Behind bin_count_kernel (block histogram mode), one work-group: the block
+// and segment starts from the block histogram, and the final pair count and
+// the device status word handed to the host.  A kernel of its own rather than
+// bin_count's last work-group: on this chip every work-group's agent-scope
+// release would write the L2 back once more.
+__global__ __launch_bounds__(kThreads) void bin_finish_kernel(
+    BlockGrid bg, const uint32_t* __restrict__ block_hist, const uint64_t* __restrict__ pair_total,
+    uint32_t* __restrict__ block_start, uint32_t* __restrict__ seg_start,
+    uint64_t* __restrict__ host_total, int* __restrict__ status) {
+    __shared__ uint32_t s_scan[kThreads / kWave];
+    __shared__ uint32_t s_v[kThreads / kWave];
+    if (threadIdx.x == 0 && host_total) {
+        const uint64_t total = *pair_total;
+        // the device status word goes to the host with the count, and is
+        // cleared: each error is reported once
+        const int stat = status ? atomicExch(status, 0) : 0;
+        __hip_atomic_store(host_total + 1, (uint64_t)(uint32_t)stat, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(host_total, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __threadfence_system();
+    }
+    block_starts_body<kThreads>(bg.nb, block_hist, block_start, seg_start, s_scan, s_v);
 }
 
 // Pairs per tile row of the frame, for planning screen bands: each Gaussian's
@@ -353,24 +356,27 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
-                            uint32_t* block_start, uint32_t* seg_start, uint32_t* done,
-                            uint64_t* host_total, int* status, hipStream_t st) {
+                            uint32_t* block_start, uint32_t* seg_start, uint64_t* host_total,
+                            int* status, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     if (tile_passes < 0 || tile_passes > 4) return hipErrorInvalidValue;
     const BlockGrid bg = block_grid((W + 15) / 16, (H + 15) / 16);
-    if (block_hist && (bg.nb > kMaxBlocks || !pair_total || !block_start || !seg_start || !done))
+    if (block_hist && (bg.nb > kMaxBlocks || !pair_total || !block_start || !seg_start))
         return hipErrorInvalidValue;
     // few work-groups: each flushes its histograms with one global atomic per
-    // bin and counts itself in behind a device-wide release.  One per two CUs
-    // up to 2^19 Gaussians; beyond, one per CU, so that each thread's
-    // grid-strided loop stays short (its loads are not overlapped across
-    // iterations).  At 1M Gaussians: 128 groups 170 us, 256 150 us, 512 157 us,
-    // 1024 199 us (bin_count + depth sort).
+    // bin.  One per two CUs up to 2^19 Gaussians; beyond, one per CU, so that
+    // each thread's grid-strided loop stays short (its loads are not
+    // overlapped across iterations).  At 1M Gaussians: 128 groups 170 us, 256
+    // 150 us, 512 157 us, 1024 199 us (bin_count + depth sort); at 100k, 64
+    // groups 21.0 us, 128 20.0, 256 27.5 (bin_count).
     const unsigned blocks = std::min(blocks_for(n), n >= (1 << 19) ? 256u : 128u);
     hipLaunchKernelGGL(bin_count_kernel, dim3(blocks), dim3(kThreads), 0, st, n, mean2d, cov2d,
                        depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist,
-                       depth_hist, bg, block_hist, pair_total, block_start, seg_start, done,
-                       block_hist ? host_total : nullptr, status);
+                       depth_hist, bg, block_hist, pair_total);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || !block_hist) return e;
+    hipLaunchKernelGGL(bin_finish_kernel, dim3(1), dim3(kThreads), 0, st, bg, block_hist,
+                       pair_total, block_start, seg_start, host_total, status);
     return hipGetLastError();
 }
 

@@ -964,6 +964,7 @@ __device__ __forceinline__ uint32_t work_bucket(uint32_t w) {
 }
 
 constexpr int kOrderThreads = 1024;
+constexpr int kOrderHeld = 8;  // 8192 tiles held in registers (1080p: 8160)
 constexpr uint32_t kSplitBuckets = 5;
 constexpr uint32_t kSplitMinWork = 256;
 // A tile alone on a CU runs at roughly a quarter of the CU's rate.
@@ -981,32 +982,41 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
     __shared__ unsigned long long s_sum;
     __shared__ uint32_t s_wmax;
     const int tid = threadIdx.x;
-    auto bucket_of = [&](int t) -> uint32_t {
-        uint32_t w;
-        if (work) {
-            w = work[t];
-        } else {
-            int start, end;
-            clamp_range(ranges[t], m, start, end);
-            w = (uint32_t)(end - start);
-        }
-        return 255u - work_bucket(w);  // descending work
+    auto work_of = [&](int t) -> uint32_t {
+        if (work) return work[t];
+        int start, end;
+        clamp_range(ranges[t], m, start, end);
+        return (uint32_t)(end - start);
     };
+    auto bucket = [](uint32_t w) -> uint32_t { return 255u - work_bucket(w); };  // descending
+    auto bucket_of = [&](int t) -> uint32_t { return bucket(work_of(t)); };
     if (tid < 256) s_cnt[tid] = 0;
     if (tid == 0) {
         s_sum = 0ull;
         s_wmax = 0u;
     }
+    // the first kOrderHeld tiles per thread are read once, all loads in
+    // flight together, and their work kept for the scatter
+    uint32_t held[kOrderHeld];
+#pragma unroll
+    for (int i = 0; i < kOrderHeld; ++i) {
+        const int t = tid + i * kOrderThreads;
+        held[i] = (t < T) ? work_of(t) : 0u;
+    }
     __syncthreads();
     uint64_t wsum = 0;
     uint32_t wmax = 0;
-    for (int t = tid; t < T; t += kOrderThreads) {
-        atomicAdd(&s_cnt[bucket_of(t)], 1u);
-        if (split_max > 0) {
-            const uint32_t w = work[t];
-            wsum += w;
-            wmax = max(wmax, w);
-        }
+#pragma unroll
+    for (int i = 0; i < kOrderHeld; ++i) {
+        if (tid + i * kOrderThreads < T) atomicAdd(&s_cnt[bucket(held[i])], 1u);
+        wsum += held[i];
+        wmax = max(wmax, held[i]);
+    }
+    for (int t = tid + kOrderHeld * kOrderThreads; t < T; t += kOrderThreads) {
+        const uint32_t w = work_of(t);
+        atomicAdd(&s_cnt[bucket(w)], 1u);
+        wsum += w;
+        wmax = max(wmax, w);
     }
     if (split_max > 0) {
         // one atomic per wave
@@ -1031,7 +1041,15 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
         s_cnt[tid] = pre + inc - c;  // first slot of the bucket
     }
     __syncthreads();
-    for (int t = tid; t < T; t += kOrderThreads) {
+#pragma unroll
+    for (int i = 0; i < kOrderHeld; ++i) {
+        const int t = tid + i * kOrderThreads;
+        if (t < T) {
+            const uint32_t pos = atomicAdd(&s_cnt[bucket(held[i])], 1u);
+            if (pos < (uint32_t)T) order[pos] = (uint32_t)t;
+        }
+    }
+    for (int t = tid + kOrderHeld * kOrderThreads; t < T; t += kOrderThreads) {
         const uint32_t pos = atomicAdd(&s_cnt[bucket_of(t)], 1u);
         if (pos < (uint32_t)T) order[pos] = (uint32_t)t;
     }

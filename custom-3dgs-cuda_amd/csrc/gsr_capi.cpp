@@ -83,7 +83,6 @@ int tile_key_bits(int64_t T) {
 struct Misc {
     uint64_t total;       // pair count
     int status;           // host copy only: the device status word
-    uint32_t bin_done;    // bin_count's finished work-groups (left at zero)
 };
 
 // The message for a non-zero device status word.
@@ -238,7 +237,7 @@ Misc* pinned_misc() {
     return p;
 }
 
-// The pair count as bin_count's last work-group stores it: one host-mapped,
+// The pair count as the kernel behind bin_count stores it: one host-mapped,
 // coherent word per host thread, with its device address.
 struct HostCount {
     volatile uint64_t* host = nullptr;
@@ -458,8 +457,8 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
                                       blocks ? at<uint32_t>(bin_ws, L.blockhist) : nullptr,
                                       blocks ? &misc->total : nullptr,
                                       at<uint32_t>(bin_ws, L.block_start),
-                                      at<uint32_t>(bin_ws, L.seg_start), &misc->bin_done,
-                                      hc.dev, dg.status, st),
+                                      at<uint32_t>(bin_ws, L.seg_start), hc.dev, dg.status,
+                                      st),
                 "rasterize: count");
     }
     Misc* host = pinned_misc();
@@ -474,8 +473,8 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
         return GSR_OK;
     };
     if (blocks) {
-        // The pair count is final after bin_count, whose last work-group
-        // stores it to host-mapped memory: queue the depth sort behind
+        // The pair count is final after bin_count, whose one-group finish
+        // kernel stores it to host-mapped memory: queue the depth sort behind
         // bin_count and wait only for bin_count, so the sort runs while the
         // host returns and queues the render.  bin_count also hands over the
         // device status word: errors of every earlier kernel on the device

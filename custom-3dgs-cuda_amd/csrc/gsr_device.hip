@@ -1,8 +1,8 @@
 // gsr_device.hip — the library's per-device globals:
 //   - the device status word: kernels that reach their look-back spin bound
 //     or find inconsistent counts OR an error bit into it (bit 0: spin
-//     bound, bit 2: inconsistent counts).  bin_count's last work-group moves
-//     it to the host with the pair count, so the next forward call reports
+//     bound, bit 2: inconsistent counts).  The one-group kernel behind
+//     bin_count moves it to the host with the pair count, so the next forward call reports
 //     what any earlier kernel on the device found, without a synchronisation
 //     of its own;
 //   - `scratch`, the fixed workspace of the allocation-free backward entry

@@ -1,6 +1,5 @@
-// gsr_group.h — work-group scans, the one-wave decoupled look-back and the
-// "last work-group" hand-off shared by the binning and scan kernels (gfx950,
-// wave64).
+// gsr_group.h — work-group scans and the one-wave decoupled look-back shared
+// by the binning and scan kernels (gfx950, wave64).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -39,27 +38,6 @@ __device__ __forceinline__ uint32_t load_agent_u32(const uint32_t* p) {
 }
 __device__ __forceinline__ void store_agent_u32(uint32_t* p, uint32_t v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// True in every thread of the last work-group of the grid to get here; that
-// work-group then sees every other work-group's writes made before its call
-// (each thread's release fence, a barrier so that the whole work-group has
-// written before it is counted, the counter, an acquire fence).  The last one
-// resets the counter, so it starts at zero for the next launch.
-__device__ __forceinline__ bool last_group(uint32_t* done, uint32_t* s_flag) {
-    __threadfence();
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const uint32_t groups = gridDim.x * gridDim.y * gridDim.z;
-        *s_flag = (atomicAdd(done, 1u) == groups - 1u) ? 1u : 0u;
-    }
-    __syncthreads();
-    const bool last = *s_flag != 0;
-    if (last) {
-        __threadfence();
-        if (threadIdx.x == 0) store_agent_u32(done, 0u);
-    }
-    return last;
 }
 
 // Decoupled look-back over 64-bit status words (flag in the top two bits,

@@ -180,24 +180,24 @@ hipError_t launch_range_keys(int T, const int32_t* ranges, const int32_t* ids, c
                              int n, uint64_t m, uint64_t* keys, hipStream_t st);
 
 // ---- binning ----
-// counts[g], packed tile rect, depth key (float bits or 0xffffffff when the
-// Gaussian touches no tile) and identity values, the digit histograms of the
-// 4-pass depth sort (depth_hist), and either the digit histograms of the tile
-// sort (tile_passes > 0: tile_hist) or the block histogram (block_hist), with
-// the pair count added to *pair_total and, by the last work-group, the block
-// and segment starts (block_start / seg_start, nb + 1 entries each; `done` a
-// zero counter, left at zero) and, when host_total is not null, the final pair
-// count stored to that host-mapped coherent word (block histogram mode only),
-// and the device status word (status, read and cleared) to host_total[1].
 // Pairs per tile row of an H x W frame (rows[tiles_y], needs tiles_y + 1
 // entries of room; tiles_y <= 4096).
 hipError_t launch_row_pairs(int n, const float* mean2d, const float* cov2d, int H, int W,
                             uint64_t* rows, hipStream_t st);
+// counts[g], packed tile rect, depth key (float bits or 0xffffffff when the
+// Gaussian touches no tile) and identity values, the digit histograms of the
+// 4-pass depth sort (depth_hist), and either the digit histograms of the tile
+// sort (tile_passes > 0: tile_hist) or the block histogram (block_hist), with
+// the pair count added to *pair_total; in block histogram mode a one-group
+// kernel behind it then writes the block and segment starts (block_start /
+// seg_start, nb + 1 entries each) and, when host_total is not null, the final
+// pair count to that host-mapped coherent word and the device status word
+// (status, read and cleared) to host_total[1].
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
-                            uint32_t* block_start, uint32_t* seg_start, uint32_t* done,
+                            uint32_t* block_start, uint32_t* seg_start,
                             uint64_t* host_total, int* status, hipStream_t st);
 
 // Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r] (perm null:
