@@ -17,32 +17,57 @@ constexpr int kShCoef = 45;
 // staged through LDS together.
 constexpr int kShThreads = 64;
 
-// Copy floats [base*45, base*45 + cnt*45) of src into LDS: 16-byte chunks
-// (base is a multiple of 64, so the block's span starts 16-byte aligned),
-// then the remainder singly.
+// Rows [base, base + cnt) of a row-major [N, kW] float array to LDS (row r
+// of the span at lds[r * kW]), by the kT threads of the work-group: 16-byte
+// loads when the span starts 16-byte aligned (base is a multiple of kT, so
+// that holds when the array does), single floats otherwise.  Per-Gaussian
+// rows of 2, 3 or 45 floats read one per thread are strided accesses; staged,
+// every global access of the work-group is a coalesced 16-byte one.
+template <int kW, int kT>
+__device__ __forceinline__ void stage_rows(float* __restrict__ lds, const float* __restrict__ src,
+                                           size_t base, int cnt) {
+    const int total = cnt * kW;
+    const float* g = src + base * kW;
+    int done = 0;
+    if ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) {
+        const int total4 = total / 4;
+        const float4* g4 = reinterpret_cast<const float4*>(g);
+        float4* l4 = reinterpret_cast<float4*>(lds);
+#pragma unroll 4
+        for (int j = threadIdx.x; j < total4; j += kT) l4[j] = g4[j];
+        done = total4 * 4;
+    }
+    for (int j = done + (int)threadIdx.x; j < total; j += kT) lds[j] = g[j];
+}
+
+// The reverse: LDS floats [0, cnt * kW) to rows [base, base + cnt) of dst.
+template <int kW, int kT>
+__device__ __forceinline__ void unstage_rows(float* __restrict__ dst, const float* __restrict__ lds,
+                                             size_t base, int cnt) {
+    const int total = cnt * kW;
+    float* g = dst + base * kW;
+    int done = 0;
+    if ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) {
+        const int total4 = total / 4;
+        float4* g4 = reinterpret_cast<float4*>(g);
+        const float4* l4 = reinterpret_cast<const float4*>(lds);
+#pragma unroll 4
+        for (int j = threadIdx.x; j < total4; j += kT) g4[j] = l4[j];
+        done = total4 * 4;
+    }
+    for (int j = done + (int)threadIdx.x; j < total; j += kT) g[j] = lds[j];
+}
+
+// The SH work-groups' coefficients: 45 floats per Gaussian.
 __device__ __forceinline__ void stage_coeffs(float* __restrict__ lds,
                                              const float* __restrict__ src, size_t base,
                                              int cnt) {
-    const int total = cnt * kShCoef, total4 = total / 4;
-    const float4* g4 = reinterpret_cast<const float4*>(src + base * kShCoef);
-    float4* l4 = reinterpret_cast<float4*>(lds);
-#pragma unroll 4
-    for (int j = threadIdx.x; j < total4; j += kShThreads) l4[j] = g4[j];
-    for (int j = total4 * 4 + threadIdx.x; j < total; j += kShThreads)
-        lds[j] = src[base * kShCoef + j];
+    stage_rows<kShCoef, kShThreads>(lds, src, base, cnt);
 }
-
-// The reverse: LDS floats [0, cnt*45) to dst[base*45 ..].
 __device__ __forceinline__ void unstage_coeffs(float* __restrict__ dst,
                                                const float* __restrict__ lds, size_t base,
                                                int cnt) {
-    const int total = cnt * kShCoef, total4 = total / 4;
-    float4* g4 = reinterpret_cast<float4*>(dst + base * kShCoef);
-    const float4* l4 = reinterpret_cast<const float4*>(lds);
-#pragma unroll 4
-    for (int j = threadIdx.x; j < total4; j += kShThreads) g4[j] = l4[j];
-    for (int j = total4 * 4 + threadIdx.x; j < total; j += kShThreads)
-        dst[base * kShCoef + j] = lds[j];
+    unstage_rows<kShCoef, kShThreads>(dst, lds, base, cnt);
 }
 
 // cam = -R^T t (the glue's -matmul(R.T, t), rasterize.py:43-44).

@@ -40,6 +40,9 @@ constexpr int kWinR = 5;                   // window radius: 11 taps
 constexpr int kWinTaps = 2 * kWinR + 1;
 constexpr int kInW = kLossTW + 2 * kWinR, kInH = kLossTH + 2 * kWinR;  // 42 x 26
 constexpr int kLossThreads = 256;
+constexpr int kRowElems = kInW * 3;                // floats of one halo row
+constexpr int kHaloElems = kInH * kRowElems;       // floats of a tile + halo
+constexpr int kHaloIters = (kHaloElems + kLossThreads - 1) / kLossThreads;
 constexpr float kC1 = 0.01f * 0.01f, kC2 = 0.03f * 0.03f;
 
 struct Window {
@@ -66,24 +69,32 @@ __global__ __launch_bounds__(kLossThreads) void ssim_fwd_kernel(
     const int x0 = blockIdx.x * kLossTW, y0 = blockIdx.y * kLossTH;
     const size_t plane = (size_t)H * W * 3;
 
-    // the tile and its halo, channels interleaved as in HBM; |gt - img| of the
-    // tile's own pixels on the way
+    // the tile and its halo, channels interleaved as in HBM, every thread's
+    // loads issued together; |gt - img| of the tile's own pixels on the way
     float l1 = 0.0f;
-    constexpr int kRowElems = kInW * 3;
-    for (int e = tid; e < kInH * kRowElems; e += kLossThreads) {
-        const int r = e / kRowElems, q = e - r * kRowElems;
-        const int cx = q / 3, ch = q - cx * 3;
-        const int gy = y0 - kWinR + r, gx = x0 - kWinR + cx;
-        float xv = 0.0f, yv = 0.0f;
-        if (gy >= 0 && gy < H && gx >= 0 && gx < W) {
-            const size_t idx = ((size_t)gy * W + gx) * 3 + ch;
-            xv = img[idx];
-            yv = gt[idx];
-            if (r >= kWinR && r < kWinR + kLossTH && cx >= kWinR && cx < kWinR + kLossTW)
-                l1 += fabsf(yv - xv);
+    {
+        float xv[kHaloIters], yv[kHaloIters];
+#pragma unroll
+        for (int it = 0; it < kHaloIters; ++it) {
+            const int e = tid + it * kLossThreads;
+            const int r = e / kRowElems, q = e - r * kRowElems;
+            const int gy = y0 - kWinR + r, gx = x0 - kWinR + q / 3;
+            const bool in = e < kHaloElems && gy >= 0 && gy < H && gx >= 0 && gx < W;
+            const size_t idx = (size_t)gy * W * 3 + (size_t)(x0 - kWinR) * 3 + q;
+            xv[it] = in ? img[idx] : 0.0f;
+            yv[it] = in ? gt[idx] : 0.0f;
         }
-        s_x[ch][r][cx] = clamp01(xv);
-        s_y[ch][r][cx] = clamp01(yv);
+#pragma unroll
+        for (int it = 0; it < kHaloIters; ++it) {
+            const int e = tid + it * kLossThreads;
+            if (e >= kHaloElems) continue;
+            const int r = e / kRowElems, q = e - r * kRowElems;
+            const int cx = q / 3, ch = q - cx * 3;
+            if (r >= kWinR && r < kWinR + kLossTH && cx >= kWinR && cx < kWinR + kLossTW)
+                l1 += fabsf(yv[it] - xv[it]);
+            s_x[ch][r][cx] = clamp01(xv[it]);
+            s_y[ch][r][cx] = clamp01(yv[it]);
+        }
     }
     __syncthreads();
 
@@ -211,19 +222,30 @@ __global__ __launch_bounds__(kLossThreads) void ssim_bwd_kernel(
     const int tid = threadIdx.x;
     const int x0 = blockIdx.x * kLossTW, y0 = blockIdx.y * kLossTH;
     const size_t plane = (size_t)H * W * 3;
-    constexpr int kRowElems = kInW * 3;
     // the derivative maps of the windows centred in the tile and its halo;
-    // zero for windows that are not inside the image
-    for (int e = tid; e < 3 * kInH * kRowElems; e += kLossThreads) {
-        const int mp = e / (kInH * kRowElems);
-        const int rest = e - mp * (kInH * kRowElems);
-        const int r = rest / kRowElems, q = rest - r * kRowElems;
-        const int cx = q / 3, ch = q - cx * 3;
-        const int gy = y0 - kWinR + r, gx = x0 - kWinR + cx;
-        float v = 0.0f;
-        if (gy >= 0 && gy < H && gx >= 0 && gx < W && interior(gy, gx, H, W))
-            v = gmaps[mp * plane + ((size_t)gy * W + gx) * 3 + ch];
-        s_g[mp][ch][r][cx] = v;
+    // zero for windows that are not inside the image.  One map at a time,
+    // every thread's loads of it issued together.
+#pragma unroll 1
+    for (int mp = 0; mp < 3; ++mp) {
+        float v[kHaloIters];
+#pragma unroll
+        for (int it = 0; it < kHaloIters; ++it) {
+            const int e = tid + it * kLossThreads;
+            const int r = e / kRowElems, q = e - r * kRowElems;
+            const int gy = y0 - kWinR + r, gx = x0 - kWinR + q / 3;
+            const bool in = e < kHaloElems && gy >= 0 && gy < H && gx >= 0 && gx < W &&
+                            interior(gy, gx, H, W);
+            v[it] = in ? gmaps[mp * plane + (size_t)gy * W * 3 + (size_t)(x0 - kWinR) * 3 + q]
+                       : 0.0f;
+        }
+#pragma unroll
+        for (int it = 0; it < kHaloIters; ++it) {
+            const int e = tid + it * kLossThreads;
+            if (e >= kHaloElems) continue;
+            const int r = e / kRowElems, q = e - r * kRowElems;
+            const int cx = q / 3, ch = q - cx * 3;
+            s_g[mp][ch][r][cx] = v[it];
+        }
     }
     const float g = grad_loss ? *grad_loss : 1.0f;
     __syncthreads();
