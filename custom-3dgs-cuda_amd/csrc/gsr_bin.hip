@@ -81,6 +81,8 @@ __device__ __forceinline__ void hist_row(uint32_t a, uint32_t w, int passes, int
     }
 }
 
+constexpr int kBinUnroll = 4;
+
 // Per Gaussian: tile rectangle and count (rasterize.cu:19-59, :98-105), the
 // depth sort's key and value, and the Gaussian's share of both sorts' global
 // digit histograms (depth_hist[p][d]: keys with digit d in pass p;
@@ -109,33 +111,51 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     const int tiles_x = (W + 15) / 16;
     uint32_t full = 0;
     uint64_t pairs = 0;
-    for (int i = blockIdx.x * kThreads + tid; i < n; i += gridDim.x * kThreads) {
-        const TileRect r = tile_rect(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1],
-                                     cov2d[3 * (size_t)i], cov2d[3 * (size_t)i + 1],
-                                     cov2d[3 * (size_t)i + 2], W, H);
-        const uint32_t cnt = r.ok ? (uint32_t)(max(0, r.x1 - r.x0) * max(0, r.y1 - r.y0)) : 0u;
-        counts[i] = cnt;
-        rects[i] = make_uint2((uint32_t)r.x0 | ((uint32_t)r.x1 << 16),
-                              (uint32_t)r.y0 | ((uint32_t)r.y1 << 16));
-        // Gaussians without tiles sort last; they emit nothing, so their place
-        // in the depth order never shows.
-        const uint32_t dk = cnt ? __float_as_uint(depth[i]) : 0xffffffffu;
-        dkeys[i] = dk;
-        dvals[i] = (uint32_t)i;
+    // the grid-strided loop takes kBinUnroll Gaussians per step, their loads
+    // issued together
+    const int64_t stride = (int64_t)gridDim.x * kThreads;
+    for (int64_t i0 = (int64_t)blockIdx.x * kThreads + tid; i0 < n; i0 += kBinUnroll * stride) {
+        float in[kBinUnroll][6];
 #pragma unroll
-        for (int p = 0; p < 4; ++p) atomicAdd(&s_dh[p][(dk >> (8 * p)) & 0xffu], 1u);
-        pairs += cnt;
-        if (cnt && passes > 0) {
-            const uint32_t w = (uint32_t)(r.x1 - r.x0);
-            for (int y = r.y0; y < r.y1; ++y)
-                hist_row((uint32_t)y * (uint32_t)tiles_x + (uint32_t)r.x0, w, passes, s_d0, s_h,
-                         &full);
+        for (int u = 0; u < kBinUnroll; ++u) {
+            const int64_t i = i0 + u * stride;
+            const bool ok = i < n;
+            in[u][0] = ok ? mean2d[2 * (size_t)i] : 0.0f;
+            in[u][1] = ok ? mean2d[2 * (size_t)i + 1] : 0.0f;
+            in[u][2] = ok ? cov2d[3 * (size_t)i] : 0.0f;
+            in[u][3] = ok ? cov2d[3 * (size_t)i + 1] : 0.0f;
+            in[u][4] = ok ? cov2d[3 * (size_t)i + 2] : 0.0f;
+            in[u][5] = ok ? depth[i] : 0.0f;
         }
-        if (cnt && blocks) {
-            // the 8x8-tile blocks the rectangle meets
-            for (int by = r.y0 >> 3; by < (r.y1 + 7) >> 3; ++by)
-                for (int bx = r.x0 >> 3; bx < (r.x1 + 7) >> 3; ++bx)
-                    atomicAdd(&s_bh[by * bg.bw + bx], 1u);
+#pragma unroll
+        for (int u = 0; u < kBinUnroll; ++u) {
+            const int64_t i = i0 + u * stride;
+            if (i >= n) break;
+            const TileRect r = tile_rect(in[u][0], in[u][1], in[u][2], in[u][3], in[u][4], W, H);
+            const uint32_t cnt = r.ok ? (uint32_t)(max(0, r.x1 - r.x0) * max(0, r.y1 - r.y0)) : 0u;
+            counts[i] = cnt;
+            rects[i] = make_uint2((uint32_t)r.x0 | ((uint32_t)r.x1 << 16),
+                                  (uint32_t)r.y0 | ((uint32_t)r.y1 << 16));
+            // Gaussians without tiles sort last; they emit nothing, so their place
+            // in the depth order never shows.
+            const uint32_t dk = cnt ? __float_as_uint(in[u][5]) : 0xffffffffu;
+            dkeys[i] = dk;
+            dvals[i] = (uint32_t)i;
+#pragma unroll
+            for (int p = 0; p < 4; ++p) atomicAdd(&s_dh[p][(dk >> (8 * p)) & 0xffu], 1u);
+            pairs += cnt;
+            if (cnt && passes > 0) {
+                const uint32_t w = (uint32_t)(r.x1 - r.x0);
+                for (int y = r.y0; y < r.y1; ++y)
+                    hist_row((uint32_t)y * (uint32_t)tiles_x + (uint32_t)r.x0, w, passes, s_d0, s_h,
+                             &full);
+            }
+            if (cnt && blocks) {
+                // the 8x8-tile blocks the rectangle meets
+                for (int by = r.y0 >> 3; by < (r.y1 + 7) >> 3; ++by)
+                    for (int bx = r.x0 >> 3; bx < (r.x1 + 7) >> 3; ++bx)
+                        atomicAdd(&s_bh[by * bg.bw + bx], 1u);
+            }
         }
     }
     const uint32_t wfull = (uint32_t)wave_sum_u32(full);
