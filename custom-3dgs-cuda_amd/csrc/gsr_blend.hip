@@ -28,7 +28,7 @@
 // gradient sums are formed in the lane, summed across the wave (one
 // transposed permlane/DPP reduction) and across the waves through LDS, then
 // stored with plain stores into the (Gaussian, tile) pair's own gradient slot
-// (nine floats and a claim flag).  pair_grad_reduce_kernel adds each
+// (nine floats and a claim bit).  pair_grad_reduce_kernel adds each
 // Gaussian's claimed slots.  Float atomics are used only for list entries
 // that have no slot of their own: pairs outside the Gaussian's tile
 // rectangle, and a repeated id within one tile's list (caller-supplied lists).
@@ -727,13 +727,10 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                                       (uint64_t)((ty - ry0) * (rx1 - rx0) + (tx - rx0));
                 bool own = tx >= rx0 && tx < rx1 && ty >= ry0 && ty < ry1 && slot < gs.slots;
                 if (own) {
-                    // claim the slot: its flag byte, through the 32-bit word
-                    // holding it (the flag array is padded to 8-byte groups).
-                    // Only an id repeated within this tile's list finds it
-                    // claimed already.
-                    const uint32_t bit = 1u << (8u * (uint32_t)(slot & 3u));
-                    own = (atomicOr(reinterpret_cast<uint32_t*>(gs.flags + (slot & ~3ull)), bit) &
-                           bit) == 0u;
+                    // claim the slot: its flag bit.  Only an id repeated
+                    // within this tile's list finds it claimed already.
+                    const uint32_t bit = 1u << (uint32_t)(slot & 31u);
+                    own = (atomicOr(gs.flags + (slot >> 5), bit) & bit) == 0u;
                 }
                 if (own) {
                     float* d = gs.sums + 9 * slot;
@@ -775,38 +772,49 @@ __device__ __forceinline__ float row_sum(float x) {
     return x;
 }
 
-// kLanes per Gaussian: 16, or 8 when Gaussians have few slots (a row then
-// covers 64 slots per flag load; half the waves wait on the dependent loads).
-template <int kReduceRowLanes>
+// kLanes per Gaussian: 16, or 8 when Gaussians have few slots (half the
+// waves then wait on the dependent loads).  Each lane reads the flag bits of
+// kGroup consecutive slots per step: 8 (one byte) when Gaussians average a
+// few hundred slots or fewer, 64 (one word) beyond, where claimed slots are
+// sparse and a row then covers 1024 slots per step.
+template <int kReduceRowLanes, int kGroup>
 __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
     int n, const BlendRec* __restrict__ recs, GradSlots gs, float* __restrict__ dmean,
     float* __restrict__ dcov, float* __restrict__ dcol, float* __restrict__ dalpha) {
     static_assert(kReduceRowLanes == 16 || kReduceRowLanes == 8, "rows of 16 or 8 lanes");
+    static_assert(kGroup == 8 || kGroup == 64, "flag groups of 8 or 64 slots");
     constexpr int kReduceGaussiansPerBlock = 256 / kReduceRowLanes;
     const int sub = threadIdx.x & (kReduceRowLanes - 1);
     const int g = blockIdx.x * kReduceGaussiansPerBlock + (int)(threadIdx.x / kReduceRowLanes);
+    // the flag bits of slots [grp, grp + kGroup), grp a multiple of kGroup
+    // (the flag array is 256-byte aligned and padded to 64-bit words)
+    auto group_bits = [&](uint64_t grp) -> uint64_t {
+        if constexpr (kGroup == 8)
+            return reinterpret_cast<const uint8_t*>(gs.flags)[grp >> 3];
+        else
+            return reinterpret_cast<const uint64_t*>(gs.flags)[grp >> 6];
+    };
     float v[kTerms] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    bool claimed = false;
     if (g < n) {
         const uint64_t base = gs.goff[g];
         const uint64_t end = min(base + (uint64_t)gs.counts[g], gs.slots);
-        // flags eight at a time from 8-byte aligned groups (the flag array is
-        // 256-byte aligned and padded to a multiple of 8 bytes); each group's
-        // flags are loaded while the group before is summed, and the sums of
-        // two flagged slots are loaded together
-        uint64_t grp = (base & ~7ull) + 8ull * sub;
-        uint64_t bits = (grp < end) ? *reinterpret_cast<const uint64_t*>(gs.flags + grp) : 0ull;
+        // each group's flags are loaded while the group before is summed, and
+        // the sums of two flagged slots are loaded together
+        uint64_t grp = (base & ~(uint64_t)(kGroup - 1)) + (uint64_t)kGroup * sub;
+        uint64_t bits = (grp < end) ? group_bits(grp) : 0ull;
         while (grp < end) {
-            const uint64_t nxt = grp + 8ull * kReduceRowLanes;
-            const uint64_t nbits =
-                (nxt < end) ? *reinterpret_cast<const uint64_t*>(gs.flags + nxt) : 0ull;
-            // only the flags of [base, end) (flag bytes hold 0 or 1)
-            if (grp < base) bits &= ~0ull << (8 * (base - grp));
-            if (end - grp < 8) bits &= ~(~0ull << (8 * (end - grp)));
+            const uint64_t nxt = grp + (uint64_t)kGroup * kReduceRowLanes;
+            const uint64_t nbits = (nxt < end) ? group_bits(nxt) : 0ull;
+            // only the flags of [base, end)
+            if (grp < base) bits &= ~0ull << (base - grp);
+            if (end - grp < (uint64_t)kGroup) bits &= ~(~0ull << (end - grp));
+            claimed |= bits != 0;
             while (bits) {
-                const uint64_t s0 = grp + (uint64_t)(__builtin_ctzll(bits) >> 3);
+                const uint64_t s0 = grp + (uint64_t)__builtin_ctzll(bits);
                 bits &= bits - 1;
                 const bool two = bits != 0;
-                const uint64_t s1 = two ? grp + (uint64_t)(__builtin_ctzll(bits) >> 3) : s0;
+                const uint64_t s1 = two ? grp + (uint64_t)__builtin_ctzll(bits) : s0;
                 if (two) bits &= bits - 1;
                 const float* d0 = gs.sums + 9 * s0;
                 const float* d1 = gs.sums + 9 * s1;
@@ -827,7 +835,12 @@ __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
     float t[kTerms];
 #pragma unroll
     for (int k = 0; k < kTerms; ++k) t[k] = row_sum<kReduceRowLanes>(v[k]);
-    if (g < n && sub == 0) {
+    // a Gaussian without claimed slots adds nothing (at 4K most Gaussians
+    // have none in a given screen band): its outputs are not read or written
+    const uint64_t row_claims =
+        (ballot(claimed) >> (lane_id() & (64 - kReduceRowLanes))) &
+        ((1ull << kReduceRowLanes) - 1);
+    if (g < n && sub == 0 && row_claims != 0) {
         const BlendRec r = recs[g];
         float dc[3];
         conic_to_cov_grad(-2.0f * r.a.z, -2.0f * r.c.y, -2.0f * r.b.x, t[2], t[3], t[4], dc);
@@ -1211,13 +1224,17 @@ hipError_t launch_pair_grad_reduce(int n, const void* recs, const GradSlots& gs,
                                    float* dcov, float* dcol, float* dalpha, hipStream_t st) {
     if (n <= 0) return hipSuccess;
     const auto* rc = static_cast<const BlendRec*>(recs);
-    // 8-lane rows when a Gaussian averages at most 64 slots (one flag load per lane)
+    // 8-lane rows when a Gaussian averages at most 64 slots (one flag load per
+    // lane); word-sized flag groups beyond 256 slots per Gaussian
     if (gs.slots <= 64ull * (uint64_t)n)
-        hipLaunchKernelGGL(pair_grad_reduce_kernel<8>, dim3((unsigned)((n + 31) / 32)), dim3(256),
-                           0, st, n, rc, gs, dmean, dcov, dcol, dalpha);
+        hipLaunchKernelGGL((pair_grad_reduce_kernel<8, 8>), dim3((unsigned)((n + 31) / 32)),
+                           dim3(256), 0, st, n, rc, gs, dmean, dcov, dcol, dalpha);
+    else if (gs.slots <= 256ull * (uint64_t)n)
+        hipLaunchKernelGGL((pair_grad_reduce_kernel<16, 8>), dim3((unsigned)((n + 15) / 16)),
+                           dim3(256), 0, st, n, rc, gs, dmean, dcov, dcol, dalpha);
     else
-        hipLaunchKernelGGL(pair_grad_reduce_kernel<16>, dim3((unsigned)((n + 15) / 16)), dim3(256),
-                           0, st, n, rc, gs, dmean, dcov, dcol, dalpha);
+        hipLaunchKernelGGL((pair_grad_reduce_kernel<16, 64>), dim3((unsigned)((n + 15) / 16)),
+                           dim3(256), 0, st, n, rc, gs, dmean, dcov, dcol, dalpha);
     return hipGetLastError();
 }
 

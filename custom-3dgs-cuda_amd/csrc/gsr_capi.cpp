@@ -214,7 +214,7 @@ BwdLayout backward_layout(int n, int64_t m, int height, int width) {
     L.ctl = off;
     L.misc = take(sizeof(Misc));
     L.scanctl = take(gsr::scan_control_bytes(n));
-    L.flags = take(align_up(um, 8));  // read as 8-byte groups
+    L.flags = take(align_up(um, 64) / 8);  // one bit per slot, read as 64-bit words
     L.ctl_end = off;
     L.sums = take(36 * um);
     L.end = off;
@@ -755,7 +755,7 @@ int rasterize_backward(int n, int height, int width, const float* grad_img,
     gs.counts = counts;
     gs.rects = rects;
     gs.sums = at<float>(ws, L.sums);
-    gs.flags = at<uint8_t>(ws, L.flags);
+    gs.flags = at<uint32_t>(ws, L.flags);
     gs.slots = (uint64_t)num_pairs;
     uint32_t* order = at<uint32_t>(ws, L.order);
     {

@@ -247,17 +247,19 @@ hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num
 
 // Gradient slots: the (Gaussian, tile) pairs in Gaussian-major order, pair
 // (g, t) at goff[g] + its index in g's tile rectangle (row-major); the backward
-// claims each processed pair's slot (flags[slot] = 1, an atomic OR on the
-// 32-bit word holding the byte) and writes its nine sums to sums[9 slot ..],
-// and pair_grad_reduce adds each Gaussian's claimed slots to the gradient
-// outputs.  Pairs without a slot of their own (outside the rectangles, or an
-// id repeated within one tile's list) fall back to atomics on the outputs.
+// claims each processed pair's slot (bit slot % 32 of flags[slot / 32], an
+// atomic OR) and writes its nine sums to sums[9 slot ..], and
+// pair_grad_reduce adds each Gaussian's claimed slots to the gradient
+// outputs.  One bit per slot: at 4K with millions of Gaussians only about one
+// slot in a thousand is claimed, and the flags are cleared and read in full.
+// Pairs without a slot of their own (outside the rectangles, or an id repeated
+// within one tile's list) fall back to atomics on the outputs.
 struct GradSlots {
     const uint32_t* goff = nullptr;
     const uint32_t* counts = nullptr;
     const uint2* rects = nullptr;
     float* sums = nullptr;
-    uint8_t* flags = nullptr;
+    uint32_t* flags = nullptr;  // one bit per slot, padded to 64-bit words
     uint64_t slots = 0;
 };
 
