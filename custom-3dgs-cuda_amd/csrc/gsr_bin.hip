@@ -97,7 +97,7 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     __shared__ int s_d0[kRadixBins + 1];
     __shared__ uint32_t s_h[3][kRadixBins];
     __shared__ uint32_t s_dh[4][kRadixBins];
-    __shared__ uint32_t s_bh[kMaxBlocks];
+    __shared__ int s_bh[kMaxBlocks];  // block histogram, first as a 2D difference array
     __shared__ uint32_t s_full[kThreads / kWave];
     __shared__ uint32_t s_scan[kThreads / kWave];
     const int tid = threadIdx.x;
@@ -151,10 +151,18 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
                              &full);
             }
             if (cnt && blocks) {
-                // the 8x8-tile blocks the rectangle meets
-                for (int by = r.y0 >> 3; by < (r.y1 + 7) >> 3; ++by)
-                    for (int bx = r.x0 >> 3; bx < (r.x1 + 7) >> 3; ++bx)
-                        atomicAdd(&s_bh[by * bg.bw + bx], 1u);
+                // the 8x8-tile blocks the rectangle meets, [bx0, bx1) x
+                // [by0, by1): +1 at its first corner, -1 past its right and
+                // bottom edges, +1 past both (corners off the grid dropped);
+                // the 2D prefix sum below turns these into the counts
+                const int bx0 = r.x0 >> 3, bx1 = (r.x1 + 7) >> 3;
+                const int by0 = r.y0 >> 3, by1 = (r.y1 + 7) >> 3;
+                atomicAdd(&s_bh[by0 * bg.bw + bx0], 1);
+                if (bx1 < bg.bw) atomicAdd(&s_bh[by0 * bg.bw + bx1], -1);
+                if (by1 < bg.bh) {
+                    atomicAdd(&s_bh[by1 * bg.bw + bx0], -1);
+                    if (bx1 < bg.bw) atomicAdd(&s_bh[by1 * bg.bw + bx1], 1);
+                }
             }
         }
     }
@@ -175,8 +183,34 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
         if (v) atomicAdd(&tile_hist[p * kRadixBins + tid], v);
     }
     if (blocks) {
+        // 2D inclusive prefix sum of the difference array: along each block
+        // row, then down each block column, one wave per row / column and 64
+        // entries per wave scan
+        const int lane = tid & 63, wave = tid >> 6;
+        for (int rr = wave; rr < bg.bh; rr += kThreads / kWave) {
+            uint32_t carry = 0;
+            for (int c0 = 0; c0 < bg.bw; c0 += kWave) {
+                const int c = c0 + lane;
+                const uint32_t v = (c < bg.bw) ? (uint32_t)s_bh[rr * bg.bw + c] : 0u;
+                const uint32_t inc = wave_inclusive_scan(v) + carry;
+                if (c < bg.bw) s_bh[rr * bg.bw + c] = (int)inc;
+                carry = (uint32_t)__builtin_amdgcn_readlane((int)inc, kWave - 1);
+            }
+        }
+        __syncthreads();
+        for (int cc = wave; cc < bg.bw; cc += kThreads / kWave) {
+            uint32_t carry = 0;
+            for (int r0 = 0; r0 < bg.bh; r0 += kWave) {
+                const int rr = r0 + lane;
+                const uint32_t v = (rr < bg.bh) ? (uint32_t)s_bh[rr * bg.bw + cc] : 0u;
+                const uint32_t inc = wave_inclusive_scan(v) + carry;
+                if (rr < bg.bh) s_bh[rr * bg.bw + cc] = (int)inc;
+                carry = (uint32_t)__builtin_amdgcn_readlane((int)inc, kWave - 1);
+            }
+        }
+        __syncthreads();
         for (int j = tid; j < bg.nb; j += kThreads) {
-            const uint32_t v = s_bh[j];
+            const uint32_t v = (uint32_t)s_bh[j];
             if (v) atomicAdd(&block_hist[j], v);
         }
         const uint64_t wp = wave_sum_u64(pairs);

@@ -25,6 +25,7 @@
 // at 1080p); level 2 reads the block lists twice and writes the M pair ids
 // once, in runs of consecutive addresses (one run per wave and tile).
 #include <algorithm>
+#include <type_traits>
 
 #include "gsr_internal.h"
 #include "gsr_common.h"
@@ -417,7 +418,6 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
     const uint32_t nseg = min(uniform(seg_start[bg.nb]), seg_cap);
     const uint32_t stride = gridDim.x * kWavesPer;
     const int lane = lane_id();
-    const uint64_t below = lanemask_lt();
     for (uint32_t k = uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6)); k < nseg;
          k += stride) {
         const SegInfo I = seg_info(k, seg_owner, seg_start, block_start, bg.bw, bg.nb);
@@ -428,21 +428,42 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
         if (tx < bg.tiles_x && ty < bg.tiles_y)
             base = (uint32_t)ranges[(size_t)ty * bg.tiles_x + tx].x +
                    tcount[(size_t)k * kWave + lane];
+        // in_row[r] / in_col[c]: this lane covers tile row r / column c; as
+        // lane masks they are the ballots, so the lanes of tile (r, c) are
+        // selected with scalar ANDs
+        bool in_row[8], in_col[8];
         uint64_t rows[8], cols[8];
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            rows[j] = seg_row(S, j);
-            cols[j] = seg_col(S, j);
+            in_row[j] = (uint32_t)(j - S.ly0) < S.lh;
+            in_col[j] = (uint32_t)(j - S.lx0) < S.lw;
+            rows[j] = ballot(in_row[j]);
+            cols[j] = ballot(in_col[j]);
         }
+        // the lanes of tile t's mask write positions b_t + their rank in it;
+        // when every run b_t + [0, 64) lies below m (all but the list's last
+        // entries) no position needs its own check
+        const bool fits = ballot((uint64_t)base + (uint64_t)kWave > m) == 0ull;
+        auto scatter = [&](auto checked) {
 #pragma unroll
-        for (int t = 0; t < 64; ++t) {
-            const uint64_t mk = rows[t >> 3] & cols[t & 7];
-            if (mk != 0) {
-                const uint64_t p = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)base, t) +
-                                   (uint64_t)popc64(mk & below);
-                if (((mk >> lane) & 1ull) && p < m) ids[p] = S.g;
+            for (int t = 0; t < 64; ++t) {
+                const uint64_t mk = rows[t >> 3] & cols[t & 7];
+                if (mk == 0) continue;
+                const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)base, t);
+                const uint32_t rank = rank_in(mk);
+                if (!(in_row[t >> 3] && in_col[t & 7])) continue;
+                if constexpr (decltype(checked)::value) {
+                    if ((uint64_t)b + rank < m) ids[(uint64_t)b + rank] = S.g;
+                } else {
+                    uint32_t* dst = ids + b;  // wave-uniform run start
+                    dst[rank] = S.g;
+                }
             }
-        }
+        };
+        if (fits)
+            scatter(std::false_type{});
+        else
+            scatter(std::true_type{});
     }
 }
 
