@@ -197,7 +197,8 @@ Tensor spherical_harmonics(int total_gaussians, const Tensor camera_position,
 // ---- rasterize (bindings.cpp:50-70 / rasterize.cu:284-487) ----
 std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_impl(
     int num_gaussians, const Tensor& depths, const Tensor& mean_2d, const Tensor& cov_2d,
-    const Tensor& colors, const Tensor& alpha, int height, int width, bool want_keys) {
+    const Tensor& colors, const Tensor& alpha, int height, int width, bool want_keys,
+    const Tensor* order = nullptr) {
     TORCH_CHECK(height >= 0 && width >= 0, "height and width must be non-negative");
     auto device = mean_2d.device();
     auto float_options = torch::TensorOptions().dtype(torch::kFloat32).device(device);
@@ -228,15 +229,28 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_impl(
                 "colors must have shape (N, 3)");
     TORCH_CHECK(depths.numel() == num_gaussians, "depths must have N elements");
     TORCH_CHECK(alpha.numel() == num_gaussians, "alpha must have N elements");
+    if (order) {
+        TORCH_CHECK(order->is_cuda() && order->device() == mean_2d.device(),
+                    "order must be a CUDA tensor on mean_2d's device");
+        TORCH_CHECK(order->is_contiguous(), "order must be contiguous");
+        TORCH_CHECK(order->scalar_type() == torch::kInt32 && order->numel() == num_gaussians,
+                    "order must be an int32 tensor of N elements");
+    }
 
     c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
     void* st = current_stream();
     Tensor bin_ws = workspace((int64_t)gsr_bin_workspace_bytes(num_gaussians, height, width),
                               mean_2d);
     int64_t m = 0;
-    check_rc(gsr_rasterize_bin(num_gaussians, cfp(depths), cfp(mean_2d), cfp(cov_2d), height,
-                               width, bin_ws.data_ptr(), (size_t)bin_ws.numel(), &m, st),
-             "rasterize");
+    if (order)
+        check_rc(gsr_rasterize_bin_ordered(num_gaussians, order->data_ptr<int32_t>(),
+                                           cfp(mean_2d), cfp(cov_2d), height, width,
+                                           bin_ws.data_ptr(), (size_t)bin_ws.numel(), &m, st),
+                 "rasterize_ordered");
+    else
+        check_rc(gsr_rasterize_bin(num_gaussians, cfp(depths), cfp(mean_2d), cfp(cov_2d), height,
+                                   width, bin_ws.data_ptr(), (size_t)bin_ws.numel(), &m, st),
+                 "rasterize");
     if (m == 0) return empty_buffers();
 
     Tensor sort_ws = workspace(
@@ -279,6 +293,33 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_with_keys(
     const Tensor colors, const Tensor alpha, int height, int width) {
     return rasterize_impl(num_gaussians, depths, mean_2d, cov_2d, colors, alpha, height, width,
                           true);
+}
+
+// Not in the reference surface: every Gaussian stably sorted by the float bits
+// of its depth (int32 [N]), shared by the screen bands of one frame.
+Tensor depth_order(int num_gaussians, const Tensor& depths) {
+    CHECK_INPUT_FP32(depths);
+    TORCH_CHECK(num_gaussians >= 0 && depths.numel() == num_gaussians,
+                "depths must have N elements");
+    auto int_options = torch::TensorOptions().dtype(torch::kInt32).device(depths.device());
+    Tensor order = torch::empty({num_gaussians}, int_options);
+    if (num_gaussians == 0) return order;
+    c10::hip::HIPGuardMasqueradingAsCUDA guard(depths.device());
+    Tensor ws = workspace((int64_t)gsr_depth_order_workspace_bytes(num_gaussians), depths);
+    check_rc(gsr_depth_order(num_gaussians, cfp(depths), ws.data_ptr(), (size_t)ws.numel(),
+                             order.data_ptr<int32_t>(), current_stream()),
+             "depth_order");
+    return order;
+}
+
+// Not in the reference surface: `rasterize` with the depth order given (from
+// depth_order) instead of sorted per call.
+std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_ordered(
+    int num_gaussians, const Tensor order, const Tensor depths, const Tensor mean_2d,
+    const Tensor cov_2d, const Tensor colors, const Tensor alpha, int height, int width) {
+    auto r = rasterize_impl(num_gaussians, depths, mean_2d, cov_2d, colors, alpha, height, width,
+                            false, &order);
+    return {std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<3>(r), std::get<4>(r)};
 }
 
 // ---- backwards_rasterization (bindings.cpp:72-100 / rasterize_backward.cu:239-309) ----
@@ -800,6 +841,10 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     m.def("backwards_SH", &backwards_SH, "3DGS backward spherical harmonics (HIP, gfx950)");
     m.def("backwards_projection", &backwards_projection,
           "3DGS backward projection (HIP, gfx950)");
+    m.def("depth_order", &depth_order,
+          "every Gaussian stably sorted by the float bits of its depth (int32 [N])");
+    m.def("rasterize_ordered", &rasterize_ordered,
+          "rasterize with a depth order from depth_order (screen bands of one frame)");
     m.def("rasterize_with_keys", &rasterize_with_keys,
           "rasterize, also returning the sorted 64-bit keys (tile << 32 | depth bits)");
     m.def("library_version", []() { return std::string(gsr_version()); });

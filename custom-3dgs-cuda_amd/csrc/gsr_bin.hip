@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
             in[u][2] = ok ? cov2d[3 * (size_t)i] : 0.0f;
             in[u][3] = ok ? cov2d[3 * (size_t)i + 1] : 0.0f;
             in[u][4] = ok ? cov2d[3 * (size_t)i + 2] : 0.0f;
-            in[u][5] = ok ? depth[i] : 0.0f;
+            in[u][5] = (ok && dkeys) ? depth[i] : 0.0f;
         }
 #pragma unroll
         for (int u = 0; u < kBinUnroll; ++u) {
@@ -136,13 +136,15 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
             counts[i] = cnt;
             rects[i] = make_uint2((uint32_t)r.x0 | ((uint32_t)r.x1 << 16),
                                   (uint32_t)r.y0 | ((uint32_t)r.y1 << 16));
-            // Gaussians without tiles sort last; they emit nothing, so their place
-            // in the depth order never shows.
-            const uint32_t dk = cnt ? __float_as_uint(in[u][5]) : 0xffffffffu;
-            dkeys[i] = dk;
-            dvals[i] = (uint32_t)i;
+            if (dkeys) {
+                // Gaussians without tiles sort last; they emit nothing, so their
+                // place in the depth order never shows.
+                const uint32_t dk = cnt ? __float_as_uint(in[u][5]) : 0xffffffffu;
+                dkeys[i] = dk;
+                dvals[i] = (uint32_t)i;
 #pragma unroll
-            for (int p = 0; p < 4; ++p) atomicAdd(&s_dh[p][(dk >> (8 * p)) & 0xffu], 1u);
+                for (int p = 0; p < 4; ++p) atomicAdd(&s_dh[p][(dk >> (8 * p)) & 0xffu], 1u);
+            }
             pairs += cnt;
             if (cnt && passes > 0) {
                 const uint32_t w = (uint32_t)(r.x1 - r.x0);
@@ -217,11 +219,26 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
         if ((tid & 63) == 0 && wp) atomicAdd(reinterpret_cast<unsigned long long*>(pair_total),
                                              (unsigned long long)wp);
     }
+    if (dkeys) {
 #pragma unroll
-    for (int p = 0; p < 4; ++p) {
-        const uint32_t v = s_dh[p][tid];
-        if (v) atomicAdd(&depth_hist[p * kRadixBins + tid], v);
+        for (int p = 0; p < 4; ++p) {
+            const uint32_t v = s_dh[p][tid];
+            if (v) atomicAdd(&depth_hist[p * kRadixBins + tid], v);
+        }
     }
+}
+
+// The depth sort's input for a depth order shared by several calls: every
+// Gaussian keyed by the bits of its depth (visible or not), valued by its
+// index.
+__global__ __launch_bounds__(kThreads) void depth_keys_kernel(int n,
+                                                              const float* __restrict__ depth,
+                                                              uint32_t* __restrict__ keys,
+                                                              uint32_t* __restrict__ vals) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    keys[i] = __float_as_uint(depth[i]);
+    vals[i] = (uint32_t)i;
 }
 
 // Behind bin_count_kernel (block histogram mode), one work-group: the block
@@ -431,6 +448,14 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
     if (e != hipSuccess || !block_hist) return e;
     hipLaunchKernelGGL(bin_finish_kernel, dim3(1), dim3(kThreads), 0, st, bg, block_hist,
                        pair_total, block_start, seg_start, host_total, status);
+    return hipGetLastError();
+}
+
+hipError_t launch_depth_keys(int n, const float* depth, uint32_t* keys, uint32_t* vals,
+                             hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(depth_keys_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, n, depth,
+                       keys, vals);
     return hipGetLastError();
 }
 

@@ -418,9 +418,16 @@ size_t gsr_bin_workspace_bytes(int n, int height, int width) {
     return bin_layout(n, height, width).end;
 }
 
-int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const float* cov2d,
-                      int height, int width, void* bin_ws, size_t bin_ws_bytes,
-                      int64_t* num_pairs, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// The bin step of gsr_rasterize_bin; with `order` (a depth order from
+// gsr_depth_order) the depth keys and the depth sort are skipped and the
+// order is copied in as the depth ranks' Gaussians.
+int rasterize_bin(int n, const float* depth, const int32_t* order, const float* mean2d,
+                  const float* cov2d, int height, int width, void* bin_ws, size_t bin_ws_bytes,
+                  int64_t* num_pairs, void* stream) {
     GSR_REQUIRE(n >= 0, "n must be non-negative");
     GSR_REQUIRE(num_pairs, "num_pairs must not be null");
     if (int rc = check_screen(height, width)) return rc;
@@ -431,7 +438,7 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
     hipStream_t st = as_stream(stream);
     GSR_HIP(gsr::zero_fill(bin_ws, L.ctl_end, st), "rasterize: clear");
     if (n == 0 || height == 0 || width == 0) return GSR_OK;
-    GSR_REQUIRE(depth && mean2d && cov2d, "null pointer");
+    GSR_REQUIRE((depth || order) && mean2d && cov2d, "null pointer");
     gsr::DeviceGlobals dg;
     GSR_HIP(gsr::device_globals(&dg), "rasterize: device globals");
     Misc* misc = at<Misc>(bin_ws, L.misc);
@@ -449,8 +456,9 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
     {
         StageTimer timer("bin_count", st);
         const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
-        GSR_HIP(gsr::launch_bin_count(n, mean2d, cov2d, depth, height, width, counts,
-                                      at<uint2>(bin_ws, L.rects), dk0, dv0,
+        GSR_HIP(gsr::launch_bin_count(n, mean2d, cov2d, order ? nullptr : depth, height, width,
+                                      counts, at<uint2>(bin_ws, L.rects),
+                                      order ? nullptr : dk0, order ? nullptr : dv0,
                                       blocks ? 0 : tile_passes(T),
                                       at<uint32_t>(bin_ws, L.tilehist),
                                       at<uint32_t>(bin_ws, L.sortctl),
@@ -465,6 +473,11 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
     if (!host) return fail(GSR_ERR_HIP, "rasterize: pinned host buffer allocation failed");
     auto depth_sort = [&]() -> int {
         StageTimer timer("depth_sort", st);
+        if (order) {
+            GSR_HIP(hipMemcpyAsync(dv0, order, 4 * (size_t)n, hipMemcpyDeviceToDevice, st),
+                    "rasterize: depth order");
+            return GSR_OK;
+        }
         GSR_HIP(gsr::launch_radix_sort(dk0, dv0, at<uint32_t>(bin_ws, L.dk1),
                                        at<uint32_t>(bin_ws, L.dv1), (uint64_t)n, 0, kDepthPasses,
                                        at<void>(bin_ws, L.sortctl), err, st,
@@ -514,6 +527,57 @@ int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const floa
                     "rasterize: " + std::to_string(host->total) +
                         " (Gaussian, tile) pairs exceed the int32 limit; render in screen bands");
     *num_pairs = (int64_t)host->total;
+    return GSR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gsr_rasterize_bin(int n, const float* depth, const float* mean2d, const float* cov2d,
+                      int height, int width, void* bin_ws, size_t bin_ws_bytes,
+                      int64_t* num_pairs, void* stream) {
+    return rasterize_bin(n, depth, nullptr, mean2d, cov2d, height, width, bin_ws, bin_ws_bytes,
+                         num_pairs, stream);
+}
+
+int gsr_rasterize_bin_ordered(int n, const int32_t* order, const float* mean2d,
+                              const float* cov2d, int height, int width, void* bin_ws,
+                              size_t bin_ws_bytes, int64_t* num_pairs, void* stream) {
+    GSR_REQUIRE(n == 0 || order, "order must not be null");
+    return rasterize_bin(n, nullptr, order, mean2d, cov2d, height, width, bin_ws, bin_ws_bytes,
+                         num_pairs, stream);
+}
+
+size_t gsr_depth_order_workspace_bytes(int n) {
+    if (n < 0) return 0;
+    const size_t un = (size_t)n;
+    return 3 * align_up(4 * un, 256) + gsr::sort_control_bytes(un, kDepthPasses);
+}
+
+int gsr_depth_order(int n, const float* depth, void* ws, size_t ws_bytes, int32_t* order,
+                    void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(depth && order, "null pointer");
+    GSR_REQUIRE(ws, "workspace must not be null");
+    if (ws_bytes < gsr_depth_order_workspace_bytes(n))
+        return fail(GSR_ERR_WORKSPACE, "depth order workspace too small");
+    hipStream_t st = as_stream(stream);
+    const size_t un = (size_t)n, w = align_up(4 * un, 256);
+    uint32_t* k0 = at<uint32_t>(ws, 0);
+    uint32_t* k1 = at<uint32_t>(ws, w);
+    uint32_t* v1 = at<uint32_t>(ws, 2 * w);
+    void* ctl = at<void>(ws, 3 * w);
+    uint32_t* v0 = reinterpret_cast<uint32_t*>(order);  // the 4-pass sort ends in (k0, v0)
+    gsr::DeviceGlobals dg;
+    GSR_HIP(gsr::device_globals(&dg), "depth order: device globals");
+    GSR_HIP(gsr::zero_fill(ctl, gsr::sort_control_bytes(un, kDepthPasses), st),
+            "depth order: clear");
+    GSR_HIP(gsr::launch_depth_keys(n, depth, k0, v0, st), "depth order: keys");
+    GSR_HIP(gsr::launch_radix_sort(k0, v0, k1, v1, (uint64_t)n, 0, kDepthPasses, ctl, dg.status,
+                                   st, /*hist_ready=*/false),
+            "depth order: sort");
     return GSR_OK;
 }
 
@@ -851,7 +915,7 @@ int gsr_rasterize_backward_noalloc(int n, int height, int width, const float* gr
     if (need > gsr::kNoAllocScratchBytes)
         return fail(GSR_ERR_WORKSPACE,
                     "backward (no allocation): the frame needs " + std::to_string(need) +
-                        " bytes of workspace (about 37 per pair and 68 per Gaussian), more than "
+                        " bytes of workspace (about 36 per pair and 68 per Gaussian), more than "
                         "the fixed scratch's " +
                         std::to_string(gsr::kNoAllocScratchBytes) +
                         "; use gsr_rasterize_backward with a workspace");

@@ -192,13 +192,19 @@ hipError_t launch_row_pairs(int n, const float* mean2d, const float* cov2d, int 
 // kernel behind it then writes the block and segment starts (block_start /
 // seg_start, nb + 1 entries each) and, when host_total is not null, the final
 // pair count to that host-mapped coherent word and the device status word
-// (status, read and cleared) to host_total[1].
+// (status, read and cleared) to host_total[1].  dkeys null: no depth keys,
+// values or depth histograms (depth is then not read).
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
                             uint32_t* block_start, uint32_t* seg_start,
                             uint64_t* host_total, int* status, hipStream_t st);
+
+// keys[i] = float bits of depth[i], vals[i] = i for every Gaussian: the input
+// of a depth order shared by several calls.
+hipError_t launch_depth_keys(int n, const float* depth, uint32_t* keys, uint32_t* vals,
+                             hipStream_t st);
 
 // Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r] (perm null:
 // the identity); the total (u64) is written to *total.

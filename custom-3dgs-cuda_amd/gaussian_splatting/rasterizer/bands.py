@@ -3,9 +3,9 @@ int32 lists of the rasterize surface (the reference keeps the pair count, the
 offsets and ``sorted_ids`` in int, rasterize.cu:382-390, rasterize.h:7-8).
 
 One autograd Function renders the frame as bands of whole tile rows:
-- forward: the fused head (camera position, project, radii, SH, sigmoid) runs
-  once; each band of rows [y0, y0 + h) is rasterized through the unchanged
-  surface from the frame's projection with the means moved up by y0 rows;
+- forward: the fused head (camera position, project, radii, SH, sigmoid) and
+  the depth sort run once; each band of rows [y0, y0 + h) is rasterized from
+  the frame's projection and depth order with the means moved up by y0 rows;
 - backward: each band's rasterize backward reads its rows of dL/dimage in
   place and adds its d mean2d, d cov2d, d colour and d opacity into the
   frame's (the first band writes them), and the fused tail (SH and
@@ -131,11 +131,14 @@ class _RasterizeBandsFunction(t.autograd.Function):
             rows = plan_bands(frame_row_pairs(mean_2d, cov_2d, H, W), H, max_pairs)
         else:
             rows = band_rows(H, band_height)
+        # one depth order for all bands: each band's visible Gaussians appear
+        # in it as that band's own depth sort would order them
+        order = crc.depth_order(n, depths)
         images, saved = [], []
         for y0, h in rows:
             mean_b = mean_2d - mean_2d.new_tensor([0.0, float(y0)])
-            img, ids, ranges, final_T, n_contrib = crc.rasterize(n, depths, mean_b, cov_2d, colors,
-                                                                 opacity, h, W)
+            img, ids, ranges, final_T, n_contrib = crc.rasterize_ordered(
+                n, order, depths, mean_b, cov_2d, colors, opacity, h, W)
             images.append(img)
             saved += [mean_b, ids, ranges, final_T, n_contrib]
         ctx.save_for_backward(cov_2d, colors, opacity, mu, q, s, albedo, k_j, cam_rotation,

@@ -109,6 +109,25 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                          size_t sort_ws_bytes, int32_t* sorted_ids, int32_t* tile_ranges,
                          float* img, float* final_T, int32_t* n_contrib, uint64_t* sorted_keys,
                          void* stream);
+
+/* No counterpart in the reference (its int32 lists cap a frame's pairs; the
+ * screen-band path renders larger frames band by band).  For callers that
+ * rasterize several screen bands of one frame:
+ *   gsr_depth_order writes order[0 .. n) = every Gaussian, visible or not,
+ *   stably sorted by the float bits of depth[i] (as unsigned); a band's
+ *   visible Gaussians then appear in it in the order the reference's
+ *   (tile << 32 | depth bits) sort gives them (rasterize.cu:423-435), ties by
+ *   index.  ws is sized by gsr_depth_order_workspace_bytes(n).
+ *   gsr_rasterize_bin_ordered is gsr_rasterize_bin with that order given
+ *   instead of computed (no depth keys, no depth sort); `order` must be a
+ *   permutation of [0, n) and stays read-only.  gsr_rasterize_render follows
+ *   as usual. */
+size_t gsr_depth_order_workspace_bytes(int n);
+int gsr_depth_order(int n, const float* depth, void* ws, size_t ws_bytes, int32_t* order,
+                    void* stream);
+int gsr_rasterize_bin_ordered(int n, const int32_t* order, const float* mean2d,
+                              const float* cov2d, int height, int width, void* bin_ws,
+                              size_t bin_ws_bytes, int64_t* num_pairs, void* stream);
 /* Synchronizes `stream`, then reads and clears the current device's status
  * word: GSR_ERR_DEVICE if a kernel queued on the device since the status was
  * last read hit its look-back spin bound or found inconsistent counts.
@@ -147,7 +166,7 @@ int gsr_tile_row_pairs(int n, const float* mean2d, const float* cov2d, int heigh
  * the length of sorted_ids (tile ranges are clamped to it); ids outside
  * [0, n) are skipped as in the reference.  Outputs: d_mean2d [N,2],
  * d_cov2d [N,3] (dL/d(a,b,c)), d_colors [N,3], d_alpha [N].  The workspace
- * (about 37 B per pair plus 68 B per Gaussian) holds the blend records, the
+ * (about 36 B per pair plus 68 B per Gaussian) holds the blend records, the
  * per-tile schedule and one gradient slot per (Gaussian, tile) pair: the
  * per-tile sums are written to their slots and summed per Gaussian, with no
  * float atomics, so the result does not depend on scheduling. */
@@ -199,7 +218,7 @@ int gsr_rasterize_backward_accumulate(int n, int height, int width, const float*
  * loops, harnesses that forbid hipMalloc).  It takes no workspace: its
  * kernels use a fixed array of GSR_NOALLOC_SCRATCH_BYTES in the library's
  * device memory, one per GPU, held until the process ends.  A frame whose
- * workspace (gsr_backward_workspace_bytes: about 37 B per pair plus 68 B per
+ * workspace (gsr_backward_workspace_bytes: about 36 B per pair plus 68 B per
  * Gaussian) exceeds it is rejected with GSR_ERR_WORKSPACE.  The call
  * allocates nothing.  Every call on one GPU shares that GPU's array, so calls
  * that overlap on one GPU (other streams, other threads) race; calls queued

@@ -53,6 +53,46 @@ def test_each_band_matches_the_oracle(crc, device):
         assert_bitwise(_np(fT), wfT, "final_T")
 
 
+def test_depth_order_is_the_stable_sort_of_the_depth_bits(crc, device):
+    """depth_order against numpy's stable argsort of the depths' float bits as
+    unsigned: ties (repeated depths), -0.0 / 0.0, negative depths, infinities
+    and NaNs of both signs, at a 1024-key partition boundary and beyond 2^18
+    keys (the depth sort's two partition sizes)."""
+    rng = np.random.default_rng(5)
+    for n in (1, 1000, 1024 * 37 + 5, 300_000):
+        print(f"[gpu] depth order of {n} keys", flush=True)
+        d = np.round(rng.uniform(-2.0, 60.0, n) * 8.0).astype(np.float32) / np.float32(8.0)
+        special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, -np.nan, 1e-30, -1e30],
+                           np.float32)
+        k = min(n, 64)
+        d[rng.integers(0, n, k)] = special[rng.integers(0, special.size, k)]
+        got = _np(crc.depth_order(n, torch.from_numpy(d).to(device)))
+        want = np.argsort(d.view(np.uint32), kind="stable").astype(np.int32)
+        assert_bitwise(got, want, f"depth order (n={n})")
+
+
+def test_rasterize_ordered_equals_rasterize(crc, device):
+    """Each band of a c5-distribution frame (30k Gaussians, 400x224, 64-row
+    bands), rasterized from the frame's depth order, equals rasterize (its own
+    depth sort) bit for bit: ids, ranges, n_contrib, image, final T.  The
+    depths are quantized so that many Gaussians tie."""
+    sc = synthetic.config_scene("c5", requires_grad=False, n=30_000, width=400, height=224)
+    a = scene_arrays(sc)
+    fw, n = gpu_forward(crc, a, device), a["mu"].shape[0]
+    t = fw["tensors"]
+    depth = (torch.from_numpy(fw["depth"]).to(device) * 4.0).round() / 4.0
+    order = crc.depth_order(n, depth)
+    for y0, h in band_rows(a["H"], 64):
+        print(f"[gpu] ordered band at row {y0}, {h} rows", flush=True)
+        mb = t["mean2d"] - t["mean2d"].new_tensor([0.0, float(y0)])
+        args = (depth, mb, t["cov2d"], t["colors"], t["alpha"], h, a["W"])
+        want = crc.rasterize(n, *args)
+        got = crc.rasterize_ordered(n, order, *args)
+        for x, y, nm in zip(got, want, ("img", "sorted_ids", "tile_ranges", "final_T",
+                                         "n_contrib")):
+            assert_bitwise(_np(x), _np(y), f"{nm} (band {y0})")
+
+
 def test_banded_glue_equals_the_whole_frame(device):
     """rasterize_bands against rasterize on a frame that fits: the image bit
     for bit, the parameter gradients and last_mean2d_grad within 1e-6

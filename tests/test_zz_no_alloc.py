@@ -84,7 +84,7 @@ def test_noalloc_backward_matches_the_workspace_entry_point(crc, device):
 def test_noalloc_backward_rejects_frames_beyond_the_scratch(device):
     L = _lib()
     n, H, W = 100_000, 1080, 1920
-    m = 20_000_000  # 37 B per pair: ~740 MB of workspace
+    m = 20_000_000  # 36 B per pair: ~720 MB of workspace
     assert L.gsr_backward_workspace_bytes(n, m, H, W) > SCRATCH
     dummy = torch.zeros(16, device=device)
     p = ctypes.c_void_p(dummy.data_ptr())
