@@ -25,7 +25,6 @@
 // at 1080p); level 2 reads the block lists twice and writes the M pair ids
 // once, in runs of consecutive addresses (one run per wave and tile).
 #include <algorithm>
-#include <type_traits>
 
 #include "gsr_internal.h"
 #include "gsr_common.h"
@@ -422,12 +421,17 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
          k += stride) {
         const SegInfo I = seg_info(k, seg_owner, seg_start, block_start, bg.bw, bg.nb);
         const SegLane S = seg_lane<true>(lists, lrects, I.first, I.end, cap, n);
-        // lane t: where segment k's entries of tile t begin
+        // lane t: where segment k's entries of tile t begin (its list start
+        // plus the segment's prefix); the block's first tile has the lowest
+        // list start, b0, and each run is addressed from ids + b0
         const int tx = I.ox + (lane & 7), ty = I.oy + (lane >> 3);
-        uint32_t base = 0;
-        if (tx < bg.tiles_x && ty < bg.tiles_y)
-            base = (uint32_t)ranges[(size_t)ty * bg.tiles_x + tx].x +
-                   tcount[(size_t)k * kWave + lane];
+        const bool on = tx < bg.tiles_x && ty < bg.tiles_y;
+        uint32_t lstart = 0, base = 0;
+        if (on) {
+            lstart = (uint32_t)ranges[(size_t)ty * bg.tiles_x + tx].x;
+            base = lstart + tcount[(size_t)k * kWave + lane];
+        }
+        const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane((int)lstart, 0);
         // in_row[r] / in_col[c]: this lane covers tile row r / column c; as
         // lane masks they are the ballots, so the lanes of tile (r, c) are
         // selected with scalar ANDs
@@ -440,30 +444,36 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
             rows[j] = ballot(in_row[j]);
             cols[j] = ballot(in_col[j]);
         }
-        // the lanes of tile t's mask write positions b_t + their rank in it;
-        // when every run b_t + [0, 64) lies below m (all but the list's last
-        // entries) no position needs its own check
-        const bool fits = ballot((uint64_t)base + (uint64_t)kWave > m) == 0ull;
-        auto scatter = [&](auto checked) {
+        // The lanes of tile t's mask write positions b_t + their rank in it.
+        // When every run b_t + [0, 64) lies in [b0, m) and within 2^30 entries
+        // of b0 (all but the list's last entries, for consistent counts), the
+        // stores take a 32-bit byte offset from ids + b0 and no position needs
+        // its own check.
+        const bool fits =
+            ballot(on && (base < b0 || base - b0 >= (1u << 30) ||
+                          (uint64_t)base + (uint64_t)kWave > m)) == 0ull;
+        if (fits) {
+            uint32_t* run0 = ids + b0;
+            const uint32_t dq = (base - b0) << 2;  // byte offset of this lane's tile's run
+#pragma unroll
+            for (int t = 0; t < 64; ++t) {
+                if (in_row[t >> 3] && in_col[t & 7]) {
+                    const uint32_t rank = rank_in(rows[t >> 3] & cols[t & 7]);
+                    const uint32_t off =
+                        (rank << 2) + (uint32_t)__builtin_amdgcn_readlane((int)dq, t);
+                    *reinterpret_cast<uint32_t*>(reinterpret_cast<char*>(run0) + off) = S.g;
+                }
+            }
+        } else {
 #pragma unroll
             for (int t = 0; t < 64; ++t) {
                 const uint64_t mk = rows[t >> 3] & cols[t & 7];
                 if (mk == 0) continue;
-                const uint32_t b = (uint32_t)__builtin_amdgcn_readlane((int)base, t);
-                const uint32_t rank = rank_in(mk);
-                if (!(in_row[t >> 3] && in_col[t & 7])) continue;
-                if constexpr (decltype(checked)::value) {
-                    if ((uint64_t)b + rank < m) ids[(uint64_t)b + rank] = S.g;
-                } else {
-                    uint32_t* dst = ids + b;  // wave-uniform run start
-                    dst[rank] = S.g;
-                }
+                const uint64_t p = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)base, t) +
+                                   (uint64_t)rank_in(mk);
+                if (in_row[t >> 3] && in_col[t & 7] && p < m) ids[p] = S.g;
             }
-        };
-        if (fits)
-            scatter(std::false_type{});
-        else
-            scatter(std::true_type{});
+        }
     }
 }
 
@@ -490,6 +500,9 @@ inline unsigned groups_for(uint64_t waves) {
 
 // Work-groups of the grid-strided segment kernels: enough for the bound on
 // segments, at most 8 per CU of a 256-CU device.
+// Pair lists beyond which tile_scatter runs fewer work-groups (1 GB of ids).
+constexpr uint64_t kScatterThrottlePairs = 1ull << 28;
+
 inline unsigned seg_groups(uint64_t seg_bound) {
     return (unsigned)std::max<uint64_t>(1, std::min<uint64_t>(groups_for(seg_bound), 2048));
 }
@@ -554,7 +567,14 @@ hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
                        bg.tiles_x * bg.tiles_y, tb.ttotal, tb.m,
                        reinterpret_cast<int2*>(tb.ranges), tb.err);
     if ((e = hipGetLastError()) != hipSuccess) return e;
-    hipLaunchKernelGGL(tile_scatter_kernel, dim3(seg_groups(segs)), dim3(kThreads), 0, st, tb.n,
+    // Each wave writes its segment's 64 runs to 64 lists.  Once the lists
+    // are gigabytes (config c5: 7.4 GB per band, runs of ~13 ids), fewer
+    // waves in flight write faster: 2 work-groups per CU took c5's binning
+    // from 24.3 to 21.7 ms per frame, while 8 stay best at c4 (166 MB of ids:
+    // 166 us against 194) and at 1080p.
+    const unsigned scatter_groups =
+        tb.m > kScatterThrottlePairs ? std::min(seg_groups(segs), 512u) : seg_groups(segs);
+    hipLaunchKernelGGL(tile_scatter_kernel, dim3(scatter_groups), dim3(kThreads), 0, st, tb.n,
                        bg, tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.lrects,
                        seg_cap, tb.tcount, reinterpret_cast<const int2*>(tb.ranges), tb.m,
                        tb.ids);
