@@ -60,11 +60,11 @@ def stage_bytes(stage: str, N: int, M: int, W: int, H: int) -> float:
         "tile_binning": 4 * M + 2 * 12 * N + 3 * 4 * N + 8 * T,
         "fwd_schedule": 16 * T,                 # ranges in, estimates + order out (walk not counted)
         "blend_fwd": 40 * M + 20 * P + 8 * T,
-        "bwd_records": 96 * N,
-        "bwd_slots": 8 * N,
+        # mean2d, cov2d, colour, opacity in; record, count, rect, slot offset out
+        "bwd_records": 100 * N,
         "bwd_schedule": 4 * P + 16 * T,
         "blend_bwd": 76 * M + 20 * P + 8 * T,
-        "grad_reduce": M + 8 * N,               # slot flags + offsets (sums of processed pairs not counted)
+        "grad_reduce": M // 8 + 8 * N,          # slot flag bits + offsets (sums of processed pairs not counted)
         "sh_bwd": 420 * N,
         "project_bwd": 100 * N,
         # the two backwards in one pass: mu read once, dL/dmu written once

@@ -393,6 +393,27 @@ __device__ __forceinline__ float alpha_q_threshold(float o) {
 // opacity and colour so the blend loads one 48 B record per list entry.
 // With counts != null (the backward), also each Gaussian's tile rectangle and
 // count, exactly as bin_count_kernel forms them.
+__device__ __forceinline__ BlendRec blend_record(float mx, float my, float a, float b, float c,
+                                                 float opacity, float r, float g, float bl) {
+    const float det = a * c - b * b;
+    const float det_inv = (det > 0.0f) ? (1.0f / det) : 0.0f;
+    const float cx = c * det_inv, cy = -b * det_inv, cz = a * det_inv;
+    BlendRec rec;
+    rec.a = make_float4(mx, my, -0.5f * cx, -cy);
+    rec.b = make_float4(-0.5f * cz, opacity, r, g);
+    rec.c = make_float4(bl, -0.5f * cy, alpha_q_threshold(opacity), 0.0f);
+    return rec;
+}
+
+__device__ __forceinline__ uint32_t rect_count(const TileRect& tr) {
+    return tr.ok ? (uint32_t)(max(0, tr.x1 - tr.x0) * max(0, tr.y1 - tr.y0)) : 0u;
+}
+
+__device__ __forceinline__ uint2 rect_word(const TileRect& tr) {
+    return make_uint2((uint32_t)tr.x0 | ((uint32_t)tr.x1 << 16),
+                      (uint32_t)tr.y0 | ((uint32_t)tr.y1 << 16));
+}
+
 __global__ __launch_bounds__(kThreads) void blend_records_kernel(
     int n, const float* __restrict__ mean2d, const float* __restrict__ cov2d,
     const float* __restrict__ colors, const float* __restrict__ alpha,
@@ -400,23 +421,101 @@ __global__ __launch_bounds__(kThreads) void blend_records_kernel(
     uint2* __restrict__ rects) {
     const int i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= n) return;
-    if (counts) {
-        const TileRect tr = tile_rect(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1],
-                                      cov2d[3 * (size_t)i], cov2d[3 * (size_t)i + 1],
-                                      cov2d[3 * (size_t)i + 2], W, H);
-        counts[i] = tr.ok ? (uint32_t)(max(0, tr.x1 - tr.x0) * max(0, tr.y1 - tr.y0)) : 0u;
-        rects[i] = make_uint2((uint32_t)tr.x0 | ((uint32_t)tr.x1 << 16),
-                              (uint32_t)tr.y0 | ((uint32_t)tr.y1 << 16));
-    }
+    const float mx = mean2d[2 * (size_t)i], my = mean2d[2 * (size_t)i + 1];
     const float a = cov2d[3 * (size_t)i], b = cov2d[3 * (size_t)i + 1], c = cov2d[3 * (size_t)i + 2];
-    const float det = a * c - b * b;
-    const float det_inv = (det > 0.0f) ? (1.0f / det) : 0.0f;
-    const float cx = c * det_inv, cy = -b * det_inv, cz = a * det_inv;
-    BlendRec r;
-    r.a = make_float4(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1], -0.5f * cx, -cy);
-    r.b = make_float4(-0.5f * cz, alpha[i], colors[3 * (size_t)i], colors[3 * (size_t)i + 1]);
-    r.c = make_float4(colors[3 * (size_t)i + 2], -0.5f * cy, alpha_q_threshold(alpha[i]), 0.0f);
-    recs[i] = r;
+    if (counts) {
+        const TileRect tr = tile_rect(mx, my, a, b, c, W, H);
+        counts[i] = rect_count(tr);
+        rects[i] = rect_word(tr);
+    }
+    recs[i] = blend_record(mx, my, a, b, c, alpha[i], colors[3 * (size_t)i],
+                           colors[3 * (size_t)i + 1], colors[3 * (size_t)i + 2]);
+}
+
+// The backward's per-Gaussian pass in one kernel: blend records, tile
+// rectangles and counts (as blend_records_kernel forms them), and the
+// Gaussian-major slot offsets goff[i] = counts[0] + ... + counts[i - 1] (the
+// total to *total) through a decoupled look-back over partitions of
+// kSlotItems x 256 Gaussians, claimed in launch order.  The records are
+// formed while the first wave looks back.
+constexpr int kSlotItems = 2;
+constexpr int kSlotPartition = kThreads * kSlotItems;
+
+__global__ __launch_bounds__(kThreads) void records_slots_kernel(
+    int n, const float* __restrict__ mean2d, const float* __restrict__ cov2d,
+    const float* __restrict__ colors, const float* __restrict__ alpha,
+    BlendRec* __restrict__ recs, int H, int W, uint32_t* __restrict__ counts,
+    uint2* __restrict__ rects, uint32_t* __restrict__ goff, uint64_t* __restrict__ total,
+    uint64_t* __restrict__ status, uint32_t* __restrict__ counter, int* __restrict__ err) {
+    __shared__ uint32_t s_part;
+    __shared__ uint32_t s_wsum[kThreads / kWave];
+    __shared__ uint64_t s_base;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_part = atomicAdd(counter, 1u);
+    __syncthreads();
+    const uint64_t part = s_part;
+    const int64_t first = (int64_t)part * kSlotPartition + (int64_t)tid * kSlotItems;
+    // every input loaded up front, all loads in flight together
+    float in[kSlotItems][9];
+#pragma unroll
+    for (int j = 0; j < kSlotItems; ++j) {
+        const int64_t i = first + j;
+        const bool ok = i < n;
+        in[j][0] = ok ? mean2d[2 * (size_t)i] : 0.0f;
+        in[j][1] = ok ? mean2d[2 * (size_t)i + 1] : 0.0f;
+        in[j][2] = ok ? cov2d[3 * (size_t)i] : 0.0f;
+        in[j][3] = ok ? cov2d[3 * (size_t)i + 1] : 0.0f;
+        in[j][4] = ok ? cov2d[3 * (size_t)i + 2] : 0.0f;
+        in[j][5] = ok ? alpha[i] : 0.0f;
+        in[j][6] = ok ? colors[3 * (size_t)i] : 0.0f;
+        in[j][7] = ok ? colors[3 * (size_t)i + 1] : 0.0f;
+        in[j][8] = ok ? colors[3 * (size_t)i + 2] : 0.0f;
+    }
+    uint32_t cnt[kSlotItems];
+    uint32_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < kSlotItems; ++j) {
+        const int64_t i = first + j;
+        cnt[j] = 0u;
+        if (i < n) {
+            const TileRect tr = tile_rect(in[j][0], in[j][1], in[j][2], in[j][3], in[j][4], W, H);
+            cnt[j] = rect_count(tr);
+            counts[i] = cnt[j];
+            rects[i] = rect_word(tr);
+        }
+        sum += cnt[j];
+    }
+    const uint32_t inc = wave_inclusive_scan(sum);
+    if (lane == 63) s_wsum[wave] = inc;
+    __syncthreads();
+    uint32_t wpre = 0, btot = 0;
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w) {
+        if (w < wave) wpre += s_wsum[w];
+        btot += s_wsum[w];
+    }
+    if (wave == 0) {
+        const uint64_t excl = wave_lookback(status, part, (uint64_t)btot, err);
+        if (lane == 0) {
+            s_base = excl;
+            if (part * kSlotPartition + kSlotPartition >= (uint64_t)n) *total = excl + btot;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < kSlotItems; ++j) {
+        const int64_t i = first + j;
+        if (i < n)
+            recs[i] = blend_record(in[j][0], in[j][1], in[j][2], in[j][3], in[j][4], in[j][5],
+                                   in[j][6], in[j][7], in[j][8]);
+    }
+    __syncthreads();
+    uint64_t run = s_base + wpre + inc - sum;
+#pragma unroll
+    for (int j = 0; j < kSlotItems; ++j) {
+        const int64_t i = first + j;
+        if (i < n) goff[i] = (uint32_t)run;
+        run += cnt[j];
+    }
 }
 
 inline unsigned blocks_for(uint64_t n) { return (unsigned)((n + kThreads - 1) / kThreads); }
@@ -501,6 +600,25 @@ hipError_t launch_full_keys(uint64_t m, const uint32_t* sorted_tiles, int shift,
     if (m == 0) return hipSuccess;
     hipLaunchKernelGGL(full_keys_kernel, dim3(blocks_for(m)), dim3(kThreads), 0, st, m,
                        sorted_tiles, shift, ids, depth, n, keys);
+    return hipGetLastError();
+}
+
+size_t records_slots_control_bytes(int n) {
+    const size_t parts = ((size_t)std::max(n, 1) + kSlotPartition - 1) / kSlotPartition;
+    return 256 + parts * 8;
+}
+
+hipError_t launch_records_slots(int n, const float* mean2d, const float* cov2d,
+                                const float* colors, const float* alpha, void* recs, int H, int W,
+                                uint32_t* counts, uint2* rects, uint32_t* goff, uint64_t* total,
+                                void* control, int* err, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    const unsigned parts = (unsigned)(((size_t)n + kSlotPartition - 1) / kSlotPartition);
+    uint32_t* counter = static_cast<uint32_t*>(control);
+    uint64_t* status = reinterpret_cast<uint64_t*>(static_cast<char*>(control) + 256);
+    hipLaunchKernelGGL(records_slots_kernel, dim3(parts), dim3(kThreads), 0, st, n, mean2d, cov2d,
+                       colors, alpha, static_cast<BlendRec*>(recs), H, W, counts, rects, goff,
+                       total, status, counter, err);
     return hipGetLastError();
 }
 

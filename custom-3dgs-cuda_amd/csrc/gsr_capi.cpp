@@ -213,7 +213,7 @@ BwdLayout backward_layout(int n, int64_t m, int height, int width) {
     L.goff = take(4 * un);
     L.ctl = off;
     L.misc = take(sizeof(Misc));
-    L.scanctl = take(gsr::scan_control_bytes(n));
+    L.scanctl = take(gsr::records_slots_control_bytes(n));
     L.flags = take(align_up(um, 64) / 8);  // one bit per slot, read as 64-bit words
     L.ctl_end = off;
     L.sums = take(36 * um);
@@ -804,15 +804,10 @@ int rasterize_backward(int n, int height, int width, const float* grad_img,
     uint32_t* goff = at<uint32_t>(ws, L.goff);
     {
         StageTimer timer("bwd_records", st);
-        GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, at<void>(ws, L.recs),
-                                          st, height, width, counts, rects),
-                "backward: records");
-    }
-    {
-        StageTimer timer("bwd_slots", st);
-        GSR_HIP(gsr::launch_scan_counts(n, nullptr, counts, goff, &misc->total,
-                                        at<void>(ws, L.scanctl), dg.status, st),
-                "backward: slot layout");
+        GSR_HIP(gsr::launch_records_slots(n, mean2d, cov2d, colors, alpha, at<void>(ws, L.recs),
+                                          height, width, counts, rects, goff, &misc->total,
+                                          at<void>(ws, L.scanctl), dg.status, st),
+                "backward: records and slot layout");
     }
     gsr::GradSlots gs;
     gs.goff = goff;

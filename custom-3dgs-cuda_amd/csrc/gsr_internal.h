@@ -201,6 +201,15 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
                             uint32_t* block_start, uint32_t* seg_start,
                             uint64_t* host_total, int* status, hipStream_t st);
 
+// The backward's per-Gaussian pass: blend records, tile rectangles and counts,
+// and the slot offsets goff (exclusive scan of the counts in Gaussian order,
+// total to *total).  control: records_slots_control_bytes(n), zeroed.
+size_t records_slots_control_bytes(int n);
+hipError_t launch_records_slots(int n, const float* mean2d, const float* cov2d,
+                                const float* colors, const float* alpha, void* recs, int H, int W,
+                                uint32_t* counts, uint2* rects, uint32_t* goff, uint64_t* total,
+                                void* control, int* err, hipStream_t st);
+
 // keys[i] = float bits of depth[i], vals[i] = i for every Gaussian: the input
 // of a depth order shared by several calls.
 hipError_t launch_depth_keys(int n, const float* depth, uint32_t* keys, uint32_t* vals,
