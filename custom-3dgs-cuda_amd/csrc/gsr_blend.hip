@@ -1132,6 +1132,22 @@ int cu_count() { return device_facts().cus; }
 // Whether the backward's whole grid of tiles is resident on the device at once.
 bool bwd_grid_fits(unsigned tiles) { return tiles <= device_facts().bwd_resident; }
 
+// Lists that average this many entries per tile or more (the screen bands of
+// config c5 average ~350k) are walked like a resident grid's: 128-entry
+// batches with the longest tiles split.  Their longest tiles set the kernel's
+// length there (c5: blend_bwd 8.0 ms per frame with 64-entry batches, 5.5 with
+// 128, 4.5 with 128 and the split), while at 1080p (1.6k entries per tile) the
+// 64-entry batch without the split stays ahead (251 us against 259).
+constexpr uint64_t kLongListAvg = 32768;
+bool bwd_long_lists(unsigned tiles, uint64_t pairs) {
+    return pairs >= kLongListAvg * (uint64_t)tiles;
+}
+
+// Whether the backward walks 128-entry batches and may split long tiles.
+bool bwd_wide(unsigned tiles, uint64_t pairs) {
+    return bwd_grid_fits(tiles) || bwd_long_lists(tiles, pairs);
+}
+
 }  // namespace
 
 hipError_t launch_fwd_schedule(int n, int H, int W, const int32_t* ranges, const int32_t* ids,
@@ -1178,7 +1194,7 @@ hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num
                        num_pairs, r, ncontrib, work, vec4);
     hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles,
                        num_pairs, r, work, order,
-                       (bwd_split() && bwd_grid_fits(tiles)) ? kSplitMax : 0,
+                       (bwd_split() && bwd_wide(tiles, num_pairs)) ? kSplitMax : 0,
                        cu_count());
     return hipGetLastError();
 }
@@ -1195,17 +1211,17 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const GradSt
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
     const auto* rc = static_cast<const BlendRec*>(recs);
-    // With a schedule and the whole grid resident at once, the longest tiles
-    // set the kernel's length: up to kSplitMax of them run as two items each.
-    // When the grid does not fit, the total work does, and the split's extra
-    // state-only walk costs more than it saves.
-    const bool fits = bwd_grid_fits(tiles);
-    const bool split = order && bwd_split() && fits;
+    // With a schedule and the whole grid resident at once, or lists long
+    // enough that the longest tiles set the kernel's length, up to kSplitMax
+    // of the longest run as two items each.  Otherwise the total work does,
+    // and the split's extra state-only walk costs more than it saves.
+    const bool wide = bwd_wide(tiles, num_pairs);
+    const bool split = order && bwd_split() && wide;
     // The 64-entry batch halves the work-group's LDS (8 KB), so registers, not
     // LDS, bound the resident waves; it pays when the grid does not fit on the
     // device at once.  When it would, the 128-entry batch leaves part of the
     // grid to be placed as CUs free up, which balances the long tiles better.
-    if (!fits)
+    if (!wide)
         hipLaunchKernelGGL((blend_bwd_kernel<2, 64, false>), dim3(tiles),
                            dim3(Layout<2>::kThreads), 0, st, n, H, W, tiles_x, num_pairs, grad, gst,
                            r, ids, rc, finalT, ncontrib, dmean, dcov, dcol, dalpha, gs, order);
