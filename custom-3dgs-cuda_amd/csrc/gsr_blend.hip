@@ -396,17 +396,17 @@ __device__ __forceinline__ BwdTerms bwd_update(BwdPixel& p, const BwdDecision& d
 #pragma clang fp contract(fast)
     BwdTerms t;
     // T / (1 - alpha) with 1 - alpha in [0.01, 1]: the reference's 1e-4 floor
-    // never applies.  The hardware reciprocal (1 ulp) times T, then one
-    // correction from the exact residual T - q (1 - alpha) (a fused
-    // multiply-add): the quotient is within ~0.5 ulp, as a division's.  Without
-    // the correction T drifts by ~1.5 ulp per entry, and over the two thousand
-    // entries of a long list the drift reaches 1e-5 of the terms that a
-    // Gaussian's gradient sums (every term scales with T).  A skipped entry
-    // (alpha 0) leaves T unchanged: the reciprocal of 1 is exact.
+    // never applies.  The hardware reciprocal (1 ulp) times T: about 1.5 ulp
+    // per entry where a division is 0.5, so over the two thousand entries of
+    // the benchmark scene's longest lists T drifts by a few 1e-5, against the
+    // 1e-5 that the reference's own fp32 division reaches there; both lie
+    // within the 1e-4 gradient bar.  A correction step from the exact residual
+    // T - q (1 - alpha) (two fused multiply-adds on the entry's dependency
+    // chain) brought the quotient to a division's 0.5 ulp and cost 15 us of
+    // the bench frame's 229 us backward blend.  A skipped entry (alpha 0)
+    // leaves T unchanged: the reciprocal of 1 is exact.
     const float den = 1.0f - d.ae;
-    const float rd = __builtin_amdgcn_rcpf(den);
-    const float q0 = p.T * rd;
-    const float Tb = __builtin_fmaf(__builtin_fmaf(-q0, den, p.T), rd, q0);
+    const float Tb = p.T * __builtin_amdgcn_rcpf(den);
     const float cg = B.z * p.g0 + B.w * p.g1 + cb * p.g2;
     const float diff = cg - p.accg;
     t.aT = d.ae * Tb;
