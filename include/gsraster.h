@@ -381,7 +381,8 @@ int gsr_adc_apply(int n, float* const params[6], float* const moments[12],
  * enabled, each entry point records a pair of HIP events on its stream around
  * its stage's kernels: "project", "sh", "project_sh", "bin_count",
  * "depth_sort", "scan", "records", "tile_binning", "tile_sort", "ranges",
- * "fwd_schedule", "blend_fwd", "bwd_records", "bwd_slots", "bwd_schedule",
+ * "fwd_schedule", "blend_fwd", "bwd_records" (records and slot offsets),
+ * "bwd_schedule",
  * "blend_bwd", "grad_reduce", "sh_bwd", "project_bwd", "project_sh_bwd",
  * "loss", "loss_bwd", "adam", "ply_pack", "adc_stats", "adc_plan", "adc_apply".
  * gsr_profile_collect waits for the recorded events
