@@ -906,13 +906,17 @@ __global__ __launch_bounds__(kWorkTilesPerBlock * kWave) void tile_work_bwd_kern
 // list until every pixel is done).  An ordering heuristic only: it uses the
 // hardware exp and log and no culling.  Measured against five points and a
 // 1024-entry cap, it costs less than it loses in ordering (render -5 us at
-// 1080p, -11 us at 720p on the bench scene, +3 us on c3).
+// 1080p, -11 us at 720p on the bench scene, +3 us on c3).  Ordering by list
+// length alone (no walk) made the bench scene's forward blend 32 us slower;
+// one centre point cost c4's blend 5 us.
 constexpr int kEstPoints = 2;
 
 // One wave per tile, 64 entries per step, the next step's ids prefetched.  A
-// sample pixel still live after kEstCap entries counts as never done.
+// sample pixel still live after kEstCap entries counts as never done.  256
+// orders as well as 512 and 1024 on the bench scene, c3 and c4 and walks
+// less (the estimate 22 to 19 us on the bench scene); 128 orders worse.
 constexpr int kEstTilesPerBlock = 4;
-constexpr int kEstCap = 512;
+constexpr int kEstCap = 256;
 
 __global__ __launch_bounds__(kEstTilesPerBlock * kWave) void tile_work_fwd_kernel(
     int T, int tiles_x, int n, uint64_t m, const int2* __restrict__ ranges,
