@@ -831,15 +831,17 @@ __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
             bits = nbits;
         }
     }
+    // a Gaussian without claimed slots adds nothing (at 4K most Gaussians
+    // have none in a given screen band): its outputs are not read or written,
+    // and a wave without any skips the row sums
+    const uint64_t wave_claims = ballot(claimed);
+    if (wave_claims == 0ull) return;
     // every lane takes part in the row sums (rows past n add zeros)
     float t[kTerms];
 #pragma unroll
     for (int k = 0; k < kTerms; ++k) t[k] = row_sum<kReduceRowLanes>(v[k]);
-    // a Gaussian without claimed slots adds nothing (at 4K most Gaussians
-    // have none in a given screen band): its outputs are not read or written
     const uint64_t row_claims =
-        (ballot(claimed) >> (lane_id() & (64 - kReduceRowLanes))) &
-        ((1ull << kReduceRowLanes) - 1);
+        (wave_claims >> (lane_id() & (64 - kReduceRowLanes))) & ((1ull << kReduceRowLanes) - 1);
     if (g < n && sub == 0 && row_claims != 0) {
         const BlendRec r = recs[g];
         float dc[3];
