@@ -200,7 +200,7 @@ __device__ __forceinline__ void fwd_step(FwdPixel& p, float fx, float fy, const 
     const float dx = fx - A.x;
     const float dy = fy - A.y;
     const float power = blend_power(dx, dy, A, B);
-    const float alpha = fminf(kAlphaMax, B.y * exp_blend(power));
+    const float alpha = fminf(kAlphaMax, B.y * exp_blend_noclamp(power));
     const bool blend = live(p) & !(power > 0.0f) & !(alpha < kAlphaMin);
     const float w = alpha * p.T;
     const float Tn = p.T * (1.0f - alpha);

@@ -64,6 +64,17 @@ __device__ __forceinline__ float exp_blend(float x) {
     return below ? 0.0f : e;
 }
 
+// exp_blend with the polynomial run on x itself below kExpLo (its value there,
+// finite or NaN, raises nothing on the GPU, and the select replaces it with
+// 0): the same result for every x, one select fewer.  The forward step uses
+// it; in the backward's exact re-evaluation the clamped form schedules better
+// (the backward blend 215 against 221 us at 1080p).
+__device__ __forceinline__ float exp_blend_noclamp(float x) {
+    const bool below = x < kExpLo;
+    const float e = exp_core(x);
+    return below ? 0.0f : e;
+}
+
 // Saturating float -> int32 with NaN -> 0 (the GPU conversion the reference's
 // (int)floorf / (int)ceilf casts rely on, rasterize.cu:38-41), written out
 // so no out-of-range cast is left to the compiler.
