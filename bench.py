@@ -342,7 +342,19 @@ def per_gaussian_stages(sc, calls: int = 20) -> dict:
         torch.cuda.synchronize()
         crc.profile_enable(False)
         stages = crc.profile_collect()
-    return _stage_rates(stages, n, 0, v["width"], v["height"])
+    out = _stage_rates(stages, n, 0, v["width"], v["height"])
+    # VALU issue beside the HBM rate: the kernels' issue quad-cycles per launch
+    # at this size (profiles/valu_per_gaussian_c5_5M.json) over the live time
+    # against VALU_PEAK_GISSUE (the projection backward is issue-bound)
+    vk = (_profile_json("valu", "per_gaussian_c5_5M") or {}).get("kernels", {})
+    if n == 5_000_000:
+        for name, entry in out.items():
+            k = vk.get(name)
+            if k and entry["ms"] > 0:
+                ach = k["issue_quads_per_launch"] / (entry["ms"] * 1e-3) / 1e9
+                entry["valu"] = {"kernel": k["kernel"], "G_issue_quads_per_s": round(ach, 1),
+                                 "frac": round(ach / VALU_PEAK_GISSUE, 4)}
+    return out
 
 
 def train_steps(sc, steps: int, warmup: int = 3) -> dict:
