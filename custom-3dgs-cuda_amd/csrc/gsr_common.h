@@ -17,6 +17,10 @@ namespace gsr {
 constexpr int kTileSize = 16;             // 16x16 pixel tiles (rasterize.cu:301)
 constexpr int kTilePixels = 256;
 constexpr int kWave = 64;                 // CDNA wavefront width
+
+// Four floats as a native vector (the operand type of the non-temporal load
+// and store builtins, which take no HIP float4).
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr float kNearZ = 0.2f;            // projection.cu:47
 constexpr float kAlphaMax = 0.99f;        // rasterize.cu:255
 constexpr float kAlphaMin = 1.0f / 255.0f;  // rasterize.cu:256

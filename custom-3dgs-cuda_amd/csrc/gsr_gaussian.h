@@ -31,10 +31,11 @@ __device__ __forceinline__ void stage_rows(float* __restrict__ lds, const float*
     int done = 0;
     if ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) {
         const int total4 = total / 4;
-        const float4* g4 = reinterpret_cast<const float4*>(g);
-        float4* l4 = reinterpret_cast<float4*>(lds);
+        // rows are read once: non-temporal (streaming) loads
+        const f32x4* g4 = reinterpret_cast<const f32x4*>(g);
+        f32x4* l4 = reinterpret_cast<f32x4*>(lds);
 #pragma unroll 4
-        for (int j = threadIdx.x; j < total4; j += kT) l4[j] = g4[j];
+        for (int j = threadIdx.x; j < total4; j += kT) l4[j] = __builtin_nontemporal_load(g4 + j);
         done = total4 * 4;
     }
     for (int j = done + (int)threadIdx.x; j < total; j += kT) lds[j] = g[j];
@@ -49,10 +50,10 @@ __device__ __forceinline__ void unstage_rows(float* __restrict__ dst, const floa
     int done = 0;
     if ((reinterpret_cast<uintptr_t>(g) & 15u) == 0) {
         const int total4 = total / 4;
-        float4* g4 = reinterpret_cast<float4*>(g);
-        const float4* l4 = reinterpret_cast<const float4*>(lds);
+        f32x4* g4 = reinterpret_cast<f32x4*>(g);
+        const f32x4* l4 = reinterpret_cast<const f32x4*>(lds);
 #pragma unroll 4
-        for (int j = threadIdx.x; j < total4; j += kT) g4[j] = l4[j];
+        for (int j = threadIdx.x; j < total4; j += kT) __builtin_nontemporal_store(l4[j], g4 + j);
         done = total4 * 4;
     }
     for (int j = done + (int)threadIdx.x; j < total; j += kT) g[j] = lds[j];

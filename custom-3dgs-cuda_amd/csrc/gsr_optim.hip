@@ -70,17 +70,24 @@ __global__ __launch_bounds__(kAdamThreads) void adam_kernel(AdamBatch b) {
     for (int k = 0; k < kAdamChunk / (kAdamThreads * kAdamVec); ++k) {
         const uint64_t e = base + ((uint64_t)k * kAdamThreads + threadIdx.x) * kAdamVec;
         if (vec && e + kAdamVec <= n) {
-            float4 p = *reinterpret_cast<const float4*>(t.param + e);
-            const float4 g = *reinterpret_cast<const float4*>(t.grad + e);
-            float4 m = *reinterpret_cast<const float4*>(t.exp_avg + e);
-            float4 v = *reinterpret_cast<const float4*>(t.exp_avg_sq + e);
-            adam_update(p.x, g.x, m.x, v.x, s);
-            adam_update(p.y, g.y, m.y, v.y, s);
-            adam_update(p.z, g.z, m.z, v.z, s);
-            adam_update(p.w, g.w, m.w, v.w, s);
-            *reinterpret_cast<float4*>(t.param + e) = p;
-            *reinterpret_cast<float4*>(t.exp_avg + e) = m;
-            *reinterpret_cast<float4*>(t.exp_avg_sq + e) = v;
+            // each element is touched once: non-temporal (streaming) loads and
+            // stores (1.54 to 1.46 ms at 5M Gaussians, 67% to 71% of HBM)
+            f32x4 p = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t.param + e));
+            const f32x4 g = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t.grad + e));
+            f32x4 m = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t.exp_avg + e));
+            f32x4 v =
+                __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(t.exp_avg_sq + e));
+#pragma unroll
+            for (int c = 0; c < kAdamVec; ++c) {
+                float pc = p[c], mc = m[c], vc = v[c];
+                adam_update(pc, g[c], mc, vc, s);
+                p[c] = pc;
+                m[c] = mc;
+                v[c] = vc;
+            }
+            __builtin_nontemporal_store(p, reinterpret_cast<f32x4*>(t.param + e));
+            __builtin_nontemporal_store(m, reinterpret_cast<f32x4*>(t.exp_avg + e));
+            __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(t.exp_avg_sq + e));
         } else {
             for (uint64_t j = e; j < e + kAdamVec && j < n; ++j) {
                 float p = t.param[j], m = t.exp_avg[j], v = t.exp_avg_sq[j];
