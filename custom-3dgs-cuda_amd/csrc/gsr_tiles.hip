@@ -50,6 +50,17 @@ __device__ __forceinline__ uint32_t uniform(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_readfirstlane((int)v);
 }
 
+// The work-group's index with the work-groups of one XCD made consecutive.
+// Work-groups are dealt to the 8 XCDs round-robin (work-group i runs on XCD
+// i % 8); renumbered, the XCD of work-group i takes a contiguous share of the
+// indices, so neighbouring segments (whose runs of a tile share cache lines)
+// are written through the same L2, which merges them into whole lines.
+// Grids that are not a multiple of 8 keep their order.
+__device__ __forceinline__ uint32_t xcd_group() {
+    const uint32_t g = blockIdx.x, n = gridDim.x;
+    return (n % 8u == 0u) ? (g % 8u) * (n / 8u) + g / 8u : g;
+}
+
 // Lanes of m below this one.
 __device__ __forceinline__ uint32_t rank_in(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
@@ -417,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
     const uint32_t nseg = min(uniform(seg_start[bg.nb]), seg_cap);
     const uint32_t stride = gridDim.x * kWavesPer;
     const int lane = lane_id();
-    for (uint32_t k = uniform(blockIdx.x * kWavesPer + (threadIdx.x >> 6)); k < nseg;
+    for (uint32_t k = uniform(xcd_group() * kWavesPer + (threadIdx.x >> 6)); k < nseg;
          k += stride) {
         const SegInfo I = seg_info(k, seg_owner, seg_start, block_start, bg.bw, bg.nb);
         const SegLane S = seg_lane<true>(lists, lrects, I.first, I.end, cap, n);
