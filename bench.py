@@ -552,7 +552,13 @@ def cpu_baseline(sc, budget_s: float = 30.0) -> dict:
     import torch
     from oracle import oracle as orc
 
-    threads = min(16, os.cpu_count() or 1)
+    # Every core the process may run on, up to the host's share for one GPU
+    # (GSR_CPU_SHARE, default 16: the GPU pool's boxes give one GPU's job 16 of
+    # their cores, whatever the machine has in all).
+    avail = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (
+        os.cpu_count() or 1)
+    share = int(os.environ.get("GSR_CPU_SHARE", "16"))
+    threads = max(1, min(avail, share) if share > 0 else avail)
     g, v = sc.gaussians, sc.view
     f = lambda t: t.detach().cpu().numpy().astype(np.float32)
     mu, q, s, A, kj = f(g.mu), f(g.q), f(g.s), f(g.A), f(g.k_j)
@@ -576,7 +582,7 @@ def cpu_baseline(sc, budget_s: float = 30.0) -> dict:
         pairs = ids.size
         return time.perf_counter() - t0
 
-    # the median of three frames on up to 16 threads, then one single-threaded
+    # the median of three frames on `threads` threads, then one single-threaded
     # frame if the budget has room for it (about 16x the threaded time)
     orc.set_threads(threads)
     times = []
@@ -600,7 +606,8 @@ def cpu_baseline(sc, budget_s: float = 30.0) -> dict:
         pass
     return {"value": round(1000.0 / ms, 4), "unit": "frames/s", "cores": threads, "kind": "port",
             "ms_per_frame": round(ms, 1), "ms_per_frame_1_thread": one,
-            "nproc": os.cpu_count(), "cpu_model": model,
+            "nproc": os.cpu_count(), "cores_available": avail, "cpu_share": share,
+            "cpu_model": model,
             "sample": f"median of {len(times)} full frame(s) fwd+bwd of the same workload "
                       f"({g.mu.shape[0]} Gaussians, {W}x{H}, {pairs} pairs) through the "
                       f"fp32 CPU oracle with {threads} OpenMP threads"

@@ -61,6 +61,31 @@ __device__ __forceinline__ uint32_t xcd_group() {
     return (n % 8u == 0u) ? (g % 8u) * (n / 8u) + g / 8u : g;
 }
 
+// tile_scatter's 32-bit addressing.  A tile's run starts at list position
+// base and holds up to kWave entries (rank 0..63).  The run's stores take the
+// byte offset (base - b0) * 4 + rank * 4 from ids + b0 in uint32 arithmetic,
+// which is exact only when the whole run, not just its start, lies within
+// 2^30 entries of b0.  run_fits is the condition; run_byte_offset the offset.
+constexpr uint32_t kRunSpan = 1u << 30;
+__host__ __device__ constexpr bool run_fits(uint32_t base, uint32_t b0, uint64_t m) {
+    return base >= b0 && base - b0 <= kRunSpan - (uint32_t)kWave &&
+           (uint64_t)base + (uint64_t)kWave <= m;
+}
+__host__ __device__ constexpr uint32_t run_byte_offset(uint32_t base, uint32_t b0,
+                                                       uint32_t rank) {
+    return ((base - b0) << 2) + (rank << 2);
+}
+// The largest admitted run's last store is exact; one entry further is
+// refused (the run would reach 2^30 entries from b0, whose byte offset wraps).
+static_assert(run_fits(7u + kRunSpan - 64u, 7u, 1ull << 40), "largest run admitted");
+static_assert(!run_fits(7u + kRunSpan - 63u, 7u, 1ull << 40), "a run reaching 2^30 refused");
+static_assert(!run_fits(7u + kRunSpan - 1u, 7u, 1ull << 40), "a run wrapping refused");
+static_assert((uint64_t)run_byte_offset(7u + kRunSpan - 64u, 7u, 63u) ==
+                  ((uint64_t)(kRunSpan - 64u) + 63u) * 4u,
+              "the largest admitted offset does not wrap");
+static_assert(!run_fits(6u, 7u, 1ull << 40), "a run before b0 refused");
+static_assert(!run_fits(100u, 7u, 163u) && run_fits(99u, 7u, 163u), "runs end at m");
+
 // Lanes of m below this one.
 __device__ __forceinline__ uint32_t rank_in(uint64_t m) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
@@ -460,12 +485,10 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
         // of b0 (all but the list's last entries, for consistent counts), the
         // stores take a 32-bit byte offset from ids + b0 and no position needs
         // its own check.
-        const bool fits =
-            ballot(on && (base < b0 || base - b0 >= (1u << 30) ||
-                          (uint64_t)base + (uint64_t)kWave > m)) == 0ull;
+        const bool fits = ballot(on && !run_fits(base, b0, m)) == 0ull;
         if (fits) {
             uint32_t* run0 = ids + b0;
-            const uint32_t dq = (base - b0) << 2;  // byte offset of this lane's tile's run
+            const uint32_t dq = run_byte_offset(base, b0, 0u);  // this lane's tile's run
 #pragma unroll
             for (int t = 0; t < 64; ++t) {
                 if (in_row[t >> 3] && in_col[t & 7]) {
