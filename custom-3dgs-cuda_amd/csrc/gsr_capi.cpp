@@ -44,7 +44,6 @@ inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
 
-constexpr int kDepthPasses = 4;         // 32-bit depth keys, 8-bit digits
 // sorted_ids and tile ranges are int32, and the kernels add up to two list
 // batches (well under 2^16) to int32 list positions: the pair count stays
 // that far below 2^31.
@@ -120,7 +119,7 @@ BinLayout bin_layout(int n, int H, int W) {
     };
     const size_t un = (size_t)(n > 0 ? n : 0);
     L.misc = take(sizeof(Misc));
-    L.sortctl = take(gsr::sort_control_bytes(un, kDepthPasses));
+    L.sortctl = take(gsr::sort_control_bytes(un));
     L.scanctl = take(gsr::scan_control_bytes(n));
     L.tilehist = take((size_t)kMaxTilePasses * 256 * 4);
     const gsr::BlockGrid bg = gsr::block_grid(tiles_x_of(W), tiles_y_of(H));
@@ -479,7 +478,7 @@ int rasterize_bin(int n, const float* depth, const int32_t* order, const float* 
             return GSR_OK;
         }
         GSR_HIP(gsr::launch_radix_sort(dk0, dv0, at<uint32_t>(bin_ws, L.dk1),
-                                       at<uint32_t>(bin_ws, L.dv1), (uint64_t)n, 0, kDepthPasses,
+                                       at<uint32_t>(bin_ws, L.dv1), (uint64_t)n,
                                        at<void>(bin_ws, L.sortctl), err, st,
                                        /*hist_ready=*/true),
                 "rasterize: depth sort");
@@ -552,7 +551,7 @@ int gsr_rasterize_bin_ordered(int n, const int32_t* order, const float* mean2d,
 size_t gsr_depth_order_workspace_bytes(int n) {
     if (n < 0) return 0;
     const size_t un = (size_t)n;
-    return 3 * align_up(4 * un, 256) + gsr::sort_control_bytes(un, kDepthPasses);
+    return 3 * align_up(4 * un, 256) + gsr::sort_control_bytes(un);
 }
 
 int gsr_depth_order(int n, const float* depth, void* ws, size_t ws_bytes, int32_t* order,
@@ -569,14 +568,13 @@ int gsr_depth_order(int n, const float* depth, void* ws, size_t ws_bytes, int32_
     uint32_t* k1 = at<uint32_t>(ws, w);
     uint32_t* v1 = at<uint32_t>(ws, 2 * w);
     void* ctl = at<void>(ws, 3 * w);
-    uint32_t* v0 = reinterpret_cast<uint32_t*>(order);  // the 4-pass sort ends in (k0, v0)
+    uint32_t* v0 = reinterpret_cast<uint32_t*>(order);  // the sort ends in (k0, v0)
     gsr::DeviceGlobals dg;
     GSR_HIP(gsr::device_globals(&dg), "depth order: device globals");
-    GSR_HIP(gsr::zero_fill(ctl, gsr::sort_control_bytes(un, kDepthPasses), st),
-            "depth order: clear");
+    GSR_HIP(gsr::zero_fill(ctl, gsr::sort_control_bytes(un), st), "depth order: clear");
     GSR_HIP(gsr::launch_depth_keys(n, depth, k0, v0, st), "depth order: keys");
-    GSR_HIP(gsr::launch_radix_sort(k0, v0, k1, v1, (uint64_t)n, 0, kDepthPasses, ctl, dg.status,
-                                   st, /*hist_ready=*/false),
+    GSR_HIP(gsr::launch_radix_sort(k0, v0, k1, v1, (uint64_t)n, ctl, dg.status, st,
+                                   /*hist_ready=*/false),
             "depth order: sort");
     return GSR_OK;
 }

@@ -70,26 +70,29 @@ hipError_t launch_project_sh_bwd(int n, const float* dmean, const float* dcov,
                                  int ref_quat, const float* dop, const float* op,
                                  float* dlogits, hipStream_t st);
 
-// ---- radix sort (u32 keys, u32 values), LSD onesweep with 8-bit digits ----
-// Partition size of one onesweep work-group.
-constexpr int kSortThreads = 256;
-constexpr int kSortItems = 16;
+// ---- radix sort (u32 keys, u32 values), 8-bit digits ----------------------
+// Partition of one onesweep work-group of the LSD tile sort.
+constexpr int kSortThreads = 1024;
+constexpr int kSortItems = 8;
 constexpr int kSortPartition = kSortThreads * kSortItems;
 constexpr int kRadixBins = 256;
 
-// Device control block of one sort: per-pass global digit histograms,
-// partition counters and look-back status words.  All of it must be zero
-// before the histogram kernel runs (sort_control_bytes / the fill kernel).
-size_t sort_control_bytes(uint64_t n, int passes);
-// Sorts keys[0..n) by bits [begin_bit, begin_bit + 8*passes), carrying vals.
-// Ping-pongs between (k0,v0) and (k1,v1); the result lands in (k0,v0) for an
-// even pass count and in (k1,v1) for an odd one.  `control` must be zeroed
-// on the stream first (zero_fill).  err (device int) is set when a look-back
-// exceeds kSpinLimit.  hist_ready: the passes' digit histograms ([passes][256]
-// u32 at the start of `control`) were accumulated already.
+// Device control block of one depth sort: the digit histograms of the key's
+// four bytes ([4][256] u32 at its start), counters and per-partition words.
+// All of it must be zero before the histogram kernel runs
+// (sort_control_bytes / the fill kernel).
+size_t sort_control_bytes(uint64_t n);
+// Stable sort of keys[0..n) (n < 2^32) on all 32 bits, carrying vals: four
+// LSD passes of 8-bit digits, ping-ponging through (k1, v1) and ending in
+// (k0, v0).  Up to 2^18 keys each pass is one onesweep kernel over 1024-key
+// partitions; beyond, each pass is an upsweep / scan / downsweep triple with
+// no waits between work-groups.  A pass whose digit is the same for every key
+// copies through.  `control` must be zeroed on the stream first (zero_fill).
+// err (device int) is set when a look-back wait exceeds kSpinLimit.
+// hist_ready: the histogram block at the start of `control` was accumulated
+// already.
 hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
-                             int begin_bit, int passes, void* control, int* err, hipStream_t st,
-                             bool hist_ready = false);
+                             void* control, int* err, hipStream_t st, bool hist_ready = false);
 
 hipError_t zero_fill(void* p, size_t bytes, hipStream_t st);
 // Several regions in one launch.

@@ -1,23 +1,39 @@
-// gsr_sort.hip — LSD onesweep radix sort (u32 keys carrying u32 values) and
-// the decoupled look-back scan of per-Gaussian tile counts.
+// gsr_sort.hip — radix sorts of u32 keys carrying u32 values (the depth order
+// and the LSD tile sort) and the decoupled look-back scan of per-Gaussian tile
+// counts.  Every sort is stable and LSD over 8-bit digits; the kernels differ
+// by size.
 //
-// Sort design (one kernel per 8-bit digit pass, plus one histogram kernel):
-//   * A work-group owns a partition of 4096 consecutive elements, claimed in
-//     launch order through an atomic counter so that every partition it waits
-//     on belongs to a work-group that is already resident.
-//   * Items are loaded wave-striped (item i of lane l in wave w is element
-//     w*1024 + i*64 + l), so each wave load is one contiguous 256 B access.
-//   * Stable in-partition ranks come from 8 ballots per item (lanes sharing a
-//     digit) plus per-wave running digit counters in LDS.
-//   * Each partition publishes its 256 digit counts, looks back over earlier
-//     partitions' published counts (decoupled look-back) and scatters its
-//     elements, first reordered in LDS so each digit's run is written with
-//     consecutive addresses.
-//   * Look-back spins are bounded by kSpinLimit; a partition that reaches it
-//     raises the error flag and finishes, so every wave exits.
-// HBM traffic per pass: 8 B read + 8 B written per element (+ 8 B per
-// partition and digit of status words).
+// Ranking (every kernel): stable in-partition ranks from 8 ballots per item
+// (the lanes sharing a digit, merged two bits per three-way OR) plus per-wave
+// running digit counters in LDS; items are loaded wave-striped (item i of lane
+// l in wave w is element w*64*items + i*64 + l), so each wave load is one
+// contiguous 256 B access and ranks follow element order.
+//
+// Depth orders of at most 2^18 keys: onesweep_small_kernel, one kernel per
+// pass, 256 threads (one per digit) over 1024-key partitions claimed in
+// launch order through an atomic counter, so that every partition a
+// work-group waits on belongs to a work-group already resident; decoupled
+// look-back over the earlier partitions' published digit counts.  These
+// passes are latency chains (claim, load, rank, look-back, scatter).
+//
+// Larger depth orders: reduce-then-scan, three kernels per pass with no
+// waits between work-groups (rts_upsweep / rts_scan / rts_downsweep).  Their
+// partitions are sized so that one round of two 1024-thread work-groups per
+// CU covers the keys; with all partitions resident at once, a decoupled
+// look-back would walk about half of its predecessors' status words (the
+// inclusive prefix spreads only quadratically in round trips).
+//
+// The LSD tile sort (fallback binning): onesweep_wide_kernel, 1024 threads
+// (16 waves) over 8192-element partitions, 16-bit per-wave counters and one
+// LDS exchange buffer for keys and then values (42 KB, two work-groups per
+// CU); its first pass generates the (tile, Gaussian) pairs in LDS.
+//
+// Look-back spins are bounded by kSpinLimit; a partition that reaches it
+// raises the error flag and finishes, so every wave exits.
+// HBM traffic per pass: 8 B read + 8 B written per element (+ 4 B read in
+// the upsweep, + the status / count words).
 #include <algorithm>
+#include <cstdlib>
 
 #include "gsr_internal.h"
 #include "gsr_common.h"
@@ -29,52 +45,83 @@ namespace {
 
 constexpr int kHistMaxPasses = 4;
 constexpr int kLookback = 4;
-static_assert(kSortThreads == kRadixBins, "one thread per digit in the onesweep kernel");
-static_assert(kSortThreads == 256, "four waves per onesweep work-group");
+// Words of the histogram block: [4][256] digit counts.
+constexpr int kHistWords = kHistMaxPasses * kRadixBins;
+
+// Inputs up to this size take onesweep passes over 1024-key partitions of 256
+// threads (onesweep_small_kernel).
+constexpr uint64_t kSmallSortMax = 1u << 18;
+constexpr int kSmallThreads = 256;
+constexpr int kSmallItems = 4;
+constexpr int kSmallPartition = kSmallThreads * kSmallItems;
+
+// The wide onesweep: 1024 threads, 8 items.
+constexpr int kWideWaves = kSortThreads / kWave;
+static_assert(kSortThreads == 1024 && kWideWaves == 16, "sixteen waves per onesweep work-group");
+static_assert(kSortPartition == kSortThreads * kSortItems, "partition of the wide onesweep");
+
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 struct SortCtl {
-    uint32_t* hist;      // [passes][256]
+    uint32_t* hist;      // [4][256]
     uint32_t* counters;  // [passes] (one per 64 B line)
     uint64_t* status;    // [passes][parts][256]
 };
 
 inline uint64_t parts_for(uint64_t n) { return (n + kSortPartition - 1) / kSortPartition; }
-
-// Items per thread of the key sort (launch_radix_sort): small inputs take
-// 1024-element partitions, so a pass runs on more work-groups, each with less
-// to rank; larger ones 4096, which keeps the look-back chain short.
-constexpr uint64_t kSmallSortMax = 1u << 18;
-inline int sort_items(uint64_t n) { return n <= kSmallSortMax ? 4 : kSortItems; }
+inline bool small_sort(uint64_t n) { return n <= kSmallSortMax; }
+// Items per thread of the large depth passes (1024 threads): one round of
+// 512 resident work-groups (two per CU) where the partitions allow it.
+inline int depth_items(uint64_t n) {
+    const uint64_t per = (n + 512 * 1024 - 1) / (512 * 1024);
+    return per <= 4 ? 4 : per <= 6 ? 6 : per <= 8 ? 8 : 10;
+}
 inline uint64_t sort_parts(uint64_t n) {
-    const uint64_t part = (uint64_t)kSortThreads * (uint64_t)sort_items(n);
+    const uint64_t part =
+        small_sort(n) ? (uint64_t)kSmallPartition : (uint64_t)kSortThreads * depth_items(n);
     return (n + part - 1) / part;
 }
+inline size_t hist_bytes() { return align_up((size_t)kHistWords * 4, 256); }
 
-SortCtl carve(void* control, uint64_t n, int passes) {
+SortCtl carve(void* control) {
     char* p = static_cast<char*>(control);
     SortCtl c;
     c.hist = reinterpret_cast<uint32_t*>(p);
-    p += align_up((size_t)passes * kRadixBins * 4, 256);
+    p += hist_bytes();
     c.counters = reinterpret_cast<uint32_t*>(p);
-    p += align_up((size_t)passes * 64, 256);
+    p += align_up((size_t)kHistMaxPasses * 64, 256);
     c.status = reinterpret_cast<uint64_t*>(p);
     return c;
 }
 
 // Lanes of `active` whose digit equals this lane's, comparing the low `bits`
-// bits (the digit's higher bits are known to be zero in every key).
+// bits (the digit's higher bits are known to be zero in every key).  Per bit:
+// y = 0 or ~0 (the lane's bit, sign-extended) and the ballot t of the bit;
+// t ^ y holds the lanes whose bit differs, and two bits' mismatches are
+// merged per 32-lane half with one three-way OR.
+__device__ __forceinline__ uint32_t bit_mask(uint32_t d, int b) {
+    return (uint32_t)(((int32_t)(d << (31 - b))) >> 31);
+}
 __device__ __forceinline__ uint64_t match_digit(uint32_t d, uint64_t active, int bits = 8) {
-    uint64_t m = active;
+    uint32_t mis_lo = ~(uint32_t)active, mis_hi = ~(uint32_t)(active >> 32);
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < 8; b += 2) {
         if (b >= bits) break;
-        const bool bit = (d >> b) & 1u;
-        const uint64_t t = ballot(bit);
-        m &= bit ? t : ~t;
+        const uint32_t y0 = bit_mask(d, b);
+        const uint64_t t0 = ballot(y0 != 0u);
+        const uint32_t lo0 = (uint32_t)t0 ^ y0, hi0 = (uint32_t)(t0 >> 32) ^ y0;
+        if (b + 1 < bits) {
+            const uint32_t y1 = bit_mask(d, b + 1);
+            const uint64_t t1 = ballot(y1 != 0u);
+            mis_lo = mis_lo | lo0 | ((uint32_t)t1 ^ y1);
+            mis_hi = mis_hi | hi0 | ((uint32_t)(t1 >> 32) ^ y1);
+        } else {
+            mis_lo |= lo0;
+            mis_hi |= hi0;
+        }
     }
-    return m;
+    return ~(((uint64_t)mis_hi << 32) | (uint64_t)mis_lo);
 }
 
 // Zeroes up to kMaxFills regions in one launch: bytes up to the first 16-byte
@@ -95,51 +142,260 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(FillList f) {
     }
 }
 
-// Global digit histograms of every pass in one read of the keys.  Digit
-// counts are aggregated per wave (ballot match) before the LDS atomics, and
-// per work-group before the global atomics.
-__global__ __launch_bounds__(256) void radix_hist_kernel(const uint32_t* __restrict__ keys,
-                                                         uint64_t n, int begin_bit, int passes,
-                                                         uint32_t* __restrict__ hist) {
-    __shared__ uint32_t s_h[kHistMaxPasses][kRadixBins];
-    for (int j = threadIdx.x; j < kHistMaxPasses * kRadixBins; j += 256) (&s_h[0][0])[j] = 0;
+// Global digit histograms of every byte in one read of the keys (LDS atomics
+// per work-group, one global atomic per non-zero bin).
+constexpr int kHistThreads = 1024;
+__global__ __launch_bounds__(kHistThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys,
+                                                                  uint64_t n,
+                                                                  uint32_t* __restrict__ hist) {
+    __shared__ uint32_t s_h[kHistWords];
+    for (int j = threadIdx.x; j < kHistWords; j += kHistThreads) s_h[j] = 0;
     __syncthreads();
-    const uint64_t stride = (uint64_t)gridDim.x * 256;
-    const uint64_t nround = (n + 255) / 256 * 256;  // keep whole waves in the loop
-    for (uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x; i < nround; i += stride) {
-        const bool valid = i < n;
-        const uint32_t k = valid ? keys[i] : 0u;
-        const uint64_t act = ballot(valid);
-        for (int p = 0; p < passes; ++p) {
-            const uint32_t d = (k >> (begin_bit + 8 * p)) & 0xffu;
-            const uint64_t peers = match_digit(d, act);
-            if (valid && (peers & lanemask_lt()) == 0)
-                atomicAdd(&s_h[p][d], (uint32_t)popc64(peers));
-        }
+    const uint64_t stride = (uint64_t)gridDim.x * kHistThreads;
+    for (uint64_t i = (uint64_t)blockIdx.x * kHistThreads + threadIdx.x; i < n; i += stride) {
+        const uint32_t k = keys[i];
+#pragma unroll
+        for (int p = 0; p < kHistMaxPasses; ++p)
+            atomicAdd(&s_h[p * kRadixBins + ((k >> (8 * p)) & 0xffu)], 1u);
     }
     __syncthreads();
-    for (int j = threadIdx.x; j < passes * kRadixBins; j += 256) {
-        const uint32_t v = (&s_h[0][0])[j];
+    for (int j = threadIdx.x; j < kHistWords; j += kHistThreads) {
+        const uint32_t v = s_h[j];
         if (v) atomicAdd(&hist[j], v);
     }
 }
 
+// Copies a partition through unchanged (every key has the pass's digit).
+// 16-byte copies when every array is 16-byte aligned, the rest word by word.
+template <bool kPacked>
+__device__ __forceinline__ void copy_partition(const uint32_t* __restrict__ kin,
+                                               const uint32_t* __restrict__ vin,
+                                               uint32_t* __restrict__ kout,
+                                               uint32_t* __restrict__ vout, uint64_t base,
+                                               int nvalid, uint32_t mask) {
+    const int nthr = (int)blockDim.x;
+    const int tid = (int)threadIdx.x;
+    const uintptr_t al = reinterpret_cast<uintptr_t>(kin + base) |
+                         reinterpret_cast<uintptr_t>(kout + base) |
+                         reinterpret_cast<uintptr_t>(vin + base) |
+                         reinterpret_cast<uintptr_t>(vout + base);
+    const int n4 = (al & 15) ? 0 : nvalid / 4;
+    const uint4* k4 = reinterpret_cast<const uint4*>(kin + base);
+    uint4* ko4 = reinterpret_cast<uint4*>(kout + base);
+#pragma unroll 2
+    for (int e = tid; e < n4; e += nthr) {
+        const uint4 k = k4[e];
+        ko4[e] = k;
+        if constexpr (kPacked) {
+            if (vout)
+                reinterpret_cast<uint4*>(vout + base)[e] =
+                    make_uint4(k.x & mask, k.y & mask, k.z & mask, k.w & mask);
+        } else {
+            reinterpret_cast<uint4*>(vout + base)[e] = reinterpret_cast<const uint4*>(vin + base)[e];
+        }
+    }
+    for (int e = 4 * n4 + tid; e < nvalid; e += nthr) {
+        const uint32_t k = kin[base + e];
+        kout[base + e] = k;
+        if constexpr (kPacked) {
+            if (vout) vout[base + e] = k & mask;
+        } else {
+            vout[base + e] = vin[base + e];
+        }
+    }
+}
+
+// Decoupled look-back for digit d of partition part over earlier partitions,
+// kLookback status words per round trip (before partition 0 reads as an
+// inclusive 0); publishes part's inclusive prefix and returns its exclusive
+// prefix.  A wait beyond kSpinLimit sets *err and ends the walk.
+template <int kWindow = kLookback>
+__device__ __forceinline__ uint64_t digit_lookback(uint64_t* __restrict__ status, uint64_t part,
+                                                   int d, uint64_t total, int* __restrict__ err) {
+    uint64_t excl = 0;
+    if (part == 0) return 0;
+    int64_t p = (int64_t)part - 1;
+    uint32_t spins = 0;
+    while (true) {
+        uint64_t sw[kWindow];
+#pragma unroll
+        for (int k = 0; k < kWindow; ++k)
+            sw[k] = (p - k >= 0) ? load_agent(status + (uint64_t)(p - k) * kRadixBins + d)
+                                 : kFlagInclusive;
+        int k = 0;
+        bool done = false;
+        for (; k < kWindow; ++k) {
+            const uint64_t flag = sw[k] & ~kValueMask;
+            if (flag == 0) break;  // not published yet: reload from here
+            excl += sw[k] & kValueMask;
+            if (flag == kFlagInclusive) {
+                done = true;
+                break;
+            }
+        }
+        if (done) break;
+        p -= k;
+        if (k < kWindow) {
+            if (++spins > kSpinLimit) {
+                atomicOr(err, 1);
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+    }
+    store_agent(status + part * kRadixBins + d, kFlagInclusive | (excl + total));
+    return excl;
+}
+
+// Threads below 256 (digit d = threadIdx.x): turns s_cnt[.][d] into the
+// exclusive prefix over the waves and returns the digit's total.
+__device__ __forceinline__ uint32_t wave_prefix(uint16_t (*s_cnt)[kRadixBins], int waves) {
+    const int d = (int)threadIdx.x;
+    uint32_t run = 0;
+    for (int w = 0; w < waves; ++w) {
+        const uint32_t c = s_cnt[w][d];
+        s_cnt[w][d] = (uint16_t)run;
+        run += c;
+    }
+    return run;
+}
+
+// ---- small inputs: onesweep over 1024-key partitions -----------------------
+
+// One LSD pass over (key >> shift) & 0xff with 256 threads, one per digit:
+// ranks by ballot match and per-wave counters, the partition's digit counts
+// published after the ranking, keys and values reordered in LDS while the
+// digit threads look back, then written in digit runs.
+__global__ __launch_bounds__(kSmallThreads) void onesweep_small_kernel(
+    const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
+    uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n, int shift,
+    const uint32_t* __restrict__ hist, uint64_t* __restrict__ status,
+    uint32_t* __restrict__ counter, int* __restrict__ err) {
+    constexpr int kItems = kSmallItems;
+    constexpr int kPart = kSmallPartition;
+    constexpr int kWaves = kSmallThreads / kWave;
+    static_assert(kSmallThreads == kRadixBins, "one thread per digit");
+    __shared__ uint32_t s_keys[kPart];
+    __shared__ uint32_t s_vals[kPart];
+    __shared__ uint32_t s_wcnt[kWaves][kRadixBins];
+    __shared__ uint32_t s_dstart[kRadixBins];
+    __shared__ uint32_t s_gbase[kRadixBins];
+    __shared__ uint32_t s_scan[kWaves];
+    __shared__ uint32_t s_hscan[kWaves];
+    __shared__ uint32_t s_part;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (tid == 0) s_part = atomicAdd(counter, 1u);
+    const uint32_t h = hist[tid];  // fetched while the claim is in flight
+    const bool same = __syncthreads_or((uint64_t)h == n);
+    const uint64_t part = s_part;
+    const uint64_t base = part * kPart;
+    const int nvalid = (int)min((uint64_t)kPart, n - base);
+    if (same) {
+        // every key has the same digit: the stable pass is the identity
+        copy_partition<false>(kin, vin, kout, vout, base, nvalid, 0u);
+        return;
+    }
+    uint32_t key[kItems], val[kItems], rank[kItems];
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const int e = wave * (kItems * 64) + i * 64 + lane;
+        key[i] = e < nvalid ? kin[base + e] : 0u;
+    }
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const int e = wave * (kItems * 64) + i * 64 + lane;
+        val[i] = e < nvalid ? vin[base + e] : 0u;
+    }
+    for (int j = tid; j < kWaves * kRadixBins; j += kSmallThreads) (&s_wcnt[0][0])[j] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const int e = wave * (kItems * 64) + i * 64 + lane;
+        const bool v = e < nvalid;
+        const uint32_t d = (key[i] >> shift) & 0xffu;
+        const uint64_t peers = match_digit(d, ballot(v));
+        rank[i] = 0;
+        if (v) {
+            const uint32_t before = s_wcnt[wave][d];
+            const uint64_t lower = peers & lanemask_lt();
+            rank[i] = before + (uint32_t)popc64(lower);
+            if (lower == 0) s_wcnt[wave][d] = before + (uint32_t)popc64(peers);
+        }
+    }
+    __syncthreads();
+    // one thread per digit: partition total (published), wave prefixes, starts
+    const int d = tid;
+    uint32_t total = 0;
+    for (int w = 0; w < kWaves; ++w) {
+        const uint32_t c = s_wcnt[w][d];
+        s_wcnt[w][d] = total;
+        total += c;
+    }
+    store_agent(status + part * kRadixBins + d,
+                (part == 0 ? kFlagInclusive : kFlagAggregate) | (uint64_t)total);
+    const uint32_t inc = wave_inclusive_scan(total);
+    const uint32_t hinc = wave_inclusive_scan(h);
+    if (lane == 63) {
+        s_scan[wave] = inc;
+        s_hscan[wave] = hinc;
+    }
+    __syncthreads();
+    uint32_t wpre = 0, hpre = 0;
+    for (int w = 0; w < wave; ++w) {
+        wpre += s_scan[w];
+        hpre += s_hscan[w];
+    }
+    const uint32_t dstart = wpre + inc - total;
+    const uint32_t hexcl = hpre + hinc - h;
+    s_dstart[d] = dstart;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const int e = wave * (kItems * 64) + i * 64 + lane;
+        if (e < nvalid) {
+            const uint32_t dd = (key[i] >> shift) & 0xffu;
+            const uint32_t pos = s_dstart[dd] + s_wcnt[wave][dd] + rank[i];
+            s_keys[pos] = key[i];
+            s_vals[pos] = val[i];
+        }
+    }
+    const uint32_t excl = (uint32_t)digit_lookback(status, part, d, total, err);
+    // element j of digit d's run goes to hexcl + excl + (j - dstart) (32 bits)
+    s_gbase[d] = hexcl + excl - dstart;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+        const int j = tid + k * kSmallThreads;
+        if (j < nvalid) {
+            const uint32_t kk = s_keys[j];
+            const uint32_t o = s_gbase[(kk >> shift) & 0xffu] + (uint32_t)j;
+            if ((uint64_t)o < n) {  // always, for consistent histograms; guards the stores
+                kout[o] = kk;
+                vout[o] = s_vals[j];
+            }
+        }
+    }
+}
+
+// ---- large inputs and the tile sort: the wide onesweep ---------------------
+
 // The emission's staging index: one padding word per 16 slots, so a wave's
-// blocked writes (16 slots per lane) and striped reads spread over the banks.
+// blocked writes (kSortItems slots per lane) spread over the banks.
 __device__ __forceinline__ int pad16(int slot) { return slot + (slot >> 4); }
 
 // Expands the (tile, Gaussian) pairs of sort slots [base, base + nvalid) into
 // s_keys / s_vals at pad16(slot) (kPacked: the one word (tile << gbits) | g in
-// s_keys).  Pair slots are laid out by depth rank r at
-// offsets[r] (ty outer, tx inner over the rank's tile rectangle), the order in
-// which the reference emits keys per Gaussian (rasterize.cu:124-135).  Ranks
-// r_lo..r_lo+nr-1 overlap the partition; the first kStageRanks of them have
-// their offset, Gaussian id and tile rectangle staged in LDS by one parallel
-// load (more only occur for partitions of very small Gaussians, or when ranks
-// without pairs sit between ranks with pairs, and are read from global
-// memory).  Each thread expands 16 consecutive slots: one binary search, one
+// s_keys).  Pair slots are laid out by depth rank r at offsets[r] (ty outer,
+// tx inner over the rank's tile rectangle), the order in which the reference
+// emits keys per Gaussian (rasterize.cu:124-135).  Ranks r_lo..r_lo+nr-1
+// overlap the partition; the first kStageRanks of them have their offset,
+// Gaussian id and tile rectangle staged in LDS by one parallel load (more
+// only occur for partitions of very small Gaussians, or when ranks without
+// pairs sit between ranks with pairs, and are read from global memory).
+// Each thread expands kSortItems consecutive slots: one binary search, one
 // division, then a walk that steps the column and row.
-constexpr int kStageRanks = 512;
+constexpr int kStageRanks = 640;
 
 struct RankStage {
     uint32_t off[kStageRanks];
@@ -147,7 +403,6 @@ struct RankStage {
     uint2 rect[kStageRanks];
 };
 constexpr int kRankStageWords = (int)(sizeof(RankStage) / 4);
-static_assert(kRankStageWords >= 7 * kRadixBins, "the aux region also holds the digit counters");
 
 template <bool kPacked>
 __device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base, int nvalid,
@@ -229,75 +484,54 @@ __device__ __forceinline__ void expand_pairs(const EmitSource& es, uint64_t base
     __syncthreads();
 }
 
-// One LSD pass over 8-bit digit (key >> shift) & 0xff.  kEmit: the partition's
-// (tile, Gaussian) pairs are generated from the depth order instead of being
-// read (the first tile pass).  kPacked: each element is the one word
-// (tile << gbits) | Gaussian id, sorted on its tile bits; kout receives the
-// words and, when vout is not null (the last pass), vout the Gaussian ids.
-// Otherwise keys and values are separate words, both written.
-template <bool kEmit, bool kPacked, int kItems = kSortItems>
-__global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
+// One LSD pass over the digit (key >> shift), digit_bits significant bits.
+// kEmit: the partition's (tile, Gaussian) pairs are generated from the depth
+// order instead of being read (the first tile pass).  kPacked: each element
+// is the one word (tile << gbits) | Gaussian id, sorted on its tile bits; kout
+// receives the words and, when vout is not null (the last pass), vout the
+// Gaussian ids.  Otherwise keys and values are separate words, both written.
+template <bool kEmit, bool kPacked>
+__global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void onesweep_wide_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n, int shift,
     int digit_bits, const uint32_t* __restrict__ hist, uint64_t* __restrict__ status,
     uint32_t* __restrict__ counter, int* __restrict__ err, EmitSource es, int gbits) {
-    // s_aux holds the emission's staged offsets first, then the digit counters,
-    // digit starts and global bases (7 KB).
-    constexpr int kAuxWords = kEmit ? kRankStageWords : 7 * kRadixBins;
-    constexpr int kPart = kSortThreads * kItems;  // elements per partition
-    static_assert(!kEmit || kItems == kSortItems, "the emission expands kSortPartition slots");
-    __shared__ uint32_t s_keys[kPart + kPart / 16];
-    __shared__ uint32_t s_vals[kPacked ? 1 : kPart + kPart / 16];
+    constexpr int kThreads = kSortThreads;
+    constexpr int kItems = kSortItems;
+    constexpr int kPart = kSortPartition;
+    constexpr int kWaves = kWideWaves;
+    constexpr bool kVals = !kPacked;
+    constexpr int kXWords = kEmit ? kPart + kPart / 16 : kPart;
+    // after the emission: u16 counters [16][256], digit starts, global bases
+    constexpr int kCntWords = kWaves * kRadixBins / 2;
+    constexpr int kScanAux = kCntWords + 2 * kRadixBins;
+    constexpr int kAuxWords = (kEmit && kRankStageWords > kScanAux) ? kRankStageWords : kScanAux;
+    __shared__ uint32_t s_x[kXWords];
+    __shared__ uint32_t s_v[(kEmit && kVals) ? kXWords : 1];
     __shared__ __align__(16) uint32_t s_aux[kAuxWords];
     __shared__ uint32_t s_scan[4];
     __shared__ uint32_t s_hscan[4];
     __shared__ uint32_t s_part;
-    uint32_t (*s_wcnt)[kRadixBins] = reinterpret_cast<uint32_t (*)[kRadixBins]>(s_aux);
-    uint32_t* s_dstart = s_aux + 4 * kRadixBins;
-    uint64_t* s_gbase = reinterpret_cast<uint64_t*>(s_aux + 5 * kRadixBins);
+    uint16_t (*s_cnt)[kRadixBins] = reinterpret_cast<uint16_t (*)[kRadixBins]>(s_aux);
+    uint32_t* s_dstart = s_aux + kCntWords;
+    uint32_t* s_gbase = s_aux + kCntWords + kRadixBins;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     if (tid == 0) s_part = atomicAdd(counter, 1u);
-    __syncthreads();
+    // the digit's global count, fetched while the claim is in flight
+    const uint32_t h = tid < kRadixBins ? hist[tid] : 0u;
+    const uint32_t gmask = kPacked ? ((1u << gbits) - 1u) : 0u;
+    bool same = false;
+    if constexpr (!kEmit) same = __syncthreads_or(tid < kRadixBins && (uint64_t)h == n);
+    else __syncthreads();
     const uint64_t part = s_part;
     const uint64_t base = part * kPart;
     const int nvalid = (int)min((uint64_t)kPart, n - base);
     if constexpr (!kEmit) {
         // Every key has the same digit: the stable pass is the identity, so the
         // partition is copied through (no ranking, no look-back).
-        if (__syncthreads_or(hist[tid] == (uint32_t)n)) {
-            // 16-byte copies when every array is 16-byte aligned (partitions start
-            // a multiple of 4 KB apart), the rest word by word
-            const uint32_t mask = kPacked ? ((1u << gbits) - 1u) : 0u;
-            const uintptr_t al = reinterpret_cast<uintptr_t>(kin) |
-                                 reinterpret_cast<uintptr_t>(kout) |
-                                 reinterpret_cast<uintptr_t>(vin) |
-                                 reinterpret_cast<uintptr_t>(vout);
-            const int n4 = (al & 15) ? 0 : nvalid / 4;
-            const uint4* k4 = reinterpret_cast<const uint4*>(kin + base);
-            uint4* ko4 = reinterpret_cast<uint4*>(kout + base);
-#pragma unroll 4
-            for (int e = tid; e < n4; e += kSortThreads) {
-                const uint4 k = k4[e];
-                ko4[e] = k;
-                if constexpr (kPacked) {
-                    if (vout)
-                        reinterpret_cast<uint4*>(vout + base)[e] =
-                            make_uint4(k.x & mask, k.y & mask, k.z & mask, k.w & mask);
-                } else {
-                    reinterpret_cast<uint4*>(vout + base)[e] =
-                        reinterpret_cast<const uint4*>(vin + base)[e];
-                }
-            }
-            for (int e = 4 * n4 + tid; e < nvalid; e += kSortThreads) {
-                const uint32_t k = kin[base + e];
-                kout[base + e] = k;
-                if constexpr (kPacked) {
-                    if (vout) vout[base + e] = k & mask;
-                } else {
-                    vout[base + e] = vin[base + e];
-                }
-            }
+        if (same) {
+            copy_partition<kPacked>(kin, vin, kout, vout, base, nvalid, gmask);
             return;
         }
     }
@@ -305,27 +539,27 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
     uint32_t key[kItems], val[kItems], rank[kItems];
     (void)val;
     if constexpr (kEmit) {
-        expand_pairs<kPacked>(es, base, nvalid, s_keys, s_vals,
-                              reinterpret_cast<RankStage*>(s_aux), gbits);  // ends with a barrier
+        expand_pairs<kPacked>(es, base, nvalid, s_x, s_v, reinterpret_cast<RankStage*>(s_aux),
+                              gbits);  // ends with a barrier
 #pragma unroll
         for (int i = 0; i < kItems; ++i) {
             const int e = wave * (kItems * 64) + i * 64 + lane;
             const bool v = e < nvalid;
-            key[i] = v ? s_keys[pad16(e)] : 0u;
-            if constexpr (!kPacked) val[i] = v ? s_vals[pad16(e)] : 0u;
+            key[i] = v ? s_x[pad16(e)] : 0u;
+            if constexpr (kVals) val[i] = v ? s_v[pad16(e)] : 0u;
         }
+        __syncthreads();  // the staged ranks' region becomes the counters
     } else {
 #pragma unroll
         for (int i = 0; i < kItems; ++i) {
             const int e = wave * (kItems * 64) + i * 64 + lane;
-            const bool v = e < nvalid;
-            key[i] = v ? kin[base + e] : 0u;
-            if constexpr (!kPacked) val[i] = v ? vin[base + e] : 0u;
+            key[i] = e < nvalid ? kin[base + e] : 0u;
         }
     }
-    for (int j = tid; j < 4 * kRadixBins; j += kSortThreads) (&s_wcnt[0][0])[j] = 0;
+    for (int j = tid; j < kCntWords; j += kThreads) s_aux[j] = 0;
     __syncthreads();
-    // Stable ranks within the wave's slice, in element order.
+    uint32_t total = 0, excl = 0;
+    // stable ranks within the wave's slice, in element order
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
         const int e = wave * (kItems * 64) + i * 64 + lane;
@@ -334,103 +568,304 @@ __global__ __launch_bounds__(kSortThreads) void onesweep_kernel(
         const uint64_t peers = match_digit(d, ballot(v), digit_bits);
         rank[i] = 0;
         if (v) {
-            const uint32_t before = s_wcnt[wave][d];
+            const uint32_t before = s_cnt[wave][d];
             const uint64_t lower = peers & lanemask_lt();
             rank[i] = before + (uint32_t)popc64(lower);
-            if (lower == 0) s_wcnt[wave][d] = before + (uint32_t)popc64(peers);
+            if (lower == 0) s_cnt[wave][d] = (uint16_t)(before + (uint32_t)popc64(peers));
         }
     }
     __syncthreads();
+    if constexpr (kVals && !kEmit) {
+        // the values are needed only for their reorder: their loads are in
+        // flight during the scans below and the key reorder
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            const int e = wave * (kItems * 64) + i * 64 + lane;
+            val[i] = e < nvalid ? vin[base + e] : 0u;
+        }
+    }
 
-    // One thread per digit: partition total, publish, prefixes.
-    const int d = tid;
-    const uint32_t c0 = s_wcnt[0][d], c1 = s_wcnt[1][d], c2 = s_wcnt[2][d], c3 = s_wcnt[3][d];
-    const uint32_t total = c0 + c1 + c2 + c3;
-    uint64_t* my_status = status + part * kRadixBins + d;
-    store_agent(my_status, (part == 0 ? kFlagInclusive : kFlagAggregate) | (uint64_t)total);
-    s_wcnt[0][d] = 0;
-    s_wcnt[1][d] = c0;
-    s_wcnt[2][d] = c0 + c1;
-    s_wcnt[3][d] = c0 + c1 + c2;
-    const uint32_t inc = wave_inclusive_scan(total);
-    const uint32_t h = hist[d];
-    const uint32_t hinc = wave_inclusive_scan(h);
-    if (lane == 63) {
-        s_scan[wave] = inc;
-        s_hscan[wave] = hinc;
+    // threads below 256, one per digit: the waves' prefixes and the digit's
+    // total (published at once), the partition-local digit start and the
+    // digit's global start
+    uint32_t inc = 0, hinc = 0;
+    if (tid < kRadixBins) {
+        total = wave_prefix(s_cnt, kWaves);
+        store_agent(status + part * kRadixBins + tid,
+                    (part == 0 ? kFlagInclusive : kFlagAggregate) | (uint64_t)total);
+        inc = wave_inclusive_scan(total);
+        hinc = wave_inclusive_scan(h);
+        if (lane == 63) {
+            s_scan[wave] = inc;
+            s_hscan[wave] = hinc;
+        }
     }
     __syncthreads();
-    uint32_t wpre = 0, hpre = 0;
-    for (int w = 0; w < wave; ++w) {
-        wpre += s_scan[w];
-        hpre += s_hscan[w];
+    uint32_t dstart = 0, hexcl = 0;
+    if (tid < kRadixBins) {
+        uint32_t wpre = 0, hpre = 0;
+        for (int w = 0; w < wave; ++w) {
+            wpre += s_scan[w];
+            hpre += s_hscan[w];
+        }
+        dstart = wpre + inc - total;
+        hexcl = hpre + hinc - h;
+        s_dstart[tid] = dstart;
     }
-    const uint32_t dstart = wpre + inc - total;
-    const uint64_t hexcl = (uint64_t)(hpre + hinc - h);
-    s_dstart[d] = dstart;
     __syncthreads();
-
-    // Reorder the partition in LDS by digit (stable).
+    // the digit threads look back while every thread reorders its keys
+    if (tid < kRadixBins) {
+        excl = (uint32_t)digit_lookback(status, part, tid, total, err);
+        // element j of digit d's run goes to hexcl + excl + (j - dstart); in
+        // 32 bits, exact below 2^32 elements
+        s_gbase[tid] = hexcl + excl - dstart;
+    }
+    uint32_t pos[kItems];
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
         const int e = wave * (kItems * 64) + i * 64 + lane;
+        pos[i] = 0xffffffffu;
         if (e < nvalid) {
-            const uint32_t dd = (key[i] >> shift) & 0xffu;
-            const uint32_t pos = s_dstart[dd] + s_wcnt[wave][dd] + rank[i];
-            s_keys[pos] = key[i];
-            if constexpr (!kPacked) s_vals[pos] = val[i];
+            const uint32_t d = (key[i] >> shift) & 0xffu;
+            pos[i] = s_dstart[d] + s_cnt[wave][d] + rank[i];
+            s_x[pos[i]] = key[i];
         }
     }
-
-    // Decoupled look-back for digit d over earlier partitions, kLookback
-    // status words per round trip (before partition 0 reads as inclusive 0).
-    uint64_t excl = 0;
-    if (part > 0) {
-        int64_t p = (int64_t)part - 1;
-        uint32_t spins = 0;
-        while (true) {
-            uint64_t sw[kLookback];
-#pragma unroll
-            for (int k = 0; k < kLookback; ++k)
-                sw[k] = (p - k >= 0) ? load_agent(status + (uint64_t)(p - k) * kRadixBins + d)
-                                     : kFlagInclusive;
-            int k = 0;
-            bool done = false;
-            for (; k < kLookback; ++k) {
-                const uint64_t flag = sw[k] & ~kValueMask;
-                if (flag == 0) break;  // not published yet: reload from here
-                excl += sw[k] & kValueMask;
-                if (flag == kFlagInclusive) {
-                    done = true;
-                    break;
-                }
-            }
-            if (done) break;
-            p -= k;
-            if (k < kLookback) {
-                if (++spins > kSpinLimit) {
-                    atomicOr(err, 1);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(1);
-            }
-        }
-        store_agent(my_status, kFlagInclusive | (excl + total));
-    }
-    s_gbase[d] = hexcl + excl - (uint64_t)dstart;
     __syncthreads();
-
-    for (int j = tid; j < nvalid; j += kSortThreads) {
-        const uint32_t k = s_keys[j];
-        const uint64_t o = s_gbase[(k >> shift) & 0xffu] + (uint64_t)j;
-        if (o < n) {  // always true for consistent histograms; guards the stores
-            if constexpr (kPacked) {
-                kout[o] = k;
-                if (vout) vout[o] = k & ((1u << gbits) - 1u);
-            } else {
-                kout[o] = k;
-                vout[o] = s_vals[j];
+    uint32_t dst[kItems];
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+        const int j = tid + k * kThreads;
+        dst[k] = 0xffffffffu;
+        if (j < nvalid) {
+            const uint32_t kk = s_x[j];
+            const uint32_t o = s_gbase[(kk >> shift) & 0xffu] + (uint32_t)j;
+            if ((uint64_t)o < n) {  // always, for consistent histograms; guards the stores
+                dst[k] = o;
+                kout[o] = kk;
+                if constexpr (kPacked) {
+                    if (vout) vout[o] = kk & gmask;
+                }
             }
+        }
+    }
+    if constexpr (kVals) {
+        __syncthreads();  // every key is read out of the exchange buffer
+#pragma unroll
+        for (int i = 0; i < kItems; ++i)
+            if (pos[i] != 0xffffffffu) s_x[pos[i]] = val[i];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) {
+            const int j = tid + k * kThreads;
+            if (dst[k] != 0xffffffffu) vout[dst[k]] = s_x[j];
+        }
+    }
+}
+
+// ---- large inputs: reduce-then-scan passes --------------------------------
+// One LSD pass as three kernels with no waits between work-groups (no claim
+// atomic, no look-back chain):
+//   rts_upsweep   — each partition's digit counts, digit-major [256][parts];
+//   rts_scan      — per digit, the exclusive prefix over the partitions plus
+//                   the digit's global start, partition-major [parts][256];
+//   rts_downsweep — stable ranks within the partition (ballot match + per-wave
+//                   16-bit counters), keys then values reordered through LDS
+//                   and written at the partition's digit offsets.
+// The keys are read twice (20 B moved per element instead of 16), but every
+// partition proceeds on its own: with all partitions resident at once, a
+// look-back walks about half of its predecessors' status words.  A pass whose
+// digit is the same for every key copies through in the downsweep; the other
+// two kernels return at once.
+
+template <int kItems>
+__global__ __launch_bounds__(kSortThreads) void rts_upsweep_kernel(
+    const uint32_t* __restrict__ kin, uint64_t n, int shift, const uint32_t* __restrict__ hist,
+    uint32_t* __restrict__ part_hist, uint32_t parts) {
+    constexpr int kPart = kSortThreads * kItems;
+    static_assert(kPart % 4 == 0, "16-byte loads");
+    __shared__ uint32_t s_h[kRadixBins];
+    const int tid = threadIdx.x;
+    const uint32_t h = tid < kRadixBins ? hist[tid] : 0u;
+    if (tid < kRadixBins) s_h[tid] = 0;
+    if (__syncthreads_or(tid < kRadixBins && (uint64_t)h == n)) return;  // constant digit
+    const uint64_t base = (uint64_t)blockIdx.x * kPart;
+    const int nvalid = (int)min((uint64_t)kPart, n - base);
+    const int n4 = nvalid / 4;
+    const uint4* k4 = reinterpret_cast<const uint4*>(kin + base);  // 16-byte aligned
+    constexpr int kQ = (kItems + 3) / 4;  // 16-byte loads per thread covering the partition
+    uint4 q[kQ];
+#pragma unroll
+    for (int i = 0; i < kQ; ++i) {
+        const int e = i * kSortThreads + tid;
+        q[i] = e < n4 ? k4[e] : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < kQ; ++i) {
+        const int e = i * kSortThreads + tid;
+        if (e < n4) {
+            atomicAdd(&s_h[(q[i].x >> shift) & 0xffu], 1u);
+            atomicAdd(&s_h[(q[i].y >> shift) & 0xffu], 1u);
+            atomicAdd(&s_h[(q[i].z >> shift) & 0xffu], 1u);
+            atomicAdd(&s_h[(q[i].w >> shift) & 0xffu], 1u);
+        }
+    }
+    for (int e = 4 * n4 + tid; e < nvalid; e += kSortThreads)
+        atomicAdd(&s_h[(kin[base + e] >> shift) & 0xffu], 1u);
+    __syncthreads();
+    if (tid < kRadixBins) part_hist[(size_t)tid * parts + blockIdx.x] = s_h[tid];
+}
+
+constexpr int kRtsScanThreads = 256;
+constexpr int kRtsScanItems = 4;
+// Work-group d: digit d's exclusive prefix over the partitions, offset by the
+// digit's global start, into part_off[p][d].
+__global__ __launch_bounds__(kRtsScanThreads) void rts_scan_kernel(
+    const uint32_t* __restrict__ hist, uint64_t n, const uint32_t* __restrict__ part_hist,
+    uint32_t parts, uint32_t* __restrict__ part_off) {
+    __shared__ uint32_t s_w[kRtsScanThreads / kWave];
+    __shared__ uint32_t s_base;
+    const int tid = threadIdx.x;
+    const int d = blockIdx.x;
+    const uint32_t hv = hist[tid];
+    if (__syncthreads_or((uint64_t)hv == n)) return;  // constant digit: nothing to place
+    uint32_t all = 0;
+    const uint32_t below = group_exclusive_scan<kRtsScanThreads>(hv, s_w, &all);
+    if (tid == d) s_base = below;  // the keys of the digits below d
+    __syncthreads();
+    uint32_t carry = s_base;
+    const uint32_t* row = part_hist + (size_t)d * parts;
+    for (uint32_t c0 = 0; c0 < parts; c0 += kRtsScanThreads * kRtsScanItems) {
+        uint32_t v[kRtsScanItems], sum = 0;
+        const uint32_t p0 = c0 + (uint32_t)tid * kRtsScanItems;
+#pragma unroll
+        for (int i = 0; i < kRtsScanItems; ++i) {
+            v[i] = p0 + i < parts ? row[p0 + i] : 0u;
+            sum += v[i];
+        }
+        uint32_t chunk = 0;
+        uint32_t run = carry + group_exclusive_scan<kRtsScanThreads>(sum, s_w, &chunk);
+#pragma unroll
+        for (int i = 0; i < kRtsScanItems; ++i) {
+            if (p0 + i < parts) part_off[(size_t)(p0 + i) * kRadixBins + d] = run;
+            run += v[i];
+        }
+        carry += chunk;
+    }
+}
+
+template <bool kPacked, int kItems>
+__global__ __launch_bounds__(kSortThreads) __attribute__((amdgpu_waves_per_eu(8, 8))) void
+rts_downsweep_kernel(const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
+                     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n,
+                     int shift, int digit_bits, const uint32_t* __restrict__ hist,
+                     const uint32_t* __restrict__ part_off, int gbits) {
+    constexpr int kPart = kSortThreads * kItems;
+    constexpr bool kVals = !kPacked;
+    __shared__ uint32_t s_x[kPart];
+    __shared__ uint16_t s_cnt[kWideWaves][kRadixBins];
+    __shared__ uint32_t s_dstart[kRadixBins];
+    __shared__ uint32_t s_gbase[kRadixBins];
+    __shared__ uint32_t s_scan[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t part = blockIdx.x;
+    const uint64_t base = part * kPart;
+    const int nvalid = (int)min((uint64_t)kPart, n - base);
+    const uint32_t gmask = kPacked ? ((1u << gbits) - 1u) : 0u;
+    const uint32_t h = tid < kRadixBins ? hist[tid] : 0u;
+    uint32_t* cnt_words = reinterpret_cast<uint32_t*>(&s_cnt[0][0]);
+    for (int j = tid; j < kWideWaves * kRadixBins / 2; j += kSortThreads) cnt_words[j] = 0;
+    if (__syncthreads_or(tid < kRadixBins && (uint64_t)h == n)) {
+        // every key has the same digit: the stable pass is the identity
+        copy_partition<kPacked>(kin, vin, kout, vout, base, nvalid, gmask);
+        return;
+    }
+    // where the partition's run of each digit starts (from the scan)
+    const uint32_t poff = tid < kRadixBins ? part_off[part * kRadixBins + tid] : 0u;
+    uint32_t key[kItems], val[kItems], rank[kItems];
+    (void)val;
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const int e = wave * (kItems * 64) + i * 64 + lane;
+        key[i] = e < nvalid ? kin[base + e] : 0u;
+    }
+    if constexpr (kVals) {
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            const int e = wave * (kItems * 64) + i * 64 + lane;
+            val[i] = e < nvalid ? vin[base + e] : 0u;
+        }
+    }
+    // stable ranks within the wave's slice, in element order
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const int e = wave * (kItems * 64) + i * 64 + lane;
+        const bool v = e < nvalid;
+        const uint32_t d = (key[i] >> shift) & 0xffu;
+        const uint64_t peers = match_digit(d, ballot(v), digit_bits);
+        rank[i] = 0;
+        if (v) {
+            const uint32_t before = s_cnt[wave][d];
+            const uint64_t lower = peers & lanemask_lt();
+            rank[i] = before + (uint32_t)popc64(lower);
+            if (lower == 0) s_cnt[wave][d] = (uint16_t)(before + (uint32_t)popc64(peers));
+        }
+    }
+    __syncthreads();
+    uint32_t total = 0, inc = 0;
+    if (tid < kRadixBins) {
+        total = wave_prefix(s_cnt, kWideWaves);
+        inc = wave_inclusive_scan(total);
+        if (lane == 63) s_scan[wave] = inc;
+    }
+    __syncthreads();
+    if (tid < kRadixBins) {
+        uint32_t wpre = 0;
+        for (int w = 0; w < wave; ++w) wpre += s_scan[w];
+        const uint32_t dstart = wpre + inc - total;
+        s_dstart[tid] = dstart;
+        s_gbase[tid] = poff - dstart;  // element j of the digit's run goes to poff + (j - dstart)
+    }
+    __syncthreads();
+    uint32_t pos[kItems];
+#pragma unroll
+    for (int i = 0; i < kItems; ++i) {
+        const int e = wave * (kItems * 64) + i * 64 + lane;
+        pos[i] = 0xffffffffu;
+        if (e < nvalid) {
+            const uint32_t d = (key[i] >> shift) & 0xffu;
+            pos[i] = s_dstart[d] + s_cnt[wave][d] + rank[i];
+            s_x[pos[i]] = key[i];
+        }
+    }
+    __syncthreads();
+    uint32_t dst[kItems];
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+        const int j = tid + k * kSortThreads;
+        dst[k] = 0xffffffffu;
+        if (j < nvalid) {
+            const uint32_t kk = s_x[j];
+            const uint32_t o = s_gbase[(kk >> shift) & 0xffu] + (uint32_t)j;
+            if ((uint64_t)o < n) {  // always, for consistent histograms; guards the stores
+                dst[k] = o;
+                kout[o] = kk;
+                if constexpr (kPacked) {
+                    if (vout) vout[o] = kk & gmask;
+                }
+            }
+        }
+    }
+    if constexpr (kVals) {
+        __syncthreads();  // every key is read out of the exchange buffer
+#pragma unroll
+        for (int i = 0; i < kItems; ++i)
+            if (pos[i] != 0xffffffffu) s_x[pos[i]] = val[i];
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) {
+            const int j = tid + k * kSortThreads;
+            if (dst[k] != 0xffffffffu) vout[dst[k]] = s_x[j];
         }
     }
 }
@@ -505,41 +940,58 @@ hipError_t zero_fill(void* p, size_t bytes, hipStream_t st) {
     return zero_fill(f, st);
 }
 
-size_t sort_control_bytes(uint64_t n, int passes) {
-    return align_up((size_t)passes * kRadixBins * 4, 256) + align_up((size_t)passes * 64, 256) +
-           (size_t)passes * sort_parts(n) * kRadixBins * 8;
+size_t sort_control_bytes(uint64_t n) {
+    return hist_bytes() + align_up((size_t)kHistMaxPasses * 64, 256) +
+           (size_t)kHistMaxPasses * sort_parts(n) * kRadixBins * 8;
 }
 
 hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
-                             int begin_bit, int passes, void* control, int* err, hipStream_t st,
-                             bool hist_ready) {
-    if (n == 0 || passes <= 0) return hipSuccess;
-    if (passes > kHistMaxPasses) return hipErrorInvalidValue;
+                             void* control, int* err, hipStream_t st, bool hist_ready) {
+    if (n == 0) return hipSuccess;
+    if (n >= (1ull << 32)) return hipErrorInvalidValue;
     const uint64_t parts = sort_parts(n);
-    const bool small = sort_items(n) == 4;
-    SortCtl c = carve(control, n, passes);
+    SortCtl c = carve(control);
     hipError_t e = hipSuccess;
     if (!hist_ready) {
-        const unsigned hblocks = (unsigned)std::min<uint64_t>(parts, 512);
-        hipLaunchKernelGGL(radix_hist_kernel, dim3(hblocks), dim3(256), 0, st, k0, n, begin_bit,
-                           passes, c.hist);
+        const unsigned hblocks =
+            (unsigned)std::max<uint64_t>(1, std::min<uint64_t>((n + 8191) / 8192, 1024));
+        hipLaunchKernelGGL(radix_hist_kernel, dim3(hblocks), dim3(kHistThreads), 0, st, k0, n,
+                           c.hist);
         e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
     uint32_t *ki = k0, *vi = v0, *ko = k1, *vo = v1;
-    for (int p = 0; p < passes; ++p) {
-        if (small)
-            hipLaunchKernelGGL((onesweep_kernel<false, false, 4>), dim3((unsigned)parts),
-                               dim3(kSortThreads), 0, st, ki, vi, ko, vo, n, begin_bit + 8 * p, 8,
-                               c.hist + p * kRadixBins,
-                               c.status + (size_t)p * parts * kRadixBins, c.counters + p * 16,
-                               err, EmitSource{}, 0);
-        else
-            hipLaunchKernelGGL((onesweep_kernel<false, false>), dim3((unsigned)parts),
-                               dim3(kSortThreads), 0, st, ki, vi, ko, vo, n, begin_bit + 8 * p, 8,
-                               c.hist + p * kRadixBins,
-                               c.status + (size_t)p * parts * kRadixBins, c.counters + p * 16,
-                               err, EmitSource{}, 0);
+    const uint32_t np = (uint32_t)parts;
+    const int items = small_sort(n) ? kSmallItems : depth_items(n);
+    for (int p = 0; p < kHistMaxPasses; ++p) {
+        const uint32_t* hp = c.hist + p * kRadixBins;
+        uint64_t* stat = c.status + (size_t)p * parts * kRadixBins;
+        if (small_sort(n)) {
+            hipLaunchKernelGGL(onesweep_small_kernel, dim3(np), dim3(kSmallThreads), 0, st, ki, vi,
+                               ko, vo, n, 8 * p, hp, stat, c.counters + p * 16, err);
+        } else {
+            // the status words of the pass hold the partitions' digit counts,
+            // then their offsets
+            uint32_t* part_hist = reinterpret_cast<uint32_t*>(stat);
+            uint32_t* part_off = part_hist + (size_t)np * kRadixBins;
+#define GSR_RTS_PASS(I)                                                                        \
+    hipLaunchKernelGGL((rts_upsweep_kernel<I>), dim3(np), dim3(kSortThreads), 0, st, ki, n, 8 * p, \
+                       hp, part_hist, np);                                                     \
+    hipLaunchKernelGGL(rts_scan_kernel, dim3(kRadixBins), dim3(kRtsScanThreads), 0, st, hp, n,  \
+                       part_hist, np, part_off);                                               \
+    hipLaunchKernelGGL((rts_downsweep_kernel<false, I>), dim3(np), dim3(kSortThreads), 0, st,  \
+                       ki, vi, ko, vo, n, 8 * p, 8, hp, part_off, 0);
+            if (items == 4) {
+                GSR_RTS_PASS(4)
+            } else if (items == 6) {
+                GSR_RTS_PASS(6)
+            } else if (items == 8) {
+                GSR_RTS_PASS(8)
+            } else {
+                GSR_RTS_PASS(10)
+            }
+#undef GSR_RTS_PASS
+        }
         e = hipGetLastError();
         if (e != hipSuccess) return e;
         std::swap(ki, ko);
@@ -557,7 +1009,7 @@ hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, int ke
                             uint32_t* k1, uint32_t* vbuf, uint32_t* out_vals, uint32_t* out_keys,
                             int* err, hipStream_t st) {
     if (m == 0) return hipSuccess;
-    if (passes < 1 || passes > 4 || !out_keys) return hipErrorInvalidValue;
+    if (passes < 1 || passes > 4 || !out_keys || m >= (1ull << 32)) return hipErrorInvalidValue;
     const bool packed = gbits > 0;
     if (packed && gbits + key_bits > 32) return hipErrorInvalidValue;
     const uint64_t parts = parts_for(m);
@@ -584,17 +1036,17 @@ hipError_t launch_tile_sort(const EmitSource& es, uint64_t m, int passes, int ke
         const int shift = (packed ? gbits : 0) + 8 * p;
         const int bits = std::max(1, std::min(8, key_bits - 8 * p));  // significant digit bits
         if (p == 0 && packed)
-            hipLaunchKernelGGL((onesweep_kernel<true, true>), grid, block, 0, st, ki, vi, ko, vo,
-                               m, shift, bits, h, stat, ctr, err, es, gbits);
+            hipLaunchKernelGGL((onesweep_wide_kernel<true, true>), grid, block, 0, st, ki, vi, ko,
+                               vo, m, shift, bits, h, stat, ctr, err, es, gbits);
         else if (p == 0)
-            hipLaunchKernelGGL((onesweep_kernel<true, false>), grid, block, 0, st, ki, vi, ko, vo,
-                               m, shift, bits, h, stat, ctr, err, es, 0);
-        else if (packed)
-            hipLaunchKernelGGL((onesweep_kernel<false, true>), grid, block, 0, st, ki, vi, ko, vo,
-                               m, shift, bits, h, stat, ctr, err, es, gbits);
-        else
-            hipLaunchKernelGGL((onesweep_kernel<false, false>), grid, block, 0, st, ki, vi, ko,
+            hipLaunchKernelGGL((onesweep_wide_kernel<true, false>), grid, block, 0, st, ki, vi, ko,
                                vo, m, shift, bits, h, stat, ctr, err, es, 0);
+        else if (packed)
+            hipLaunchKernelGGL((onesweep_wide_kernel<false, true>), grid, block, 0, st, ki, vi, ko,
+                               vo, m, shift, bits, h, stat, ctr, err, es, gbits);
+        else
+            hipLaunchKernelGGL((onesweep_wide_kernel<false, false>), grid, block, 0, st, ki, vi,
+                               ko, vo, m, shift, bits, h, stat, ctr, err, es, 0);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
