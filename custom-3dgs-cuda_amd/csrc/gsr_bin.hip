@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
                 dkeys[i] = dk;
                 dvals[i] = (uint32_t)i;
 #pragma unroll
-                for (int p = 0; p < 4; ++p) atomicAdd(&s_dh[p][(dk >> (8 * p)) & 0xffu], 1u);
+                for (int p = 0; p < 4; ++p) lds_hist_add(s_dh[p], (dk >> (8 * p)) & 0xffu);
             }
             pairs += cnt;
             if (cnt && passes > 0) {
@@ -226,19 +226,6 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
             if (v) atomicAdd(&depth_hist[p * kRadixBins + tid], v);
         }
     }
-}
-
-// The depth sort's input for a depth order shared by several calls: every
-// Gaussian keyed by the bits of its depth (visible or not), valued by its
-// index.
-__global__ __launch_bounds__(kThreads) void depth_keys_kernel(int n,
-                                                              const float* __restrict__ depth,
-                                                              uint32_t* __restrict__ keys,
-                                                              uint32_t* __restrict__ vals) {
-    const int i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    keys[i] = __float_as_uint(depth[i]);
-    vals[i] = (uint32_t)i;
 }
 
 // Behind bin_count_kernel (block histogram mode), one work-group: the block
@@ -547,14 +534,6 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
     if (e != hipSuccess || !block_hist) return e;
     hipLaunchKernelGGL(bin_finish_kernel, dim3(1), dim3(kThreads), 0, st, bg, block_hist,
                        pair_total, block_start, seg_start, host_total, status);
-    return hipGetLastError();
-}
-
-hipError_t launch_depth_keys(int n, const float* depth, uint32_t* keys, uint32_t* vals,
-                             hipStream_t st) {
-    if (n <= 0) return hipSuccess;
-    hipLaunchKernelGGL(depth_keys_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, n, depth,
-                       keys, vals);
     return hipGetLastError();
 }
 

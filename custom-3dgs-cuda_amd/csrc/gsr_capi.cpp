@@ -572,9 +572,9 @@ int gsr_depth_order(int n, const float* depth, void* ws, size_t ws_bytes, int32_
     gsr::DeviceGlobals dg;
     GSR_HIP(gsr::device_globals(&dg), "depth order: device globals");
     GSR_HIP(gsr::zero_fill(ctl, gsr::sort_control_bytes(un), st), "depth order: clear");
-    GSR_HIP(gsr::launch_depth_keys(n, depth, k0, v0, st), "depth order: keys");
+    GSR_HIP(gsr::launch_depth_keys_hist((uint64_t)n, depth, k0, v0, ctl, st), "depth order: keys");
     GSR_HIP(gsr::launch_radix_sort(k0, v0, k1, v1, (uint64_t)n, ctl, dg.status, st,
-                                   /*hist_ready=*/false),
+                                   /*hist_ready=*/true),
             "depth order: sort");
     return GSR_OK;
 }

@@ -119,6 +119,20 @@ __device__ __forceinline__ uint64_t lanemask_lt() {
 
 __device__ __forceinline__ int popc64(uint64_t m) { return __builtin_popcountll(m); }
 
+// Adds one to LDS histogram bin d for every active lane.  A wave whose active
+// lanes all have the same bin adds their count once: a bin hit by whole waves
+// (a byte every key shares) would otherwise take 64 same-address atomics per
+// instruction.
+__device__ __forceinline__ void lds_hist_add(uint32_t* h, uint32_t d) {
+    const uint64_t act = ballot(true);
+    const uint32_t d0 = (uint32_t)__builtin_amdgcn_readfirstlane((int)d);
+    if (ballot(d != d0) == 0ull) {
+        if ((act & lanemask_lt()) == 0ull) atomicAdd(&h[d0], (uint32_t)popc64(act));
+    } else {
+        atomicAdd(&h[d], 1u);
+    }
+}
+
 // Sum over the 64 lanes of a wave (result valid in every lane).
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -93,6 +93,11 @@ size_t sort_control_bytes(uint64_t n);
 // already.
 hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
                              void* control, int* err, hipStream_t st, bool hist_ready = false);
+// The depth order's input: keys = the bits of depth[i], vals = i, and the
+// keys' histogram block at the start of `control` (zeroed first), so that
+// launch_radix_sort runs with hist_ready.
+hipError_t launch_depth_keys_hist(uint64_t n, const float* depth, uint32_t* keys, uint32_t* vals,
+                                  void* control, hipStream_t st);
 
 hipError_t zero_fill(void* p, size_t bytes, hipStream_t st);
 // Several regions in one launch.
@@ -212,11 +217,6 @@ hipError_t launch_records_slots(int n, const float* mean2d, const float* cov2d,
                                 const float* colors, const float* alpha, void* recs, int H, int W,
                                 uint32_t* counts, uint2* rects, uint32_t* goff, uint64_t* total,
                                 void* control, int* err, hipStream_t st);
-
-// keys[i] = float bits of depth[i], vals[i] = i for every Gaussian: the input
-// of a depth order shared by several calls.
-hipError_t launch_depth_keys(int n, const float* depth, uint32_t* keys, uint32_t* vals,
-                             hipStream_t st);
 
 // Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r] (perm null:
 // the identity); the total (u64) is written to *total.

@@ -156,7 +156,31 @@ __global__ __launch_bounds__(kHistThreads) void radix_hist_kernel(const uint32_t
         const uint32_t k = keys[i];
 #pragma unroll
         for (int p = 0; p < kHistMaxPasses; ++p)
-            atomicAdd(&s_h[p * kRadixBins + ((k >> (8 * p)) & 0xffu)], 1u);
+            lds_hist_add(s_h + p * kRadixBins, (k >> (8 * p)) & 0xffu);
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < kHistWords; j += kHistThreads) {
+        const uint32_t v = s_h[j];
+        if (v) atomicAdd(&hist[j], v);
+    }
+}
+
+// The depth order's keys (the bits of each depth, every Gaussian) and values
+// (indices), with the keys' digit histograms, in one read of the depths.
+__global__ __launch_bounds__(kHistThreads) void depth_keys_hist_kernel(
+    const float* __restrict__ depth, uint64_t n, uint32_t* __restrict__ keys,
+    uint32_t* __restrict__ vals, uint32_t* __restrict__ hist) {
+    __shared__ uint32_t s_h[kHistWords];
+    for (int j = threadIdx.x; j < kHistWords; j += kHistThreads) s_h[j] = 0;
+    __syncthreads();
+    const uint64_t stride = (uint64_t)gridDim.x * kHistThreads;
+    for (uint64_t i = (uint64_t)blockIdx.x * kHistThreads + threadIdx.x; i < n; i += stride) {
+        const uint32_t k = __float_as_uint(depth[i]);
+        keys[i] = k;
+        vals[i] = (uint32_t)i;
+#pragma unroll
+        for (int p = 0; p < kHistMaxPasses; ++p)
+            lds_hist_add(s_h + p * kRadixBins, (k >> (8 * p)) & 0xffu);
     }
     __syncthreads();
     for (int j = threadIdx.x; j < kHistWords; j += kHistThreads) {
@@ -943,6 +967,16 @@ hipError_t zero_fill(void* p, size_t bytes, hipStream_t st) {
 size_t sort_control_bytes(uint64_t n) {
     return hist_bytes() + align_up((size_t)kHistMaxPasses * 64, 256) +
            (size_t)kHistMaxPasses * sort_parts(n) * kRadixBins * 8;
+}
+
+hipError_t launch_depth_keys_hist(uint64_t n, const float* depth, uint32_t* keys, uint32_t* vals,
+                                  void* control, hipStream_t st) {
+    if (n == 0) return hipSuccess;
+    const unsigned blocks =
+        (unsigned)std::max<uint64_t>(1, std::min<uint64_t>((n + 8191) / 8192, 1024));
+    hipLaunchKernelGGL(depth_keys_hist_kernel, dim3(blocks), dim3(kHistThreads), 0, st, depth, n,
+                       keys, vals, carve(control).hist);
+    return hipGetLastError();
 }
 
 hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
