@@ -54,7 +54,8 @@ def assert_bitwise(got, want, what: str) -> None:
 
 
 def assert_grad_close(got, want, absum, what: str, rel: float = 1e-4,
-                      want64=None, floor: float = 0.05) -> tuple[float, float]:
+                      want64=None, floor: float = 0.05,
+                      tensor_vs64: bool = False) -> tuple[float, float]:
     """fp32 gradient vs float64 oracle sum.
 
     Bar: |got - want| <= rel * max(|want|, absum_floor) per element, where the
@@ -78,7 +79,12 @@ def assert_grad_close(got, want, absum, what: str, rel: float = 1e-4,
     evaluations of one sum, each with its own rounding).
 
     Returns (max scaled error over the elements held to the first bar, tensor
-    relative error); the tensor relative error is always held to rel.
+    relative error).  The tensor relative error is held to rel against want;
+    with tensor_vs64 (needs want64) it is taken against want64 instead and
+    held to max(rel, 1.5 x the fp32 oracle's own tensor error against want64):
+    over lists of ~1e5 entries per tile the reference's fp32 arithmetic is
+    itself a few 1e-4 from float64, and the bar is then to be no less
+    accurate than it.
     """
     got = np.asarray(got, dtype=np.float64).reshape(np.shape(want))
     want = np.asarray(want, dtype=np.float64)
@@ -97,8 +103,18 @@ def assert_grad_close(got, want, absum, what: str, rel: float = 1e-4,
         + (f" want64 {np.asarray(want64).reshape(want.shape)[worst]!r}" if want64 is not None
            else ""))
     # tensor-level relative error, the plain 1e-4 rel bar
-    den = np.linalg.norm(want.ravel())
     tot = 0.0
+    if tensor_vs64:
+        w64 = np.asarray(want64, dtype=np.float64).reshape(want.shape)
+        den = np.linalg.norm(w64.ravel())
+        if den > 0:
+            tot = float(np.linalg.norm((got - w64).ravel()) / den)
+            own = float(np.linalg.norm((want - w64).ravel()) / den)
+            bar = max(rel, 1.5 * own)
+            assert tot <= bar, (f"{what}: tensor relative error against float64 {tot:.3e} > "
+                                f"{bar:.3e} (fp32 oracle's own {own:.3e})")
+        return (float(err.max()) if err.size else 0.0), tot
+    den = np.linalg.norm(want.ravel())
     if den > 0:
         tot = float(np.linalg.norm((got - want).ravel()) / den)
         assert tot <= rel, f"{what}: tensor relative error {tot:.3e} > {rel}"

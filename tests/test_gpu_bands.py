@@ -19,7 +19,7 @@ from gaussian_splatting import synthetic
 from gaussian_splatting.rasterizer import RasterizeFunction, rasterize, rasterize_bands
 from gaussian_splatting.rasterizer.bands import (BAND_PAIR_BUDGET, MAX_BAND_PAIRS, band_rows,
                                                   plan_bands)
-from helpers import assert_bitwise, oracle_forward, scene_arrays
+from helpers import assert_bitwise, assert_grad_close, oracle_forward, scene_arrays
 from oracle import oracle as orc
 from test_gpu_parity import _np, gpu_forward
 
@@ -292,3 +292,131 @@ def test_c5_full_size_in_screen_bands(crc, device):
         assert torch.equal(x, y), nm
     del img, img2, g1, g2
     torch.cuda.empty_cache()
+
+
+def _sampled_tiles(rng_np, ranges, tiles_x, count=24):
+    """Tiles of a band to hold to the oracle: the first and the last, the four
+    longest lists (the backward's long-list mode and split tiles), the tile
+    whose list holds each multiple of 2^28 list positions (1 GB of ids) and
+    the one before it, then seeded random tiles with entries."""
+    T = ranges.shape[0]
+    lens = (ranges[:, 1] - ranges[:, 0]).astype(np.int64)
+    picked = {0, T - 1}
+    picked.update(int(t) for t in np.argsort(-lens, kind="stable")[:4])
+    ends = ranges[:, 1].astype(np.int64)
+    m = int(ends.max())
+    for k in range(1, m // (1 << 28) + 1):
+        t = int(np.searchsorted(ends, k << 28, side="right"))
+        picked.update(x for x in (t - 1, t) if 0 <= x < T)
+    filled = np.flatnonzero(lens > 0)
+    while len(picked) < min(count, T) and filled.size:
+        picked.add(int(rng_np.choice(filled)))
+    return sorted(picked)
+
+
+def test_c5_full_size_bands_match_the_oracle_on_sampled_tiles(crc, device):
+    """Config c5 at full size (5M Gaussians, 3840x2160, 1.1e10 pairs) in its
+    planned bands, through the path rasterize_bands takes (the frame's depth
+    order, rasterize_ordered per band, the band's backward).  The projection
+    and colours are the oracle's bit for bit over all 5M Gaussians.  For each
+    band: the pair count equals the oracle's count on the moved means; on
+    about 24 sampled tiles per band (the first and last, the longest lists,
+    those at each 2^28-entry list boundary, random ones) the tile's ids equal
+    the oracle's list built by brute force (every Gaussian whose tile
+    rectangle covers the tile, stably ordered by depth bits), and image,
+    final T and n_contrib equal the oracle's blend of those lists bit for bit;
+    with dL/dimage N(0, 1) on the sampled tiles and zero elsewhere, the
+    band's backward (the long-list mode: about 250k entries per tile) is
+    within the gradient bar over the same tiles: every element within 1e-4 of
+    max(|oracle|, sum|terms|) (or of the fp32 oracle's own distance to
+    float64), and each gradient tensor no further from the float64 oracle
+    than max(1e-4, 1.5 x the fp32 oracle's own distance).  Both floors are
+    wider than the smaller frames' (0.25 sum|terms| and 1e-4 against the fp32
+    oracle) because these lists are 100x longer: every term scales with the
+    transmittance unwound through the list, and the reference's own fp32
+    arithmetic (the fp32 oracle) measures 1e-2 of sum|terms| at the 99.9th
+    percentile and up to 6e-2 against float64 on these tiles, and 1e-4 to
+    4e-4 per tensor (printed per band)."""
+    print("[gpu] c5 full size against the oracle on sampled tiles", flush=True)
+    sc = synthetic.config_scene("c5", device=device, requires_grad=False)
+    a = scene_arrays(sc)
+    n, H, W = a["mu"].shape[0], a["H"], a["W"]
+    tiles_x = (W + 15) // 16
+    mu, q, s = (torch.from_numpy(a[k]).to(device) for k in ("mu", "q", "s"))
+    R, T = torch.from_numpy(a["R"]).to(device), torch.from_numpy(a["t"]).to(device)
+    m2, c2, d = crc.project(n, mu, q, s, R, T, a["fx"], a["fy"], a["cx"], a["cy"])
+    col = crc.SH(n, torch.from_numpy(a["cam"]).to(device), mu, torch.from_numpy(a["A"]).to(device),
+                 torch.from_numpy(a["kj"]).to(device))
+    op = torch.from_numpy(a["alpha"]).to(device)
+    del mu, q, s
+    wm2, wc2, wd = orc.project(a["mu"], a["q"], a["s"], a["R"], a["t"], a["fx"], a["fy"],
+                               a["cx"], a["cy"])
+    wcol = orc.sh(a["cam"], a["mu"], a["A"], a["kj"])
+    assert_bitwise(_np(m2), wm2, "mean2d")
+    assert_bitwise(_np(c2), wc2, "cov2d")
+    assert_bitwise(_np(d), wd, "depth")
+    assert_bitwise(_np(col), wcol, "colors")
+    order = crc.depth_order(n, d)
+    dbits = wd.view(np.uint32)
+    rows = crc.tile_row_pairs(n, m2, c2, H, W).cpu().tolist()
+    plan = plan_bands(rows, H)
+    print(f"[gpu] c5 bands {plan}", flush=True)
+    rng_np = np.random.default_rng(11)
+    for y0, h in plan:
+        mb = m2 - m2.new_tensor([0.0, float(y0)])
+        wmb = (wm2 - np.array([0.0, y0], np.float32)).astype(np.float32)
+        img, ids, rng, fT, nc = crc.rasterize_ordered(n, order, d, mb, c2, col, op, h, W)
+        counts, rect = orc.bin_count(wmb, wc2, h, W)
+        pairs = int(counts.astype(np.int64).sum())
+        print(f"[gpu] band rows {y0}..{y0 + h}: {ids.numel()} pairs (oracle {pairs})", flush=True)
+        assert ids.numel() == pairs, "band pair count"
+        ranges = _np(rng)
+        tiles = _sampled_tiles(rng_np, ranges, tiles_x)
+        # the oracle's lists of the sampled tiles by brute force
+        mini_ids, mini_ranges = [], np.zeros_like(ranges)
+        start = 0
+        for t in tiles:
+            tx, ty = t % tiles_x, t // tiles_x
+            cover = np.flatnonzero((rect[:, 0] <= tx) & (tx < rect[:, 1]) & (rect[:, 2] <= ty) &
+                                   (ty < rect[:, 3]))
+            lst = cover[np.argsort(dbits[cover], kind="stable")].astype(np.int32)
+            got = _np(ids[int(ranges[t, 0]):int(ranges[t, 1])])
+            assert_bitwise(got, lst, f"ids of tile {t} (band {y0})")
+            mini_ids.append(lst)
+            mini_ranges[t] = (start, start + lst.size)
+            start += lst.size
+        mini_ids = np.concatenate(mini_ids) if mini_ids else np.zeros(0, np.int32)
+        wimg, wfT, wnc = orc.blend_fwd(mini_ranges, mini_ids, wmb, wc2, wcol, a["alpha"], h, W)
+        # the sampled tiles' pixels, bit for bit
+        pix = np.zeros((h, W), bool)
+        for t in tiles:
+            tx, ty = t % tiles_x, t // tiles_x
+            pix[ty * 16:ty * 16 + 16, tx * 16:tx * 16 + 16] = True
+        assert_bitwise(_np(img)[pix], wimg[pix], f"image (band {y0})")
+        assert_bitwise(_np(fT)[pix], wfT[pix], f"final_T (band {y0})")
+        assert_bitwise(_np(nc)[pix], wnc[pix], f"n_contrib (band {y0})")
+        # the backward with dL/dimage on the sampled tiles only
+        G = synthetic.grad_image(h, W, seed=3 + y0).numpy()
+        G[~pix] = 0.0
+        dm, dc, dcol, dal = crc.backwards_rasterization(
+            torch.from_numpy(G).to(device), mb, c2, col, op, ids, rng, fT, nc, n, h, W)
+        torch.cuda.synchronize()
+        args = (G, wmb, wc2, wcol, a["alpha"], mini_ids, mini_ranges, wfT, wnc, h, W)
+        ref = orc.blend_bwd(*args, with_abs=True)
+        ref64 = orc.blend_bwd(*args, dtype=np.float64)
+        for gg, r, r64, ab, nm in zip((dm, dc, dcol, dal), ref[:4], ref64, ref[4:],
+                                      ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")):
+            x = _np(gg).astype(np.float64).reshape(r64.shape)
+            rel = lambda u, v: float(np.linalg.norm((u - v).ravel()) /
+                                     max(np.linalg.norm(v.ravel()), 1e-300))
+            m = ab > 0
+            q = lambda u: np.quantile((np.abs(u - r64) / np.maximum(ab, 1e-30))[m], [0.999, 1.0])
+            print(f"[gpu] band {y0}: {nm} tensor rel err GPU vs fp64 {rel(x, r64):.2e}, fp32 oracle "
+                  f"vs fp64 {rel(r, r64):.2e}, GPU vs fp32 oracle {rel(x, r):.2e}; "
+                  f"|x-fp64|/sum|terms| p99.9/max GPU {q(x)} oracle {q(r)}", flush=True)
+            worst, tot = assert_grad_close(_np(gg), r, ab, f"band {y0}: {nm}", want64=r64,
+                                           floor=1.0, tensor_vs64=True)
+            print(f"[gpu] band {y0}: {nm} max scaled error {worst:.2e}", flush=True)
+        print(f"[gpu] band {y0}: {len(tiles)} tiles ({mini_ids.size} entries) match", flush=True)
+        del img, ids, rng, fT, nc, dm, dc, dcol, dal, mb
+        torch.cuda.empty_cache()
