@@ -286,15 +286,15 @@ __device__ __forceinline__ uint32_t wave_prefix(uint16_t (*s_cnt)[kRadixBins], i
 
 // ---- small inputs: onesweep over 1024-key partitions -----------------------
 
-// One LSD pass over (key >> shift) & 0xff with 256 threads, one per digit:
+// One LSD pass over (key >> shift) & 0xff with 256 threads, one per digit
+// (inputs of at most 2^18 keys: at most 256 work-groups):
 // ranks by ballot match and per-wave counters, the partition's digit counts
 // published after the ranking, keys and values reordered in LDS while the
 // digit threads look back, then written in digit runs.
 __global__ __launch_bounds__(kSmallThreads) void onesweep_small_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n, int shift,
-    const uint32_t* __restrict__ hist, uint64_t* __restrict__ status,
-    uint32_t* __restrict__ counter, int* __restrict__ err) {
+    const uint32_t* __restrict__ hist, uint64_t* __restrict__ status, int* __restrict__ err) {
     constexpr int kItems = kSmallItems;
     constexpr int kPart = kSmallPartition;
     constexpr int kWaves = kSmallThreads / kWave;
@@ -306,20 +306,18 @@ __global__ __launch_bounds__(kSmallThreads) void onesweep_small_kernel(
     __shared__ uint32_t s_gbase[kRadixBins];
     __shared__ uint32_t s_scan[kWaves];
     __shared__ uint32_t s_hscan[kWaves];
-    __shared__ uint32_t s_part;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_part = atomicAdd(counter, 1u);
-    const uint32_t h = hist[tid];  // fetched while the claim is in flight
-    const bool same = __syncthreads_or((uint64_t)h == n);
-    const uint64_t part = s_part;
+    // The grid (at most 256 work-groups of 256 threads) is resident on the
+    // device at once, whatever order the work-groups start in: a partition
+    // waits only on partitions whose work-groups are running, so the
+    // partition is the work-group's index (no claim atomic).
+    const uint64_t part = blockIdx.x;
     const uint64_t base = part * kPart;
     const int nvalid = (int)min((uint64_t)kPart, n - base);
-    if (same) {
-        // every key has the same digit: the stable pass is the identity
-        copy_partition<false>(kin, vin, kout, vout, base, nvalid, 0u);
-        return;
-    }
+    const uint32_t h = hist[tid];
+    // the keys and values are loaded before the digit check, so its load is
+    // in flight with them
     uint32_t key[kItems], val[kItems], rank[kItems];
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
@@ -332,7 +330,18 @@ __global__ __launch_bounds__(kSmallThreads) void onesweep_small_kernel(
         val[i] = e < nvalid ? vin[base + e] : 0u;
     }
     for (int j = tid; j < kWaves * kRadixBins; j += kSmallThreads) (&s_wcnt[0][0])[j] = 0;
-    __syncthreads();
+    if (__syncthreads_or((uint64_t)h == n)) {
+        // every key has the same digit: the stable pass is the identity
+#pragma unroll
+        for (int i = 0; i < kItems; ++i) {
+            const int e = wave * (kItems * 64) + i * 64 + lane;
+            if (e < nvalid) {
+                kout[base + e] = key[i];
+                vout[base + e] = val[i];
+            }
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
         const int e = wave * (kItems * 64) + i * 64 + lane;
@@ -1002,7 +1011,7 @@ hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t*
         uint64_t* stat = c.status + (size_t)p * parts * kRadixBins;
         if (small_sort(n)) {
             hipLaunchKernelGGL(onesweep_small_kernel, dim3(np), dim3(kSmallThreads), 0, st, ki, vi,
-                               ko, vo, n, 8 * p, hp, stat, c.counters + p * 16, err);
+                               ko, vo, n, 8 * p, hp, stat, err);
         } else {
             // the status words of the pass hold the partitions' digit counts,
             // then their offsets
