@@ -85,6 +85,30 @@ def build_library(jobs: int = 8) -> Path:
     return LIB
 
 
+SAN_DIR = BUILD / "san"
+SAN_LIB = SAN_DIR / "libgsraster_hostsan.so"
+
+
+def build_host_sanitized() -> Path:
+    """libgsraster with its host code (the C ABI: argument checks, layouts,
+    launches) under AddressSanitizer and UndefinedBehaviorSanitizer, for the
+    CPU tests in tests/test_sanitizers.py.  Only gsr_capi.cpp is recompiled
+    (host code only, the sanitizers passed with -Xarch_host so no device code
+    is instrumented); the kernels' objects are the ones build_library made."""
+    objs = sorted(BUILD.glob("*.hip.o"))
+    if not objs:
+        raise RuntimeError("build the library first (its kernel objects are reused)")
+    SAN_DIR.mkdir(parents=True, exist_ok=True)
+    capi = SAN_DIR / "gsr_capi_san.o"
+    san = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+           "-Xarch_host", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", "-g"]
+    _run([HIPCC, *[f for f in HIP_FLAGS if f != "-O3"], "-O1", *san, "-c",
+          str(CSRC / "gsr_capi.cpp"), "-o", str(capi)])
+    _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *san, *map(str, objs), str(capi),
+          "-o", str(SAN_LIB)])
+    return SAN_LIB
+
+
 def build_extension() -> Path:
     import torch
     from torch.utils.cpp_extension import include_paths, library_paths

@@ -17,7 +17,9 @@ from pathlib import Path
 import numpy as np
 
 _HERE = Path(__file__).resolve().parent
-_LIB_PATH = _HERE / "libgs_oracle.so"
+# GSR_ORACLE_LIB selects another build of the same source (the sanitizer
+# build of tests/test_sanitizers.py)
+_LIB_PATH = Path(os.environ.get("GSR_ORACLE_LIB", str(_HERE / "libgs_oracle.so")))
 _lib = None
 
 _f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
