@@ -115,6 +115,40 @@ def _profile_json(kind: str, workload: str):
     return None
 
 
+# Sources whose change can change any stage's kernels: the shared device headers
+# and the host code that sizes the workspaces and sets the launch order.
+SHARED_SOURCES = ("gsr_common.h", "gsr_math.h", "gsr_gaussian.h", "gsr_group.h",
+                  "gsr_internal.h", "gsr_capi.cpp")
+
+
+def library_sources() -> dict:
+    """{file: sha256 prefix} of the sources the loaded libgsraster.so was built
+    from (gsr_build_sources)."""
+    import custom_rasterizer_cuda as crc
+
+    return dict(item.split("=", 1) for item in crc.library_sources().split(";") if "=" in item)
+
+
+def stale_reason(profile, entry) -> str | None:
+    """None when the kernels a profile entry measured are built from the same
+    sources as the loaded library: every file in the entry's "source_files"
+    plus SHARED_SOURCES has the hash the profile's "sources" recorded.
+    Otherwise the reason its counters no longer describe this build."""
+    if not profile or not entry:
+        return "no profile entry"
+    rec = profile.get("sources")
+    if not rec:
+        return "the profile records no source hashes"
+    cur = library_sources()
+    if not cur:
+        return "the loaded library records no source hashes"
+    files = sorted(set(entry.get("source_files") or cur) | set(SHARED_SOURCES))
+    changed = [f for f in files if rec.get(f) != cur.get(f)]
+    if changed:
+        return "sources changed since the profile: " + ", ".join(changed)
+    return None
+
+
 def dominant_roofline(stage: str, per_stage: dict, N: int, M: int, W: int, H: int,
                       workload: str) -> dict:
     """The roofline object of the frame's dominant stage, its average launch
@@ -130,10 +164,20 @@ def dominant_roofline(stage: str, per_stage: dict, N: int, M: int, W: int, H: in
     their formula bytes / launch time."""
     avg_s = per_stage[stage]["ms"] * 1e-3
     alg = stage_bytes(stage, N, M, W, H)
-    tr = (_profile_json("traffic", workload) or {}).get("stages", {}).get(stage)
-    traffic = tr.get("bytes_per_call") if tr else None
+    tp = _profile_json("traffic", workload)
+    tr = (tp or {}).get("stages", {}).get(stage)
+    tr_stale = stale_reason(tp, tr)
+    traffic = tr.get("bytes_per_call") if tr and not tr_stale else None
     va = (_profile_json("valu", workload) or {})
     vk = va.get("kernels", {}).get(stage)
+    va_stale = stale_reason(va, vk)
+    if stage in VALU_BOUND_STAGES and va_stale:
+        # the issue counts were measured on other kernel code: no fraction
+        return {"bound": "valu", "kernel": stage, "achieved": None, "peak": VALU_PEAK_GISSUE,
+                "unit": "G VALU issue quad-cycles/s", "frac": None, "traffic": traffic,
+                "avg_launch_ms": per_stage[stage]["ms"],
+                "reason": "VALU counters: " + va_stale
+                + ("" if not tr_stale else "; HBM counters: " + tr_stale)}
     if stage in VALU_BOUND_STAGES and vk:
         ach = vk["issue_quads_per_launch"] / avg_s / 1e9
         out = {"bound": "valu", "kernel": stage, "achieved": round(ach, 1),
@@ -157,9 +201,12 @@ def dominant_roofline(stage: str, per_stage: dict, N: int, M: int, W: int, H: in
         return out
     b = traffic or alg
     ach = (b / avg_s / 1e9) if b else 0.0
-    return {"bound": "hbm", "kernel": stage, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "algorithmic_bytes": alg, "avg_launch_ms": per_stage[stage]["ms"]}
+    out = {"bound": "hbm", "kernel": stage, "achieved": round(ach, 1), "peak": HBM_PEAK_GBS,
+           "unit": "GB/s", "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic,
+           "algorithmic_bytes": alg, "avg_launch_ms": per_stage[stage]["ms"]}
+    if tr and tr_stale:
+        out["traffic_note"] = "measured traffic not used: " + tr_stale
+    return out
 
 
 def _clear(g):
@@ -235,7 +282,8 @@ def _stage_rates(stages: dict, N: int, M: int, W: int, H: int, keep=None,
     FETCH_SIZE + WRITE_SIZE per call where profiles/traffic_<workload>.json
     holds them ("bytes": "measured"), else the per-stage formula
     ("bytes": "formula"); the VALU-bound blends get no formula rate."""
-    measured = (_profile_json("traffic", workload) or {}).get("stages", {}) if workload else {}
+    prof = _profile_json("traffic", workload) if workload else None
+    measured = (prof or {}).get("stages", {})
     out = {}
     for name, (count, ms) in stages.items():
         if keep is not None and name not in keep:
@@ -243,10 +291,13 @@ def _stage_rates(stages: dict, N: int, M: int, W: int, H: int, keep=None,
         avg = ms / max(count, 1)
         entry = {"ms": round(avg, 4), "calls": int(count)}
         b, src = None, None
-        if name in measured and measured[name].get("bytes_per_call"):
+        stale = stale_reason(prof, measured.get(name)) if name in measured else None
+        if name in measured and measured[name].get("bytes_per_call") and not stale:
             b, src = float(measured[name]["bytes_per_call"]), "measured"
         elif name not in VALU_BOUND_STAGES:
             b, src = stage_bytes(name, N, M, W, H), "formula"
+        if stale:
+            entry["measured_bytes_not_used"] = stale
         if b is not None and avg > 0:
             gbs = b / (avg * 1e-3) / 1e9
             entry.update({"GBps": round(gbs, 1), "pct_hbm_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
@@ -346,11 +397,15 @@ def per_gaussian_stages(sc, calls: int = 20) -> dict:
     # VALU issue beside the HBM rate: the kernels' issue quad-cycles per launch
     # at this size (profiles/valu_per_gaussian_c5_5M.json) over the live time
     # against VALU_PEAK_GISSUE (the projection backward is issue-bound)
-    vk = (_profile_json("valu", "per_gaussian_c5_5M") or {}).get("kernels", {})
+    vp = _profile_json("valu", "per_gaussian_c5_5M")
+    vk = (vp or {}).get("kernels", {})
     if n == 5_000_000:
         for name, entry in out.items():
             k = vk.get(name)
-            if k and entry["ms"] > 0:
+            stale = stale_reason(vp, k) if k else None
+            if stale:
+                entry["valu"] = {"kernel": k["kernel"], "frac": None, "reason": stale}
+            elif k and entry["ms"] > 0:
                 ach = k["issue_quads_per_launch"] / (entry["ms"] * 1e-3) / 1e9
                 entry["valu"] = {"kernel": k["kernel"], "G_issue_quads_per_s": round(ach, 1),
                                  "frac": round(ach / VALU_PEAK_GISSUE, 4)}
@@ -725,6 +780,8 @@ def main() -> int:
         "binning": binning_summary(per_stage, N, M, W, H),
         "stages": per_stage,
         "profiled_ms_per_step": round(ptot, 4),
+        # the sha256 prefixes of the sources the measured library was built from
+        "build_sources": library_sources(),
     }
     if not args.no_extra:
         extra = {}

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import argparse
 import concurrent.futures as cf
+import hashlib
 import os
 import shutil
 import subprocess
@@ -60,6 +61,21 @@ def _run(cmd: list[str]) -> None:
         print(out)
 
 
+def source_hashes() -> dict[str, str]:
+    """The first 16 hex digits of the sha256 of every file the library is built
+    from.  The library returns them (gsr_build_sources) so that a measurement
+    can name the sources it measured and a later run can tell whether they
+    changed."""
+    files = (sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + [CSRC / "gsr_capi.cpp"]
+             + [INCLUDE / "gsraster.h"])
+    return {f.name: hashlib.sha256(f.read_bytes()).hexdigest()[:16] for f in files}
+
+
+def _sources_define() -> str:
+    text = ";".join(f"{k}={v}" for k, v in source_hashes().items())
+    return f'-DGSR_SOURCES="{text}"'
+
+
 def _hip_objects(jobs: int) -> list[Path]:
     BUILD.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip")) + [CSRC / "gsr_capi.cpp"]
@@ -68,7 +84,8 @@ def _hip_objects(jobs: int) -> list[Path]:
     for src in sources:
         obj = BUILD / (src.name + ".o")
         lang = ["-x", "hip"] if src.suffix == ".hip" else []
-        cmds.append([HIPCC, *HIP_FLAGS, *lang, "-c", str(src), "-o", str(obj)])
+        extra = [_sources_define()] if src.name == "gsr_capi.cpp" else []
+        cmds.append([HIPCC, *HIP_FLAGS, *lang, *extra, "-c", str(src), "-o", str(obj)])
         objs.append(obj)
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         list(ex.map(_run, cmds))
@@ -102,7 +119,7 @@ def build_host_sanitized() -> Path:
     capi = SAN_DIR / "gsr_capi_san.o"
     san = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
            "-Xarch_host", "-fno-sanitize-recover=undefined", "-fno-omit-frame-pointer", "-g"]
-    _run([HIPCC, *[f for f in HIP_FLAGS if f != "-O3"], "-O1", *san, "-c",
+    _run([HIPCC, *[f for f in HIP_FLAGS if f != "-O3"], "-O1", *san, _sources_define(), "-c",
           str(CSRC / "gsr_capi.cpp"), "-o", str(capi)])
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *san, *map(str, objs), str(capi),
           "-o", str(SAN_LIB)])

@@ -848,6 +848,7 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     m.def("rasterize_with_keys", &rasterize_with_keys,
           "rasterize, also returning the sorted 64-bit keys (tile << 32 | depth bits)");
     m.def("library_version", []() { return std::string(gsr_version()); });
+    m.def("library_sources", []() { return std::string(gsr_build_sources()); });
     m.def("screen_radii", &screen_radii, "glue: approximate screen radii (one kernel)");
     m.def("camera_position", &camera_position, "glue: camera position -R^T t (one kernel)");
     m.def("project_sh", &project_sh,

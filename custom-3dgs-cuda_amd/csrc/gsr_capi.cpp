@@ -16,6 +16,12 @@
 #include "gsr_internal.h"
 #include "../../include/gsraster.h"
 
+// "file=hash;..." over the sources this library was built from (build.py
+// passes it); a build by other means reports that it recorded none.
+#ifndef GSR_SOURCES
+#define GSR_SOURCES ""
+#endif
+
 namespace {
 
 thread_local std::string g_err;
@@ -350,6 +356,8 @@ extern "C" {
 const char* gsr_last_error(void) { return g_err.c_str(); }
 
 const char* gsr_version(void) { return "gsraster 0.1 (gfx950)"; }
+
+const char* gsr_build_sources(void) { return GSR_SOURCES; }
 
 int gsr_project(int n, const float* mu, const float* q, const float* s, const float* rot,
                 const float* trans, float fx, float fy, float cx, float cy, float* mean2d,

@@ -45,6 +45,11 @@ extern "C" {
 
 const char* gsr_last_error(void);
 const char* gsr_version(void);
+/* Build identification, no counterpart in the reference: "file=hash;..." with
+ * the first 16 hex digits of the sha256 of each source file the library was
+ * built from (empty when the build recorded none).  Measurements record it so a
+ * later run can tell whether the kernels it measured have changed. */
+const char* gsr_build_sources(void);
 
 /* Replaces project_gaussians_to_2d (csrc/forward/projection.h:5,
  * launcher csrc/forward/projection.cu:109-153; bound as `project` at

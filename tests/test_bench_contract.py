@@ -68,10 +68,21 @@ def test_valu_peak_is_the_published_fp32_figure_per_packed_wave64_fma():
     assert bench.VALU_PEAK_GISSUE == pytest.approx(157.3e12 / 256 / 1e9, rel=1e-3)
 
 
-def _fake_profiles(monkeypatch, traffic=None, valu=None):
+SOURCES = {f: "%016x" % i for i, f in enumerate(
+    ("gsr_blend.hip", "gsr_tiles.hip", "gsr_bin.hip") + bench.SHARED_SOURCES)}
+
+
+def _fake_profiles(monkeypatch, traffic=None, valu=None, library=None):
+    """Profiles recorded on SOURCES; the loaded library built from ``library``
+    (default: the same sources)."""
+    for prof in (traffic, valu):
+        if prof is not None:
+            prof.setdefault("sources", dict(SOURCES))
+
     def fake(kind, workload):
         return {"traffic": traffic, "valu": valu}.get(kind)
     monkeypatch.setattr(bench, "_profile_json", fake)
+    monkeypatch.setattr(bench, "library_sources", lambda: dict(library or SOURCES))
 
 
 def test_stage_rates_use_measured_bytes_and_never_a_formula_for_the_blends(monkeypatch):
@@ -115,3 +126,56 @@ def test_committed_profiles_cover_the_bench_roofline():
     assert 0 < v["kernels"]["blend_bwd"]["issue_util"] <= 1.0
     for c in v["calibration"].values():
         assert 0.8 < c["issue_util"] <= 1.0
+
+
+def _changed(name):
+    out = dict(SOURCES)
+    out[name] = "f" * 16
+    return out
+
+
+def test_profiles_of_changed_sources_give_no_valu_fraction(monkeypatch):
+    """A blend profile measured on other gsr_blend.hip code: frac is null with the
+    reason, and the measured traffic is not used."""
+    _fake_profiles(monkeypatch,
+                   traffic={"stages": {"blend_bwd": {"bytes_per_call": 1.46e8,
+                                                     "source_files": ["gsr_blend.hip"]}}},
+                   valu={"kernels": {"blend_bwd": {"issue_quads_per_launch": 1.255e8,
+                                                   "source_files": ["gsr_blend.hip"]}}},
+                   library=_changed("gsr_blend.hip"))
+    r = bench.dominant_roofline("blend_bwd", {"blend_bwd": {"ms": 0.25}}, 100_000,
+                                13_000_000, 1920, 1080, "w")
+    assert r["frac"] is None and r["achieved"] is None and r["traffic"] is None
+    assert "gsr_blend.hip" in r["reason"]
+
+
+def test_a_shared_header_change_also_makes_a_profile_stale(monkeypatch):
+    _fake_profiles(monkeypatch,
+                   valu={"kernels": {"blend_fwd": {"issue_quads_per_launch": 1e8,
+                                                   "source_files": ["gsr_blend.hip"]}}},
+                   library=_changed("gsr_common.h"))
+    r = bench.dominant_roofline("blend_fwd", {"blend_fwd": {"ms": 0.2}}, 100_000,
+                                13_000_000, 1920, 1080, "w")
+    assert r["frac"] is None and "gsr_common.h" in r["reason"]
+
+
+def test_a_profile_without_hashes_is_not_trusted(monkeypatch):
+    _fake_profiles(monkeypatch, valu={"sources": {}, "kernels": {
+        "blend_bwd": {"issue_quads_per_launch": 1e8}}})
+    r = bench.dominant_roofline("blend_bwd", {"blend_bwd": {"ms": 0.2}}, 100_000,
+                                13_000_000, 1920, 1080, "w")
+    assert r["frac"] is None and "no source hashes" in r["reason"]
+
+
+def test_stage_rates_fall_back_to_formula_bytes_for_changed_kernels(monkeypatch):
+    """Only the stage whose kernel file changed loses its measured bytes."""
+    _fake_profiles(monkeypatch, traffic={"stages": {
+        "tile_binning": {"bytes_per_call": 1.1e8, "source_files": ["gsr_tiles.hip"]},
+        "bin_count": {"bytes_per_call": 2.0e7, "source_files": ["gsr_bin.hip"]}}},
+        library=_changed("gsr_tiles.hip"))
+    st = {"tile_binning": (10, 0.5), "bin_count": (10, 0.2)}
+    r = bench._stage_rates(st, 100_000, 13_000_000, 1920, 1080, workload="w")
+    assert r["tile_binning"]["bytes"] == "formula"
+    assert "gsr_tiles.hip" in r["tile_binning"]["measured_bytes_not_used"]
+    assert r["bin_count"]["bytes"] == "measured"
+    assert "measured_bytes_not_used" not in r["bin_count"]

@@ -28,6 +28,7 @@ def lib():
     L = ctypes.CDLL(str(LIB))
     L.gsr_last_error.restype = ctypes.c_char_p
     L.gsr_version.restype = ctypes.c_char_p
+    L.gsr_build_sources.restype = ctypes.c_char_p
     L.gsr_bin_workspace_bytes.restype = ctypes.c_size_t
     L.gsr_bin_workspace_bytes.argtypes = [ctypes.c_int] * 3
     L.gsr_sort_workspace_bytes.restype = ctypes.c_size_t
@@ -47,6 +48,20 @@ def test_header_declares_the_six_stages():
 def test_every_declared_symbol_is_exported(lib):
     missing = [n for n in _declared() if not hasattr(lib, n)]
     assert not missing, missing
+
+
+def test_library_names_the_sources_it_was_built_from(lib):
+    """gsr_build_sources holds one sha256 prefix per source file; against the
+    files in this tree it says whether the built library is current."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("gsr_build", ROOT / "custom-3dgs-cuda_amd" / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    text = lib.gsr_build_sources().decode()
+    got = dict(item.split("=") for item in text.split(";"))
+    assert {"gsr_blend.hip", "gsr_common.h", "gsr_capi.cpp", "gsraster.h"} <= set(got)
+    assert all(len(h) == 16 and int(h, 16) >= 0 for h in got.values())
+    assert got == mod.source_hashes(), "libgsraster.so is older than its sources: rebuild"
 
 
 def test_host_side_queries_and_validation(lib):
