@@ -4,7 +4,8 @@
 // with the SSIM of torchmetrics (>= 1.0, the reference's requirement; not
 // vendored): an 11x11 Gaussian window of sigma 1.5 normalised to sum 1,
 // C1 = (0.01)^2, C2 = (0.03)^2 for data range 1, per-window statistics
-// sigma_x^2 = E[x^2] - mu_x^2 and sigma_xy = E[xy] - mu_x mu_y, averaged over
+// sigma_x^2 = max(E[x^2] - mu_x^2, 0) (torchmetrics clamps both variances at 0
+// since its releases after 1.0) and sigma_xy = E[xy] - mu_x mu_y, averaged over
 // the windows whose 11x11 support lies inside the image (torchmetrics pads by
 // reflection and crops the 5-pixel margin of the index map, which leaves
 // exactly those windows) and over the 3 channels.  Images are [H, W, 3] fp32.
@@ -143,7 +144,9 @@ __global__ __launch_bounds__(kLossThreads) void ssim_fwd_kernel(
             const int gy = y0 + vr + j, gx = x0 + vc;
             if (!interior(gy, gx, H, W)) continue;
             const float mux = m[j][0], muy = m[j][1];
-            const float sxx = m[j][2] - mux * mux, syy = m[j][3] - muy * muy;
+            // the variances clamped at 0 (torch.clamp: NaN stays NaN)
+            const float vxx = m[j][2] - mux * mux, vyy = m[j][3] - muy * muy;
+            const float sxx = vxx < 0.0f ? 0.0f : vxx, syy = vyy < 0.0f ? 0.0f : vyy;
             const float sxy = m[j][4] - mux * muy;
             const float a1 = 2.0f * mux * muy + kC1, a2 = 2.0f * sxy + kC2;
             const float b1 = mux * mux + muy * muy + kC1, b2 = sxx + syy + kC2;
@@ -156,10 +159,12 @@ __global__ __launch_bounds__(kLossThreads) void ssim_fwd_kernel(
                 // A1 = 2 mux muy + C1, A2 = 2 (E[xy] - mux muy) + C2,
                 // B1 = mux^2 + muy^2 + C1, B2 = E[x^2] - mux^2 + E[y^2] - muy^2 + C2
                 const float dA1 = a2 * inv, dA2 = a1 * inv, dB1 = -s * rb1, dB2 = -s * rb2;
-                const float g1 = 2.0f * muy * (dA1 - dA2) + 2.0f * mux * (dB1 - dB2);
+                // the clamp of sigma_x^2 passes its gradient where sigma_x^2 >= 0
+                const float dBx = (vxx >= 0.0f) ? dB2 : 0.0f;
+                const float g1 = 2.0f * muy * (dA1 - dA2) + 2.0f * mux * (dB1 - dBx);
                 const size_t idx = ((size_t)gy * W + gx) * 3 + ch;
                 gmaps[idx] = g1;              // dS/dmu_x
-                gmaps[plane + idx] = dB2;     // dS/dE[x^2]
+                gmaps[plane + idx] = dBx;     // dS/dE[x^2]
                 gmaps[2 * plane + idx] = 2.0f * dA2;  // dS/dE[xy]
             }
         }

@@ -7,16 +7,19 @@
 // streams parameter, gradient and both moments through registers in 16-byte
 // loads: 16 B in and 12 B out per element, nothing else.
 //
-// Arithmetic per element, fp32, in torch's order (torch/optim/adam.py,
-// _single_tensor_adam), every scalar rounded to fp32 once from the host's
-// double as torch does with a Python scalar:
-//   m = fma(1 - b1, g - m, m)             (lerp_)
-//   v = fma((1 - b2) g, g, v b2)          (mul_ then addcmul_)
-//   p = p + (-step_size m) / (sqrt(v) / sqrt(bc2) + eps)   (addcdiv_)
-//   p = clamp(p, lo, hi), NaN kept        (clamp_)
+// Arithmetic per element, fp32, as torch.optim.Adam's default path evaluates it
+// on the device (torch/optim/adam.py, _multi_tensor_adam: the foreach kernels,
+// whose device code forms these fused multiply-adds), every scalar rounded to
+// fp32 once from the host's double as torch does with a Python scalar:
+//   m = fma(1 - b1, g - m, m)                          (_foreach_lerp_)
+//   v = fma(1 - b2, g g, v b2)                         (_foreach_mul_, _foreach_addcmul_)
+//   p = fma(-step_size, m / (sqrt(v) / sqrt(bc2) + eps), p)   (_foreach_addcdiv_)
+//   p = clamp(p, lo, hi), NaN kept                     (clamp_)
 // with correctly rounded sqrt (sqrt_rn, gsr_common.h) and division (__fdiv_rn: the
 // div_scale / div_fmas / div_fixup sequence) and no other contraction (the
-// library is built with -ffp-contract=off).
+// library is built with -ffp-contract=off).  The trainer runs Adam on the
+// device, so this is the rounding it trains with; torch's CPU single-tensor
+// path forms v = fma((1 - b2) g, g, v b2) and p + (-step_size m) / d instead.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -39,10 +42,9 @@ struct AdamScalars {
 __device__ __forceinline__ void adam_update(float& p, float g, float& m, float& v,
                                             const AdamScalars& s) {
     m = __builtin_fmaf(s.w1, g - m, m);
-    v = __builtin_fmaf(s.w2 * g, g, v * s.b2);
+    v = __builtin_fmaf(s.w2, g * g, v * s.b2);
     const float d = __fdiv_rn(sqrt_rn(v), s.bc2s) + s.eps;
-    float q = __fdiv_rn(s.neg_step * m, d);
-    float x = p + q;
+    float x = __builtin_fmaf(s.neg_step, __fdiv_rn(m, d), p);
     x = (x < s.lo) ? s.lo : x;
     x = (x > s.hi) ? s.hi : x;
     p = x;

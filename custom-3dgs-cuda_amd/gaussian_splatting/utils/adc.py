@@ -166,6 +166,15 @@ def adaptive_density_control(
     ensure_densification_state(gaussians)
     if scene_extent is None:
         raise ValueError("scene_extent must be provided.")
+    if not allow_densify:
+        # no clone, split, prune or reset (adc.py:351-384): the Parameters and
+        # the optimizer state stay as they are; the buffers start again
+        n = int(gaussians.mu.shape[0])
+        gaussians.xyz_grad_accum = t.zeros(n, 1, device=gaussians.mu.device,
+                                           dtype=gaussians.mu.dtype)
+        gaussians.denom = t.zeros(n, 1, device=gaussians.mu.device, dtype=gaussians.mu.dtype)
+        gaussians.max_radii2D.zero_()
+        return gaussians, optimizer, {"cloned": 0, "split": 0, "pruned": 0}
     crc = _crc()
     attrs = {_GROUP_TO_ATTR[g["name"]]: g["params"][0] for g in optimizer.param_groups}
     missing = [a for a in _ATTRS if a not in attrs]

@@ -7,7 +7,8 @@ arguments, parameter groups and per-parameter state (``step``, ``exp_avg``,
 ``exp_avg_sq``; the densification code of the reference rewrites that state when
 it prunes or grows the parameters, utils/adc.py:122-165), whose ``step()`` runs
 the whole update of every group in one launch (libgsraster ``gsr_adam_step``).
-Its arithmetic is torch's single-tensor Adam's for fp32 tensors.  A group may
+Its arithmetic is torch.optim.Adam's default (multi-tensor) path on the
+device for fp32 tensors, bit for bit.  A group may
 also carry ``clamp_min`` / ``clamp_max``: the updated parameter is clamped in the
 same pass, which is how the trainer's clamps after each step
 (scripts/train.py:171-176: opacity logits to [logit(1e-4), logit(0.99)];

@@ -836,21 +836,29 @@ ORC_EXPORT void orc_project_bwd_f64(int n, const double* dmean, const double* dc
 }
 
 // ---- the trainer's optimizer step: torch.optim.Adam (the reference's
-// utils/optim.py:12-31, eps 1e-15, default betas), as torch's single-tensor
-// path evaluates it for an fp32 tensor (torch/optim/adam.py,
-// _single_tensor_adam), followed by the trainer's clamps of the updated
-// parameter (scripts/train.py:171-176, utils/adc.py:90-93):
-//   m = fma(1 - b1, g - m, m)                 exp_avg.lerp_(grad, 1 - b1)
-//   v = fma((1 - b2) g, g, v b2)              exp_avg_sq.mul_(b2).addcmul_(grad, grad, 1 - b2)
-//   d = sqrt(v) / sqrt(1 - b2^t) + eps        (exp_avg_sq.sqrt() / bc2_sqrt).add_(eps)
-//   p = p + (-(lr / (1 - b1^t)) m) / d        param.addcdiv_(exp_avg, denom, -step_size)
-//   p = min(max(p, lo), hi), NaN kept         param.clamp_(lo, hi)
-// The scalars are formed in double (Python floats) and rounded to fp32 once,
-// as torch does when it applies a Python scalar to an fp32 tensor; the fused
-// multiply-adds are the ones torch's CPU lerp and addcmul kernels form.
+// utils/optim.py:12-31, eps 1e-15, default betas) on an fp32 tensor, followed
+// by the trainer's clamps of the updated parameter (scripts/train.py:171-176,
+// utils/adc.py:90-93).  Two paths of torch/optim/adam.py, which differ only in
+// rounding:
+//   device (_multi_tensor_adam, the default on the GPU, where the trainer runs;
+//   device_path != 0):
+//     m = fma(1 - b1, g - m, m)               _foreach_lerp_
+//     v = fma(1 - b2, g g, v b2)              _foreach_mul_, _foreach_addcmul_
+//     p = fma(-(lr / (1 - b1^t)), m / d, p)   _foreach_addcdiv_
+//   CPU (_single_tensor_adam):
+//     m = fma(1 - b1, g - m, m)               exp_avg.lerp_(grad, 1 - b1)
+//     v = fma((1 - b2) g, g, v b2)            exp_avg_sq.mul_(b2).addcmul_(grad, grad, 1 - b2)
+//     p = p + (-(lr / (1 - b1^t)) m) / d      param.addcdiv_(exp_avg, denom, -step_size)
+// with d = sqrt(v) / sqrt(1 - b2^t) + eps and then p = min(max(p, lo), hi),
+// NaN kept (param.clamp_(lo, hi)).  The scalars are formed in double (Python
+// floats) and rounded to fp32 once, as torch does when it applies a Python
+// scalar to an fp32 tensor; the fused multiply-adds are the ones torch's
+// kernels form (the CPU path pinned against torch on the CPU in
+// tests/test_oracle_adam.py, the device path against torch on the GPU in
+// tests/test_gpu_optim.py).
 ORC_EXPORT void orc_adam_step_f32(int64_t n, float* p, const float* g, float* m, float* v,
                                   double lr, double beta1, double beta2, double eps, int64_t step,
-                                  float lo, float hi) {
+                                  float lo, float hi, int device_path) {
     const float w1 = (float)(1.0 - beta1), b2 = (float)beta2, w2 = (float)(1.0 - beta2);
     const double bc1 = 1.0 - std::pow(beta1, (double)step);
     const double bc2 = 1.0 - std::pow(beta2, (double)step);
@@ -861,9 +869,10 @@ ORC_EXPORT void orc_adam_step_f32(int64_t n, float* p, const float* g, float* m,
     for (int64_t i = 0; i < n; ++i) {
         const float gi = g[i];
         const float mi = std::fma(w1, gi - m[i], m[i]);
-        const float vi = std::fma(w2 * gi, gi, v[i] * b2);
+        const float vi = device_path ? std::fma(w2, gi * gi, v[i] * b2)
+                                     : std::fma(w2 * gi, gi, v[i] * b2);
         const float d = std::sqrt(vi) / bc2s + e;
-        float pi = p[i] + (neg_step * mi) / d;
+        float pi = device_path ? std::fma(neg_step, mi / d, p[i]) : p[i] + (neg_step * mi) / d;
         pi = (pi < lo) ? lo : pi;
         pi = (pi > hi) ? hi : pi;
         m[i] = mi;

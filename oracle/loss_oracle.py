@@ -11,7 +11,9 @@ reference's arguments (loss.py:30, data_range=1.0) and defaults: a Gaussian
 window of 11 taps and sigma 1.5 (the 1D kernel exp(-(d/sigma)^2/2) over
 d = -5..5, normalised to sum 1, used separably), K1 = 0.01, K2 = 0.03,
 C1 = (K1 L)^2, C2 = (K2 L)^2, L = 1, the moments mu = w * x,
-sigma_x^2 = w * x^2 - mu_x^2, sigma_xy = w * xy - mu_x mu_y, and the index
+sigma_x^2 = max(w * x^2 - mu_x^2, 0) (torchmetrics clamps both variances at 0
+since its releases after 1.0; 1.0 itself did not, which differs only where a
+variance rounds below 0), sigma_xy = w * xy - mu_x mu_y, and the index
 ((2 mu_x mu_y + C1)(2 sigma_xy + C2)) / ((mu_x^2 + mu_y^2 + C1)(sigma_x^2 +
 sigma_y^2 + C2)) averaged over channels and window centres (Wang et al. 2004).
 torchmetrics pads by reflection and crops the index map by the window radius
@@ -56,12 +58,17 @@ def _moments(x: np.ndarray, y: np.ndarray):
     return mx, my, exx, eyy, exy
 
 
+def _clamp0(v: np.ndarray) -> np.ndarray:
+    """torch.clamp(v, min=0): NaN stays NaN."""
+    return np.where(v < 0.0, 0.0, v)
+
+
 def ssim_map(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     """The SSIM index of each valid window and channel of two [H, W, 3] images
     (already in the data range): [H - 10, W - 10, 3]."""
     x, y = np.asarray(a, np.float64), np.asarray(b, np.float64)
     mx, my, exx, eyy, exy = _moments(x, y)
-    sxx, syy, sxy = exx - mx * mx, eyy - my * my, exy - mx * my
+    sxx, syy, sxy = _clamp0(exx - mx * mx), _clamp0(eyy - my * my), exy - mx * my
     return ((2 * mx * my + C1) * (2 * sxy + C2)) / ((mx * mx + my * my + C1) * (sxx + syy + C2))
 
 
@@ -79,6 +86,24 @@ def l1_dssim(rendered, gt, lambda_dssim: float = LAMBDA_DSSIM) -> tuple[float, f
     l1 = float(np.mean(np.abs(g - r)))
     s = ssim(clamp01(r), clamp01(g))
     return (1.0 - lambda_dssim) * l1 + lambda_dssim * (1.0 - s), s, l1
+
+
+def index_derivatives(mx, my, exx, eyy, exy):
+    """The SSIM index S of windows with moments (mu_x, mu_y, E[x^2], E[y^2],
+    E[xy]) and its partial derivatives (dS/dmu_x, dS/dE[x^2], dS/dE[xy]).  The
+    clamp of sigma_x^2 at 0 passes its gradient where sigma_x^2 >= 0 (torch's
+    clamp backward)."""
+    vxx = exx - mx * mx
+    sxx, syy, sxy = _clamp0(vxx), _clamp0(eyy - my * my), exy - mx * my
+    a1, a2 = 2 * mx * my + C1, 2 * sxy + C2
+    b1, b2 = mx * mx + my * my + C1, sxx + syy + C2
+    s = a1 * a2 / (b1 * b2)
+    dA1, dA2, dB1, dB2 = a2 / (b1 * b2), a1 / (b1 * b2), -s / b1, -s / b2
+    dBx = np.where(vxx >= 0.0, dB2, 0.0)
+    g1 = 2 * my * (dA1 - dA2) + 2 * mx * (dB1 - dBx)  # dS/dmu_x (through sigma_x^2, sigma_xy)
+    g2 = dBx                                          # dS/dE[x^2]
+    g3 = 2 * dA2                                      # dS/dE[xy]
+    return s, g1, g2, g3
 
 
 def _blur_adjoint(m: np.ndarray, w: np.ndarray, H: int, W: int) -> np.ndarray:
@@ -105,15 +130,7 @@ def l1_dssim_grad(rendered, gt, lambda_dssim: float = LAMBDA_DSSIM, grad_loss: f
     r, g = np.asarray(rendered, np.float64), np.asarray(gt, np.float64)
     H, W = r.shape[:2]
     x, y = clamp01(r), clamp01(g)
-    mx, my, exx, eyy, exy = _moments(x, y)
-    sxx, syy, sxy = exx - mx * mx, eyy - my * my, exy - mx * my
-    a1, a2 = 2 * mx * my + C1, 2 * sxy + C2
-    b1, b2 = mx * mx + my * my + C1, sxx + syy + C2
-    s = a1 * a2 / (b1 * b2)
-    dA1, dA2, dB1, dB2 = a2 / (b1 * b2), a1 / (b1 * b2), -s / b1, -s / b2
-    g1 = 2 * my * (dA1 - dA2) + 2 * mx * (dB1 - dB2)  # dS/dmu_x (through sigma_x^2, sigma_xy)
-    g2 = dB2                                          # dS/dE[x^2]
-    g3 = 2 * dA2                                      # dS/dE[xy]
+    s, g1, g2, g3 = index_derivatives(*_moments(x, y))
     w = gaussian_window()
     n_win = s.size
     mask = (r >= 0.0) & (r <= 1.0)

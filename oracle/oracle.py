@@ -66,7 +66,7 @@ def lib():
     L.orc_sh_bwd_f64.argtypes = [c_int] + [_f64p] * 8
     L.orc_project_bwd_f32.argtypes = [c_int] + [_f32p] * 7 + [c_f] * 4 + [_f32p] * 3 + [c_int]
     L.orc_project_bwd_f64.argtypes = [c_int] + [_f64p] * 7 + [c_d] * 4 + [_f64p] * 3 + [c_int]
-    L.orc_adam_step_f32.argtypes = [c_i64] + [_f32p] * 4 + [c_d] * 4 + [c_i64, c_f, c_f]
+    L.orc_adam_step_f32.argtypes = [c_i64] + [_f32p] * 4 + [c_d] * 4 + [c_i64, c_f, c_f, c_int]
     _lib = L
     return L
 
@@ -242,15 +242,18 @@ def tiles(H: int, W: int) -> int:
 
 
 def adam_step(p, g, m, v, lr, step, beta1=0.9, beta2=0.999, eps=1e-15, clamp_min=None,
-              clamp_max=None):
-    """One Adam step with the trainer's clamps (utils/optim.py:12-31 with
-    torch.optim.Adam's single-tensor arithmetic; scripts/train.py:171-176,
-    utils/adc.py:90-93) on fp32 copies: returns (p, m, v) after the step
-    (``step`` is the step number after the update, 1 for the first)."""
+              clamp_max=None, path="device"):
+    """One Adam step with the trainer's clamps (utils/optim.py:12-31;
+    scripts/train.py:171-176, utils/adc.py:90-93) on fp32 copies: returns
+    (p, m, v) after the step (``step`` is the step number after the update, 1
+    for the first).  ``path`` "device": torch.optim.Adam's default path on the
+    GPU (multi-tensor); "cpu": its single-tensor path on the CPU."""
+    if path not in ("device", "cpu"):
+        raise ValueError("path must be 'device' or 'cpu'")
     p, m, v = (np.array(a, dtype=np.float32, copy=True, order="C").ravel() for a in (p, m, v))
     g = _c(g, np.float32).ravel()
     lo = np.float32(-np.inf if clamp_min is None else clamp_min)
     hi = np.float32(np.inf if clamp_max is None else clamp_max)
     lib().orc_adam_step_f32(p.size, p, g, m, v, float(lr), float(beta1), float(beta2), float(eps),
-                            int(step), lo, hi)
+                            int(step), lo, hi, 1 if path == "device" else 0)
     return p, m, v

@@ -127,3 +127,30 @@ def test_adc_all_pruned_and_no_state(device):
     for k in NAMES:
         assert np.array_equal(getattr(g, k).detach().cpu().numpy(), want[k]), k
     assert len(opt.state) == 0
+
+
+def test_adc_without_densify_leaves_the_cloud_untouched(device):
+    """allow_densify=False (the reference's frozen topology, adc.py:351-384):
+    the same Parameter objects and optimizer state, values unchanged, only the
+    densification buffers restarted; the oracle agrees."""
+    from gaussian_splatting.utils.adc import adaptive_density_control
+
+    g, opt, c, m, accum, denom, maxr = _setup(device, 2000, 5)
+    params = {k: getattr(g, k) for k in NAMES}
+    before = {k: v.detach().clone() for k, v in params.items()}
+    states = {k: dict(opt.state[v]) for k, v in params.items()}
+    radii = g.max_radii2D.data_ptr()
+    g, opt, st = adaptive_density_control(g, opt, scene_extent=5.0, reset_opacity=True,
+                                          allow_densify=False)
+    want, _, wst = ao.adc(c, m, accum, denom, maxr, None, scene_extent=5.0, reset_opacity=True,
+                          allow_densify=False)
+    assert st == wst == {"cloned": 0, "split": 0, "pruned": 0}
+    for k in NAMES:
+        assert getattr(g, k) is params[k]
+        assert torch.equal(getattr(g, k).detach(), before[k])
+        assert np.array_equal(getattr(g, k).detach().cpu().numpy(), want[k]), k
+        for key in ("exp_avg", "exp_avg_sq"):
+            assert opt.state[params[k]][key] is states[k][key]
+    # cleared in place, as the reference's max_radii2D.zero_()
+    assert g.max_radii2D.data_ptr() == radii and not g.max_radii2D.any()
+    assert not g.xyz_grad_accum.any() and not g.denom.any()

@@ -81,7 +81,8 @@ def _torch_ssim_padded(a, b):
     inp = torch.cat((xp, yp, xp * xp, yp * yp, xp * yp))
     out = torch.nn.functional.conv2d(inp, k, groups=3)
     mx, my, exx, eyy, exy = out.split(1)
-    sxx, syy, sxy = exx - mx * mx, eyy - my * my, exy - mx * my
+    # the variances clamped at 0, as torchmetrics after 1.0
+    sxx, syy, sxy = (exx - mx * mx).clamp(min=0.0), (eyy - my * my).clamp(min=0.0), exy - mx * my
     s = ((2 * mx * my + lo.C1) * (2 * sxy + lo.C2)) / ((mx * mx + my * my + lo.C1) * (sxx + syy + lo.C2))
     return s[..., p:-p, p:-p].mean()
 
@@ -99,7 +100,9 @@ def _torch_loss(r, g, lam):
     k = torch.outer(w1, w1).expand(3, 1, 11, 11).contiguous()
     conv = lambda t: torch.nn.functional.conv2d(t, k, groups=3)
     mx, my = conv(x), conv(y)
-    sxx, syy, sxy = conv(x * x) - mx * mx, conv(y * y) - my * my, conv(x * y) - mx * my
+    sxx = (conv(x * x) - mx * mx).clamp(min=0.0)
+    syy = (conv(y * y) - my * my).clamp(min=0.0)
+    sxy = conv(x * y) - mx * my
     s = ((2 * mx * my + lo.C1) * (2 * sxy + lo.C2)) / ((mx * mx + my * my + lo.C1) * (sxx + syy + lo.C2))
     return (1 - lam) * l1 + lam * (1 - s.mean())
 
@@ -140,3 +143,31 @@ def test_clamped_pixels_get_only_the_l1_term():
     n = r.size
     assert grad[3, 4, 1] == pytest.approx(0.8 / n)   # rendered above gt: +1/n of the L1 term
     assert grad[8, 2, 0] == pytest.approx(-0.8 / n)  # below gt
+
+
+def test_index_derivatives_through_the_variance_clamp():
+    """dS/d(mu_x, E[x^2], E[xy]) against torch autograd of the clamped index,
+    on moments whose sigma_x^2 or sigma_y^2 lies below, at and above 0 (the
+    clamp passes the gradient at 0, as torch's clamp backward)."""
+    rng = np.random.default_rng(8)
+    mx = rng.uniform(0.05, 0.95, 64)
+    my = rng.uniform(0.05, 0.95, 64)
+    vx = np.concatenate([rng.uniform(-2e-3, -1e-6, 16), np.zeros(16), rng.uniform(1e-6, 2e-2, 32)])
+    vy = rng.permutation(np.concatenate([rng.uniform(-2e-3, -1e-6, 20), rng.uniform(1e-6, 2e-2, 44)]))
+    exx, eyy = vx + mx * mx, vy + my * my
+    exy = mx * my + rng.uniform(-5e-3, 5e-3, 64)
+    t = [torch.from_numpy(a.copy()).requires_grad_(True) for a in (mx, my, exx, eyy, exy)]
+    tmx, tmy, texx, teyy, texy = t
+    sxx = (texx - tmx * tmx).clamp(min=0.0)
+    syy = (teyy - tmy * tmy).clamp(min=0.0)
+    sxy = texy - tmx * tmy
+    st = ((2 * tmx * tmy + lo.C1) * (2 * sxy + lo.C2)) / (
+        (tmx * tmx + tmy * tmy + lo.C1) * (sxx + syy + lo.C2))
+    st.sum().backward()
+    s, g1, g2, g3 = lo.index_derivatives(mx, my, exx, eyy, exy)
+    assert np.allclose(s, st.detach().numpy(), rtol=1e-13, atol=0)
+    for got, want in ((g1, tmx.grad), (g2, texx.grad), (g3, texy.grad)):
+        want = want.numpy()
+        assert np.allclose(got, want, rtol=1e-11, atol=1e-11 * np.abs(want).max())
+    # below 0 the E[x^2] path carries nothing; above it, -S / B2
+    assert np.all(g2[:16] == 0.0) and np.all(g2[16:] != 0.0)
