@@ -543,7 +543,7 @@ def frame_stages(sc, steps: int, binning: str | None = None) -> dict:
             os.environ["GSR_TILE_BINNING"] = old
     v = sc.view
     rates = _stage_rates(stages, sc.n, M, v["width"], v["height"],
-                         workload=None if binning else sc.name + "_randn_grad")
+                         workload=sc.name + "_randn_grad" + (f"_tile_{binning}" if binning else ""))
     return {"fwd_ms": round(fwd, 4), "bwd_ms": round(bwd, 4), "ms_per_frame": round(total, 4),
             "fps": round(1000.0 / total, 1), "pairs": M,
             "binning": binning_summary(rates, sc.n, M, v["width"], v["height"]),

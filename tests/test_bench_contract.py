@@ -128,6 +128,35 @@ def test_committed_profiles_cover_the_bench_roofline():
         assert 0.8 < c["issue_util"] <= 1.0
 
 
+def _tree_sources():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("gsr_build", ROOT / "custom-3dgs-cuda_amd" / "build.py")
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    return mod.source_hashes()
+
+
+PROFILE_JSONS = ("traffic_bench_100k_1920x1080", "traffic_c4_1000000_1920x1080_randn_grad",
+                 "traffic_c4_1000000_1920x1080_randn_grad_tile_sort", "valu_bench_100k_1920x1080",
+                 "valu_per_gaussian_c5_5M")
+
+
+@pytest.mark.parametrize("name", PROFILE_JSONS)
+def test_committed_profiles_were_measured_on_these_sources(monkeypatch, name):
+    """Every stage or kernel entry of the committed profiles names its source
+    files, and they (with the shared sources) hash as in this tree: the
+    counters bench.py uses describe the kernels that are built here."""
+    kind, workload = name.split("_", 1)
+    prof = bench._profile_json(kind, workload)
+    assert prof and set(prof["sources"]) == set(_tree_sources())
+    monkeypatch.setattr(bench, "library_sources", _tree_sources)
+    entries = prof["stages"] if kind == "traffic" else prof["kernels"]
+    assert entries
+    for key, entry in entries.items():
+        assert entry["source_files"], key
+        assert bench.stale_reason(prof, entry) is None, (key, bench.stale_reason(prof, entry))
+
+
 def _changed(name):
     out = dict(SOURCES)
     out[name] = "f" * 16
