@@ -61,14 +61,43 @@ def _run(cmd: list[str]) -> None:
         print(out)
 
 
+def code_of(text: str) -> str:
+    """C/C++ source without its comments, blank lines and runs of blanks: what
+    an edit has to change to change the compiled code.  String and character
+    literals are kept as they are."""
+    out, i, n = [], 0, len(text)
+    while i < n:
+        c = text[i]
+        if c in "\"'":
+            j = i + 1
+            while j < n and text[j] != c:
+                j += 2 if text[j] == "\\" else 1
+            out.append(text[i:j + 1])
+            i = j + 1
+        elif text.startswith("//", i):
+            while i < n and text[i] != "\n":
+                i += 1
+        elif text.startswith("/*", i):
+            j = text.find("*/", i + 2)
+            i = n if j < 0 else j + 2
+            out.append(" ")
+        else:
+            out.append(c)
+            i += 1
+    lines = (" ".join(line.split()) for line in "".join(out).splitlines())
+    return "\n".join(line for line in lines if line)
+
+
 def source_hashes() -> dict[str, str]:
-    """The first 16 hex digits of the sha256 of every file the library is built
-    from.  The library returns them (gsr_build_sources) so that a measurement
-    can name the sources it measured and a later run can tell whether they
-    changed."""
+    """The first 16 hex digits of the sha256 of the code (code_of) of every
+    file the library is built from.  The library returns them
+    (gsr_build_sources) so that a measurement can name the code it measured and
+    a later run can tell whether it changed; edits to comments alone change no
+    hash."""
     files = (sorted(CSRC.glob("*.hip")) + sorted(CSRC.glob("*.h")) + [CSRC / "gsr_capi.cpp"]
              + [INCLUDE / "gsraster.h"])
-    return {f.name: hashlib.sha256(f.read_bytes()).hexdigest()[:16] for f in files}
+    return {f.name: hashlib.sha256(code_of(f.read_text()).encode()).hexdigest()[:16]
+            for f in files}
 
 
 def _sources_define() -> str:

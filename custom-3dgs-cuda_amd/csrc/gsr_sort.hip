@@ -10,11 +10,14 @@
 // contiguous 256 B access and ranks follow element order.
 //
 // Depth orders of at most 2^18 keys: onesweep_small_kernel, one kernel per
-// pass, 256 threads (one per digit) over 1024-key partitions claimed in
-// launch order through an atomic counter, so that every partition a
-// work-group waits on belongs to a work-group already resident; decoupled
-// look-back over the earlier partitions' published digit counts.  These
-// passes are latency chains (claim, load, rank, look-back, scatter).
+// pass, 256 threads (one per digit) over 1024-key partitions; the grid (at
+// most 256 work-groups) is resident on the device at once, so the partition
+// is the work-group's index and every partition a work-group waits on
+// belongs to a running work-group; decoupled look-back over the earlier
+// partitions' published digit counts.  The keys and the four passes' digit
+// histograms come from the binning's count kernel (or depth_keys_hist_kernel)
+// in one pass.  These passes are latency chains (load, rank, look-back,
+// scatter).
 //
 // Larger depth orders: reduce-then-scan, three kernels per pass with no
 // waits between work-groups (rts_upsweep / rts_scan / rts_downsweep).  Their
