@@ -68,3 +68,84 @@ def test_full_size_forward_and_backward(crc, device, name, make):
         print(f"[gpu] {name}: {nm} max scaled error {worst:.2e}, tensor relative error "
               f"{tot:.2e}; |x - fp64|/sum|terms| p99.9/max: GPU {g99:.1e}/{gmax:.1e}, "
               f"fp32 oracle {o99:.1e}/{omax:.1e}", flush=True)
+
+
+def _rel(x, ref):
+    den = np.linalg.norm(ref.ravel())
+    return float(np.linalg.norm((x - ref).ravel()) / den) if den > 0 else 0.0
+
+
+GLUE = [
+    ("bench_100k_1920x1080_sum", lambda d: synthetic.bench_scene(n=100_000, width=1920,
+                                                                height=1080, device=d), False),
+    ("c3_100k_1920x1080_randn", lambda d: synthetic.config_scene("c3", device=d), True),
+]
+
+
+@pytest.mark.parametrize("name,make,randn", GLUE, ids=[g[0] for g in GLUE])
+def test_full_size_glue_path_parameter_gradients(device, name, make, randn):
+    """The path bench.py times, at its own size: rasterize() on the bench scene
+    (100k Gaussians, 1920x1080) through the fused head (camera position,
+    projection, radii, SH, sigmoid), image.sum().backward() with its broadcast
+    gradient read in place, and the fused tail (SH and projection backward,
+    sigmoid backward); and config c3 (100k anisotropic, rotated Gaussians at
+    1080p) with a seeded N(0, 1) dL/dimage.  The image against the oracle's forward; the six
+    parameter gradients against the oracle chain (blend backward, SH backward,
+    projection backward, sigmoid backward) evaluated in float64 on the oracle's
+    fp32 forward: each tensor's relative error within max(1e-4, 1.5x the fp32
+    chain's own error against float64), and each element within 1e-4 of the
+    tensor's largest element or within twice the fp32 chain's own error on it.
+    The bench scene's Gaussians are isotropic and unrotated, so its d_q is zero
+    in exact arithmetic: rounding noise, held to twice the fp32 chain's largest."""
+    from gaussian_splatting.rasterizer.rasterize import rasterize
+
+    print(f"[gpu] full-size glue path: {name}", flush=True)
+    sc = make(device)
+    a = scene_arrays(sc)
+    g, v = sc.gaussians, sc.view
+    H, W = a["H"], a["W"]
+    G = synthetic.grad_image(H, W, seed=3).numpy() if randn else np.ones((H, W, 3), np.float32)
+    img = rasterize(g, v)
+    if randn:
+        img.backward(torch.from_numpy(G).to(device))
+    else:
+        img.sum().backward()
+    torch.cuda.synchronize()
+    want = oracle_forward(a)
+    gi = _np(img)
+    assert np.abs(gi - want["img"]).max() <= 1e-5
+    print(f"[gpu] {name} image: {np.mean(gi == want['img']) * 100:.4f}% bit for bit, max |diff| "
+          f"{np.abs(gi - want['img']).max():.1e}", flush=True)
+    chains = {}
+    for dt in (np.float32, np.float64):
+        dm, dc, dcol, dal = orc.blend_bwd(G, want["mean2d"], want["cov2d"], want["colors"],
+                                          a["alpha"], want["ids"], want["ranges"],
+                                          want["final_T"], want["n_contrib"], H, W, dtype=dt)
+        dA, dkj, dmu_sh = orc.sh_bwd(dcol.astype(dt), a["mu"], a["A"], a["kj"], a["cam"], dtype=dt)
+        dmu_p, dq, ds = orc.project_bwd(dm.astype(dt), dc.astype(dt), a["mu"], a["q"], a["s"],
+                                        a["R"], a["t"], a["fx"], a["fy"], a["cx"], a["cy"], dtype=dt)
+        sig = a["alpha"].astype(np.float64)
+        chains[dt] = {"mu": dmu_p.astype(np.float64) + dmu_sh, "q": dq, "s": ds,
+                      "alpha": np.asarray(dal, np.float64) * sig * (1.0 - sig), "A": dA, "k_j": dkj}
+    fails, tag = [], name
+    for name in ("mu", "q", "s", "alpha", "A", "k_j"):
+        got = _np(getattr(g, name).grad).astype(np.float64)
+        w64 = np.asarray(chains[np.float64][name], np.float64).reshape(got.shape)
+        w32 = np.asarray(chains[np.float32][name], np.float64).reshape(got.shape)
+        tot, own = _rel(got, w64), _rel(w32, w64)
+        diff, own_el = np.abs(got - w64), np.abs(w32 - w64)
+        top = np.abs(w64).max()
+        if own > 1.0:
+            # zero in exact arithmetic: rounding noise, held to the fp32 chain's
+            bar = np.full(diff.shape, 2.0 * own_el.max())
+        else:
+            # 1e-4 of the tensor's largest element, or twice the fp32 chain's
+            # own error on the element
+            bar = np.maximum(1e-4 * top, 2.0 * own_el)
+        bad = diff > bar
+        print(f"[gpu] {tag} d_{name}: tensor relative error {tot:.2e} (fp32 chain {own:.2e}); "
+              f"max |x| {top:.2e}, max |got - fp64| {diff.max():.2e} (fp32 chain {own_el.max():.2e}), "
+              f"elements beyond the bar: {int(bad.sum())}", flush=True)
+        fails += [f"d_{name}: tensor {tot:.3e}"] if tot > max(1e-4, 1.5 * own) else []
+        fails += [f"d_{name}: {int(bad.sum())} elements"] if bad.any() else []
+    assert not fails, fails
