@@ -40,6 +40,8 @@ namespace gsr {
 namespace {
 
 constexpr int kAdcThreads = 256;
+// Elements per thread whose loads copy_rows issues together.
+constexpr int kAdcUnroll = 4;
 constexpr int kWidths[6] = {3, 4, 3, 1, 3, 45};  // mu, q, s, alpha, A, k_j
 
 // flag bits of a source Gaussian
@@ -193,20 +195,32 @@ __device__ __forceinline__ void copy_rows(const float* __restrict__ src, float* 
                                           int mode, bool skip_split, bool clamp, float clamp_hi,
                                           bool zero_all) {
     const float* sp = src ? src + (size_t)g0 * W : nullptr;
-    for (int e = threadIdx.x; e < cnt * W; e += kAdcThreads) {
-        const int g = e / W, k = e - g * W;
-        const float v = sp ? sp[e] : 0.0f;
+    const int total = cnt * W;
+    // kAdcUnroll elements per thread and step, their loads issued together
+    for (int e0 = threadIdx.x; e0 < total; e0 += kAdcUnroll * kAdcThreads) {
+        float v[kAdcUnroll];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-            const uint32_t row = s_dst[d][g];
-            if (row == kNoRow) continue;
-            if (mode == 0) {
-                if (skip_split && d >= 2) continue;
-                float x = v;
-                if (clamp) x = isnan_f(x) ? x : fminf(x, clamp_hi);
-                dst[(size_t)row * W + k] = x;
-            } else {
-                dst[(size_t)row * W + k] = (d == 0 && !zero_all) ? v : 0.0f;
+        for (int u = 0; u < kAdcUnroll; ++u) {
+            const int e = e0 + u * kAdcThreads;
+            v[u] = (sp && e < total) ? sp[e] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < kAdcUnroll; ++u) {
+            const int e = e0 + u * kAdcThreads;
+            if (e >= total) break;
+            const int g = e / W, k = e - g * W;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const uint32_t row = s_dst[d][g];
+                if (row == kNoRow) continue;
+                if (mode == 0) {
+                    if (skip_split && d >= 2) continue;
+                    float x = v[u];
+                    if (clamp) x = isnan_f(x) ? x : fminf(x, clamp_hi);
+                    dst[(size_t)row * W + k] = x;
+                } else {
+                    dst[(size_t)row * W + k] = (d == 0 && !zero_all) ? v[u] : 0.0f;
+                }
             }
         }
     }
