@@ -57,7 +57,8 @@ def test_depth_order_is_the_stable_sort_of_the_depth_bits(crc, device):
     """depth_order against numpy's stable argsort of the depths' float bits as
     unsigned: ties (repeated depths), -0.0 / 0.0, negative depths, infinities
     and NaNs of both signs, at a 1024-key partition boundary and beyond 2^18
-    keys (the depth sort's two partition sizes)."""
+    keys (the depth sort's two partition sizes); and keys that all share their
+    top byte (the pass over it copies through) up to 2^18 keys."""
     rng = np.random.default_rng(5)
     for n in (1, 1000, 1024 * 37 + 5, 300_000):
         print(f"[gpu] depth order of {n} keys", flush=True)
@@ -69,6 +70,15 @@ def test_depth_order_is_the_stable_sort_of_the_depth_bits(crc, device):
         got = _np(crc.depth_order(n, torch.from_numpy(d).to(device)))
         want = np.argsort(d.view(np.uint32), kind="stable").astype(np.int32)
         assert_bitwise(got, want, f"depth order (n={n})")
+    # depths in [2, 8): the keys' top byte is the same for all (a pass that
+    # copies through), at the largest small-sort size and a partition multiple
+    for n in (1024 * 98, 1 << 18):
+        print(f"[gpu] depth order of {n} keys in [2, 8)", flush=True)
+        d = rng.uniform(2.0, 8.0, n).astype(np.float32)
+        d[rng.integers(0, n, 64)] = np.float32(5.0)
+        got = _np(crc.depth_order(n, torch.from_numpy(d).to(device)))
+        want = np.argsort(d.view(np.uint32), kind="stable").astype(np.int32)
+        assert_bitwise(got, want, f"depth order (n={n}, one top byte)")
 
 
 def test_rasterize_ordered_equals_rasterize(crc, device):
