@@ -42,7 +42,6 @@ namespace {
 constexpr int kAdcThreads = 256;
 // Elements per thread whose loads copy_rows issues together.
 constexpr int kAdcUnroll = 4;
-constexpr int kWidths[6] = {3, 4, 3, 1, 3, 45};  // mu, q, s, alpha, A, k_j
 
 // flag bits of a source Gaussian
 constexpr uint8_t kKeepOrig = 1, kKeepClone = 2, kKeepSplit = 4, kSplitSrc = 8, kCloneSrc = 16;
