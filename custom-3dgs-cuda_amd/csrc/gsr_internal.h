@@ -84,9 +84,9 @@ constexpr int kRadixBins = 256;
 size_t sort_control_bytes(uint64_t n);
 // Stable sort of keys[0..n) (n < 2^32) on all 32 bits, carrying vals: four
 // LSD passes of 8-bit digits, ping-ponging through (k1, v1) and ending in
-// (k0, v0).  Up to 2^18 keys each pass is one onesweep kernel over 1024-key
-// partitions; beyond, each pass is an upsweep / scan / downsweep triple with
-// no waits between work-groups.  A pass whose digit is the same for every key
+// (k0, v0).  Up to 2^20 keys each pass is one onesweep kernel over at most
+// 256 partitions (a fan-in of their digit counts); beyond, each pass is an
+// upsweep / scan / downsweep triple with no waits between work-groups.  A pass whose digit is the same for every key
 // copies through.  `control` must be zeroed on the stream first (zero_fill).
 // err (device int) is set when a look-back wait exceeds kSpinLimit.
 // hist_ready: the histogram block at the start of `control` was accumulated

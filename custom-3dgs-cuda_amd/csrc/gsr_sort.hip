@@ -9,20 +9,21 @@
 // l in wave w is element w*64*items + i*64 + l), so each wave load is one
 // contiguous 256 B access and ranks follow element order.
 //
-// Depth orders of at most 2^18 keys: onesweep_small_kernel, one kernel per
-// pass, 256 threads (one per digit) over 1024-key partitions; the grid (at
-// most 256 work-groups) is resident on the device at once, so the partition
-// is the work-group's index and every partition a work-group waits on
-// belongs to a running work-group.  Each partition publishes its digit
-// counts and sums those of every earlier partition (a fan-in of 1 KB per
-// partition, all loads in flight together): no partition waits on another's
-// prefix, so there is no look-back chain.  The keys and the four passes' digit
+// Depth orders of at most 2^20 keys: onesweep_small_kernel, one kernel per
+// pass, over at most 256 partitions (256 threads and 1024 keys per partition
+// up to 2^18 keys, 1024 threads and 4096 keys beyond); the partition is the
+// work-group's index, and a partition waits only on partitions dispatched
+// before it.  Each partition publishes its digit counts and sums those of
+// every earlier partition (a fan-in of 512 B per partition, the loads in
+// flight together): no partition waits on another's prefix, so there is no
+// look-back chain.  The keys and the four passes' digit
 // histograms come from the binning's count kernel (or depth_keys_hist_kernel)
 // in one pass.  These passes are latency chains (load, rank, look-back,
 // scatter).
 //
-// Larger depth orders: reduce-then-scan, three kernels per pass with no
-// waits between work-groups (rts_upsweep / rts_scan / rts_downsweep).  Their
+// Larger depth orders (beyond 2^20 keys): reduce-then-scan, three kernels per
+// pass with no waits between work-groups (rts_upsweep / rts_scan /
+// rts_downsweep).  Their
 // partitions are sized so that one round of two 1024-thread work-groups per
 // CU covers the keys; with all partitions resident at once, a decoupled
 // look-back would walk about half of its predecessors' status words (the
@@ -59,12 +60,21 @@ constexpr uint64_t kSmallSortMax = 1u << 18;
 constexpr int kSmallThreads = 256;
 constexpr int kSmallItems = 4;
 constexpr int kSmallPartition = kSmallThreads * kSmallItems;
+// Inputs up to kMediumSortMax keys take the same passes with 1024 threads
+// over 4096-key partitions (onesweep_small_kernel<1024>): again at most
+// kMaxSmallParts partitions.
+constexpr uint64_t kMediumSortMax = 1u << 20;
+constexpr int kMediumThreads = 1024;
+constexpr int kMediumPartition = kMediumThreads * kSmallItems;
+constexpr int kMaxSmallParts = 256;
+static_assert(kSmallSortMax / kSmallPartition == kMaxSmallParts &&
+                  kMediumSortMax / kMediumPartition == kMaxSmallParts,
+              "at most 256 partitions per fan-in pass");
 // Small passes' status: a partition's count of a digit (at most 1024) in a
 // 16-bit word with this flag once published, two digits per 32-bit store;
 // rows of the fan-in in flight per thread.
 constexpr uint32_t kSmallPublished = 1u << 15;
 constexpr uint64_t kSmallAll = 0x8000800080008000ull;
-constexpr int kSmallFan = 32;
 
 // The wide onesweep: 1024 threads, 8 items.
 constexpr int kWideWaves = kSortThreads / kWave;
@@ -82,6 +92,8 @@ struct SortCtl {
 
 inline uint64_t parts_for(uint64_t n) { return (n + kSortPartition - 1) / kSortPartition; }
 inline bool small_sort(uint64_t n) { return n <= kSmallSortMax; }
+// Fan-in passes (onesweep_small_kernel): up to kMediumSortMax keys.
+inline bool fanin_sort(uint64_t n) { return n <= kMediumSortMax; }
 // Items per thread of the large depth passes (1024 threads): one round of
 // 512 resident work-groups (two per CU) where the partitions allow it.
 inline int depth_items(uint64_t n) {
@@ -90,7 +102,9 @@ inline int depth_items(uint64_t n) {
 }
 inline uint64_t sort_parts(uint64_t n) {
     const uint64_t part =
-        small_sort(n) ? (uint64_t)kSmallPartition : (uint64_t)kSortThreads * depth_items(n);
+        small_sort(n)   ? (uint64_t)kSmallPartition
+        : fanin_sort(n) ? (uint64_t)kMediumPartition
+                        : (uint64_t)kSortThreads * depth_items(n);
     return (n + part - 1) / part;
 }
 inline size_t hist_bytes() { return align_up((size_t)kHistWords * 4, 256); }
@@ -306,17 +320,18 @@ __device__ __forceinline__ void lds_barrier() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// The sum over rows q0, q0 + 4, ... < part (at most kSmallFan of them) of the
-// 16-bit counts in the 64-bit status word col[q * 64] (four digits), once
+// The sum over rows q0, q0 + kStride, ... < part (at most kFan of them) of
+// the 16-bit counts in the 64-bit status word col[q * 64] (four digits), once
 // every row's four flags are set; rows not yet published are read again, all
 // together.  v holds the words as first read.
+template <int kFan, int kStride>
 __device__ __forceinline__ void small_fan_sum(const uint64_t* col, int q0, int part,
-                                              uint64_t (&v)[kSmallFan], uint32_t (&s)[4],
+                                              uint64_t (&v)[kFan], uint32_t (&s)[4],
                                               int* __restrict__ err) {
     for (uint32_t spins = 0;; ++spins) {
         bool all = true;
 #pragma unroll
-        for (int k = 0; k < kSmallFan; ++k) all &= (v[k] & kSmallAll) == kSmallAll;
+        for (int k = 0; k < kFan; ++k) all &= (v[k] & kSmallAll) == kSmallAll;
         if (all) break;
         if (spins >= kSpinLimit) {
             atomicOr(err, 1);
@@ -324,12 +339,12 @@ __device__ __forceinline__ void small_fan_sum(const uint64_t* col, int q0, int p
         }
         __builtin_amdgcn_s_sleep(1);
 #pragma unroll
-        for (int k = 0; k < kSmallFan; ++k)
+        for (int k = 0; k < kFan; ++k)
             if ((v[k] & kSmallAll) != kSmallAll)
-                v[k] = load_agent(col + (size_t)(q0 + 4 * k) * (kRadixBins / 4));
+                v[k] = load_agent(col + (size_t)(q0 + kStride * k) * (kRadixBins / 4));
     }
 #pragma unroll
-    for (int k = 0; k < kSmallFan; ++k) {
+    for (int k = 0; k < kFan; ++k) {
         const uint64_t c = v[k] & ~kSmallAll;
         s[0] += (uint32_t)c & 0xffffu;
         s[1] += (uint32_t)(c >> 16) & 0xffffu;
@@ -338,47 +353,55 @@ __device__ __forceinline__ void small_fan_sum(const uint64_t* col, int q0, int p
     }
 }
 
+template <int kFan, int kStride>
 __device__ __forceinline__ void small_fan_issue(const uint64_t* col, int q0, int part,
-                                                uint64_t (&v)[kSmallFan]) {
+                                                uint64_t (&v)[kFan]) {
 #pragma unroll
-    for (int k = 0; k < kSmallFan; ++k) {
-        const int q = q0 + 4 * k;
+    for (int k = 0; k < kFan; ++k) {
+        const int q = q0 + kStride * k;
         v[k] = q < part ? load_agent(col + (size_t)q * (kRadixBins / 4)) : kSmallAll;
     }
 }
 
-// One LSD pass over (key >> shift) & 0xff with 256 threads, one per digit
-// (inputs of at most 2^18 keys: at most 256 work-groups): ranks by ballot
-// match and per-wave counters; the partition's digit counts are published,
-// the digit starts scanned and the keys and values reordered in LDS; the
-// digit offsets are the sums of the earlier partitions' published counts (a
-// fan-in, no chain); then keys and values are written in digit runs.
-__global__ __launch_bounds__(kSmallThreads) void onesweep_small_kernel(
+// One LSD pass over (key >> shift) & 0xff, kThreads threads over partitions
+// of 4 kThreads keys (at most 256 of them: inputs of at most 2^18 keys with
+// 256 threads, 2^20 with 1024): ranks by ballot match and per-wave counters;
+// the partition's digit counts are published, the digit starts scanned and
+// the keys and values reordered in LDS; the digit offsets are the sums of the
+// earlier partitions' published counts (a fan-in, no chain); then keys and
+// values are written in digit runs.  The first 256 threads are the digit
+// threads (digit d = thread d).
+template <int kThreads>
+__global__ __launch_bounds__(kThreads) void onesweep_small_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n, int shift,
     const uint32_t* __restrict__ hist, uint16_t* __restrict__ status, int* __restrict__ err) {
     constexpr int kItems = kSmallItems;
-    constexpr int kPart = kSmallPartition;
-    constexpr int kWaves = kSmallThreads / kWave;
-    static_assert(kSmallThreads == kRadixBins && kWaves == 4, "one thread per digit");
+    constexpr int kPart = kThreads * kItems;
+    constexpr int kWaves = kThreads / kWave;
+    constexpr int kDigitWaves = kRadixBins / kWave;
+    // rows of the fan-in per wave and batch: at most 32 loads in flight
+    constexpr int kFan = std::min(32, (kMaxSmallParts + kWaves - 1) / kWaves);
+    static_assert(kThreads >= kRadixBins && kThreads % kRadixBins == 0, "digit threads");
     __shared__ uint32_t s_keys[kPart];
     __shared__ uint32_t s_vals[kPart];
     __shared__ uint32_t s_wcnt[kWaves][kRadixBins];
     __shared__ uint32_t s_dstart[kRadixBins];
     __shared__ uint32_t s_gbase[kRadixBins];
-    __shared__ uint32_t s_scan[kWaves];
-    __shared__ uint32_t s_hscan[kWaves];
+    __shared__ uint32_t s_scan[kDigitWaves];
+    __shared__ uint32_t s_hscan[kDigitWaves];
     __shared__ uint32_t s_fan[kWaves][kRadixBins];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // The grid (at most 256 work-groups of 256 threads) is resident on the
-    // device at once, whatever order the work-groups start in: a partition
-    // waits only on partitions whose work-groups are running, so the
-    // partition is the work-group's index (no claim atomic).
+    // A partition waits only on the partitions before it, whose work-groups
+    // were dispatched before its own and wait on nothing before publishing,
+    // so the partition is the work-group's index (no claim atomic).
     const int part = (int)blockIdx.x;  // scalar
     const uint64_t base = (uint64_t)part * kPart;
     const int nvalid = (int)min((uint64_t)kPart, n - base);
-    const uint32_t h = hist[tid];
+    const bool digit_thread = tid < kRadixBins;
+    const int d = tid & (kRadixBins - 1);
+    const uint32_t h = hist[d];
     // the keys and values are loaded before the digit check, so its load is
     // in flight with them
     uint32_t key[kItems], val[kItems], rank[kItems];
@@ -392,8 +415,8 @@ __global__ __launch_bounds__(kSmallThreads) void onesweep_small_kernel(
         const int e = wave * (kItems * 64) + i * 64 + lane;
         val[i] = e < nvalid ? vin[base + e] : 0u;
     }
-    for (int j = tid; j < kWaves * kRadixBins; j += kSmallThreads) (&s_wcnt[0][0])[j] = 0;
-    if (__syncthreads_or((uint64_t)h == n)) {
+    for (int j = tid; j < kWaves * kRadixBins; j += kThreads) (&s_wcnt[0][0])[j] = 0;
+    if (__syncthreads_or(digit_thread && (uint64_t)h == n)) {
         // every key has the same digit: the stable pass is the identity
 #pragma unroll
         for (int i = 0; i < kItems; ++i) {
@@ -420,41 +443,46 @@ __global__ __launch_bounds__(kSmallThreads) void onesweep_small_kernel(
         }
     }
     lds_barrier();
-    // one thread per digit: the partition's count (published: digits d and
-    // d + 1 in one 32-bit word, from the even thread), wave prefixes and the
-    // digit's start in the partition
-    const int d = tid;
+    // the digit threads: the partition's count (published: digits d and d + 1
+    // in one 32-bit word, from the even thread), wave prefixes and the digit's
+    // start in the partition
     uint32_t total = 0;
-    for (int w = 0; w < kWaves; ++w) {
-        const uint32_t c = s_wcnt[w][d];
-        s_wcnt[w][d] = total;
-        total += c;
+    if (digit_thread) {
+        for (int w = 0; w < kWaves; ++w) {
+            const uint32_t c = s_wcnt[w][d];
+            s_wcnt[w][d] = total;
+            total += c;
+        }
     }
-    {
+    uint32_t inc = 0, hinc = 0;
+    if (wave < kDigitWaves) {  // whole waves: the shuffles and scans see only digit threads
         const uint32_t other = __shfl_xor(total, 1, kWave);
         if ((d & 1) == 0)
             __hip_atomic_store(
                 reinterpret_cast<uint32_t*>(status + (size_t)part * kRadixBins + d),
                 (kSmallPublished | total) | ((kSmallPublished | other) << 16), __ATOMIC_RELAXED,
                 __HIP_MEMORY_SCOPE_AGENT);
+        inc = wave_inclusive_scan(total);
+        hinc = wave_inclusive_scan(h);
+        if (lane == 63) {
+            s_scan[wave] = inc;
+            s_hscan[wave] = hinc;
+        }
     }
     const uint64_t* col = reinterpret_cast<const uint64_t*>(status) + lane;
-    uint64_t fan[kSmallFan];
-    const uint32_t inc = wave_inclusive_scan(total);
-    const uint32_t hinc = wave_inclusive_scan(h);
-    if (lane == 63) {
-        s_scan[wave] = inc;
-        s_hscan[wave] = hinc;
-    }
+    uint64_t fan[kFan];
     lds_barrier();
-    uint32_t wpre = 0, hpre = 0;
-    for (int w = 0; w < wave; ++w) {
-        wpre += s_scan[w];
-        hpre += s_hscan[w];
+    uint32_t dstart = 0, hexcl = 0;
+    if (digit_thread) {
+        uint32_t wpre = 0, hpre = 0;
+        for (int w = 0; w < wave; ++w) {
+            wpre += s_scan[w];
+            hpre += s_hscan[w];
+        }
+        dstart = wpre + inc - total;
+        hexcl = hpre + hinc - h;
+        s_dstart[d] = dstart;
     }
-    const uint32_t dstart = wpre + inc - total;
-    const uint32_t hexcl = hpre + hinc - h;
-    s_dstart[d] = dstart;
     lds_barrier();
 #pragma unroll
     for (int i = 0; i < kItems; ++i) {
@@ -467,17 +495,17 @@ __global__ __launch_bounds__(kSmallThreads) void onesweep_small_kernel(
         }
     }
     // Fan-in: lane l of wave w sums digits 4l .. 4l + 3 (one 64-bit status
-    // word) over rows w, w + 4, ..., kSmallFan rows' loads in flight at once.
+    // word) over rows w, w + kWaves, ..., kFan rows' loads in flight at once.
     // Issued here, after the reorder, rather than right after publishing:
     // fewer rows are then still unpublished and read twice (the pass at 100k
     // keys is about 1 us faster per pass this way).
-    small_fan_issue(col, wave, part, fan);
+    small_fan_issue<kFan, kWaves>(col, wave, part, fan);
     {
         uint32_t sum[4] = {0u, 0u, 0u, 0u};
-        small_fan_sum(col, wave, part, fan, sum, err);
-        for (int q0 = wave + kWaves * kSmallFan; q0 < part; q0 += kWaves * kSmallFan) {
-            small_fan_issue(col, q0, part, fan);
-            small_fan_sum(col, q0, part, fan, sum, err);
+        small_fan_sum<kFan, kWaves>(col, wave, part, fan, sum, err);
+        for (int q0 = wave + kWaves * kFan; q0 < part; q0 += kWaves * kFan) {
+            small_fan_issue<kFan, kWaves>(col, q0, part, fan);
+            small_fan_sum<kFan, kWaves>(col, q0, part, fan, sum, err);
         }
         s_fan[wave][4 * lane] = sum[0];
         s_fan[wave][4 * lane + 1] = sum[1];
@@ -485,13 +513,17 @@ __global__ __launch_bounds__(kSmallThreads) void onesweep_small_kernel(
         s_fan[wave][4 * lane + 3] = sum[3];
     }
     __syncthreads();
-    const uint32_t excl = s_fan[0][d] + s_fan[1][d] + s_fan[2][d] + s_fan[3][d];
-    // element j of digit d's run goes to hexcl + excl + (j - dstart) (32 bits)
-    s_gbase[d] = hexcl + excl - dstart;
+    if (digit_thread) {
+        uint32_t excl = 0;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) excl += s_fan[w][d];
+        // element j of digit d's run goes to hexcl + excl + (j - dstart) (32 bits)
+        s_gbase[d] = hexcl + excl - dstart;
+    }
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < kItems; ++k) {
-        const int j = tid + k * kSmallThreads;
+        const int j = tid + k * kThreads;
         if (j < nvalid) {
             const uint32_t kk = s_keys[j];
             const uint32_t o = s_gbase[(kk >> shift) & 0xffu] + (uint32_t)j;
@@ -1069,7 +1101,7 @@ size_t sort_control_bytes(uint64_t n) {
     // per partition and pass: 256 16-bit status words (small inputs), or 256
     // digit counts and 256 offsets (reduce-then-scan)
     return hist_bytes() + align_up((size_t)kHistMaxPasses * 64, 256) +
-           (size_t)kHistMaxPasses * sort_parts(n) * kRadixBins * (small_sort(n) ? 2 : 8);
+           (size_t)kHistMaxPasses * sort_parts(n) * kRadixBins * (fanin_sort(n) ? 2 : 8);
 }
 
 hipError_t launch_depth_keys_hist(uint64_t n, const float* depth, uint32_t* keys, uint32_t* vals,
@@ -1099,14 +1131,20 @@ hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t*
     }
     uint32_t *ki = k0, *vi = v0, *ko = k1, *vo = v1;
     const uint32_t np = (uint32_t)parts;
-    const int items = small_sort(n) ? kSmallItems : depth_items(n);
+    const int items = fanin_sort(n) ? kSmallItems : depth_items(n);
     for (int p = 0; p < kHistMaxPasses; ++p) {
         const uint32_t* hp = c.hist + p * kRadixBins;
         uint64_t* stat = c.status + (size_t)p * parts * kRadixBins;
-        if (small_sort(n)) {
+        if (fanin_sort(n)) {
             uint16_t* stat16 = reinterpret_cast<uint16_t*>(c.status) + (size_t)p * parts * kRadixBins;
-            hipLaunchKernelGGL(onesweep_small_kernel, dim3(np), dim3(kSmallThreads), 0, st, ki, vi,
-                               ko, vo, n, 8 * p, hp, stat16, err);
+            if (small_sort(n))
+                hipLaunchKernelGGL(onesweep_small_kernel<kSmallThreads>, dim3(np),
+                                   dim3(kSmallThreads), 0, st, ki, vi, ko, vo, n, 8 * p, hp,
+                                   stat16, err);
+            else
+                hipLaunchKernelGGL(onesweep_small_kernel<kMediumThreads>, dim3(np),
+                                   dim3(kMediumThreads), 0, st, ki, vi, ko, vo, n, 8 * p, hp,
+                                   stat16, err);
         } else {
             // the status words of the pass hold the partitions' digit counts,
             // then their offsets

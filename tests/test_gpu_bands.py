@@ -56,11 +56,12 @@ def test_each_band_matches_the_oracle(crc, device):
 def test_depth_order_is_the_stable_sort_of_the_depth_bits(crc, device):
     """depth_order against numpy's stable argsort of the depths' float bits as
     unsigned: ties (repeated depths), -0.0 / 0.0, negative depths, infinities
-    and NaNs of both signs, at a 1024-key partition boundary and beyond 2^18
-    keys (the depth sort's two partition sizes); and keys that all share their
-    top byte (the pass over it copies through) up to 2^18 keys."""
+    and NaNs of both signs, at a 1024-key partition boundary, beyond 2^18 keys,
+    at 2^20 and one beyond (the depth sort's three pass kinds); and keys that
+    all share their top byte (the pass over it copies through) up to 2^18
+    keys."""
     rng = np.random.default_rng(5)
-    for n in (1, 1000, 1024 * 37 + 5, 300_000):
+    for n in (1, 1000, 1024 * 37 + 5, 300_000, 1 << 20, (1 << 20) + 1):
         print(f"[gpu] depth order of {n} keys", flush=True)
         d = np.round(rng.uniform(-2.0, 60.0, n) * 8.0).astype(np.float32) / np.float32(8.0)
         special = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, -np.nan, 1e-30, -1e30],
