@@ -422,9 +422,12 @@ __global__ __launch_bounds__(kThreads) void blend_records_kernel(
 // The backward's per-Gaussian pass in one kernel: blend records, tile
 // rectangles and counts (as blend_records_kernel forms them), and the
 // Gaussian-major slot offsets goff[i] = counts[0] + ... + counts[i - 1] (the
-// total to *total) through a decoupled look-back over partitions of
-// kSlotItems x 256 Gaussians, claimed in launch order.  The records are
-// formed while the first wave looks back.
+// total to *total) over partitions of kSlotItems x 256 Gaussians (at most
+// 512: up to 2^18 Gaussians).  The partition is the work-group's index: a
+// partition waits only on the ones before it, which were dispatched before it
+// and publish their counts before they wait on anything.  Its offset is a
+// fan-in of their published counts (wave_fanin), during which the other
+// waves form the records.
 constexpr int kSlotItems = 2;
 constexpr int kSlotPartition = kThreads * kSlotItems;
 
@@ -433,14 +436,11 @@ __global__ __launch_bounds__(kThreads) void records_slots_kernel(
     const float* __restrict__ colors, const float* __restrict__ alpha,
     BlendRec* __restrict__ recs, int H, int W, uint32_t* __restrict__ counts,
     uint2* __restrict__ rects, uint32_t* __restrict__ goff, uint64_t* __restrict__ total,
-    uint64_t* __restrict__ status, uint32_t* __restrict__ counter, int* __restrict__ err) {
-    __shared__ uint32_t s_part;
+    uint64_t* __restrict__ status, int* __restrict__ err) {
     __shared__ uint32_t s_wsum[kThreads / kWave];
     __shared__ uint64_t s_base;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_part = atomicAdd(counter, 1u);
-    __syncthreads();
-    const uint64_t part = s_part;
+    const uint64_t part = blockIdx.x;
     const int64_t first = (int64_t)part * kSlotPartition + (int64_t)tid * kSlotItems;
     // every input loaded up front, all loads in flight together
     float in[kSlotItems][9];
@@ -482,7 +482,7 @@ __global__ __launch_bounds__(kThreads) void records_slots_kernel(
         btot += s_wsum[w];
     }
     if (wave == 0) {
-        const uint64_t excl = wave_lookback(status, part, (uint64_t)btot, err);
+        const uint64_t excl = wave_fanin(status, (uint32_t)part, (uint64_t)btot, err);
         if (lane == 0) {
             s_base = excl;
             if (part * kSlotPartition + kSlotPartition >= (uint64_t)n) *total = excl + btot;
@@ -606,11 +606,12 @@ hipError_t launch_records_slots(int n, const float* mean2d, const float* cov2d,
         return launch_scan_counts(n, nullptr, counts, goff, total, control, err, st);
     }
     const unsigned parts = (unsigned)(((size_t)n + kSlotPartition - 1) / kSlotPartition);
-    uint32_t* counter = static_cast<uint32_t*>(control);
+    static_assert(kRecordsSlotsFusedMax / kSlotPartition <= 64 * kFanPerLane,
+                  "the fan-in covers every partition");
     uint64_t* status = reinterpret_cast<uint64_t*>(static_cast<char*>(control) + 256);
     hipLaunchKernelGGL(records_slots_kernel, dim3(parts), dim3(kThreads), 0, st, n, mean2d, cov2d,
                        colors, alpha, static_cast<BlendRec*>(recs), H, W, counts, rects, goff,
-                       total, status, counter, err);
+                       total, status, err);
     return hipGetLastError();
 }
 

@@ -82,6 +82,45 @@ __device__ inline uint64_t wave_lookback(uint64_t* status, uint64_t part, uint64
     return excl;
 }
 
+// Fan-in over 64-bit status words (flag in the top two bits, value below),
+// run by one whole wave: publishes agg as partition part's aggregate and
+// returns, in every lane, the sum of the aggregates of partitions
+// 0 .. part - 1 (lane l reads partitions l, l + 64, ..., all its loads in
+// flight together), waiting only for those not yet published.  No partition
+// publishes a prefix, so no partition waits on another's wait.  For at most
+// 64 kFanPerLane partitions.  A wait beyond kSpinLimit sets bit 0 of *err and
+// ends it (the sum is then incomplete), so no wave can hang.
+constexpr int kFanPerLane = 8;
+__device__ inline uint64_t wave_fanin(uint64_t* status, uint32_t part, uint64_t agg, int* err) {
+    const int lane = lane_id();
+    if (lane == 0) store_agent(status + part, kFlagAggregate | agg);
+    uint64_t v[kFanPerLane];
+#pragma unroll
+    for (int k = 0; k < kFanPerLane; ++k) {
+        const uint32_t q = (uint32_t)lane + 64u * (uint32_t)k;
+        v[k] = q < part ? load_agent(status + q) : kFlagAggregate;
+    }
+    for (uint32_t spins = 0;; ++spins) {
+        bool all = true;
+#pragma unroll
+        for (int k = 0; k < kFanPerLane; ++k) all &= (v[k] & ~kValueMask) != 0;
+        if (all) break;
+        if (spins >= kSpinLimit) {
+            atomicOr(err, 1);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < kFanPerLane; ++k)
+            if ((v[k] & ~kValueMask) == 0)
+                v[k] = load_agent(status + (uint32_t)lane + 64u * (uint32_t)k);
+    }
+    uint64_t sum = 0;
+#pragma unroll
+    for (int k = 0; k < kFanPerLane; ++k) sum += v[k] & kValueMask;
+    return wave_sum_u64(sum);
+}
+
 // block_start[b] / seg_start[b] (nb + 1 entries each): exclusive prefixes of
 // the block histogram and of its 64-entry segment counts.  One work-group of
 // kT threads; s_w and s_v hold kT / 64 words each.
