@@ -1027,7 +1027,7 @@ rts_downsweep_kernel(const uint32_t* __restrict__ kin, const uint32_t* __restric
     }
 }
 
-// ---- exclusive scan of counts[perm[r]] (decoupled look-back) -------------
+// ---- exclusive scan of counts[perm[r]] (fan-in, or decoupled look-back) -----
 constexpr int kScanThreads = 256;
 constexpr int kScanItems = 16;
 constexpr int kScanPartition = kScanThreads * kScanItems;
@@ -1035,14 +1035,18 @@ constexpr int kScanPartition = kScanThreads * kScanItems;
 __global__ __launch_bounds__(kScanThreads) void scan_counts_kernel(
     int n, const uint32_t* __restrict__ perm, const uint32_t* __restrict__ counts,
     uint32_t* __restrict__ offsets, uint64_t* __restrict__ total, uint64_t* __restrict__ status,
-    uint32_t* __restrict__ counter, int* __restrict__ err) {
+    uint32_t* __restrict__ counter, int* __restrict__ err, int fanin) {
     __shared__ uint32_t s_part;
     __shared__ uint32_t s_wsum[4];
     __shared__ uint64_t s_base;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    if (tid == 0) s_part = atomicAdd(counter, 1u);
+    // fanin (at most 64 kFanPerLane partitions): the partition is the
+    // work-group's index and its prefix a fan-in of the earlier partitions'
+    // published counts; beyond, partitions claimed in launch order and a
+    // look-back
+    if (!fanin && tid == 0) s_part = atomicAdd(counter, 1u);
     __syncthreads();
-    const uint64_t part = s_part;
+    const uint64_t part = fanin ? (uint64_t)blockIdx.x : (uint64_t)s_part;
     const int64_t first = (int64_t)part * kScanPartition + (int64_t)tid * kScanItems;
     uint32_t c[kScanItems];
     uint32_t sum = 0;
@@ -1061,9 +1065,10 @@ __global__ __launch_bounds__(kScanThreads) void scan_counts_kernel(
         if (w < wave) wpre += s_wsum[w];
         btot += s_wsum[w];
     }
-    // look-back by the first wave, 64 predecessors per step
+    // the prefix by the first wave
     if (wave == 0) {
-        const uint64_t excl = wave_lookback(status, part, (uint64_t)btot, err);
+        const uint64_t excl = fanin ? wave_fanin(status, (uint32_t)part, (uint64_t)btot, err)
+                                    : wave_lookback(status, part, (uint64_t)btot, err);
         if (lane == 0) {
             s_base = excl;
             const uint64_t pbeg = part * kScanPartition;
@@ -1241,8 +1246,9 @@ hipError_t launch_scan_counts(int n, const uint32_t* perm, const uint32_t* count
     const unsigned parts = (unsigned)(((size_t)n + kScanPartition - 1) / kScanPartition);
     uint32_t* counter = static_cast<uint32_t*>(control);
     uint64_t* status = reinterpret_cast<uint64_t*>(static_cast<char*>(control) + 256);
+    const int fanin = parts <= 64u * (unsigned)kFanPerLane ? 1 : 0;
     hipLaunchKernelGGL(scan_counts_kernel, dim3(parts), dim3(kScanThreads), 0, st, n, perm, counts,
-                       offsets, total, status, counter, err);
+                       offsets, total, status, counter, err, fanin);
     return hipGetLastError();
 }
 
