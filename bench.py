@@ -118,7 +118,7 @@ def _profile_json(kind: str, workload: str):
 # Sources whose change can change any stage's kernels: the shared device headers
 # and the host code that sizes the workspaces and sets the launch order.
 SHARED_SOURCES = ("gsr_common.h", "gsr_math.h", "gsr_gaussian.h", "gsr_group.h",
-                  "gsr_internal.h", "gsr_capi.cpp")
+                  "gsr_internal.h", "gsr_schedule.h", "gsr_capi.cpp")
 
 
 def library_sources() -> dict:

@@ -18,6 +18,7 @@
 #include "gsr_internal.h"
 #include "gsr_common.h"
 #include "gsr_group.h"
+#include "gsr_schedule.h"
 
 namespace gsr {
 
@@ -427,7 +428,9 @@ __global__ __launch_bounds__(kThreads) void blend_records_kernel(
 // partition waits only on the ones before it, which were dispatched before it
 // and publish their counts before they wait on anything.  Its offset is a
 // fan-in of their published counts (wave_fanin), during which the other
-// waves form the records.
+// waves form the records.  Work-groups from `parts` on compute the backward
+// blend's per-tile work estimate instead (tile_work_bwd_wave, one wave per
+// tile): work independent of the records, in the same launch.
 constexpr int kSlotItems = 2;
 constexpr int kSlotPartition = kThreads * kSlotItems;
 
@@ -436,10 +439,15 @@ __global__ __launch_bounds__(kThreads) void records_slots_kernel(
     const float* __restrict__ colors, const float* __restrict__ alpha,
     BlendRec* __restrict__ recs, int H, int W, uint32_t* __restrict__ counts,
     uint2* __restrict__ rects, uint32_t* __restrict__ goff, uint64_t* __restrict__ total,
-    uint64_t* __restrict__ status, int* __restrict__ err) {
+    uint64_t* __restrict__ status, int* __restrict__ err, uint32_t parts, BwdWork bw) {
     __shared__ uint32_t s_wsum[kThreads / kWave];
     __shared__ uint64_t s_base;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (blockIdx.x >= parts) {  // whole work-groups: no barriers in this branch
+        const int tile = (int)(blockIdx.x - parts) * kWorkTilesPerBlock + wave;
+        if (tile < bw.T) tile_work_bwd_wave(bw, tile);
+        return;
+    }
     const uint64_t part = blockIdx.x;
     const int64_t first = (int64_t)part * kSlotPartition + (int64_t)tid * kSlotItems;
     // every input loaded up front, all loads in flight together
@@ -595,7 +603,10 @@ size_t records_slots_control_bytes(int n) {
 hipError_t launch_records_slots(int n, const float* mean2d, const float* cov2d,
                                 const float* colors, const float* alpha, void* recs, int H, int W,
                                 uint32_t* counts, uint2* rects, uint32_t* goff, uint64_t* total,
-                                void* control, int* err, hipStream_t st) {
+                                void* control, int* err, hipStream_t st, const int32_t* ranges,
+                                uint64_t num_pairs, const int32_t* ncontrib, uint32_t* work,
+                                bool* work_done) {
+    if (work_done) *work_done = false;
     if (n <= 0) return hipSuccess;
     if (n > kRecordsSlotsFusedMax) {
         hipLaunchKernelGGL(blend_records_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, st, n,
@@ -609,9 +620,17 @@ hipError_t launch_records_slots(int n, const float* mean2d, const float* cov2d,
     static_assert(kRecordsSlotsFusedMax / kSlotPartition <= 64 * kFanPerLane,
                   "the fan-in covers every partition");
     uint64_t* status = reinterpret_cast<uint64_t*>(static_cast<char*>(control) + 256);
-    hipLaunchKernelGGL(records_slots_kernel, dim3(parts), dim3(kThreads), 0, st, n, mean2d, cov2d,
-                       colors, alpha, static_cast<BlendRec*>(recs), H, W, counts, rects, goff,
-                       total, status, err);
+    BwdWork bw{};
+    unsigned work_groups = 0;
+    if (work && ranges && ncontrib) {
+        static_assert(kThreads == kWorkTilesPerBlock * kWave, "one wave per tile");
+        bw = make_bwd_work(H, W, ranges, num_pairs, ncontrib, work);
+        work_groups = (unsigned)((bw.T + kWorkTilesPerBlock - 1) / kWorkTilesPerBlock);
+    }
+    hipLaunchKernelGGL(records_slots_kernel, dim3(parts + work_groups), dim3(kThreads), 0, st, n,
+                       mean2d, cov2d, colors, alpha, static_cast<BlendRec*>(recs), H, W, counts,
+                       rects, goff, total, status, err, parts, bw);
+    if (work_done) *work_done = work_groups > 0;
     return hipGetLastError();
 }
 

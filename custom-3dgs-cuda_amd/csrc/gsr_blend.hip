@@ -42,6 +42,7 @@
 
 #include "gsr_internal.h"
 #include "gsr_common.h"
+#include "gsr_schedule.h"
 
 namespace gsr {
 
@@ -74,13 +75,6 @@ __device__ __forceinline__ Pixels<kPix> pixels_of(int tile, int tiles_x, int W, 
         p.in[k] = p.px < W && p.py[k] < H;
     }
     return p;
-}
-
-__device__ __forceinline__ void clamp_range(int2 rg, uint64_t m, int& start, int& end) {
-    const int64_t s = min<int64_t>(max<int64_t>(rg.x, 0), (int64_t)m);
-    const int64_t e = min<int64_t>(max<int64_t>(rg.y, s), (int64_t)m);
-    start = (int)s;
-    end = (int)e;
 }
 
 // Minimum over the pixel rectangle [x0, x1] x [y0, y1] of the quadratic form
@@ -869,37 +863,13 @@ __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
 // The order changes no result: every tile's pixels are computed by one
 // work-group on their own. ----
 
-// Backward work of a tile: its list entries up to the largest n_contrib.  One
-// wave per tile, lane l reading row l / 4, columns 4 (l % 4) .. + 3 (one
-// 16-byte load when vec4: the image rows are 16-byte aligned).
-constexpr int kWorkTilesPerBlock = 4;
-
-__global__ __launch_bounds__(kWorkTilesPerBlock * kWave) void tile_work_bwd_kernel(
-    int T, int H, int W, int tiles_x, uint64_t m, const int2* __restrict__ ranges,
-    const int32_t* __restrict__ ncontrib, uint32_t* __restrict__ work, int vec4) {
-    const int lane = threadIdx.x & 63;
+// Backward work of a tile: its list entries up to the largest n_contrib
+// (tile_work_bwd_wave, one wave per tile).  Run here, or by the backward
+// records kernel in work-groups of its own launch.
+__global__ __launch_bounds__(kWorkTilesPerBlock * kWave) void tile_work_bwd_kernel(BwdWork b) {
     const int tile = blockIdx.x * kWorkTilesPerBlock + (int)(threadIdx.x >> 6);
-    if (tile >= T) return;  // whole waves; no barriers below
-    const int py = (tile / tiles_x) * kTileSize + (lane >> 2);
-    const int px = (tile % tiles_x) * kTileSize + 4 * (lane & 3);
-    int c = 0;
-    if (py < H) {
-        const int32_t* row = ncontrib + (size_t)py * W;
-        if (vec4 && px + 3 < W) {
-            const int4 v = *reinterpret_cast<const int4*>(row + px);
-            c = max(max(v.x, v.y), max(v.z, v.w));
-        } else {
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                if (px + k < W) c = max(c, row[px + k]);
-        }
-    }
-    const uint32_t mx = wave_max_u32((uint32_t)max(c, 0));
-    if (lane == 0) {
-        int start, end;
-        clamp_range(ranges[tile], m, start, end);
-        work[tile] = min(mx, (uint32_t)(end - start));
-    }
+    if (tile >= b.T) return;  // whole waves
+    tile_work_bwd_wave(b, tile);
 }
 
 // Forward work of a tile: the list entries it takes until two sample pixels
@@ -1188,16 +1158,16 @@ hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const in
 
 hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num_pairs,
                                const int32_t* ncontrib, uint32_t* work, uint32_t* order,
-                               hipStream_t st) {
+                               hipStream_t st, bool work_ready) {
     const int tiles_x = (W + kTileSize - 1) / kTileSize;
     const unsigned tiles = (unsigned)(tiles_x * ((H + kTileSize - 1) / kTileSize));
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
-    const int vec4 = (W % 4 == 0) && ((reinterpret_cast<uintptr_t>(ncontrib) & 15) == 0);
-    hipLaunchKernelGGL(tile_work_bwd_kernel,
-                       dim3((tiles + kWorkTilesPerBlock - 1) / kWorkTilesPerBlock),
-                       dim3(kWorkTilesPerBlock * kWave), 0, st, (int)tiles, H, W, tiles_x,
-                       num_pairs, r, ncontrib, work, vec4);
+    if (!work_ready)
+        hipLaunchKernelGGL(tile_work_bwd_kernel,
+                           dim3((tiles + kWorkTilesPerBlock - 1) / kWorkTilesPerBlock),
+                           dim3(kWorkTilesPerBlock * kWave), 0, st,
+                           make_bwd_work(H, W, ranges, num_pairs, ncontrib, work));
     hipLaunchKernelGGL(tile_order_kernel, dim3(1), dim3(kOrderThreads), 0, st, (int)tiles,
                        num_pairs, r, work, order,
                        (bwd_split() && bwd_wide(tiles, num_pairs)) ? kSplitMax : 0,

@@ -808,11 +808,16 @@ int rasterize_backward(int n, int height, int width, const float* grad_img,
     uint32_t* counts = at<uint32_t>(ws, L.counts);
     uint2* rects = at<uint2>(ws, L.rects);
     uint32_t* goff = at<uint32_t>(ws, L.goff);
+    // the records kernel also computes the schedule's per-tile work when it can
+    // (independent work in one launch)
+    bool work_ready = false;
     {
         StageTimer timer("bwd_records", st);
         GSR_HIP(gsr::launch_records_slots(n, mean2d, cov2d, colors, alpha, at<void>(ws, L.recs),
                                           height, width, counts, rects, goff, &misc->total,
-                                          at<void>(ws, L.scanctl), dg.status, st),
+                                          at<void>(ws, L.scanctl), dg.status, st, tile_ranges,
+                                          (uint64_t)num_pairs, n_contrib, at<uint32_t>(ws, L.work),
+                                          &work_ready),
                 "backward: records and slot layout");
     }
     gsr::GradSlots gs;
@@ -826,7 +831,7 @@ int rasterize_backward(int n, int height, int width, const float* grad_img,
     {
         StageTimer timer("bwd_schedule", st);
         GSR_HIP(gsr::launch_bwd_schedule(height, width, tile_ranges, (uint64_t)num_pairs, n_contrib,
-                                         at<uint32_t>(ws, L.work), order, st),
+                                         at<uint32_t>(ws, L.work), order, st, work_ready),
                 "backward: schedule");
     }
     {

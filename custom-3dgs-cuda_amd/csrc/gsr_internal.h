@@ -211,12 +211,19 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
 
 // The backward's per-Gaussian pass: blend records, tile rectangles and counts,
 // and the slot offsets goff (exclusive scan of the counts in Gaussian order,
-// total to *total).  control: records_slots_control_bytes(n), zeroed.
+// total to *total).  control: records_slots_control_bytes(n), zeroed.  With
+// `work` (up to 2^18 Gaussians; returns true when taken) the same launch also
+// computes the backward's per-tile work estimate from the tile ranges (num_pairs
+// entries) and n_contrib into work (launch_bwd_schedule then runs with
+// work_ready).
 size_t records_slots_control_bytes(int n);
 hipError_t launch_records_slots(int n, const float* mean2d, const float* cov2d,
                                 const float* colors, const float* alpha, void* recs, int H, int W,
                                 uint32_t* counts, uint2* rects, uint32_t* goff, uint64_t* total,
-                                void* control, int* err, hipStream_t st);
+                                void* control, int* err, hipStream_t st,
+                                const int32_t* ranges = nullptr, uint64_t num_pairs = 0,
+                                const int32_t* ncontrib = nullptr, uint32_t* work = nullptr,
+                                bool* work_done = nullptr);
 
 // Exclusive scan of counts[perm[r]] over depth rank r -> offsets[r] (perm null:
 // the identity); the total (u64) is written to *total.
@@ -258,10 +265,11 @@ hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const in
                             uint64_t m, const void* recs, float* img, float* finalT,
                             int32_t* ncontrib, const uint32_t* order, hipStream_t st);
 
-// Backward schedule: entries up to each tile's largest n_contrib, then the order.
+// Backward schedule: entries up to each tile's largest n_contrib (unless
+// work_ready: computed already), then the order.
 hipError_t launch_bwd_schedule(int H, int W, const int32_t* ranges, uint64_t num_pairs,
                                const int32_t* ncontrib, uint32_t* work, uint32_t* order,
-                               hipStream_t st);
+                               hipStream_t st, bool work_ready = false);
 
 // Gradient slots: the (Gaussian, tile) pairs in Gaussian-major order, pair
 // (g, t) at goff[g] + its index in g's tile rectangle (row-major); the backward
