@@ -367,32 +367,6 @@ __global__ __launch_bounds__(kThreads) void full_keys_kernel(uint64_t m,
     keys[i] = ((uint64_t)(tiles[i] >> shift) << 32) | (uint64_t)dbits;
 }
 
-// Threshold on q = d^T conic d above which o * exp(-q/2) < 1/255, so alpha
-// stays below 1/255 (rasterize.cu:256): 2 ln(255 o), computed in double and
-// raised by 1e-5 relative + 1e-4 to cover exp_gs (<= 1 ulp), the o * G
-// product and the rounding of this threshold.  NaN for a NaN opacity, which
-// then disables every cull.
-__device__ __forceinline__ float alpha_q_threshold(float o) {
-    const double t = 2.0 * log(255.0 * (double)o);
-    return (float)(t + 1e-5 * fabs(t) + 1e-4);
-}
-
-// Conic = cov^-1 with 1/det first (rasterize.cu:224-232), packed with mean,
-// opacity and colour so the blend loads one 48 B record per list entry.
-// With counts != null (the backward), also each Gaussian's tile rectangle and
-// count, exactly as bin_count_kernel forms them.
-__device__ __forceinline__ BlendRec blend_record(float mx, float my, float a, float b, float c,
-                                                 float opacity, float r, float g, float bl) {
-    const float det = a * c - b * b;
-    const float det_inv = (det > 0.0f) ? (1.0f / det) : 0.0f;
-    const float cx = c * det_inv, cy = -b * det_inv, cz = a * det_inv;
-    BlendRec rec;
-    rec.a = make_float4(mx, my, -0.5f * cx, -cy);
-    rec.b = make_float4(-0.5f * cz, opacity, r, g);
-    rec.c = make_float4(bl, -0.5f * cy, alpha_q_threshold(opacity), 0.0f);
-    return rec;
-}
-
 __device__ __forceinline__ uint32_t rect_count(const TileRect& tr) {
     return tr.ok ? (uint32_t)(max(0, tr.x1 - tr.x0) * max(0, tr.y1 - tr.y0)) : 0u;
 }

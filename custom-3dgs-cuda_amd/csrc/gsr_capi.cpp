@@ -626,7 +626,8 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
         GSR_REQUIRE(sort_ws && sorted_ids, "null pointer");
         if (sort_ws_bytes < SL.end) return fail(GSR_ERR_WORKSPACE, "sort workspace too small");
         GSR_REQUIRE(mean2d && cov2d && colors && alpha && depth, "null pointer");
-        {
+        // the block binning's first kernel forms the records in its own launch
+        if (!blocks) {
             StageTimer timer("records", st);
             GSR_HIP(gsr::launch_blend_records(n, mean2d, cov2d, colors, alpha, recs, st),
                     "rasterize: records");
@@ -658,6 +659,11 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                 tb.ranges = tile_ranges;
                 tb.ids = ids;
                 tb.err = dg.status;
+                tb.rec_mean2d = mean2d;
+                tb.rec_cov2d = cov2d;
+                tb.rec_colors = colors;
+                tb.rec_alpha = alpha;
+                tb.recs = recs;
                 GSR_HIP(gsr::launch_tile_binning(tb, st), "rasterize: tile binning");
             }
             if (sorted_keys)

@@ -180,6 +180,13 @@ struct TileBinning {
     int32_t* ranges = nullptr;              // out: [tiles][2]
     uint32_t* ids = nullptr;                // out: sorted ids (m)
     int* err = nullptr;                     // bit 2: inconsistent counts
+    // optional: the blend records (n) from these, formed in extra work-groups
+    // of the level-1 count kernel's launch (independent work, one launch fewer)
+    const float* rec_mean2d = nullptr;
+    const float* rec_cov2d = nullptr;
+    const float* rec_colors = nullptr;
+    const float* rec_alpha = nullptr;
+    void* recs = nullptr;
 };
 // sorted ids and tile ranges from the depth order and tile rectangles.
 hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st);

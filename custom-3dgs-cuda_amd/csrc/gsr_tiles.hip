@@ -201,10 +201,32 @@ __device__ __forceinline__ int window_col(const WindowMasks& W, const BlockGrid&
 
 // counts[b * cstride + c] = how many of chunk c's 64 ranks meet block b, for
 // every block (zeros included); lane l counts block 64 w + l.
+// Records of the blends, formed by the count kernel's work-groups from
+// `first` on (one Gaussian per thread), when `recs` is set.
+struct RecordArgs {
+    const float* mean2d;
+    const float* cov2d;
+    const float* colors;
+    const float* alpha;
+    BlendRec* recs;
+    uint32_t first;
+};
+
 __global__ __launch_bounds__(kThreads) void block_count_kernel(
     int n, const uint32_t* __restrict__ perm, const uint2* __restrict__ rects,
     const uint2* __restrict__ drects, BlockGrid bg,
-    int chunks, int windows, int cstride, uint32_t* __restrict__ counts) {
+    int chunks, int windows, int cstride, uint32_t* __restrict__ counts, RecordArgs ra) {
+    if (ra.recs && blockIdx.x >= ra.first) {
+        const int i = (int)(blockIdx.x - ra.first) * kThreads + (int)threadIdx.x;
+        if (i < n) {
+            const float mx = ra.mean2d[2 * (size_t)i], my = ra.mean2d[2 * (size_t)i + 1];
+            const float a = ra.cov2d[3 * (size_t)i], b = ra.cov2d[3 * (size_t)i + 1],
+                        c = ra.cov2d[3 * (size_t)i + 2];
+            ra.recs[i] = blend_record(mx, my, a, b, c, ra.alpha[i], ra.colors[3 * (size_t)i],
+                                      ra.colors[3 * (size_t)i + 1], ra.colors[3 * (size_t)i + 2]);
+        }
+        return;
+    }
     const int lane = lane_id();
     const ChunkWindow cw = chunk_window(windows);
     if (cw.chunk >= chunks) return;
@@ -578,9 +600,13 @@ hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
                            dim3(kThreads), 0, st, tb.n, tb.perm, tb.rects, tb.drects);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(block_count_kernel, dim3(groups_for(l1_waves)), dim3(kThreads), 0, st,
+    RecordArgs ra{tb.rec_mean2d, tb.rec_cov2d, tb.rec_colors, tb.rec_alpha,
+                  static_cast<BlendRec*>(tb.recs), groups_for(l1_waves)};
+    const unsigned rec_groups =
+        ra.recs ? (unsigned)(((size_t)tb.n + kThreads - 1) / kThreads) : 0u;
+    hipLaunchKernelGGL(block_count_kernel, dim3(ra.first + rec_groups), dim3(kThreads), 0, st,
                        tb.n, tb.perm, tb.rects, tb.drects, bg, chunks, windows, cstride,
-                       tb.bcount);
+                       tb.bcount, ra);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(block_scan_kernel, dim3(bg.nb), dim3(kThreads), 0, st, chunks, cstride,
                        tb.bcount, tb.block_hist, tb.block_start, tb.seg_start, tb.seg_owner,
