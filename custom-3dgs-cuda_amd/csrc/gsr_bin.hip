@@ -229,28 +229,15 @@ __global__ __launch_bounds__(kThreads) void bin_count_kernel(
     }
 }
 
-// Behind bin_count_kernel (block histogram mode), one work-group: the block
-// and segment starts from the block histogram, and the final pair count and
-// the device status word handed to the host.  A kernel of its own rather than
-// bin_count's last work-group: on this chip every work-group's agent-scope
-// release would write the L2 back once more.
-__global__ __launch_bounds__(kThreads) void bin_finish_kernel(
-    BlockGrid bg, const uint32_t* __restrict__ block_hist, const uint64_t* __restrict__ pair_total,
-    uint32_t* __restrict__ block_start, uint32_t* __restrict__ seg_start,
-    uint64_t* __restrict__ host_total, int* __restrict__ status) {
+// Behind bin_count_kernel (block histogram mode), one work-group: the hand-off
+// (bin_finish_body: the pair count and status word to the host, the block and
+// segment starts).  A kernel of its own, or a work-group of the depth sort's
+// first pass, rather than bin_count's last work-group: on this chip every
+// work-group's agent-scope release would write the L2 back once more.
+__global__ __launch_bounds__(kThreads) void bin_finish_kernel(BinFinish f) {
     __shared__ uint32_t s_scan[kThreads / kWave];
     __shared__ uint32_t s_v[kThreads / kWave];
-    if (threadIdx.x == 0 && host_total) {
-        const uint64_t total = *pair_total;
-        // the device status word goes to the host with the count, and is
-        // cleared: each error is reported once
-        const int stat = status ? atomicExch(status, 0) : 0;
-        __hip_atomic_store(host_total + 1, (uint64_t)(uint32_t)stat, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_SYSTEM);
-        __hip_atomic_store(host_total, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-        __threadfence_system();
-    }
-    block_starts_body<kThreads>(bg.nb, block_hist, block_start, seg_start, s_scan, s_v);
+    bin_finish_body<kThreads>(f, s_scan, s_v);
 }
 
 // Pairs per tile row of the frame, for planning screen bands: each Gaussian's
@@ -496,7 +483,7 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
                             uint32_t* block_start, uint32_t* seg_start, uint64_t* host_total,
-                            int* status, hipStream_t st) {
+                            int* status, hipStream_t st, bool finish) {
     if (n <= 0) return hipSuccess;
     if (tile_passes < 0 || tile_passes > 4) return hipErrorInvalidValue;
     const BlockGrid bg = block_grid((W + 15) / 16, (H + 15) / 16);
@@ -513,9 +500,9 @@ hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, cons
                        depth, H, W, counts, rects, dkeys, dvals, tile_passes, tile_hist,
                        depth_hist, bg, block_hist, pair_total);
     hipError_t e = hipGetLastError();
-    if (e != hipSuccess || !block_hist) return e;
-    hipLaunchKernelGGL(bin_finish_kernel, dim3(1), dim3(kThreads), 0, st, bg, block_hist,
-                       pair_total, block_start, seg_start, host_total, status);
+    if (e != hipSuccess || !block_hist || !finish) return e;
+    const BinFinish f{bg.nb, block_hist, pair_total, block_start, seg_start, host_total, status};
+    hipLaunchKernelGGL(bin_finish_kernel, dim3(1), dim3(kThreads), 0, st, f);
     return hipGetLastError();
 }
 

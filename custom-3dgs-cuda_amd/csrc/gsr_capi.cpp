@@ -460,6 +460,9 @@ int rasterize_bin(int n, const float* depth, const int32_t* order, const float* 
         hc.host[0] = kNoCount;
         hc.host[1] = 0;
     }
+    // the binning's hand-off (the pair count to the host, the block starts)
+    // runs in the depth sort's first pass when that pass can take it
+    const bool finish_in_sort = blocks && !order && gsr::radix_sort_takes_finish((uint64_t)n);
     {
         StageTimer timer("bin_count", st);
         const int64_t T = (int64_t)tiles_x_of(width) * tiles_y_of(height);
@@ -473,12 +476,12 @@ int rasterize_bin(int n, const float* depth, const int32_t* order, const float* 
                                       blocks ? &misc->total : nullptr,
                                       at<uint32_t>(bin_ws, L.block_start),
                                       at<uint32_t>(bin_ws, L.seg_start), hc.dev, dg.status,
-                                      st),
+                                      st, /*finish=*/!finish_in_sort),
                 "rasterize: count");
     }
     Misc* host = pinned_misc();
     if (!host) return fail(GSR_ERR_HIP, "rasterize: pinned host buffer allocation failed");
-    auto depth_sort = [&]() -> int {
+    auto depth_sort = [&](const gsr::BinFinish* fin, hipEvent_t after_first) -> int {
         StageTimer timer("depth_sort", st);
         if (order) {
             GSR_HIP(hipMemcpyAsync(dv0, order, 4 * (size_t)n, hipMemcpyDeviceToDevice, st),
@@ -488,22 +491,31 @@ int rasterize_bin(int n, const float* depth, const int32_t* order, const float* 
         GSR_HIP(gsr::launch_radix_sort(dk0, dv0, at<uint32_t>(bin_ws, L.dk1),
                                        at<uint32_t>(bin_ws, L.dv1), (uint64_t)n,
                                        at<void>(bin_ws, L.sortctl), err, st,
-                                       /*hist_ready=*/true),
+                                       /*hist_ready=*/true, fin, after_first),
                 "rasterize: depth sort");
         return GSR_OK;
     };
     if (blocks) {
-        // The pair count is final after bin_count, whose one-group finish
-        // kernel stores it to host-mapped memory: queue the depth sort behind
-        // bin_count and wait only for bin_count, so the sort runs while the
-        // host returns and queues the render.  bin_count also hands over the
+        // The pair count is final after bin_count; the hand-off (a work-group
+        // of the depth sort's first pass, or a one-group kernel of its own)
+        // stores it to host-mapped memory: queue the depth sort and wait only
+        // for the hand-off, so the rest of the sort runs while the host
+        // returns and queues the render.  The hand-off also passes on the
         // device status word: errors of every earlier kernel on the device
         // (an earlier frame's sorts, binning and backward) are reported here;
         // this frame's own, at the next forward or gsr_rasterize_status.
         hipEvent_t ev = count_event();
         if (!ev) return fail(GSR_ERR_HIP, "rasterize: event creation failed");
-        GSR_HIP(hipEventRecord(ev, st), "rasterize: record");
-        if (int rc = depth_sort()) return rc;
+        if (finish_in_sort) {
+            const gsr::BlockGrid bg = gsr::block_grid(tiles_x_of(width), tiles_y_of(height));
+            const gsr::BinFinish fin{bg.nb, at<uint32_t>(bin_ws, L.blockhist), &misc->total,
+                                     at<uint32_t>(bin_ws, L.block_start),
+                                     at<uint32_t>(bin_ws, L.seg_start), hc.dev, dg.status};
+            if (int rc = depth_sort(&fin, ev)) return rc;
+        } else {
+            GSR_HIP(hipEventRecord(ev, st), "rasterize: record");
+            if (int rc = depth_sort(nullptr, nullptr)) return rc;
+        }
         GSR_HIP(hipEventSynchronize(ev), "rasterize: synchronize");
         const uint64_t total = hc.host[0];
         if (total == kNoCount) return fail(GSR_ERR_DEVICE, "rasterize: pair count not stored");
@@ -516,7 +528,7 @@ int rasterize_bin(int n, const float* depth, const int32_t* order, const float* 
         *num_pairs = (int64_t)total;
         return GSR_OK;
     } else {
-        if (int rc = depth_sort()) return rc;
+        if (int rc = depth_sort(nullptr, nullptr)) return rc;
         StageTimer timer("scan", st);
         GSR_HIP(gsr::launch_scan_counts(n, dv0, counts, at<uint32_t>(bin_ws, L.offsets),
                                         &misc->total, at<void>(bin_ws, L.scanctl), err, st),

@@ -158,6 +158,24 @@ __device__ void block_starts_body(int nb, const uint32_t* hist, uint32_t* block_
     }
 }
 
+// The binning's hand-off after its count kernel (one work-group of kT
+// threads): the final pair count and the device status word (read and
+// cleared: each error is reported once) stored to the host-mapped words
+// host_total[0, 1] with system scope, then the block and segment starts from
+// the block histogram.
+template <int kT>
+__device__ void bin_finish_body(const BinFinish& f, uint32_t* s_w, uint32_t* s_v) {
+    if (threadIdx.x == 0 && f.host_total) {
+        const uint64_t total = *f.pair_total;
+        const int stat = f.status ? atomicExch(f.status, 0) : 0;
+        __hip_atomic_store(f.host_total + 1, (uint64_t)(uint32_t)stat, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_SYSTEM);
+        __hip_atomic_store(f.host_total, total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+        __threadfence_system();
+    }
+    block_starts_body<kT>(f.nb, f.block_hist, f.block_start, f.seg_start, s_w, s_v);
+}
+
 // ranges[t] = [start, start + count) from the tile totals in tile order,
 // (0, 0) for tiles without pairs (rasterize.cu:140-166); a grand total other
 // than m sets err bit 2.  One work-group of kT threads; s_w holds kT / 64 words.

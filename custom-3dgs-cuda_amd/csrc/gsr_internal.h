@@ -91,8 +91,13 @@ size_t sort_control_bytes(uint64_t n);
 // err (device int) is set when a look-back wait exceeds kSpinLimit.
 // hist_ready: the histogram block at the start of `control` was accumulated
 // already.
+struct BinFinish;
 hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
-                             void* control, int* err, hipStream_t st, bool hist_ready = false);
+                             void* control, int* err, hipStream_t st, bool hist_ready = false,
+                             const BinFinish* finish = nullptr, hipEvent_t after_first = nullptr);
+// Whether launch_radix_sort runs `finish` (in one extra work-group of its first
+// pass, after which it records `after_first`) for n keys: up to 2^20.
+bool radix_sort_takes_finish(uint64_t n);
 // The depth order's input: keys = the bits of depth[i], vals = i, and the
 // keys' histogram block at the start of `control` (zeroed first), so that
 // launch_radix_sort runs with hist_ready.
@@ -152,6 +157,19 @@ struct BlockGrid {
     int bw = 0, bh = 0, nb = 0;
 };
 BlockGrid block_grid(int tiles_x, int tiles_y);
+
+// The binning's hand-off after its count kernel (bin_finish_body): the pair
+// count and the device status word to host_total[0, 1], the block and segment
+// starts from the block histogram.
+struct BinFinish {
+    int nb;
+    const uint32_t* block_hist;
+    const uint64_t* pair_total;
+    uint32_t* block_start;
+    uint32_t* seg_start;
+    uint64_t* host_total;
+    int* status;
+};
 // Blocks the binning's per-work-group block histogram holds.
 constexpr int kMaxBlocks = 8192;
 
@@ -207,14 +225,17 @@ hipError_t launch_row_pairs(int n, const float* mean2d, const float* cov2d, int 
 // kernel behind it then writes the block and segment starts (block_start /
 // seg_start, nb + 1 entries each) and, when host_total is not null, the final
 // pair count to that host-mapped coherent word and the device status word
-// (status, read and cleared) to host_total[1].  dkeys null: no depth keys,
-// values or depth histograms (depth is then not read).
+// (status, read and cleared) to host_total[1] (with finish false that kernel is
+// not launched: the caller runs the hand-off itself, in the depth sort's
+// first pass).  dkeys null: no depth keys, values or depth histograms (depth
+// is then not read).
 hipError_t launch_bin_count(int n, const float* mean2d, const float* cov2d, const float* depth,
                             int H, int W, uint32_t* counts, uint2* rects, uint32_t* dkeys,
                             uint32_t* dvals, int tile_passes, uint32_t* tile_hist,
                             uint32_t* depth_hist, uint32_t* block_hist, uint64_t* pair_total,
                             uint32_t* block_start, uint32_t* seg_start,
-                            uint64_t* host_total, int* status, hipStream_t st);
+                            uint64_t* host_total, int* status, hipStream_t st,
+                            bool finish = true);
 
 // The backward's per-Gaussian pass: blend records, tile rectangles and counts,
 // and the slot offsets goff (exclusive scan of the counts in Gaussian order,

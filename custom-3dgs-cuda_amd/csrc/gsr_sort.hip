@@ -375,7 +375,16 @@ template <int kThreads>
 __global__ __launch_bounds__(kThreads) void onesweep_small_kernel(
     const uint32_t* __restrict__ kin, const uint32_t* __restrict__ vin,
     uint32_t* __restrict__ kout, uint32_t* __restrict__ vout, uint64_t n, int shift,
-    const uint32_t* __restrict__ hist, uint16_t* __restrict__ status, int* __restrict__ err) {
+    const uint32_t* __restrict__ hist, uint16_t* __restrict__ status, int* __restrict__ err,
+    BinFinish fin, uint32_t fin_group) {
+    // the binning's hand-off, in a work-group of its own after the partitions'
+    // (independent of the pass: one launch fewer than a kernel of its own)
+    if (blockIdx.x == fin_group) {
+        __shared__ uint32_t s_fw[kThreads / kWave];
+        __shared__ uint32_t s_fv[kThreads / kWave];
+        bin_finish_body<kThreads>(fin, s_fw, s_fv);
+        return;
+    }
     constexpr int kItems = kSmallItems;
     constexpr int kPart = kThreads * kItems;
     constexpr int kWaves = kThreads / kWave;
@@ -1119,8 +1128,11 @@ hipError_t launch_depth_keys_hist(uint64_t n, const float* depth, uint32_t* keys
     return hipGetLastError();
 }
 
+bool radix_sort_takes_finish(uint64_t n) { return n > 0 && fanin_sort(n); }
+
 hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t* v1, uint64_t n,
-                             void* control, int* err, hipStream_t st, bool hist_ready) {
+                             void* control, int* err, hipStream_t st, bool hist_ready,
+                             const BinFinish* finish, hipEvent_t after_first) {
     if (n == 0) return hipSuccess;
     if (n >= (1ull << 32)) return hipErrorInvalidValue;
     const uint64_t parts = sort_parts(n);
@@ -1142,14 +1154,24 @@ hipError_t launch_radix_sort(uint32_t* k0, uint32_t* v0, uint32_t* k1, uint32_t*
         uint64_t* stat = c.status + (size_t)p * parts * kRadixBins;
         if (fanin_sort(n)) {
             uint16_t* stat16 = reinterpret_cast<uint16_t*>(c.status) + (size_t)p * parts * kRadixBins;
+            const bool fin = p == 0 && finish;
+            const BinFinish f = fin ? *finish : BinFinish{};
+            const uint32_t fin_group = fin ? np : 0xffffffffu;
+            const unsigned groups = np + (fin ? 1u : 0u);
             if (small_sort(n))
-                hipLaunchKernelGGL(onesweep_small_kernel<kSmallThreads>, dim3(np),
+                hipLaunchKernelGGL(onesweep_small_kernel<kSmallThreads>, dim3(groups),
                                    dim3(kSmallThreads), 0, st, ki, vi, ko, vo, n, 8 * p, hp,
-                                   stat16, err);
+                                   stat16, err, f, fin_group);
             else
-                hipLaunchKernelGGL(onesweep_small_kernel<kMediumThreads>, dim3(np),
+                hipLaunchKernelGGL(onesweep_small_kernel<kMediumThreads>, dim3(groups),
                                    dim3(kMediumThreads), 0, st, ki, vi, ko, vo, n, 8 * p, hp,
-                                   stat16, err);
+                                   stat16, err, f, fin_group);
+            if (p == 0 && after_first) {
+                e = hipGetLastError();
+                if (e != hipSuccess) return e;
+                e = hipEventRecord(after_first, st);
+                if (e != hipSuccess) return e;
+            }
         } else {
             // the status words of the pass hold the partitions' digit counts,
             // then their offsets
