@@ -188,14 +188,16 @@ __device__ __forceinline__ float blend_power(float dx, float dy, const float4& A
 
 // One pixel's forward step for one list entry (rasterize.cu:243-268), with the
 // reference's skips as selects: the same fp32 operations in the same order,
-// the colour sums fused (pix_color += colour * weight).
-__device__ __forceinline__ void fwd_step(FwdPixel& p, float fx, float fy, const float4& A,
-                                         const float4& B, float cb, int contributor) {
+// the colour sums fused (pix_color += colour * weight).  `on` is live(p), the
+// lane mask the caller's early-exit ballot already holds.
+__device__ __forceinline__ void fwd_step(FwdPixel& p, bool on, float fx, float fy,
+                                         const float4& A, const float4& B, float cb,
+                                         int contributor) {
     const float dx = fx - A.x;
     const float dy = fy - A.y;
     const float power = blend_power(dx, dy, A, B);
     const float alpha = fminf(kAlphaMax, B.y * exp_blend_noclamp(power));
-    const bool blend = live(p) & !(power > 0.0f) & !(alpha < kAlphaMin);
+    const bool blend = on & !(power > 0.0f) & !(alpha < kAlphaMin);
     const float w = alpha * p.T;
     const float Tn = p.T * (1.0f - alpha);
     p.C0 = blend ? __builtin_fmaf(B.z, w, p.C0) : p.C0;
@@ -275,17 +277,20 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_fwd_kernel(
                 const int e = c0 + lane;
                 uint64_t todo = ballot(e < cnt && (s_bits[min(e, kBatch - 1)] & my_bit) != 0u);
                 while (todo) {
+                    // the wave stops once no pixel is live, tested before each
+                    // entry with the same compares the step's skip uses
+                    if (ballot(any_live(p)) == 0) {
+                        done = true;
+                        break;
+                    }
                     const int j = c0 + (int)__builtin_ctzll(todo);
                     todo &= todo - 1;
                     const float4 A = s_a[j];
                     const float4 B = s_b[j];
                     const float cb = s_c[j].x;
 #pragma unroll
-                    for (int k = 0; k < kPix; ++k) fwd_step(p[k], fx, fy[k], A, B, cb, cbase + j);
-                    if (ballot(any_live(p)) == 0) {
-                        done = true;
-                        break;
-                    }
+                    for (int k = 0; k < kPix; ++k)
+                        fwd_step(p[k], live(p[k]), fx, fy[k], A, B, cb, cbase + j);
                 }
             }
         }
@@ -345,23 +350,25 @@ __device__ __forceinline__ void decide_exact(BwdDecision& d, float o, int contri
 // within 1e-6 relative of exp_blend wherever alpha can reach 1/255 (power in
 // [-5.6, 0]), so the alpha >= 1/255 test agrees with the exact one unless
 // alpha lies within kNearAlpha of 1/255; alpha <= opacity < 0.99 is never
-// clamped.  near_fast says whether the lane needs the exact evaluation (near
-// the threshold, or a NaN alpha).
+// clamped.  Alpha at or above kAlphaMin + kNearAlpha passes the test, below
+// kAlphaMin - kNearAlpha fails it; the returned mask holds the lanes in
+// neither case (near the threshold, or a NaN alpha), which need the exact
+// evaluation.  Two compares per pixel, each ballot a compare's own mask.
 constexpr float kNearAlpha = kAlphaMin * 2e-5f;
-__device__ __forceinline__ void decide_fast(BwdDecision& d, float o, int contributor, int last) {
+constexpr float kAlphaLo = kAlphaMin - kNearAlpha, kAlphaHi = kAlphaMin + kNearAlpha;
+__device__ __forceinline__ uint64_t decide_fast(BwdDecision& d, float o, int contributor,
+                                                int last) {
     d.alpha = o * __builtin_amdgcn_exp2f(d.power * 1.44269504088896341f);
-    d.act = (contributor <= last) & !(d.power > 0.0f) & !(d.alpha < kAlphaMin);
+    const bool pass = d.alpha >= kAlphaHi;
+    d.act = (contributor <= last) & !(d.power > 0.0f) & pass;
     d.ae = d.act ? d.alpha : 0.0f;
     d.ag = d.ae;
-}
-__device__ __forceinline__ bool near_fast(const BwdDecision& d) {
-    return !(fabsf(d.alpha - kAlphaMin) > kNearAlpha);
+    return ballot(!(d.alpha < kAlphaLo)) & ~ballot(pass);
 }
 
 // The wave's decisions for one entry: the fast evaluation where the record
 // allows it, the exact one for the whole wave when any lane is near the
-// threshold (one ballot per pixel of a single compare: no lane-mask
-// materialisation).
+// threshold.
 template <int kPix>
 __device__ __forceinline__ void decide_entry(BwdDecision (&d)[kPix], float o, bool fast,
                                              int contributor, const BwdPixel (&p)[kPix]) {
@@ -369,10 +376,7 @@ __device__ __forceinline__ void decide_entry(BwdDecision (&d)[kPix], float o, bo
     if (!exact) {
         uint64_t near = 0;
 #pragma unroll
-        for (int k = 0; k < kPix; ++k) {
-            decide_fast(d[k], o, contributor, p[k].last);
-            near |= ballot(near_fast(d[k]));
-        }
+        for (int k = 0; k < kPix; ++k) near |= decide_fast(d[k], o, contributor, p[k].last);
         exact = near != 0;
     }
     if (exact) {
@@ -985,11 +989,15 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
         s_wmax = 0u;
     }
     // the first kOrderHeld tiles per thread are read once, all loads in
-    // flight together, and their work kept for the scatter
+    // flight together, and their work kept for the scatter.  The lanes of a
+    // wave take tiles 16 apart (held_tile): neighbouring tiles often share a
+    // bucket, and a wave's LDS atomics on one address are serialised.
+    static_assert(kOrderThreads == 16 * kWave, "held_tile permutes 16 waves of 64 lanes");
+    auto held_tile = [&](int i) { return (tid & 63) * 16 + (tid >> 6) + i * kOrderThreads; };
     uint32_t held[kOrderHeld];
 #pragma unroll
     for (int i = 0; i < kOrderHeld; ++i) {
-        const int t = tid + i * kOrderThreads;
+        const int t = held_tile(i);
         held[i] = (t < T) ? work_of(t) : 0u;
     }
     __syncthreads();
@@ -997,7 +1005,7 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
     uint32_t wmax = 0;
 #pragma unroll
     for (int i = 0; i < kOrderHeld; ++i) {
-        if (tid + i * kOrderThreads < T) atomicAdd(&s_cnt[bucket(held[i])], 1u);
+        if (held_tile(i) < T) atomicAdd(&s_cnt[bucket(held[i])], 1u);
         wsum += held[i];
         wmax = max(wmax, held[i]);
     }
@@ -1032,7 +1040,7 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
     __syncthreads();
 #pragma unroll
     for (int i = 0; i < kOrderHeld; ++i) {
-        const int t = tid + i * kOrderThreads;
+        const int t = held_tile(i);
         if (t < T) {
             const uint32_t pos = atomicAdd(&s_cnt[bucket(held[i])], 1u);
             if (pos < (uint32_t)T) order[pos] = (uint32_t)t;
