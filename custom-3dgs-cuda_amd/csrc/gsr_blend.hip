@@ -989,11 +989,8 @@ __global__ __launch_bounds__(kOrderThreads) void tile_order_kernel(
         s_wmax = 0u;
     }
     // the first kOrderHeld tiles per thread are read once, all loads in
-    // flight together, and their work kept for the scatter.  The lanes of a
-    // wave take tiles 16 apart (held_tile): neighbouring tiles often share a
-    // bucket, and a wave's LDS atomics on one address are serialised.
-    static_assert(kOrderThreads == 16 * kWave, "held_tile permutes 16 waves of 64 lanes");
-    auto held_tile = [&](int i) { return (tid & 63) * 16 + (tid >> 6) + i * kOrderThreads; };
+    // flight together, and their work kept for the scatter
+    auto held_tile = [&](int i) { return tid + i * kOrderThreads; };
     uint32_t held[kOrderHeld];
 #pragma unroll
     for (int i = 0; i < kOrderHeld; ++i) {
@@ -1159,7 +1156,7 @@ hipError_t launch_blend_fwd(int n, int H, int W, const int32_t* ranges, const in
     if (tiles == 0) return hipSuccess;
     const auto* r = reinterpret_cast<const int2*>(ranges);
     const auto* rc = static_cast<const BlendRec*>(recs);
-    hipLaunchKernelGGL(blend_fwd_kernel<1>, dim3(tiles), dim3(Layout<1>::kThreads), 0, st, n, H,
+    hipLaunchKernelGGL(blend_fwd_kernel<2>, dim3(tiles), dim3(Layout<2>::kThreads), 0, st, n, H,
                        W, tiles_x, m, r, ids, rc, img, finalT, ncontrib, order);
     return hipGetLastError();
 }

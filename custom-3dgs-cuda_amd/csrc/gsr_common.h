@@ -196,9 +196,14 @@ __device__ __forceinline__ float wave_reduce_columns(float s0, float p2, float p
     const float r0 = fold32(s0, c0);
     const float r1 = fold32(p2, c1);
     const float r2 = fold32(p5, c2);
-    // column totals: a = (S0, P2, c0, c1) in rows 0-3, b = (P5, P5, c2, c2)
-    const float a = fold16(r0, r1);
-    const float b = fold16(r2, r2);
+    // column totals: a = (S0, P2, c0, c1) in rows 0-3, b = (P5, -, c2, -): b's
+    // swap takes the first swap's spent register as its partner (its rows 1
+    // and 3, summed into b's rows 1 and 3, reach no lane that holds a value)
+    const auto s01 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r0), __float_as_uint(r1),
+                                                      false, false);
+    const float a = __uint_as_float(s01[0]) + __uint_as_float(s01[1]);
+    const auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(r2), s01[0], false, false);
+    const float b = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
     const float t1 = dx * a;   // row 0: dx S0, row 1: dx P2
     const float t2 = dx * t1;  // row 0: dx^2 S0
     const int l = lane_id();
@@ -209,6 +214,10 @@ __device__ __forceinline__ float wave_reduce_columns(float s0, float p2, float p
     float w = (b2 ? u1 : u0) + lane_xor4(b2 ? u0 : u1);
     w = w + dpp_move<kDppQuadXor2>(w);
     w = w + dpp_move<kDppQuadXor1>(w);
+    // formed here with every lane active, so the last level stays one DPP add
+    // (a caller that only keeps the value in some lanes would otherwise have
+    // the add sunk into its branch and the lane move split from it)
+    asm volatile("" : "+v"(w));
     return w;
 }
 
