@@ -605,7 +605,10 @@ def banded_frame(sc, band_height: int | None, steps: int) -> dict:
     G = config_grad(sc)
     fwd, bwd, total, _ = time_frames(sc, steps, 1, profile=False, render=render, grad=G)
     _, _, _, stages = time_frames(sc, 1, 0, profile=True, render=render, grad=G)
-    print(f"[bench] {sc.name}: {total:.1f} ms per frame", file=sys.stderr, flush=True)
+    from gaussian_splatting.rasterizer import bands as bands_mod
+    prefix_stats = dict(bands_mod.last_stats)
+    print(f"[bench] {sc.name}: {total:.1f} ms per frame ({prefix_stats})", file=sys.stderr,
+          flush=True)
     torch.cuda.empty_cache()
     v = sc.view
     rates = {}
@@ -617,6 +620,9 @@ def banded_frame(sc, band_height: int | None, steps: int) -> dict:
             "band_plan": "pairs per tile row, at most (2^31 - 2^16) x 127/128 per band"
             if band_height is None else f"{band_height} rows",
             "max_band_pairs": max(pairs),
+            # what the frames rendered: depth-prefix rendering's two passes
+            # (prefix, pairs and bands of each) or the planned bands
+            "rendered": prefix_stats,
             "stages": rates, "width": v["width"], "height": v["height"], "gaussians": sc.n}
 
 

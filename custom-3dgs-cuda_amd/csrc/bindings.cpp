@@ -902,6 +902,30 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
                  "tile_row_pairs");
         return rows.narrow(0, 0, ty);
     }, py::arg("n"), py::arg("mean_2d"), py::arg("cov_2d"), py::arg("height"), py::arg("width"));
+    // the Gaussians whose tile rectangle (widened by a tile row each way) holds
+    // a tile marked in tile_mask [ceil(H / 16), ceil(W / 16)] (no reference
+    // counterpart: depth-prefix screen bands)
+    m.def("tiles_touch", [](int64_t n, const Tensor& mean_2d, const Tensor& cov_2d,
+                            int64_t height, int64_t width, const Tensor& tile_mask) {
+        CHECK_INPUT_FP32(mean_2d);
+        CHECK_INPUT_FP32(cov_2d);
+        const int64_t ty = (height + 15) / 16, tx = (width + 15) / 16;
+        TORCH_CHECK(tile_mask.is_cuda() && tile_mask.dim() == 2 && tile_mask.size(0) == ty &&
+                        tile_mask.size(1) == tx,
+                    "tile_mask must be a CUDA tensor of shape [ceil(H/16), ceil(W/16)]");
+        TORCH_CHECK(mean_2d.size(0) >= n && cov_2d.size(0) >= n, "fewer than n Gaussians");
+        auto sat = torch::constant_pad_nd(
+                       tile_mask.to(torch::kInt32).cumsum(0, torch::kInt32).cumsum(1, torch::kInt32),
+                       {1, 0, 1, 0}, 0)
+                       .contiguous();
+        auto flags = torch::empty({n}, mean_2d.options().dtype(torch::kUInt8));
+        check_rc(gsr_tiles_touch((int)n, mean_2d.data_ptr<float>(), cov_2d.data_ptr<float>(),
+                                 (int)height, (int)width, sat.data_ptr<int32_t>(),
+                                 flags.data_ptr<uint8_t>(), current_stream()),
+                 "tiles_touch");
+        return flags.to(torch::kBool);
+    }, py::arg("n"), py::arg("mean_2d"), py::arg("cov_2d"), py::arg("height"), py::arg("width"),
+       py::arg("tile_mask"));
     // VALU issue-rate calibration kernels (measurement support for bench.py)
     m.def("calibrate_valu", [](int kind, int iters) {
         auto out = torch::empty({(int64_t)gsr_calibrate_valu_out_floats()},

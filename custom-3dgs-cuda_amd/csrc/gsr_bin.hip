@@ -271,6 +271,36 @@ __global__ __launch_bounds__(kThreads) void row_pairs_kernel(int n,
     }
 }
 
+// flags[i] = 1 when Gaussian i's tile rectangle (tile_rect, as bin_count_kernel
+// forms it on this H x W frame), widened by one tile row above and below, holds
+// a marked tile, else 0.  sat is the summed-area table of the marked tiles:
+// (tiles_y + 1) x (tiles_x + 1) int32, row-major, row 0 and column 0 zero.
+// The widening covers a render of the same Gaussians in a screen band, whose
+// means are moved by the band's first row: the move can round a mean far above
+// the band in its last bit, which moves its rectangle's rows by at most one.
+__global__ __launch_bounds__(kThreads) void tiles_touch_kernel(int n,
+                                                               const float* __restrict__ mean2d,
+                                                               const float* __restrict__ cov2d,
+                                                               int H, int W,
+                                                               const int32_t* __restrict__ sat,
+                                                               uint8_t* __restrict__ flags) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const TileRect r = tile_rect(mean2d[2 * (size_t)i], mean2d[2 * (size_t)i + 1],
+                                 cov2d[3 * (size_t)i], cov2d[3 * (size_t)i + 1],
+                                 cov2d[3 * (size_t)i + 2], W, H);
+    const int tiles_x = (W + 15) / 16, tiles_y = (H + 15) / 16;
+    const int y0 = max(0, r.y0 - 1), y1 = min(tiles_y, r.y1 + 1);
+    bool hit = false;
+    if (r.ok && r.x1 > r.x0 && y1 > y0) {
+        const int sx = tiles_x + 1;
+        hit = sat[y1 * sx + r.x1] - sat[y0 * sx + r.x1] - sat[y1 * sx + r.x0] +
+                  sat[y0 * sx + r.x0] >
+              0;
+    }
+    flags[i] = hit ? 1 : 0;
+}
+
 // In place: diff[0 .. tiles_y) becomes its inclusive prefix sums (the pairs of
 // each tile row).  One work-group.
 __global__ __launch_bounds__(kThreads) void row_pairs_scan_kernel(
@@ -521,6 +551,14 @@ hipError_t launch_row_pairs(int n, const float* mean2d, const float* cov2d, int 
     }
     hipLaunchKernelGGL(row_pairs_scan_kernel, dim3(1), dim3(kThreads), 0, st, tiles_y,
                        reinterpret_cast<unsigned long long*>(rows));
+    return hipGetLastError();
+}
+
+hipError_t launch_tiles_touch(int n, const float* mean2d, const float* cov2d, int H, int W,
+                              const int32_t* sat, uint8_t* flags, hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(tiles_touch_kernel, dim3(blocks_for((uint64_t)n)), dim3(kThreads), 0, st,
+                       n, mean2d, cov2d, H, W, sat, flags);
     return hipGetLastError();
 }
 

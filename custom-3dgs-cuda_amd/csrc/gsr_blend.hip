@@ -401,8 +401,11 @@ __device__ __forceinline__ BwdTerms bwd_update(BwdPixel& p, const BwdDecision& d
     // within the 1e-4 gradient bar.  A correction step from the exact residual
     // T - q (1 - alpha) (two fused multiply-adds on the entry's dependency
     // chain) brought the quotient to a division's 0.5 ulp and cost 15 us of
-    // the bench frame's 229 us backward blend.  A skipped entry (alpha 0)
-    // leaves T unchanged: the reciprocal of 1 is exact.
+    // the bench frame's 229 us backward blend; on c5's distributions (walks
+    // of 1.5e4 entries) it left the gradients unchanged to 1e-3 of their
+    // error against float64, as did the forward's own alpha in place of the
+    // fast one.  A skipped entry (alpha 0) leaves T unchanged: the reciprocal
+    // of 1 is exact.
     const float den = 1.0f - d.ae;
     const float Tb = p.T * __builtin_amdgcn_rcpf(den);
     const float cg = B.z * p.g0 + B.w * p.g1 + cb * p.g2;
@@ -438,7 +441,8 @@ __device__ __forceinline__ BwdPixel load_bwd_pixel(bool in, int px, int py, int 
 // S0 = sum dpw, P2 = sum dpw dy, P5 = sum dpw dy^2, with dx applied once the
 // lanes of a column are summed (wave_reduce_columns): P1 = sum dx S0,
 // Q1 = sum dx^2 S0, Q2 = sum dx P2.  Then dL/dmean = (cx P1 + cy P2,
-// cy P1 + cz P2), dL/dconic = (-Q1 / 2, -Q2, -P5 / 2), dL/dcolour the sums of
+// cy P1 + cz P2), dL/dconic = (-Q1 / 2, -Q2, -P5 / 2) (converted to dL/dcov2d
+// per (tile, entry), before any sum over tiles), dL/dcolour the sums of
 // alpha T dL/dpixel and dL/dopacity = S0 / opacity.  Value k sits in slot
 // kCol* of the reduction's result.
 constexpr int kTerms = 9;
@@ -708,9 +712,14 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                 const float S0 = tot[kColS0], P1 = tot[kColP1], P2 = tot[kColP2];
                 t[0] = -2.0f * (ha * P1 + hb * P2);  // dL/dmean.x = cx P1 + cy P2
                 t[1] = -2.0f * (hb * P1 + hc * P2);  // dL/dmean.y = cy P1 + cz P2
-                t[2] = -0.5f * tot[kColQ1];          // dL/dconic.x
-                t[3] = -tot[kColQ2];                 // dL/dconic.y (full off-diagonal)
-                t[4] = -0.5f * tot[kColP5];          // dL/dconic.z
+                // dL/dcov2d from this (tile, entry)'s dL/dconic (x, full
+                // off-diagonal y, z), converted here as the reference converts
+                // each flushed batch (rasterize_backward.cu:211-221): for a
+                // near-singular covariance the conversion's terms cancel, and
+                // they then cancel at one tile's magnitude instead of at the
+                // Gaussian's total over all its tiles
+                conic_to_cov_grad(-2.0f * ha, -2.0f * hb, -2.0f * hc, -0.5f * tot[kColQ1],
+                                  -tot[kColQ2], -0.5f * tot[kColP5], t + 2);
                 t[5] = tot[kColC0];                  // dL/dcolour
                 t[6] = tot[kColC1];
                 t[7] = tot[kColC2];
@@ -737,15 +746,11 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
                 } else {
                     // no slot of its own (outside the rectangles, or a repeated
                     // id): straight to the outputs
-                    const float cx = -2.0f * s_a[tid].z, cy = -2.0f * s_c[tid].y,
-                                cz = -2.0f * s_b[tid].x;
-                    float dc[3];
-                    conic_to_cov_grad(cx, cy, cz, t[2], t[3], t[4], dc);
                     unsafeAtomicAdd(&dmean[2 * (size_t)g], t[0]);
                     unsafeAtomicAdd(&dmean[2 * (size_t)g + 1], t[1]);
-                    unsafeAtomicAdd(&dcov[3 * (size_t)g], dc[0]);
-                    unsafeAtomicAdd(&dcov[3 * (size_t)g + 1], dc[1]);
-                    unsafeAtomicAdd(&dcov[3 * (size_t)g + 2], dc[2]);
+                    unsafeAtomicAdd(&dcov[3 * (size_t)g], t[2]);
+                    unsafeAtomicAdd(&dcov[3 * (size_t)g + 1], t[3]);
+                    unsafeAtomicAdd(&dcov[3 * (size_t)g + 2], t[4]);
                     unsafeAtomicAdd(&dcol[3 * (size_t)g], t[5]);
                     unsafeAtomicAdd(&dcol[3 * (size_t)g + 1], t[6]);
                     unsafeAtomicAdd(&dcol[3 * (size_t)g + 2], t[7]);
@@ -757,8 +762,8 @@ __global__ __launch_bounds__(Layout<kPix>::kThreads) void blend_bwd_kernel(
 }
 
 // One 16-lane row per Gaussian (four per wave): the nine sums of its flagged
-// slots, the conic part converted to the covariance gradient, added to the
-// outputs (which hold zeros and any fallback atomics from the blend).
+// slots (d mean2d, d cov2d, d colour, d opacity), added to the outputs (which
+// hold zeros and any fallback atomics from the blend).
 // Sum over the kLanes (16 or 8) lanes of each row, result in every lane of
 // the row.
 template <int kLanes>
@@ -777,8 +782,8 @@ __device__ __forceinline__ float row_sum(float x) {
 // sparse and a row then covers 1024 slots per step.
 template <int kReduceRowLanes, int kGroup>
 __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
-    int n, const BlendRec* __restrict__ recs, GradSlots gs, float* __restrict__ dmean,
-    float* __restrict__ dcov, float* __restrict__ dcol, float* __restrict__ dalpha) {
+    int n, GradSlots gs, float* __restrict__ dmean, float* __restrict__ dcov,
+    float* __restrict__ dcol, float* __restrict__ dalpha) {
     static_assert(kReduceRowLanes == 16 || kReduceRowLanes == 8, "rows of 16 or 8 lanes");
     static_assert(kGroup == 8 || kGroup == 64, "flag groups of 8 or 64 slots");
     constexpr int kReduceGaussiansPerBlock = 256 / kReduceRowLanes;
@@ -841,9 +846,6 @@ __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
     const uint64_t row_claims =
         (wave_claims >> (lane_id() & (64 - kReduceRowLanes))) & ((1ull << kReduceRowLanes) - 1);
     if (g < n && sub == 0 && row_claims != 0) {
-        const BlendRec r = recs[g];
-        float dc[3];
-        conic_to_cov_grad(-2.0f * r.a.z, -2.0f * r.c.y, -2.0f * r.b.x, t[2], t[3], t[4], dc);
         const float m0 = dmean[2 * (size_t)g], m1 = dmean[2 * (size_t)g + 1];
         const float c0 = dcov[3 * (size_t)g], c1 = dcov[3 * (size_t)g + 1],
                     c2 = dcov[3 * (size_t)g + 2];
@@ -852,9 +854,9 @@ __global__ __launch_bounds__(256) void pair_grad_reduce_kernel(
         const float a0 = dalpha[g];
         dmean[2 * (size_t)g] = m0 + t[0];
         dmean[2 * (size_t)g + 1] = m1 + t[1];
-        dcov[3 * (size_t)g] = c0 + dc[0];
-        dcov[3 * (size_t)g + 1] = c1 + dc[1];
-        dcov[3 * (size_t)g + 2] = c2 + dc[2];
+        dcov[3 * (size_t)g] = c0 + t[2];
+        dcov[3 * (size_t)g + 1] = c1 + t[3];
+        dcov[3 * (size_t)g + 2] = c2 + t[4];
         dcol[3 * (size_t)g] = k0 + t[5];
         dcol[3 * (size_t)g + 1] = k1 + t[6];
         dcol[3 * (size_t)g + 2] = k2 + t[7];
@@ -1228,21 +1230,20 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const GradSt
     return hipGetLastError();
 }
 
-hipError_t launch_pair_grad_reduce(int n, const void* recs, const GradSlots& gs, float* dmean,
-                                   float* dcov, float* dcol, float* dalpha, hipStream_t st) {
+hipError_t launch_pair_grad_reduce(int n, const GradSlots& gs, float* dmean, float* dcov,
+                                   float* dcol, float* dalpha, hipStream_t st) {
     if (n <= 0) return hipSuccess;
-    const auto* rc = static_cast<const BlendRec*>(recs);
     // 8-lane rows when a Gaussian averages at most 64 slots (one flag load per
     // lane); word-sized flag groups beyond 256 slots per Gaussian
     if (gs.slots <= 64ull * (uint64_t)n)
         hipLaunchKernelGGL((pair_grad_reduce_kernel<8, 8>), dim3((unsigned)((n + 31) / 32)),
-                           dim3(256), 0, st, n, rc, gs, dmean, dcov, dcol, dalpha);
+                           dim3(256), 0, st, n, gs, dmean, dcov, dcol, dalpha);
     else if (gs.slots <= 256ull * (uint64_t)n)
         hipLaunchKernelGGL((pair_grad_reduce_kernel<16, 8>), dim3((unsigned)((n + 15) / 16)),
-                           dim3(256), 0, st, n, rc, gs, dmean, dcov, dcol, dalpha);
+                           dim3(256), 0, st, n, gs, dmean, dcov, dcol, dalpha);
     else
         hipLaunchKernelGGL((pair_grad_reduce_kernel<16, 64>), dim3((unsigned)((n + 15) / 16)),
-                           dim3(256), 0, st, n, rc, gs, dmean, dcov, dcol, dalpha);
+                           dim3(256), 0, st, n, gs, dmean, dcov, dcol, dalpha);
     return hipGetLastError();
 }
 

@@ -746,6 +746,18 @@ int gsr_tile_row_pairs(int n, const float* mean2d, const float* cov2d, int heigh
     return GSR_OK;
 }
 
+int gsr_tiles_touch(int n, const float* mean2d, const float* cov2d, int height, int width,
+                    const int32_t* sat, uint8_t* flags, void* stream) {
+    GSR_REQUIRE(n >= 0, "n must be non-negative");
+    if (int rc = check_screen(height, width)) return rc;
+    if (n == 0) return GSR_OK;
+    GSR_REQUIRE(mean2d && cov2d && sat && flags, "null pointer");
+    GSR_HIP(gsr::launch_tiles_touch(n, mean2d, cov2d, height, width, sat, flags,
+                                    as_stream(stream)),
+            "tiles touch");
+    return GSR_OK;
+}
+
 int gsr_rasterize_status(void* bin_ws, size_t bin_ws_bytes, void* stream) {
     (void)bin_ws;
     (void)bin_ws_bytes;
@@ -861,8 +873,7 @@ int rasterize_backward(int n, int height, int width, const float* grad_img,
                 "backward: blend");
     }
     StageTimer timer("grad_reduce", st);
-    GSR_HIP(gsr::launch_pair_grad_reduce(n, at<void>(ws, L.recs), gs, d_mean2d, d_cov2d, d_colors,
-                                         d_alpha, st),
+    GSR_HIP(gsr::launch_pair_grad_reduce(n, gs, d_mean2d, d_cov2d, d_colors, d_alpha, st),
             "backward: gradient sums");
     return GSR_OK;
 }

@@ -217,6 +217,10 @@ hipError_t launch_range_keys(int T, const int32_t* ranges, const int32_t* ids, c
 // entries of room; tiles_y <= 4096).
 hipError_t launch_row_pairs(int n, const float* mean2d, const float* cov2d, int H, int W,
                             uint64_t* rows, hipStream_t st);
+// flags[i]: Gaussian i's tile rectangle, widened by one tile row each way,
+// holds a tile marked in the summed-area table sat ((tiles_y+1) x (tiles_x+1)).
+hipError_t launch_tiles_touch(int n, const float* mean2d, const float* cov2d, int H, int W,
+                              const int32_t* sat, uint8_t* flags, hipStream_t st);
 // counts[g], packed tile rect, depth key (float bits or 0xffffffff when the
 // Gaussian touches no tile) and identity values, the digit histograms of the
 // 4-pass depth sort (depth_hist), and either the digit histograms of the tile
@@ -330,10 +334,10 @@ hipError_t launch_blend_bwd(int n, int H, int W, const float* grad, const GradSt
                             float* dcov, float* dcol, float* dalpha, const GradSlots& gs,
                             const uint32_t* order, hipStream_t st);
 
-// outputs += the per-Gaussian sums of the flagged slots (conic gradient
-// converted to the covariance gradient after the sum).
-hipError_t launch_pair_grad_reduce(int n, const void* recs, const GradSlots& gs, float* dmean,
-                                   float* dcov, float* dcol, float* dalpha, hipStream_t st);
+// outputs += the per-Gaussian sums of the flagged slots (each slot holds its
+// (tile, entry)'s covariance gradient, converted from the conic's in the blend).
+hipError_t launch_pair_grad_reduce(int n, const GradSlots& gs, float* dmean, float* dcov,
+                                   float* dcol, float* dalpha, hipStream_t st);
 
 // ---- training loss (gsr_loss.hip) ----
 // Work-group partial sums of the loss's forward kernel for an H x W image

@@ -165,6 +165,18 @@ int gsr_calibrate_valu(int kind, int iters, float* out, void* stream);
 int gsr_tile_row_pairs(int n, const float* mean2d, const float* cov2d, int height, int width,
                        uint64_t* rows, void* stream);
 
+/* No counterpart in the reference (screen-band support, like
+ * gsr_tile_row_pairs): flags[i] = 1 when Gaussian i's tile rectangle, formed
+ * as gsr_rasterize_bin forms it on the height x width frame and widened by one
+ * tile row above and below, holds a marked tile, else 0.  `sat` (device) is
+ * the summed-area table of the marked tiles: (ceil(height / 16) + 1) x
+ * (ceil(width / 16) + 1) int32, row-major, its first row and column zero.  The
+ * widening makes the flagged set cover every Gaussian that a render of a band
+ * of whole tile rows (means moved up by the band's first row) bins into a
+ * marked tile. */
+int gsr_tiles_touch(int n, const float* mean2d, const float* cov2d, int height, int width,
+                    const int32_t* sat, uint8_t* flags, void* stream);
+
 /* Replaces launch_backward_rasterization (csrc/backward/rasterize_backward.h:5,
  * csrc/backward/rasterize_backward.cu:239-309; bound as
  * `backwards_rasterization` at csrc/bindings.cpp:72-100,147).  num_pairs is

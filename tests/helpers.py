@@ -119,3 +119,60 @@ def assert_grad_close(got, want, absum, what: str, rel: float = 1e-4,
         tot = float(np.linalg.norm((got - want).ravel()) / den)
         assert tot <= rel, f"{what}: tensor relative error {tot:.3e} > {rel}"
     return (float(err.max()) if err.size else 0.0), tot
+
+
+PARAMS = ("mu", "q", "s", "alpha", "A", "k_j")
+
+
+def rel_error(x, ref) -> float:
+    den = np.linalg.norm(ref.ravel())
+    return float(np.linalg.norm((x - ref).ravel()) / den) if den > 0 else 0.0
+
+
+def oracle_chain(a: dict, G, want: dict) -> dict:
+    """The six parameter gradients of dL/dimage G through the oracle chain
+    (blend backward, SH backward, projection backward, sigmoid backward) on the
+    oracle's fp32 forward ``want``, evaluated in float32 and in float64:
+    {np.float32: {name: array}, np.float64: {...}}."""
+    H, W = a["H"], a["W"]
+    chains = {}
+    for dt in (np.float32, np.float64):
+        dm, dc, dcol, dal = orc.blend_bwd(G, want["mean2d"], want["cov2d"], want["colors"],
+                                          a["alpha"], want["ids"], want["ranges"],
+                                          want["final_T"], want["n_contrib"], H, W, dtype=dt)
+        dA, dkj, dmu_sh = orc.sh_bwd(dcol.astype(dt), a["mu"], a["A"], a["kj"], a["cam"], dtype=dt)
+        dmu_p, dq, ds = orc.project_bwd(dm.astype(dt), dc.astype(dt), a["mu"], a["q"], a["s"],
+                                        a["R"], a["t"], a["fx"], a["fy"], a["cx"], a["cy"], dtype=dt)
+        sig = a["alpha"].astype(np.float64)
+        chains[dt] = {"mu": dmu_p.astype(np.float64) + dmu_sh, "q": dq, "s": ds,
+                      "alpha": np.asarray(dal, np.float64) * sig * (1.0 - sig), "A": dA, "k_j": dkj}
+    return chains
+
+
+def chain_failures(grads: dict, chains: dict, tag: str) -> list[str]:
+    """GPU parameter gradients (name -> float array) against the oracle chain:
+    each tensor's relative error to the float64 chain within max(1e-4, 1.5x the
+    fp32 chain's own), each element within 1e-4 of the tensor's largest element
+    or within twice the fp32 chain's own error on it (a tensor that is zero in
+    exact arithmetic, whose fp32 chain is all rounding noise, within twice the
+    fp32 chain's largest error).  Prints each tensor's figures; returns the
+    failures."""
+    fails = []
+    for name in PARAMS:
+        got = np.asarray(grads[name], np.float64)
+        w64 = np.asarray(chains[np.float64][name], np.float64).reshape(got.shape)
+        w32 = np.asarray(chains[np.float32][name], np.float64).reshape(got.shape)
+        tot, own = rel_error(got, w64), rel_error(w32, w64)
+        diff, own_el = np.abs(got - w64), np.abs(w32 - w64)
+        top = np.abs(w64).max()
+        if own > 1.0:
+            bar = np.full(diff.shape, 2.0 * own_el.max())
+        else:
+            bar = np.maximum(1e-4 * top, 2.0 * own_el)
+        bad = diff > bar
+        print(f"[gpu] {tag} d_{name}: tensor relative error {tot:.2e} (fp32 chain {own:.2e}); "
+              f"max |x| {top:.2e}, max |got - fp64| {diff.max():.2e} (fp32 chain "
+              f"{own_el.max():.2e}), elements beyond the bar: {int(bad.sum())}", flush=True)
+        fails += [f"{tag} d_{name}: tensor {tot:.3e}"] if tot > max(1e-4, 1.5 * own) else []
+        fails += [f"{tag} d_{name}: {int(bad.sum())} elements"] if bad.any() else []
+    return fails

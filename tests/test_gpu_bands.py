@@ -11,12 +11,16 @@ error, and the banded frame is checked by size-independent properties.
 
 from __future__ import annotations
 
+import importlib
+import math
+
 import numpy as np
 import pytest
 import torch
 
 from gaussian_splatting import synthetic
 from gaussian_splatting.rasterizer import RasterizeFunction, rasterize, rasterize_bands
+from gaussian_splatting.rasterizer import bands as bands_mod
 from gaussian_splatting.rasterizer.bands import (BAND_PAIR_BUDGET, MAX_BAND_PAIRS, band_rows,
                                                   plan_bands)
 from helpers import assert_bitwise, assert_grad_close, oracle_forward, scene_arrays
@@ -24,6 +28,9 @@ from oracle import oracle as orc
 from test_gpu_parity import _np, gpu_forward
 
 pytestmark = pytest.mark.gpu
+
+# the glue module (the package exports its rasterize function under the same name)
+glue = importlib.import_module("gaussian_splatting.rasterizer.rasterize")
 
 NAMES = ("mu", "q", "s", "alpha", "A", "k_j")
 
@@ -189,6 +196,113 @@ def test_planned_bands_equal_the_whole_frame(crc, device):
         assert err <= 1e-6, f"d {nm}: {err:.2e}"
 
 
+def test_tiles_touch_flags_the_gaussians_of_marked_tiles(crc, device):
+    """tiles_touch against the oracle's tile rectangles widened by a tile row
+    each way, Gaussian by Gaussian, on a seeded mask; every Gaussian the
+    rasterizer bins into a marked tile is flagged, whole frame and a band
+    rendered from moved means; an empty mask flags none."""
+    sc = synthetic.config_scene("c3", device=device, n=20_000, width=480, height=272)
+    g, view = sc.gaussians, sc.view
+    H, W, ty, tx = 272, 480, 17, 30
+    n, m2, c2, d, col = _project(crc, g, view)
+    mask = torch.rand(ty, tx, generator=torch.Generator().manual_seed(5)) < 0.1
+    got = crc.tiles_touch(n, m2, c2, H, W, mask.to(device)).cpu().numpy()
+    _, rect = orc.bin_count(_np(m2), _np(c2), H, W)
+    mk = mask.numpy()
+    want = np.array([x1 > x0 and bool(mk[max(0, y0 - 1):min(ty, y1 + 1), x0:x1].any())
+                     for x0, x1, y0, y1 in rect])
+    assert got.dtype == np.bool_ and np.array_equal(got, want)
+    op = torch.sigmoid(g.alpha.detach())
+    out = crc.rasterize(n, d, m2, c2, col, op, H, W)
+    ids, rng = _np(out[1]), _np(out[2]).reshape(-1, 2)
+    listed = np.concatenate([ids[a:b] for a, b in rng[mk.reshape(-1)]])
+    assert listed.size > 0 and got[listed].all()
+    y0, h = 96, 96  # a band: rows 6..11, means moved up by 96
+    band = crc.rasterize(n, d, m2 - m2.new_tensor([0.0, 96.0]), c2, col, op, h, W)
+    ids_b, rng_b = _np(band[1]), _np(band[2]).reshape(-1, 2)
+    listed_b = np.concatenate([ids_b[a:b] for a, b in rng_b[mk[6:12].reshape(-1)]])
+    assert listed_b.size > 0 and got[listed_b].all()
+    none = crc.tiles_touch(n, m2, c2, H, W, torch.zeros(ty, tx, dtype=torch.bool, device=device))
+    assert not none.any()
+
+
+class _TailCapture:
+    """Stands in for the extension module: records the four rasterize-backward
+    gradients (d mean2d, d cov2d, d colour, d opacity) that the glue hands to
+    the fused tail, backwards_project_sh, and calls it."""
+
+    def __init__(self, mod):
+        self._mod = mod
+        self.last = None
+
+    def __getattr__(self, name):
+        return getattr(self._mod, name)
+
+    def backwards_project_sh(self, *args):
+        self.last = [args[k].detach().clone() for k in (0, 1, 2, 13)]
+        return self._mod.backwards_project_sh(*args)
+
+
+def test_depth_prefix_equals_the_whole_frame(crc, device, monkeypatch):
+    """rasterize_bands in depth-prefix mode (a share of the depth order on the
+    whole screen, then the Gaussians of the tiles it left unfinished) against
+    rasterize, on c5's distributions at 1M Gaussians and 480x272 (a pixel's
+    coverage depends on the Gaussian count, not on the resolution, so tiles
+    finish as in c5's full frame), with a seeded N(0, 1) dL/dimage: a prefix of
+    0.3 with one band per pass, and 0.1 with an eighth of the frame's pairs as
+    the band budget (passes in bands), both passes owning tiles.  The image bit
+    for bit rasterize's.  The rasterize-backward gradients the glue hands to
+    the fused tail (d mean2d, d cov2d, d colour, d opacity) are the same
+    per-(tile, entry) terms summed in another order (the passes' sums added per
+    Gaussian): each element within 2e-5 of its sum of |terms| (the oracle's,
+    float64) of rasterize's, each tensor within 1e-5 relative.  rasterize's own
+    oracle parity is held by the full-size tests."""
+    sc = synthetic.config_scene("c5", device=device, n=1_000_000, width=480, height=272)
+    g, view = sc.gaussians, sc.view
+    a = scene_arrays(sc)
+    n, m2, c2, d, col = _project(crc, g, view)
+    rows = crc.tile_row_pairs(n, m2, c2, 272, 480).cpu().tolist()
+    G = synthetic.grad_image(272, 480, seed=3)
+    Gd = G.to(device)
+    cap = _TailCapture(glue.crc)
+    monkeypatch.setattr(glue, "crc", cap)
+
+    def run(render):
+        for nm in NAMES:
+            getattr(g, nm).grad = None
+        img = render()
+        img.backward(Gd)
+        torch.cuda.synchronize()
+        return img.detach().clone(), [_np(x) for x in cap.last]
+
+    want = oracle_forward(a)
+    args = (G.numpy(), want["mean2d"], want["cov2d"], want["colors"], a["alpha"], want["ids"],
+            want["ranges"], want["final_T"], want["n_contrib"], 272, 480)
+    absum = orc.blend_bwd(*args, with_abs=True)[4:]
+    names = ("d_mean2d", "d_cov2d", "d_colors", "d_alpha")
+
+    wi, wb = run(lambda: rasterize(g, view))
+    assert np.abs(_np(wi) - want["img"]).max() <= 1e-5
+    for prefix, bands in ((0.3, 1), (0.1, 3)):
+        budget = BAND_PAIR_BUDGET if bands == 1 else max(max(rows), sum(rows) // 8)
+        pi, pb = run(lambda: rasterize_bands(g, view, max_pairs=budget, depth_prefix=prefix))
+        st = dict(bands_mod.last_stats)
+        print(f"[gpu] depth prefix {prefix}: {st}", flush=True)
+        assert st["prefix"] == math.ceil(n * prefix)
+        assert 0 < st["open_tiles"] < st["tiles"] and st["second_pairs"] > 0
+        assert 0 < st["second_gaussians"] < n
+        if bands > 1:
+            assert st["first_bands"] + st["second_bands"] > 2
+        assert_bitwise(_np(pi), _np(wi), f"image (prefix {prefix})")
+        for x, y, ab, nm in zip(pb, wb, absum, names):
+            x, y = x.reshape(ab.shape).astype(np.float64), y.reshape(ab.shape).astype(np.float64)
+            scaled = np.abs(x - y) / np.maximum(ab, 1e-30)
+            rel = np.linalg.norm(x - y) / max(np.linalg.norm(y), 1e-30)
+            print(f"[gpu] prefix {prefix}: {nm} against rasterize's: relative {rel:.2e}, "
+                  f"max |diff| / sum|terms| {scaled.max():.2e}", flush=True)
+            assert scaled.max() <= 2e-5 and rel <= 1e-5, nm
+
+
 def test_backward_accumulate_equals_the_band_sums(crc, device):
     """backwards_rasterization_accumulate (one set of outputs, each band
     added in place) against each band's own backward summed in torch in the
@@ -243,13 +357,15 @@ def test_bands_without_gaussians(device):
         assert err <= 1e-6, f"d {nm}: {err:.2e}"
 
 
-def test_c5_full_size_in_screen_bands(crc, device):
+def test_c5_full_size_in_screen_bands(crc, device, monkeypatch):
     """Config c5 at full size.  The whole frame needs more pairs than int32
     lists hold and is refused; in 256-row bands every band fits and the pairs
     add up to more than 2^31; the pairs per tile row add up to each band's;
-    the planned bands are fewer and each within the limit; the planned frame's
-    image is finite and in [0, 1], and its gradients are finite and
-    deterministic."""
+    the planned bands are fewer and each within the limit; the frame rendered
+    by default (depth-prefix mode) has a finite image in [0, 1] and finite,
+    deterministic gradients, and its image is bit for bit the planned bands'
+    render of every Gaussian (the rasterize backward's sums within 1e-5
+    relative, the parameter gradients within 1e-3)."""
     print("[gpu] c5 full size: 5M Gaussians, 3840x2160", flush=True)
     sc = synthetic.config_scene("c5", device=device)
     g, view = sc.gaussians, sc.view
@@ -282,15 +398,23 @@ def test_c5_full_size_in_screen_bands(crc, device):
     assert max(planned) <= BAND_PAIR_BUDGET < MAX_BAND_PAIRS and len(plan) < len(pairs)
     del m2, c2, d, col
 
-    def frame():
+    cap = _TailCapture(glue.crc)
+    monkeypatch.setattr(glue, "crc", cap)
+
+    def frame(depth_prefix=None):
         for nm in NAMES:
             getattr(g, nm).grad = None
-        img = rasterize_bands(g, view)
+        img = rasterize_bands(g, view, depth_prefix=depth_prefix)
         img.sum().backward()
         torch.cuda.synchronize()
-        return img.detach(), [getattr(g, nm).grad.clone() for nm in NAMES]
+        return img.detach(), [getattr(g, nm).grad.clone() for nm in NAMES] + cap.last
 
+    # the default: depth-prefix rendering (the frame needs several bands)
     img, g1 = frame()
+    st = dict(bands_mod.last_stats)
+    print(f"[gpu] c5 depth-prefix frame: {st}", flush=True)
+    assert st["prefix"] == math.ceil(n * bands_mod.PREFIX_FRACTION)
+    assert st["first_pairs"] + st["second_pairs"] < sum(planned) // 2
     assert img.shape == (2160, 3840, 3)
     assert torch.isfinite(img).all() and img.min() >= 0 and img.max() <= 1
     assert img.max() > 0
@@ -301,7 +425,24 @@ def test_c5_full_size_in_screen_bands(crc, device):
     assert torch.equal(img, img2)
     for x, y, nm in zip(g1, g2, NAMES):
         assert torch.equal(x, y), nm
-    del img, img2, g1, g2
+    del img2, g2
+    # every Gaussian in every planned band: the same image bit for bit, the
+    # same gradients up to the order of their sums
+    print("[gpu] c5 frame in the planned bands without the depth prefix", flush=True)
+    img0, g0 = frame(depth_prefix=0.0)
+    assert bands_mod.last_stats["prefix"] == 0 and bands_mod.last_stats["bands"] == len(plan)
+    assert torch.equal(img, img0)
+    blend = ("mean2d", "cov2d", "colors", "alpha (rasterize)")
+    for got, want, nm in zip(g1, g0, NAMES + blend):
+        err = float((got - want).norm() / want.norm().clamp_min(1e-30))
+        print(f"[gpu] c5 d {nm}: prefix vs plain relative error {err:.2e}", flush=True)
+        # the rasterize backward's sums within 1e-5; the parameter gradients
+        # within 1e-3: a needle-shaped splat's d cov2d cancels to ~1e-6 of its
+        # sum of |terms|, so the order of an fp32 sum moves it by up to ~10%,
+        # and the projection backward carries that into d q and d s (the
+        # tensors differ by ~1e-4 between the two orders of the same terms)
+        assert err <= (1e-5 if nm in blend else 1e-3), f"d {nm}: {err:.2e}"
+    del img, img0, g1, g0
     torch.cuda.empty_cache()
 
 

@@ -24,7 +24,8 @@ import pytest
 import torch
 
 from gaussian_splatting import synthetic
-from helpers import assert_grad_close, oracle_forward, scene_arrays
+from helpers import (PARAMS, assert_grad_close, chain_failures, oracle_chain,
+                     oracle_forward, scene_arrays)
 from oracle import oracle as orc
 from test_gpu_parity import _check_forward, _dev, _np, gpu_forward
 
@@ -70,11 +71,6 @@ def test_full_size_forward_and_backward(crc, device, name, make):
               f"fp32 oracle {o99:.1e}/{omax:.1e}", flush=True)
 
 
-def _rel(x, ref):
-    den = np.linalg.norm(ref.ravel())
-    return float(np.linalg.norm((x - ref).ravel()) / den) if den > 0 else 0.0
-
-
 GLUE = [
     ("bench_100k_1920x1080_sum", lambda d: synthetic.bench_scene(n=100_000, width=1920,
                                                                 height=1080, device=d), False),
@@ -116,36 +112,7 @@ def test_full_size_glue_path_parameter_gradients(device, name, make, randn):
     assert np.abs(gi - want["img"]).max() <= 1e-5
     print(f"[gpu] {name} image: {np.mean(gi == want['img']) * 100:.4f}% bit for bit, max |diff| "
           f"{np.abs(gi - want['img']).max():.1e}", flush=True)
-    chains = {}
-    for dt in (np.float32, np.float64):
-        dm, dc, dcol, dal = orc.blend_bwd(G, want["mean2d"], want["cov2d"], want["colors"],
-                                          a["alpha"], want["ids"], want["ranges"],
-                                          want["final_T"], want["n_contrib"], H, W, dtype=dt)
-        dA, dkj, dmu_sh = orc.sh_bwd(dcol.astype(dt), a["mu"], a["A"], a["kj"], a["cam"], dtype=dt)
-        dmu_p, dq, ds = orc.project_bwd(dm.astype(dt), dc.astype(dt), a["mu"], a["q"], a["s"],
-                                        a["R"], a["t"], a["fx"], a["fy"], a["cx"], a["cy"], dtype=dt)
-        sig = a["alpha"].astype(np.float64)
-        chains[dt] = {"mu": dmu_p.astype(np.float64) + dmu_sh, "q": dq, "s": ds,
-                      "alpha": np.asarray(dal, np.float64) * sig * (1.0 - sig), "A": dA, "k_j": dkj}
-    fails, tag = [], name
-    for name in ("mu", "q", "s", "alpha", "A", "k_j"):
-        got = _np(getattr(g, name).grad).astype(np.float64)
-        w64 = np.asarray(chains[np.float64][name], np.float64).reshape(got.shape)
-        w32 = np.asarray(chains[np.float32][name], np.float64).reshape(got.shape)
-        tot, own = _rel(got, w64), _rel(w32, w64)
-        diff, own_el = np.abs(got - w64), np.abs(w32 - w64)
-        top = np.abs(w64).max()
-        if own > 1.0:
-            # zero in exact arithmetic: rounding noise, held to the fp32 chain's
-            bar = np.full(diff.shape, 2.0 * own_el.max())
-        else:
-            # 1e-4 of the tensor's largest element, or twice the fp32 chain's
-            # own error on the element
-            bar = np.maximum(1e-4 * top, 2.0 * own_el)
-        bad = diff > bar
-        print(f"[gpu] {tag} d_{name}: tensor relative error {tot:.2e} (fp32 chain {own:.2e}); "
-              f"max |x| {top:.2e}, max |got - fp64| {diff.max():.2e} (fp32 chain {own_el.max():.2e}), "
-              f"elements beyond the bar: {int(bad.sum())}", flush=True)
-        fails += [f"d_{name}: tensor {tot:.3e}"] if tot > max(1e-4, 1.5 * own) else []
-        fails += [f"d_{name}: {int(bad.sum())} elements"] if bad.any() else []
+    chains = oracle_chain(a, G, want)
+    grads = {nm: _np(getattr(g, nm).grad).astype(np.float64) for nm in PARAMS}
+    fails = chain_failures(grads, chains, name)
     assert not fails, fails
