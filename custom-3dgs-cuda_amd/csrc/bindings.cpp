@@ -198,7 +198,7 @@ Tensor spherical_harmonics(int total_gaussians, const Tensor camera_position,
 std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_impl(
     int num_gaussians, const Tensor& depths, const Tensor& mean_2d, const Tensor& cov_2d,
     const Tensor& colors, const Tensor& alpha, int height, int width, bool want_keys,
-    const Tensor* order = nullptr) {
+    const Tensor* order = nullptr, const Tensor* tile_skip = nullptr) {
     TORCH_CHECK(height >= 0 && width >= 0, "height and width must be non-negative");
     auto device = mean_2d.device();
     auto float_options = torch::TensorOptions().dtype(torch::kFloat32).device(device);
@@ -236,6 +236,14 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_impl(
         TORCH_CHECK(order->scalar_type() == torch::kInt32 && order->numel() == num_gaussians,
                     "order must be an int32 tensor of N elements");
     }
+    if (tile_skip) {
+        TORCH_CHECK(tile_skip->is_cuda() && tile_skip->device() == mean_2d.device(),
+                    "tile_skip must be a CUDA tensor on mean_2d's device");
+        TORCH_CHECK(tile_skip->is_contiguous() && tile_skip->numel() == tiles &&
+                        (tile_skip->scalar_type() == torch::kUInt8 ||
+                         tile_skip->scalar_type() == torch::kBool),
+                    "tile_skip must be a contiguous uint8 or bool tensor of one entry per tile");
+    }
 
     c10::hip::HIPGuardMasqueradingAsCUDA guard(device);
     void* st = current_stream();
@@ -261,6 +269,17 @@ std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_impl(
     Tensor final_T = torch::empty({height, width}, float_options);
     Tensor n_contrib = torch::empty({height, width}, int_options);
     Tensor sorted_keys = want_keys ? torch::empty({m}, key_options) : torch::empty({0}, key_options);
+    if (tile_skip) {
+        check_rc(gsr_rasterize_render_skip(
+                     num_gaussians, cfp(depths), cfp(mean_2d), cfp(cov_2d), cfp(colors),
+                     cfp(alpha), height, width, bin_ws.data_ptr(), (size_t)bin_ws.numel(), m,
+                     sort_ws.data_ptr(), (size_t)sort_ws.numel(),
+                     static_cast<const uint8_t*>(tile_skip->data_ptr()),
+                     sorted_ids.data_ptr<int32_t>(), tile_ranges.data_ptr<int32_t>(),
+                     fp(rendered_img), fp(final_T), n_contrib.data_ptr<int32_t>(), st),
+                 "rasterize_ordered");
+        return {rendered_img, sorted_ids, tile_ranges, final_T, n_contrib, sorted_keys};
+    }
     check_rc(gsr_rasterize_render(
                  num_gaussians, cfp(depths), cfp(mean_2d), cfp(cov_2d), cfp(colors), cfp(alpha),
                  height, width, bin_ws.data_ptr(), (size_t)bin_ws.numel(), m,
@@ -313,12 +332,15 @@ Tensor depth_order(int num_gaussians, const Tensor& depths) {
 }
 
 // Not in the reference surface: `rasterize` with the depth order given (from
-// depth_order) instead of sorted per call.
+// depth_order) instead of sorted per call; with tile_skip (one uint8 or bool
+// per tile) the lists of the marked tiles may be left empty
+// (gsr_rasterize_render_skip).
 std::tuple<Tensor, Tensor, Tensor, Tensor, Tensor> rasterize_ordered(
     int num_gaussians, const Tensor order, const Tensor depths, const Tensor mean_2d,
-    const Tensor cov_2d, const Tensor colors, const Tensor alpha, int height, int width) {
+    const Tensor cov_2d, const Tensor colors, const Tensor alpha, int height, int width,
+    const c10::optional<Tensor>& tile_skip) {
     auto r = rasterize_impl(num_gaussians, depths, mean_2d, cov_2d, colors, alpha, height, width,
-                            false, &order);
+                            false, &order, tile_skip.has_value() ? &*tile_skip : nullptr);
     return {std::get<0>(r), std::get<1>(r), std::get<2>(r), std::get<3>(r), std::get<4>(r)};
 }
 
@@ -844,7 +866,11 @@ PYBIND11_MODULE(custom_rasterizer_cuda, m) {
     m.def("depth_order", &depth_order,
           "every Gaussian stably sorted by the float bits of its depth (int32 [N])");
     m.def("rasterize_ordered", &rasterize_ordered,
-          "rasterize with a depth order from depth_order (screen bands of one frame)");
+          "rasterize with a depth order from depth_order (screen bands of one frame); with "
+          "tile_skip the lists of the marked tiles may be left empty",
+          py::arg("num_gaussians"), py::arg("order"), py::arg("depths"), py::arg("mean_2d"),
+          py::arg("cov_2d"), py::arg("colors"), py::arg("alpha"), py::arg("height"),
+          py::arg("width"), py::arg("tile_skip") = py::none());
     m.def("rasterize_with_keys", &rasterize_with_keys,
           "rasterize, also returning the sorted 64-bit keys (tile << 32 | depth bits)");
     m.def("library_version", []() { return std::string(gsr_version()); });

@@ -605,12 +605,12 @@ size_t gsr_sort_workspace_bytes(int64_t num_pairs, int n, int height, int width)
     return sort_layout(num_pairs, tile_passes(T), T, n, height, width).end;
 }
 
-int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const float* cov2d,
-                         const float* colors, const float* alpha, int height, int width,
-                         void* bin_ws, size_t bin_ws_bytes, int64_t num_pairs, void* sort_ws,
-                         size_t sort_ws_bytes, int32_t* sorted_ids, int32_t* tile_ranges,
-                         float* img, float* final_T, int32_t* n_contrib, uint64_t* sorted_keys,
-                         void* stream) {
+static int rasterize_render(int n, const float* depth, const float* mean2d, const float* cov2d,
+                            const float* colors, const float* alpha, int height, int width,
+                            void* bin_ws, size_t bin_ws_bytes, int64_t num_pairs, void* sort_ws,
+                            size_t sort_ws_bytes, int32_t* sorted_ids, int32_t* tile_ranges,
+                            float* img, float* final_T, int32_t* n_contrib,
+                            uint64_t* sorted_keys, const uint8_t* tile_skip, void* stream) {
     GSR_REQUIRE(n >= 0, "n must be non-negative");
     if (int rc = check_screen(height, width)) return rc;
     GSR_REQUIRE(num_pairs >= 0 && num_pairs <= kMaxPairs, "num_pairs out of range");
@@ -671,6 +671,7 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                 tb.ranges = tile_ranges;
                 tb.ids = ids;
                 tb.err = dg.status;
+                tb.skip = reinterpret_cast<const uint8_t*>(tile_skip);
                 tb.rec_mean2d = mean2d;
                 tb.rec_cov2d = cov2d;
                 tb.rec_colors = colors;
@@ -732,6 +733,29 @@ int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const f
                                   n_contrib, order, st),
             "rasterize: blend");
     return GSR_OK;
+}
+
+int gsr_rasterize_render(int n, const float* depth, const float* mean2d, const float* cov2d,
+                         const float* colors, const float* alpha, int height, int width,
+                         void* bin_ws, size_t bin_ws_bytes, int64_t num_pairs, void* sort_ws,
+                         size_t sort_ws_bytes, int32_t* sorted_ids, int32_t* tile_ranges,
+                         float* img, float* final_T, int32_t* n_contrib, uint64_t* sorted_keys,
+                         void* stream) {
+    return rasterize_render(n, depth, mean2d, cov2d, colors, alpha, height, width, bin_ws,
+                            bin_ws_bytes, num_pairs, sort_ws, sort_ws_bytes, sorted_ids,
+                            tile_ranges, img, final_T, n_contrib, sorted_keys, nullptr, stream);
+}
+
+int gsr_rasterize_render_skip(int n, const float* depth, const float* mean2d, const float* cov2d,
+                              const float* colors, const float* alpha, int height, int width,
+                              void* bin_ws, size_t bin_ws_bytes, int64_t num_pairs,
+                              void* sort_ws, size_t sort_ws_bytes, const uint8_t* tile_skip,
+                              int32_t* sorted_ids, int32_t* tile_ranges, float* img,
+                              float* final_T, int32_t* n_contrib, void* stream) {
+    GSR_REQUIRE(tile_skip, "tile_skip must not be null");
+    return rasterize_render(n, depth, mean2d, cov2d, colors, alpha, height, width, bin_ws,
+                            bin_ws_bytes, num_pairs, sort_ws, sort_ws_bytes, sorted_ids,
+                            tile_ranges, img, final_T, n_contrib, nullptr, tile_skip, stream);
 }
 
 int gsr_tile_row_pairs(int n, const float* mean2d, const float* cov2d, int height, int width,

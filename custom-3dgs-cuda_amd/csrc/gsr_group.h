@@ -178,12 +178,13 @@ __device__ void bin_finish_body(const BinFinish& f, uint32_t* s_w, uint32_t* s_v
 
 // ranges[t] = [start, start + count) from the tile totals in tile order,
 // (0, 0) for tiles without pairs (rasterize.cu:140-166); a grand total other
-// than m sets err bit 2.  One work-group of kT threads; s_w holds kT / 64 words.
+// than m (above m, with at_most: skipped tiles' lists stay empty) sets err bit 2.  One work-group of kT threads; s_w holds kT / 64 words.
 // Each thread takes 8 consecutive tiles per step, their loads issued together
 // (8192 tiles, 1080p's 8160, in one step of 1024 threads).
 template <int kT>
 __device__ void tile_starts_body(int T, const uint32_t* __restrict__ ttotal, uint64_t m,
-                                 int2* __restrict__ ranges, int* err, uint32_t* s_w) {
+                                 int2* __restrict__ ranges, int* err, uint32_t* s_w,
+                                 bool at_most = false) {
     constexpr int kItems = 8;
     const int tid = threadIdx.x;
     uint32_t carry = 0;
@@ -212,7 +213,7 @@ __device__ void tile_starts_body(int T, const uint32_t* __restrict__ ttotal, uin
         }
         carry += tot;
     }
-    if (tid == 0 && (uint64_t)carry != m) atomicOr(err, 2);
+    if (tid == 0 && (at_most ? (uint64_t)carry > m : (uint64_t)carry != m)) atomicOr(err, 2);
 }
 
 }  // namespace gsr

@@ -198,6 +198,9 @@ struct TileBinning {
     int32_t* ranges = nullptr;              // out: [tiles][2]
     uint32_t* ids = nullptr;                // out: sorted ids (m)
     int* err = nullptr;                     // bit 2: inconsistent counts
+    // optional: tiles (nonzero) whose lists stay empty; the lists then hold
+    // fewer than m entries
+    const uint8_t* skip = nullptr;
     // optional: the blend records (n) from these, formed in extra work-groups
     // of the level-1 count kernel's launch (independent work, one launch fewer)
     const float* rec_mean2d = nullptr;

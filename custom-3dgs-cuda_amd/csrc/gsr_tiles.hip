@@ -386,14 +386,25 @@ __device__ __forceinline__ SegInfo seg_info(uint32_t k, const uint32_t* __restri
     return I;
 }
 
+// Whether the block's tile of this lane (lane t: tile t of the 8 x 8 block at
+// (ox, oy)) is on the screen and its list is to be built: skip (optional) marks
+// tiles whose lists stay empty.
+__device__ __forceinline__ bool lane_tile_live(const BlockGrid& bg, int ox, int oy,
+                                               const uint8_t* __restrict__ skip) {
+    const int lane = lane_id();
+    const int tx = ox + (lane & 7), ty = oy + (lane >> 3);
+    const bool on = tx < bg.tiles_x && ty < bg.tiles_y;
+    return on && !(skip && skip[(size_t)ty * bg.tiles_x + tx]);
+}
+
 // tcount[k * 64 + t] = entries of segment k covering the block's tile t
-// (rows[t / 8] & cols[t % 8]).  Segments k < seg_start[nb] (at most
-// seg_cap), grid-strided.
+// (rows[t / 8] & cols[t % 8]; 0 for a skipped tile).  Segments k <
+// seg_start[nb] (at most seg_cap), grid-strided.
 __global__ __launch_bounds__(kThreads) void tile_count_kernel(
     int n, BlockGrid bg, const uint32_t* __restrict__ seg_owner,
     const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ block_start,
     const uint32_t* __restrict__ lists, uint64_t cap, const uint16_t* __restrict__ lrects,
-    uint32_t seg_cap, uint32_t* __restrict__ tcount) {
+    uint32_t seg_cap, uint32_t* __restrict__ tcount, const uint8_t* __restrict__ skip) {
     const uint32_t nseg = min(uniform(seg_start[bg.nb]), seg_cap);
     const uint32_t stride = gridDim.x * kWavesPer;
     const int lane = lane_id();
@@ -409,7 +420,8 @@ __global__ __launch_bounds__(kThreads) void tile_count_kernel(
             colv = (lane == j) ? c : colv;
         }
         const uint64_t m = lane_u64(rowv, lane >> 3) & lane_u64(colv, lane & 7);
-        tcount[(size_t)k * kWave + lane] = (uint32_t)popc64(m);
+        const bool keep = !skip || lane_tile_live(bg, I.ox, I.oy, skip);
+        tcount[(size_t)k * kWave + lane] = keep ? (uint32_t)popc64(m) : 0u;
     }
 }
 
@@ -457,21 +469,21 @@ __global__ __launch_bounds__(kScanWaves * kWave) void tile_scan_kernel(
 constexpr int kStartsThreads = 1024;
 __global__ __launch_bounds__(kStartsThreads) void tile_starts_kernel(
     int T, const uint32_t* __restrict__ ttotal, uint64_t m, int2* __restrict__ ranges,
-    int* __restrict__ err) {
+    int* __restrict__ err, bool at_most) {
     __shared__ uint32_t s_w[kStartsThreads / kWave];
-    tile_starts_body<kStartsThreads>(T, ttotal, m, ranges, err, s_w);
+    tile_starts_body<kStartsThreads>(T, ttotal, m, ranges, err, s_w, at_most);
 }
 
 // Each segment entry's Gaussian id into the lists of the tiles it covers, at
 // the tile's start + the segment's prefix + the lane's rank.  The tile masks
 // rows[t / 8] & cols[t % 8] are wave-uniform.  Positions at or beyond m are
-// dropped.
+// dropped, and so are the entries of skipped tiles (skip optional).
 __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
     int n, BlockGrid bg, const uint32_t* __restrict__ seg_owner,
     const uint32_t* __restrict__ seg_start, const uint32_t* __restrict__ block_start,
     const uint32_t* __restrict__ lists, uint64_t cap, const uint16_t* __restrict__ lrects,
     uint32_t seg_cap, const uint32_t* __restrict__ tcount, const int2* __restrict__ ranges,
-    uint64_t m, uint32_t* __restrict__ ids) {
+    uint64_t m, uint32_t* __restrict__ ids, const uint8_t* __restrict__ skip) {
     const uint32_t nseg = min(uniform(seg_start[bg.nb]), seg_cap);
     const uint32_t stride = gridDim.x * kWavesPer;
     const int lane = lane_id();
@@ -480,16 +492,20 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
         const SegInfo I = seg_info(k, seg_owner, seg_start, block_start, bg.bw, bg.nb);
         const SegLane S = seg_lane<true>(lists, lrects, I.first, I.end, cap, n);
         // lane t: where segment k's entries of tile t begin (its list start
-        // plus the segment's prefix); the block's first tile has the lowest
-        // list start, b0, and each run is addressed from ids + b0
+        // plus the segment's prefix); the block's first built tile (lists are
+        // laid out in row-major tile order) has the lowest list start, b0,
+        // and each run is addressed from ids + b0
         const int tx = I.ox + (lane & 7), ty = I.oy + (lane >> 3);
-        const bool on = tx < bg.tiles_x && ty < bg.tiles_y;
+        const bool on = lane_tile_live(bg, I.ox, I.oy, skip);
+        // bit t: tile t's list is built (scalar)
+        const uint64_t live = ballot(on);
         uint32_t lstart = 0, base = 0;
         if (on) {
             lstart = (uint32_t)ranges[(size_t)ty * bg.tiles_x + tx].x;
             base = lstart + tcount[(size_t)k * kWave + lane];
         }
-        const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane((int)lstart, 0);
+        const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane(
+            (int)lstart, live ? (int)__builtin_ctzll(live) : 0);
         // in_row[r] / in_col[c]: this lane covers tile row r / column c; as
         // lane masks they are the ballots, so the lanes of tile (r, c) are
         // selected with scalar ANDs
@@ -513,7 +529,7 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
             const uint32_t dq = run_byte_offset(base, b0, 0u);  // this lane's tile's run
 #pragma unroll
             for (int t = 0; t < 64; ++t) {
-                if (in_row[t >> 3] && in_col[t & 7]) {
+                if (((live >> t) & 1u) && in_row[t >> 3] && in_col[t & 7]) {
                     const uint32_t rank = rank_in(rows[t >> 3] & cols[t & 7]);
                     const uint32_t off =
                         (rank << 2) + (uint32_t)__builtin_amdgcn_readlane((int)dq, t);
@@ -524,7 +540,7 @@ __global__ __launch_bounds__(kThreads) void tile_scatter_kernel(
 #pragma unroll
             for (int t = 0; t < 64; ++t) {
                 const uint64_t mk = rows[t >> 3] & cols[t & 7];
-                if (mk == 0) continue;
+                if (mk == 0 || !((live >> t) & 1u)) continue;
                 const uint64_t p = (uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)base, t) +
                                    (uint64_t)rank_in(mk);
                 if (in_row[t >> 3] && in_col[t & 7] && p < m) ids[p] = S.g;
@@ -618,14 +634,14 @@ hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(tile_count_kernel, dim3(seg_groups(segs)), dim3(kThreads), 0, st, tb.n, bg,
                        tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.lrects,
-                       seg_cap, tb.tcount);
+                       seg_cap, tb.tcount, tb.skip);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(tile_scan_kernel, dim3(bg.nb), dim3(kScanWaves * kWave), 0, st, bg,
                        tb.seg_start, seg_cap, tb.tcount, tb.ttotal);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(tile_starts_kernel, dim3(1), dim3(kStartsThreads), 0, st,
                        bg.tiles_x * bg.tiles_y, tb.ttotal, tb.m,
-                       reinterpret_cast<int2*>(tb.ranges), tb.err);
+                       reinterpret_cast<int2*>(tb.ranges), tb.err, tb.skip != nullptr);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     // Each wave writes its segment's 64 runs to 64 lists.  Once the lists
     // are gigabytes (config c5: 7.4 GB per band, runs of ~13 ids), fewer
@@ -637,7 +653,7 @@ hipError_t launch_tile_binning(const TileBinning& tb, hipStream_t st) {
     hipLaunchKernelGGL(tile_scatter_kernel, dim3(scatter_groups), dim3(kThreads), 0, st, tb.n,
                        bg, tb.seg_owner, tb.seg_start, tb.block_start, tb.lists, tb.m, tb.lrects,
                        seg_cap, tb.tcount, reinterpret_cast<const int2*>(tb.ranges), tb.m,
-                       tb.ids);
+                       tb.ids, tb.skip);
     return hipGetLastError();
 }
 

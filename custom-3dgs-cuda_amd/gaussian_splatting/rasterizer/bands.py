@@ -34,8 +34,9 @@ writes every entry.  So the frame is rendered from two sets of Gaussians:
   final T, n_contrib and the entries its backward walks ([0, max n_contrib))
   are the full render's, bit for bit;
 - then every Gaussian whose tile rectangle (widened by a tile row each way,
-  ``tiles_touch``) meets an unfinished tile, on the tile rows that hold one:
-  each unfinished tile's list is then its full list.
+  ``tiles_touch``) meets an unfinished tile, on the tile rows that hold one,
+  with the finished tiles' lists left empty (``tile_skip``): each unfinished
+  tile's list is then its full list.
 The image takes each tile from the pass that owns it; each pass's backward
 walks only its own tiles (the other pass's tile ranges are emptied), and the
 two passes' gradient sums are added per Gaussian.  The image is a full
@@ -177,7 +178,10 @@ class _Pass:
         self.sel, self.rows, self.bands = sel, rows, []
 
 
-def _render_pass(crc, ps: _Pass, n, order, depths, mean_2d, cov_2d, colors, opacity, width):
+def _render_pass(crc, ps: _Pass, n, order, depths, mean_2d, cov_2d, colors, opacity, width,
+                 skip=None):
+    """Renders the pass's bands; ``skip`` (the frame's [ceil(H/16), ceil(W/16)]
+    bool tiles) marks tiles whose lists may be left empty."""
     if ps.sel is None:
         m, od, dp, mn, cv, cl, op = n, order, depths, mean_2d, cov_2d, colors, opacity
     else:
@@ -188,8 +192,12 @@ def _render_pass(crc, ps: _Pass, n, order, depths, mean_2d, cov_2d, colors, opac
         cl, op = colors[ps.sel], opacity[ps.sel]
     for y0, h in ps.rows:
         mean_b = mn - mn.new_tensor([0.0, float(y0)])
+        band_skip = None
+        if skip is not None:
+            r0 = y0 // TILE
+            band_skip = skip[r0:r0 + (h + TILE - 1) // TILE].contiguous().view(t.uint8)
         img, ids, ranges, final_T, n_contrib = crc.rasterize_ordered(
-            m, od, dp, mean_b, cv, cl, op, h, width)
+            m, od, dp, mean_b, cv, cl, op, h, width, band_skip)
         ps.bands.append([img, mean_b, ids, ranges, final_T, n_contrib])
 
 
@@ -238,8 +246,10 @@ def _render_depth_prefix(crc, prefix, n, order, depths, mean_2d, cov_2d, colors,
             second = _Pass(sel, None)
             second.rows = _plan_rows(mean_2d[sel], cov_2d[sel], height, width, max_pairs,
                                      open_tiles.any(dim=1).tolist())
+            # the finished tiles' lists stay empty: the second set's Gaussians
+            # also cover many of them
             _render_pass(crc, second, n, order, depths, mean_2d, cov_2d, colors, opacity,
-                         width)
+                         width, skip=~open_tiles)
             for (y0, h), b in zip(second.rows, second.bands):
                 own = _tile_pixels(open_tiles, y0, h, width)
                 image[y0:y0 + h] = t.where(own[..., None], b[0], image[y0:y0 + h])
@@ -249,7 +259,9 @@ def _render_depth_prefix(crc, prefix, n, order, depths, mean_2d, cov_2d, colors,
                 r0 = y0 // TILE
                 b[3][open_tiles[r0:r0 + (h + TILE - 1) // TILE].reshape(-1)] = 0
             stats["second_bands"] = len(second.rows)
-            stats["second_pairs"] = sum(int(b[2].numel()) for b in second.bands)
+            # the pairs binned: the lists of the open tiles (sorted_ids keeps
+            # the room of every tile the set covers)
+            stats["second_pairs"] = sum(int((b[3][:, 1] - b[3][:, 0]).sum()) for b in second.bands)
             passes.append(second)
     return image, passes, stats
 

@@ -133,6 +133,22 @@ int gsr_depth_order(int n, const float* depth, void* ws, size_t ws_bytes, int32_
 int gsr_rasterize_bin_ordered(int n, const int32_t* order, const float* mean2d,
                               const float* cov2d, int height, int width, void* bin_ws,
                               size_t bin_ws_bytes, int64_t* num_pairs, void* stream);
+
+/* No counterpart in the reference (depth-prefix rendering of screen bands):
+ * gsr_rasterize_render with tile_skip (device, one byte per tile of the
+ * height x width screen, row-major): the lists of tiles marked nonzero may be
+ * left empty (their ranges (0, 0), their pixels then blend nothing); every
+ * other tile's list, range offsets aside, and its image, final_T and n_contrib
+ * are gsr_rasterize_render's.  The block binning leaves them empty, so the
+ * lists hold fewer than num_pairs entries (sorted_ids keeps its num_pairs
+ * room); the tile-sort binning (screens beyond 8192 8x8-tile blocks) builds
+ * them as usual. */
+int gsr_rasterize_render_skip(int n, const float* depth, const float* mean2d, const float* cov2d,
+                              const float* colors, const float* alpha, int height, int width,
+                              void* bin_ws, size_t bin_ws_bytes, int64_t num_pairs,
+                              void* sort_ws, size_t sort_ws_bytes, const uint8_t* tile_skip,
+                              int32_t* sorted_ids, int32_t* tile_ranges, float* img,
+                              float* final_T, int32_t* n_contrib, void* stream);
 /* Synchronizes `stream`, then reads and clears the current device's status
  * word: GSR_ERR_DEVICE if a kernel queued on the device since the status was
  * last read hit its look-back spin bound or found inconsistent counts.

@@ -226,6 +226,42 @@ def test_tiles_touch_flags_the_gaussians_of_marked_tiles(crc, device):
     assert not none.any()
 
 
+@pytest.mark.parametrize("order_kind", ["depth_order", "subset"])
+def test_tile_skip_leaves_only_the_marked_lists_empty(crc, device, order_kind):
+    """rasterize_ordered with tile_skip against the same call without: every
+    unmarked tile's list (its ids), image, final T and n_contrib bit for bit,
+    every marked tile's range (0, 0) and its pixels blended from nothing (T 1,
+    n_contrib 0, black), the lists' total the unmarked tiles' pairs; for the
+    frame's depth order and for a subset of the Gaussians in depth order with
+    the identity order (as depth-prefix rendering calls it)."""
+    sc = synthetic.config_scene("c3", device=device, n=20_000, width=480, height=272)
+    g, view = sc.gaussians, sc.view
+    H, W, ty, tx = 272, 480, 17, 30
+    n, m2, c2, d, col = _project(crc, g, view)
+    op = torch.sigmoid(g.alpha.detach())
+    order = crc.depth_order(n, d)
+    if order_kind == "subset":
+        sel = order[::3].long()
+        n = int(sel.numel())
+        order = torch.arange(n, dtype=torch.int32, device=device)
+        m2, c2, d, col, op = m2[sel], c2[sel], d[sel], col[sel], op[sel]
+    skip = torch.rand(ty, tx, generator=torch.Generator().manual_seed(7)) < 0.4
+    full = crc.rasterize_ordered(n, order, d, m2, c2, col, op, H, W)
+    part = crc.rasterize_ordered(n, order, d, m2, c2, col, op, H, W, skip.to(device))
+    rf, rp = _np(full[2]).reshape(-1, 2), _np(part[2]).reshape(-1, 2)
+    idf, idp = _np(full[1]), _np(part[1])
+    sk = skip.numpy().reshape(-1)
+    assert (rp[sk] == 0).all()
+    for t in np.flatnonzero(~sk):
+        assert_bitwise(idp[rp[t, 0]:rp[t, 1]], idf[rf[t, 0]:rf[t, 1]], f"ids of tile {t}")
+    assert int((rp[:, 1] - rp[:, 0]).sum()) == int((rf[~sk, 1] - rf[~sk, 0]).sum())
+    pix = np.repeat(np.repeat(skip.numpy(), 16, 0), 16, 1)[:H, :W]
+    for k, nm in ((0, "image"), (3, "final_T"), (4, "n_contrib")):
+        assert_bitwise(_np(part[k])[~pix], _np(full[k])[~pix], nm)
+    assert (_np(part[0])[pix] == 0).all() and (_np(part[3])[pix] == 1).all()
+    assert (_np(part[4])[pix] == 0).all()
+
+
 class _TailCapture:
     """Stands in for the extension module: records the four rasterize-backward
     gradients (d mean2d, d cov2d, d colour, d opacity) that the glue hands to
