@@ -66,7 +66,7 @@ MAX_BAND_PAIRS = 2**31 - 2**16
 BAND_PAIR_BUDGET = MAX_BAND_PAIRS - (MAX_BAND_PAIRS >> 7)
 # Depth-prefix rendering: the share of the depth order the first pass renders
 # when rasterize_bands picks the mode itself.
-PREFIX_FRACTION = 1.0 / 32
+PREFIX_FRACTION = 1.0 / 64
 # A pixel's blend stops once T falls below this (rasterize.cu:264-267).
 T_MIN = 1e-4
 # The last forward's passes, bands and pairs (rasterize_bands).
