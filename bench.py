@@ -606,7 +606,7 @@ def banded_frame(sc, band_height: int | None, steps: int) -> dict:
     fwd, bwd, total, _ = time_frames(sc, steps, 1, profile=False, render=render, grad=G)
     _, _, _, stages = time_frames(sc, 1, 0, profile=True, render=render, grad=G)
     from gaussian_splatting.rasterizer import bands as bands_mod
-    prefix_stats = dict(bands_mod.last_stats)
+    prefix_stats = bands_mod.prefix_stats()
     print(f"[bench] {sc.name}: {total:.1f} ms per frame ({prefix_stats})", file=sys.stderr,
           flush=True)
     torch.cuda.empty_cache()

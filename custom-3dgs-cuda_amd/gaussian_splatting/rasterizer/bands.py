@@ -69,8 +69,15 @@ BAND_PAIR_BUDGET = MAX_BAND_PAIRS - (MAX_BAND_PAIRS >> 7)
 PREFIX_FRACTION = 1.0 / 64
 # A pixel's blend stops once T falls below this (rasterize.cu:264-267).
 T_MIN = 1e-4
-# The last forward's passes, bands and pairs (rasterize_bands).
+# The last forward's passes, bands and pairs (rasterize_bands; prefix_stats()
+# gives them with the device-side counts read back).
 last_stats: dict = {}
+
+
+def prefix_stats() -> dict:
+    """last_stats with every count a Python int (device counts are read here,
+    not in the forward, so the forward does not wait for its own kernels)."""
+    return {k: (int(v) if isinstance(v, t.Tensor) else v) for k, v in last_stats.items()}
 
 
 def plan_bands(row_pairs, height: int, max_pairs: int = BAND_PAIR_BUDGET) -> list[tuple[int, int]]:
@@ -233,19 +240,23 @@ def _render_depth_prefix(crc, prefix, n, order, depths, mean_2d, cov_2d, colors,
     # later Gaussians of its list are never reached
     t_min = t.tensor(T_MIN, dtype=final_T.dtype, device=final_T.device)
     open_tiles = ~_tile_all(final_T < t_min, height, width)
+    # one read-back: the unfinished tiles' count, then per tile row whether it holds any
+    row_open = open_tiles.any(dim=1)
+    counts = t.cat([open_tiles.sum().view(1), row_open.to(t.int64)]).cpu()
+    n_open, row_flags = int(counts[0]), counts[1:].bool().tolist()
     stats = {"prefix": int(prefix), "first_bands": len(first.rows),
              "first_pairs": sum(int(b[2].numel()) for b in first.bands),
-             "open_tiles": int(open_tiles.sum()), "tiles": ty * tx,
+             "open_tiles": n_open, "tiles": ty * tx,
              "second_gaussians": 0, "second_bands": 0, "second_pairs": 0}
     passes = [first]
-    if stats["open_tiles"]:
+    if n_open:
         touch = crc.tiles_touch(n, mean_2d, cov_2d, height, width, open_tiles)
         sel = order[touch[order.long()]].long()
         stats["second_gaussians"] = int(sel.numel())
         if sel.numel():
             second = _Pass(sel, None)
             second.rows = _plan_rows(mean_2d[sel], cov_2d[sel], height, width, max_pairs,
-                                     open_tiles.any(dim=1).tolist())
+                                     row_flags)
             # the finished tiles' lists stay empty: the second set's Gaussians
             # also cover many of them
             _render_pass(crc, second, n, order, depths, mean_2d, cov_2d, colors, opacity,
@@ -254,14 +265,15 @@ def _render_depth_prefix(crc, prefix, n, order, depths, mean_2d, cov_2d, colors,
                 own = _tile_pixels(open_tiles, y0, h, width)
                 image[y0:y0 + h] = t.where(own[..., None], b[0], image[y0:y0 + h])
                 r0 = y0 // TILE
-                b[3][~open_tiles[r0:r0 + (h + TILE - 1) // TILE].reshape(-1)] = 0
+                b[3].masked_fill_(~open_tiles[r0:r0 + (h + TILE - 1) // TILE].reshape(-1, 1), 0)
             for (y0, h), b in zip(first.rows, first.bands):
                 r0 = y0 // TILE
-                b[3][open_tiles[r0:r0 + (h + TILE - 1) // TILE].reshape(-1)] = 0
+                b[3].masked_fill_(open_tiles[r0:r0 + (h + TILE - 1) // TILE].reshape(-1, 1), 0)
             stats["second_bands"] = len(second.rows)
             # the pairs binned: the lists of the open tiles (sorted_ids keeps
-            # the room of every tile the set covers)
-            stats["second_pairs"] = sum(int((b[3][:, 1] - b[3][:, 0]).sum()) for b in second.bands)
+            # the room of every tile the set covers); a device count, read by
+            # prefix_stats()
+            stats["second_pairs"] = sum((b[3][:, 1] - b[3][:, 0]).sum() for b in second.bands)
             passes.append(second)
     return image, passes, stats
 
@@ -379,8 +391,8 @@ def rasterize_bands(gaussians: gaussian, view: dict, band_height: int | None = N
     depth-prefix rendering (module docstring); 0 renders every Gaussian in
     every band; None (default) takes PREFIX_FRACTION for frames that need more
     than one planned band and 0 otherwise.  The image is the same either way;
-    the gradients are the same sums in another order.  ``last_stats`` holds
-    the last forward's passes, bands and pairs."""
+    the gradients are the same sums in another order.  ``prefix_stats()``
+    gives the last forward's passes, bands and pairs."""
     RasterizeFunction.last_mean2d_grad = None
     RasterizeFunction.last_radii2d = None
     if band_height is not None:

@@ -322,7 +322,7 @@ def test_depth_prefix_equals_the_whole_frame(crc, device, monkeypatch):
     for prefix, bands in ((0.3, 1), (0.1, 3)):
         budget = BAND_PAIR_BUDGET if bands == 1 else max(max(rows), sum(rows) // 8)
         pi, pb = run(lambda: rasterize_bands(g, view, max_pairs=budget, depth_prefix=prefix))
-        st = dict(bands_mod.last_stats)
+        st = bands_mod.prefix_stats()
         print(f"[gpu] depth prefix {prefix}: {st}", flush=True)
         assert st["prefix"] == math.ceil(n * prefix)
         assert 0 < st["open_tiles"] < st["tiles"] and st["second_pairs"] > 0
@@ -447,7 +447,7 @@ def test_c5_full_size_in_screen_bands(crc, device, monkeypatch):
 
     # the default: depth-prefix rendering (the frame needs several bands)
     img, g1 = frame()
-    st = dict(bands_mod.last_stats)
+    st = bands_mod.prefix_stats()
     print(f"[gpu] c5 depth-prefix frame: {st}", flush=True)
     assert st["prefix"] == math.ceil(n * bands_mod.PREFIX_FRACTION)
     assert st["first_pairs"] + st["second_pairs"] < sum(planned) // 2
